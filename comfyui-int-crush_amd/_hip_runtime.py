@@ -1,0 +1,516 @@
+"""HIP kernel runtime for INT-Crush on MI355X (gfx950).
+
+Counterpart of the reference's _triton_runtime.py:1-130: it loads the
+hand-written gfx950 kernels (libintcrush_gfx950.so, C ABI in include/intcrush.h)
+through ctypes, exposes one Python callable per kernel with the reference's
+signatures, and publishes availability flags plus the USE_FUSED_W8A8 /
+USE_CUDA_GRAPHS toggles and the INTCRUSH_NO_CUDA_GRAPHS environment switch.
+
+Differences from the reference runtime:
+  * there is no silent degradation for device tensors: every callable raises
+    RuntimeError when the library is missing or a kernel reports an error;
+  * the only CPU branch is the one the reference itself documents for
+    dynamic_quantize_activation on CPU tensors (kernels/triton_quantize.py:176-179);
+  * the flags keep the reference names (TRITON_*) as aliases of the HIP ones so
+    that code written against the reference runtime keeps working.
+
+Every kernel is enqueued on torch's current stream of the tensor's device, with
+no host synchronisation, so all callables may be captured into a hipGraph
+(torch.cuda.CUDAGraph) provided the caller pre-allocates the outputs.
+"""
+from __future__ import annotations
+
+import ctypes
+import logging
+import os
+
+import torch
+
+log = logging.getLogger(__name__)
+
+LIB_NAME = "libintcrush_gfx950.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+IC_DTYPE_F16, IC_DTYPE_BF16, IC_DTYPE_F32 = 0, 1, 2
+_DT_CODE = {torch.float16: IC_DTYPE_F16, torch.bfloat16: IC_DTYPE_BF16, torch.float32: IC_DTYPE_F32}
+VALID_ROT_SIZES = (0, 16, 64, 256, 1024, 4096)
+
+# ── Availability flags (reference names below) ──────────────────────────────
+KERNELS_AVAILABLE = False
+HIP_DYNQUANT = False
+HIP_ROTATE_QUANT = False
+HIP_INT8_GEMM = False
+HIP_W4A8_GEMM = False
+HIP_W4A16_GEMM = False
+HIP_INT4_UNPACK = False
+HIP_INT4_INT8_UNPACK = False
+HIP_FUSED_QGD = False
+LOAD_ERROR: str | None = None
+
+# ── User toggles (same meaning as _triton_runtime.py:24-32, :60-61) ─────────
+USE_FUSED_W8A8: bool = False
+USE_CUDA_GRAPHS: bool = True
+if os.environ.get("INTCRUSH_NO_CUDA_GRAPHS", "0") == "1":
+    USE_CUDA_GRAPHS = False
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+# name -> (argtypes, restype); kept in the order of include/intcrush.h
+SIGNATURES: dict[str, tuple[list, object]] = {
+    "ic_version": ([], ctypes.c_char_p),
+    "ic_last_error": ([], ctypes.c_char_p),
+    "ic_max_fused_row": ([], _L),
+    "ic_smoothrot_prepare": ([_P, _L, _I, _P, _P, _P], _I),
+    "ic_rotate_quantize": ([_P, _I, _L, _L, _L, _P, _P, _I, _L, _P, _P, _P, _P, _L, _P, _P], _I),
+    "ic_prepare_activation": ([_P, _I, _L, _L, _L, _P, _P, _I, _L, _P, _P, _P, _P, _L, _P], _I),
+    "ic_dynamic_quantize": ([_P, _I, _L, _L, _L, _P, _L, _P, _P], _I),
+    "ic_gemm_w8a8": ([_P, _L, _L, _L, _P, _L, _L, _P, _P, _P, _I, _P, _I, _L, _P], _I),
+    "ic_gemm_w4a8": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _P, _I, _P, _I, _L, _P], _I),
+    "ic_gemm_w4a16": ([_P, _I, _L, _L, _L, _P, _L, _L, _P, _L, _P, _I, _P, _L, _P], _I),
+    "ic_unpack_int4_to_int8": ([_P, _L, _L, _L, _P, _L, _P], _I),
+    "ic_unpack_int4_to_float": ([_P, _P, _L, _L, _L, _L, _P, _I, _L, _P], _I),
+    "ic_gemm_w8a8_acc_i32": ([_P, _L, _L, _L, _P, _L, _L, _P, _I, _P], _I),
+    "ic_gemm_w4a8_acc_i32": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _I, _P], _I),
+    "ic_gemm_w8a8_generic": ([_P, _L, _L, _L, _P, _L, _L, _P, _P, _P, _I, _P, _I, _L, _P], _I),
+}
+
+_lib = None
+
+
+def _load():
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (args, res) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    return lib
+
+
+def load_library(reload: bool = False):
+    """(Re)load the shared library and refresh the availability flags."""
+    global _lib, LOAD_ERROR
+    if _lib is not None and not reload:
+        return _lib
+    try:
+        _lib = _load()
+        LOAD_ERROR = None
+        log.info("[INT-Crush] HIP kernels loaded: %s", _lib.ic_version().decode())
+    except (OSError, AttributeError) as exc:
+        _lib = None
+        LOAD_ERROR = f"{type(exc).__name__}: {exc}"
+        log.debug("[INT-Crush] HIP kernels not available: %s", LOAD_ERROR)
+    _set_flags(_lib is not None)
+    return _lib
+
+
+def _set_flags(ok: bool) -> None:
+    g = globals()
+    for name in ("KERNELS_AVAILABLE", "HIP_DYNQUANT", "HIP_ROTATE_QUANT", "HIP_INT8_GEMM",
+                 "HIP_W4A8_GEMM", "HIP_W4A16_GEMM", "HIP_INT4_UNPACK", "HIP_INT4_INT8_UNPACK",
+                 "HIP_FUSED_QGD"):
+        g[name] = ok
+    # reference flag names (_triton_runtime.py:16-22, :74-81)
+    g["TRITON_AVAILABLE"] = ok
+    g["TRITON_INT4_UNPACK"] = ok
+    g["TRITON_INT8_GEMM"] = ok
+    g["TRITON_INT4_INT8_UNPACK"] = ok
+    g["TRITON_DYNQUANT"] = ok
+    g["TRITON_W4A8_GEMM"] = ok
+    g["TRITON_FUSED_QGD"] = ok
+
+
+TRITON_AVAILABLE = TRITON_INT4_UNPACK = TRITON_INT8_GEMM = TRITON_INT4_INT8_UNPACK = False
+TRITON_DYNQUANT = TRITON_W4A8_GEMM = TRITON_FUSED_QGD = False
+load_library()
+
+
+# ── helpers ─────────────────────────────────────────────────────────────────
+def lib():
+    if _lib is None:
+        raise RuntimeError(
+            f"INT-Crush gfx950 kernels are not loaded ({LOAD_ERROR}); build them with "
+            "__graft_entry__.build() or comfyui-int-crush_amd/_build_lib.py")
+    return _lib
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _call(name: str, *args) -> None:
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        raise RuntimeError(f"[INT-Crush] {name} failed ({rc}): {lib().ic_last_error().decode()}")
+
+
+def _dt(t: torch.dtype, who: str) -> int:
+    if t not in _DT_CODE:
+        raise TypeError(f"{who}: unsupported dtype {t} (expected float16, bfloat16 or float32)")
+    return _DT_CODE[t]
+
+
+def _need_cuda(*tensors: torch.Tensor | None) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError("INT-Crush HIP kernels need device tensors; got a CPU tensor")
+
+
+def _rows(t: torch.Tensor) -> torch.Tensor:
+    """2-D view with unit column stride (copy only when required)."""
+    t2 = t.reshape(-1, t.shape[-1])
+    if t2.stride(-1) != 1 or (t2.shape[0] > 1 and t2.stride(0) < t2.shape[1]):
+        t2 = t2.contiguous()
+    return t2
+
+
+def _alloc_or_reuse(shape, dtype, device, existing):
+    """kernels/triton_quantize.py:57-66: reuse a matching pre-allocated buffer."""
+    if existing is not None and tuple(existing.shape) == tuple(shape) and existing.dtype == dtype:
+        return existing
+    return torch.empty(shape, dtype=dtype, device=device)
+
+
+# ── SmoothRot / SmoothQuant factors ─────────────────────────────────────────
+class PreparedFactors:
+    """Per-channel divide factors rounded to the activation dtype plus their
+    reciprocals (ic_smoothrot_prepare); built once per layer and dtype."""
+
+    __slots__ = ("fdt", "rcp", "dtype", "K")
+
+    def __init__(self, factors: torch.Tensor, dtype: torch.dtype):
+        _need_cuda(factors)
+        f = factors.detach().reshape(-1).to(torch.float32).contiguous()
+        self.K = f.numel()
+        self.dtype = dtype
+        self.fdt = torch.empty_like(f)
+        self.rcp = torch.empty_like(f)
+        with torch.cuda.device(f.device):
+            _call("ic_smoothrot_prepare", _ptr(f), self.K, _dt(dtype, "prepare_factors"),
+                  _ptr(self.fdt), _ptr(self.rcp), _stream(f))
+
+
+def prepare_factors(factors: torch.Tensor | None, dtype: torch.dtype) -> PreparedFactors | None:
+    return None if factors is None else PreparedFactors(factors, dtype)
+
+
+def prepare_perm(perm: torch.Tensor | None, width: int | None = None) -> torch.Tensor | None:
+    """PermuQuant indices as a contiguous int32 device tensor, range-checked once."""
+    if perm is None:
+        return None
+    p = perm.detach().reshape(-1)
+    if width is not None and p.numel() != width:
+        raise ValueError(f"perm has {p.numel()} entries, expected {width}")
+    if p.numel() and (int(p.min()) < 0 or int(p.max()) >= p.numel()):
+        raise ValueError("perm entries must lie in [0, len(perm))")
+    return p.to(torch.int32).contiguous()
+
+
+# ── fused prep + quantization ───────────────────────────────────────────────
+def rotate_quantize(x: torch.Tensor, *, rot_size: int = 0, w_in: int | None = None,
+                    smoothrot: PreparedFactors | None = None, perm: torch.Tensor | None = None,
+                    smooth: PreparedFactors | None = None, s_a_out: torch.Tensor | None = None,
+                    x_int8_out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """SmoothRot divide -> Hadamard(rot_size) -> pad to w_in -> perm gather ->
+    old-smooth divide -> per-token INT8 quant, one kernel (one HBM pass).
+
+    Semantics of _ops.py:337-365 + :529-533 followed by
+    dynamic_quantize_activation (kernels/triton_quantize.py:151-198).
+    Returns (x_int8 [M, w_in], s_a [M] float32).
+    """
+    _need_cuda(x)
+    x2 = _rows(x)
+    M, K_in = x2.shape
+    R = int(rot_size)
+    if R not in VALID_ROT_SIZES:
+        raise ValueError(f"rot_size must be one of {VALID_ROT_SIZES}, got {R}")
+    K_r = ((K_in + R - 1) // R) * R if R else K_in
+    K_w = max(int(w_in) if w_in is not None else K_r, K_r)
+    dt = _dt(x2.dtype, "rotate_quantize")
+    for f in (smoothrot, smooth):
+        if f is not None and f.dtype != x2.dtype:
+            raise ValueError("prepared factors were built for another activation dtype")
+    if smoothrot is not None and smoothrot.K != K_in:
+        raise ValueError(f"SmoothRot factors have {smoothrot.K} entries, expected {K_in}")
+    if smooth is not None and smooth.K != K_w:
+        raise ValueError(f"smooth factors have {smooth.K} entries, expected {K_w}")
+    if perm is not None and (perm.dtype != torch.int32 or perm.numel() != K_w or not perm.is_cuda):
+        raise ValueError("perm must be an int32 device tensor of length w_in (see prepare_perm)")
+    s_a = _alloc_or_reuse((M,), torch.float32, x2.device, s_a_out)
+    q = _alloc_or_reuse((M, K_w), torch.int8, x2.device, x_int8_out)
+    with torch.cuda.device(x2.device):
+        if K_w <= lib().ic_max_fused_row() // (2 if dt == IC_DTYPE_F32 else 1):
+            _call("ic_rotate_quantize", _ptr(x2), dt, M, K_in, x2.stride(0),
+                  _ptr(smoothrot.rcp) if smoothrot else None, _ptr(smoothrot.fdt) if smoothrot else None,
+                  R, K_w, _ptr(perm), _ptr(smooth.rcp) if smooth else None,
+                  _ptr(smooth.fdt) if smooth else None, _ptr(q), q.stride(0), _ptr(s_a), _stream(x2))
+        else:
+            # rows wider than one workgroup holds: prepare, then quantize (two passes)
+            y = prepare_activation(x2, rot_size=R, w_in=K_w, smoothrot=smoothrot, perm=perm, smooth=smooth)
+            _call("ic_dynamic_quantize", _ptr(y), dt, M, K_w, y.stride(0), _ptr(q), q.stride(0),
+                  _ptr(s_a), _stream(y))
+    return q, s_a
+
+
+def prepare_activation(x: torch.Tensor, *, rot_size: int = 0, w_in: int | None = None,
+                       smoothrot: PreparedFactors | None = None, perm: torch.Tensor | None = None,
+                       smooth: PreparedFactors | None = None,
+                       out: torch.Tensor | None = None) -> torch.Tensor:
+    """_prep_activation (_ops.py:337-365) on the GPU, result in x.dtype [M, w_in]."""
+    _need_cuda(x)
+    x2 = _rows(x)
+    M, K_in = x2.shape
+    R = int(rot_size)
+    if R not in VALID_ROT_SIZES:
+        raise ValueError(f"rot_size must be one of {VALID_ROT_SIZES}, got {R}")
+    K_r = ((K_in + R - 1) // R) * R if R else K_in
+    K_w = max(int(w_in) if w_in is not None else K_r, K_r)
+    dt = _dt(x2.dtype, "prepare_activation")
+    lim = lib().ic_max_fused_row() // (2 if dt == IC_DTYPE_F32 else 1)
+    if K_w > lim:
+        raise ValueError(f"prepare_activation: rows wider than {lim} are not supported")
+    if perm is not None and (perm.dtype != torch.int32 or perm.numel() != K_w):
+        raise ValueError("perm must be an int32 device tensor of length w_in (see prepare_perm)")
+    y = _alloc_or_reuse((M, K_w), x2.dtype, x2.device, out)
+    with torch.cuda.device(x2.device):
+        _call("ic_prepare_activation", _ptr(x2), dt, M, K_in, x2.stride(0),
+              _ptr(smoothrot.rcp) if smoothrot else None, _ptr(smoothrot.fdt) if smoothrot else None,
+              R, K_w, _ptr(perm), _ptr(smooth.rcp) if smooth else None,
+              _ptr(smooth.fdt) if smooth else None, _ptr(y), y.stride(0), _stream(x2))
+    return y
+
+
+def _cpu_per_row_int8_quant(x: torch.Tensor):
+    """Reference CPU semantics, kernels/triton_quantize.py:43-54 (torch.round)."""
+    s_a = x.abs().amax(dim=1).clamp(min=1e-8) / 127.0
+    x_int8 = (x / s_a.unsqueeze(1)).round().clamp(-128, 127).to(torch.int8)
+    return x_int8, s_a
+
+
+def dynamic_quantize_activation(x: torch.Tensor, s_a_out: torch.Tensor | None = None,
+                                x_int8_out: torch.Tensor | None = None):
+    """kernels/triton_quantize.py:151-198: per-token symmetric INT8, s = max|x|/127.
+
+    Device tensors run the gfx950 kernel (rounding q = trunc(x/s +- 0.5), the
+    reference GPU rule); CPU tensors follow the reference CPU branch.
+    """
+    orig_shape = x.shape
+    x2 = x.reshape(-1, x.shape[-1])
+    M, K = x2.shape
+    if not x2.is_cuda:
+        q, s = _cpu_per_row_int8_quant(x2.to(torch.float32))
+    else:
+        x2 = _rows(x2)
+        s = _alloc_or_reuse((M,), torch.float32, x2.device, s_a_out)
+        q = _alloc_or_reuse((M, K), torch.int8, x2.device, x_int8_out)
+        with torch.cuda.device(x2.device):
+            _call("ic_dynamic_quantize", _ptr(x2), _dt(x2.dtype, "dynamic_quantize_activation"), M, K,
+                  x2.stride(0), _ptr(q), q.stride(0), _ptr(s), _stream(x2))
+    if orig_shape != x2.shape:
+        q = q.reshape(orig_shape)
+        s = s.reshape(*orig_shape[:-1])
+    return q, s
+
+
+# ── GEMMs ───────────────────────────────────────────────────────────────────
+def _bias_args(bias: torch.Tensor | None, N: int):
+    if bias is None:
+        return None, 0, None
+    b = bias.detach().reshape(-1)
+    if b.numel() != N:
+        raise ValueError(f"bias has {b.numel()} entries, expected {N}")
+    b = b.contiguous()
+    return _ptr(b), _dt(b.dtype, "bias"), b
+
+
+def _out_buffer(out, M, N, out_dtype, device):
+    if out is not None:
+        assert tuple(out.shape) == (M, N), f"out shape mismatch: {tuple(out.shape)} vs ({M}, {N})"
+        assert out.stride(-1) == 1, "out must have unit column stride"
+        return out
+    return torch.empty((M, N), dtype=out_dtype, device=device)
+
+
+def fused_int8_gemm_dequant(x_int8: torch.Tensor, w_int8: torch.Tensor, s_w: torch.Tensor,
+                            s_a: torch.Tensor, bias: torch.Tensor | None = None,
+                            out_dtype: torch.dtype = torch.bfloat16, activation: int = 0,
+                            residual: torch.Tensor | None = None,
+                            out: torch.Tensor | None = None) -> torch.Tensor:
+    """W8A8: f32(x_int8 @ w_int8^T) * (s_a[m] * s_w[n]) + bias, cast to out_dtype.
+
+    Signature of kernels/triton_int8_gemm.py:135-205.  The optional SiLU/GELU
+    and residual epilogues of the reference (unused by its ops layer) are not
+    part of this path.
+    """
+    assert x_int8.dtype == torch.int8, f"x_int8 must be int8, got {x_int8.dtype}"
+    assert w_int8.dtype == torch.int8, f"w_int8 must be int8, got {w_int8.dtype}"
+    if activation != 0 or residual is not None:
+        raise NotImplementedError("activation/residual epilogues are not implemented on gfx950")
+    _need_cuda(x_int8, w_int8, s_w, s_a, bias)
+    M, K = x_int8.shape
+    N, K_w = w_int8.shape
+    assert K == K_w, f"K mismatch: {K} vs {K_w}"
+    xq = _rows(x_int8)
+    w = _rows(w_int8)
+    sw = s_w.detach().reshape(-1).to(torch.float32).contiguous()
+    if sw.numel() != N:
+        raise ValueError(f"s_w must hold one scale per output channel ({N}), got {sw.numel()}")
+    sa = s_a.detach().reshape(-1).to(torch.float32).contiguous()
+    bp, bdt, _keep = _bias_args(bias, N)
+    c = _out_buffer(out, M, N, out_dtype, x_int8.device)
+    with torch.cuda.device(xq.device):
+        _call("ic_gemm_w8a8", _ptr(xq), M, K, xq.stride(0), _ptr(w), N, w.stride(0), _ptr(sa),
+              _ptr(sw), bp, bdt, _ptr(c), _dt(c.dtype, "out"), c.stride(0), _stream(xq))
+    return c
+
+
+def fused_w4a8_gemm_dequant(x_int8, w_int8, s_w, s_a, bias=None, out_dtype=torch.bfloat16, out=None):
+    """kernels/triton_w4a8_gemm.py:111-169: the INT8 GEMM on already unpacked
+    INT4 weights ([N, K] int8, per-row s_w).  gemm_w4a8 is the fused path."""
+    return fused_int8_gemm_dequant(x_int8, w_int8, s_w, s_a, bias=bias, out_dtype=out_dtype, out=out)
+
+
+def gemm_w4a8(x_int8: torch.Tensor, w_packed: torch.Tensor, s_w: torch.Tensor, s_a: torch.Tensor,
+              bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    """W4A8 with the INT4 unpack fused into the GEMM.
+
+    w_packed [N, K/2] uint8; s_w [N, G] (or [N]) float scales, group size K/G.
+    out = (sum_g f32(acc_g) * s_w[n,g]) * s_a[m] + bias  (G > 1)
+    out = f32(acc) * (s_a[m] * s_w[n]) + bias           (G == 1)
+    """
+    assert x_int8.dtype == torch.int8, f"x_int8 must be int8, got {x_int8.dtype}"
+    assert w_packed.dtype == torch.uint8, f"w_packed must be uint8, got {w_packed.dtype}"
+    _need_cuda(x_int8, w_packed, s_w, s_a, bias)
+    xq = _rows(x_int8)
+    M, K = xq.shape
+    N = w_packed.shape[0]
+    assert w_packed.shape[1] * 2 >= K, f"packed weight too narrow for K={K}"
+    w = _rows(w_packed)
+    sw = s_w.detach().reshape(N, -1).to(torch.float32).contiguous()
+    G = sw.shape[1]
+    if K % G:
+        raise ValueError(f"K={K} is not a multiple of the {G} scale groups")
+    sa = s_a.detach().reshape(-1).to(torch.float32).contiguous()
+    bp, bdt, _keep = _bias_args(bias, N)
+    c = _out_buffer(out, M, N, out_dtype, xq.device)
+    with torch.cuda.device(xq.device):
+        _call("ic_gemm_w4a8", _ptr(xq), M, K, xq.stride(0), _ptr(w), N, w.stride(0), _ptr(sw), G,
+              _ptr(sa), bp, bdt, _ptr(c), _dt(c.dtype, "out"), c.stride(0), _stream(xq))
+    return c
+
+
+def gemm_w4a16(x: torch.Tensor, w_packed: torch.Tensor, s_w: torch.Tensor,
+               bias: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """W4A16: x @ RN_dt(q * RN_dt(s))^T (+ bias) in x.dtype (fp16/bf16)."""
+    assert w_packed.dtype == torch.uint8, f"w_packed must be uint8, got {w_packed.dtype}"
+    _need_cuda(x, w_packed, s_w, bias)
+    x2 = _rows(x)
+    M, K = x2.shape
+    N = w_packed.shape[0]
+    assert w_packed.shape[1] * 2 >= K, f"packed weight too narrow for K={K}"
+    w = _rows(w_packed)
+    sw = s_w.detach().reshape(N, -1).to(torch.float32).contiguous()
+    G = sw.shape[1]
+    if K % G:
+        raise ValueError(f"K={K} is not a multiple of the {G} scale groups")
+    dt = _dt(x2.dtype, "gemm_w4a16")
+    if dt == IC_DTYPE_F32:
+        raise TypeError("gemm_w4a16 needs float16 or bfloat16 activations")
+    bp, bdt, _keep = _bias_args(bias, N)
+    c = _out_buffer(out, M, N, x2.dtype, x2.device)
+    with torch.cuda.device(x2.device):
+        _call("ic_gemm_w4a16", _ptr(x2), dt, M, K, x2.stride(0), _ptr(w), N, w.stride(0), _ptr(sw), G,
+              bp, bdt, _ptr(c), c.stride(0), _stream(x2))
+    return c
+
+
+def fused_quant_int8_gemm_dequant(x: torch.Tensor, w_int8: torch.Tensor, s_w: torch.Tensor,
+                                  bias: torch.Tensor | None = None,
+                                  out_dtype: torch.dtype = torch.bfloat16,
+                                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """kernels/triton_int8_gemm.py:331-389: quantize fp16/bf16 x per token, then
+    the W8A8 GEMM (two launches, same numbers as the reference single kernel)."""
+    assert x.dtype in (torch.float16, torch.bfloat16), f"x must be fp16/bf16, got {x.dtype}"
+    assert w_int8.dtype == torch.int8, f"w_int8 must be int8, got {w_int8.dtype}"
+    M, K = x.shape
+    N, K_w = w_int8.shape
+    assert K == K_w, f"K mismatch: {K} vs {K_w}"
+    q, s = dynamic_quantize_activation(x)
+    if out is not None and tuple(out.shape) != (M, N):
+        out = None
+    return fused_int8_gemm_dequant(q, w_int8, s_w, s, bias=bias, out_dtype=out_dtype, out=out)
+
+
+# ── unpack ──────────────────────────────────────────────────────────────────
+def unpack_int4_to_int8(packed: torch.Tensor, K: int) -> torch.Tensor:
+    """kernels/triton_int4_to_int8_unpack.py:55-81: [N, K/2] uint8 -> [N, K] int8."""
+    _need_cuda(packed)
+    p = _rows(packed)
+    N = p.shape[0]
+    out = torch.empty(N, K, dtype=torch.int8, device=p.device)
+    with torch.cuda.device(p.device):
+        _call("ic_unpack_int4_to_int8", _ptr(p), N, K, p.stride(0), _ptr(out), out.stride(0), _stream(p))
+    return out
+
+
+def unpack_int4_to_float(packed: torch.Tensor, scale: torch.Tensor, K: int,
+                         dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """INT4 -> fp16/bf16 with per-row or per-group scale, w = RN_dt(q * RN_dt(s))."""
+    _need_cuda(packed, scale)
+    p = _rows(packed)
+    N = p.shape[0]
+    sw = scale.detach().reshape(N, -1).to(torch.float32).contiguous()
+    G = sw.shape[1]
+    if K % G:
+        raise ValueError(f"K={K} is not a multiple of the {G} scale groups")
+    out = torch.empty(N, K, dtype=dtype, device=p.device)
+    with torch.cuda.device(p.device):
+        _call("ic_unpack_int4_to_float", _ptr(p), _ptr(sw), G, N, K, p.stride(0), _ptr(out),
+              _dt(dtype, "unpack_int4_to_float"), out.stride(0), _stream(p))
+    return out
+
+
+def unpack_int4_to_float16(packed: torch.Tensor, scale: torch.Tensor, K: int) -> torch.Tensor:
+    """kernels/triton_int4_unpack.py:62-88 (scale [N] or [N, G])."""
+    return unpack_int4_to_float(packed, scale, K, torch.float16)
+
+
+# ── debug: raw accumulators ─────────────────────────────────────────────────
+def gemm_acc_i32(x_int8: torch.Tensor, w: torch.Tensor, *, int4: bool = False,
+                 s_w: torch.Tensor | None = None, generic: bool = False) -> torch.Tensor:
+    """int32 accumulators of the production GEMM: [M, N], or [G, M, N] for
+    grouped INT4 weights (s_w [N, G] selects the grouping)."""
+    _need_cuda(x_int8, w, s_w)
+    xq = _rows(x_int8)
+    M, K = xq.shape
+    wr = _rows(w)
+    N = wr.shape[0]
+    with torch.cuda.device(xq.device):
+        if int4:
+            sw = (s_w if s_w is not None else torch.ones(N, 1, device=xq.device)).detach()
+            sw = sw.reshape(N, -1).to(torch.float32).contiguous()
+            G = sw.shape[1]
+            acc = torch.empty((G, M, N) if G > 1 else (M, N), dtype=torch.int32, device=xq.device)
+            _call("ic_gemm_w4a8_acc_i32", _ptr(xq), M, K, xq.stride(0), _ptr(wr), N, wr.stride(0),
+                  _ptr(sw), G, _ptr(acc), 1 if generic else 0, _stream(xq))
+        else:
+            acc = torch.empty((M, N), dtype=torch.int32, device=xq.device)
+            _call("ic_gemm_w8a8_acc_i32", _ptr(xq), M, K, xq.stride(0), _ptr(wr), N, wr.stride(0),
+                  _ptr(acc), 1 if generic else 0, _stream(xq))
+    return acc
+
+
+__all__ = [
+    "KERNELS_AVAILABLE", "TRITON_AVAILABLE", "TRITON_INT4_UNPACK", "TRITON_INT8_GEMM",
+    "TRITON_INT4_INT8_UNPACK", "TRITON_DYNQUANT", "TRITON_W4A8_GEMM", "TRITON_FUSED_QGD",
+    "USE_FUSED_W8A8", "USE_CUDA_GRAPHS", "dynamic_quantize_activation", "fused_int8_gemm_dequant",
+    "fused_quant_int8_gemm_dequant", "fused_w4a8_gemm_dequant", "unpack_int4_to_int8",
+    "unpack_int4_to_float16", "rotate_quantize", "prepare_activation", "gemm_w4a8", "gemm_w4a16",
+    "unpack_int4_to_float", "prepare_factors", "prepare_perm", "PreparedFactors", "gemm_acc_i32",
+    "load_library",
+]

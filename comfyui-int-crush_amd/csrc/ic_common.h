@@ -1,0 +1,142 @@
+// Shared device helpers for the INT-Crush gfx950 kernels.
+//
+// Numeric conventions (all kernels):
+//   * dtype codes follow include/intcrush.h: 0 = fp16, 1 = bf16, 2 = fp32.
+//   * Every float conversion is IEEE round-to-nearest-even.  The library is
+//     built with -ffp-contract=off so that a*b+c is never silently fused;
+//     fused multiply-adds are written explicitly where the algorithm wants them.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/intcrush.h"
+
+#define IC_DEV __device__ __forceinline__
+
+// ---------------------------------------------------------------- host side
+// Thread-local error message + launch checking (defined in capi.cpp).
+int ic_set_error(int code, const char* fmt, ...);
+int ic_check_launch(const char* who);
+
+// Arguments of the fused preparation kernels (internal; the ABI is flat).
+struct ic_rotq_args {
+  const void* x; int dtype; int64_t M, K_in, ldx;
+  const float* sr_rcp; const float* sr_f; int rot_size; int64_t K_w;
+  const int32_t* perm; const float* sm_rcp; const float* sm_f;
+  int8_t* q_out; int64_t ldq; float* s_out;
+  void* y_out; int64_t ldy;
+};
+
+typedef uint16_t u16;
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------- 16-bit floats
+IC_DEV float f16_to_f32(u16 h) { return (float)__builtin_bit_cast(_Float16, h); }
+IC_DEV u16 f32_to_f16(float f) { return __builtin_bit_cast(u16, (_Float16)f); }
+IC_DEV float bf16_to_f32(u16 b) { return __uint_as_float((uint32_t)b << 16); }
+IC_DEV u16 f32_to_bf16(float f) {
+  // Round-to-nearest-even on the bit pattern; NaN stays a quiet NaN.
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u16)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (u16)(u >> 16);
+}
+
+template <int DT> IC_DEV float ld_as_f32(const void* p, int64_t i) {
+  if constexpr (DT == IC_DTYPE_F16) return f16_to_f32(((const u16*)p)[i]);
+  else if constexpr (DT == IC_DTYPE_BF16) return bf16_to_f32(((const u16*)p)[i]);
+  else return ((const float*)p)[i];
+}
+IC_DEV float ld_any_f32(const void* p, int dt, int64_t i) {
+  if (dt == IC_DTYPE_F16) return f16_to_f32(((const u16*)p)[i]);
+  if (dt == IC_DTYPE_BF16) return bf16_to_f32(((const u16*)p)[i]);
+  return ((const float*)p)[i];
+}
+template <int DT> IC_DEV void st_from_f32(void* p, int64_t i, float v) {
+  if constexpr (DT == IC_DTYPE_F16) ((u16*)p)[i] = f32_to_f16(v);
+  else if constexpr (DT == IC_DTYPE_BF16) ((u16*)p)[i] = f32_to_bf16(v);
+  else ((float*)p)[i] = v;
+}
+
+// Round an f32 to the 16-bit activation type and back (RN-even), f32 passes through.
+template <int DT> IC_DEV float round_to_dt(float v) {
+  if constexpr (DT == IC_DTYPE_F16) return f16_to_f32(f32_to_f16(v));
+  else if constexpr (DT == IC_DTYPE_BF16) return bf16_to_f32(f32_to_bf16(v));
+  else return v;
+}
+
+// Smallest positive normal of the activation type: below it the type is
+// subnormal and the reciprocal-multiply shortcut of the divide is not exact.
+template <int DT> IC_DEV constexpr float dt_min_normal() {
+  if constexpr (DT == IC_DTYPE_F16) return 6.103515625e-05f;  // 2^-14
+  else return 1.1754943508222875e-38f;                        // 2^-126
+}
+
+// Correctly rounded RN_dt(x / f) for x, f values of type DT, given
+// rcp = RN32(1/f) and f itself (read only on the slow path).
+// Fast path: RN_dt(RN32(x*rcp)).  Exhaustive CPU checks over every finite
+// (x, f) fp16 and bf16 pair show the fast path equals the exactly rounded
+// quotient unless the product is non-finite or nonzero below the normal range
+// of DT; those lanes take the IEEE f32 divide (RN32 then RN_dt is innocuous
+// for a quotient of two values with <= 11 significant bits).
+template <int DT> IC_DEV float div_round_dt(float x, float rcp, const float* fptr, int64_t k) {
+  if constexpr (DT == IC_DTYPE_F32) {
+    return x / fptr[k];  // f32 activations: the reference divides in f32 directly
+  } else {
+    float p = x * rcp;
+    float ap = __builtin_fabsf(p);
+    bool fast = (ap >= dt_min_normal<DT>() && ap <= 3.4028234663852886e38f) || p == 0.0f;
+    if (__builtin_expect(fast, 1)) return round_to_dt<DT>(p);
+    return round_to_dt<DT>(x / fptr[k]);
+  }
+}
+
+// ------------------------------------------------------------ fp64 -> 16-bit
+// Round-to-odd to 24 significant bits: truncate the 29 low mantissa bits of an
+// fp64 and set the kept LSB if any dropped bit was set.  The result is exactly
+// representable in f32, and RN_dt(rto24(y)) == RN_dt(y) for any 16-bit type
+// (24 >= p + 2 with p <= 11), which is the classic round-to-odd argument.
+IC_DEV float rto24(double y) {
+  uint64_t b = (uint64_t)__double_as_longlong(y);
+  uint32_t lo = (uint32_t)b;
+  uint32_t hi = (uint32_t)(b >> 32);
+  uint32_t sticky = (lo & 0x1fffffffu) ? 1u : 0u;
+  lo = (lo & 0xe0000000u) | (sticky << 29);
+  return (float)__longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// RN of an fp64 value to DT, returned as the f32 holding that exact value.
+template <int DT> IC_DEV float round_f64_to_dt(double y) {
+  if constexpr (DT == IC_DTYPE_F32) return (float)y;
+  else return round_to_dt<DT>(rto24(y));
+}
+
+// ------------------------------------------------------------ quantization
+// Reference rule (triton_quantize.py:133-146): s = max(m, 1e-8)/127 in f32;
+// q = trunc(RN32(RN32(v/s) +- 0.5)) clamped to [-128, 127].  v/s is formed as
+// RN32(v * RN64(1/s)) in fp64, which equals the IEEE f32 quotient for every v
+// with <= 24 significant bits and normal s (the quotient is never an f32
+// midpoint and lies >= 2^-48 relative from one; the fp64 error is < 2^-52).
+IC_DEV float quant_scale(float m) { return __builtin_fmaxf(m, 1e-8f) / 127.0f; }
+IC_DEV int quant_code(float v, double rs) {
+  float q = (float)((double)v * rs);
+  float r = q >= 0.0f ? q + 0.5f : q - 0.5f;
+  int c = (int)r;  // v_cvt_i32_f32 truncates toward zero (saturating)
+  c = c < -128 ? -128 : c;
+  c = c > 127 ? 127 : c;
+  return c;
+}
+
+// ------------------------------------------------------------ reductions
+IC_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}

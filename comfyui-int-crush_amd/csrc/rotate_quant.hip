@@ -1,0 +1,451 @@
+// Fused activation preparation + per-token dynamic INT8 quantization (gfx950).
+//
+// One workgroup (256 threads, 4 waves) owns one activation row.  The row is
+// read from HBM once and the INT8 codes are written once; every intermediate
+// lives in registers or LDS:
+//
+//   x[K_in] (fp16/bf16/f32)
+//     -> SmoothRot divide, rounded to the activation type      (_ops.py:347-350)
+//     -> zero pad to a multiple of R, block Hadamard of size R   (_quant_utils.py:117-147)
+//        computed with fp64 butterflies: exact for fp16 inputs, then rounded
+//        once to the activation type
+//     -> zero pad to K_w                                          (_ops.py:355-358)
+//     -> PermuQuant gather out[j] = rot[perm[j]]                  (_ops.py:360-363)
+//     -> optional old-SmoothQuant divide after the gather         (_ops.py:529-533)
+//     -> per-row abs-max, s = max(m,1e-8)/127, q = trunc(v/s +- 0.5) (triton_quantize.py:109-146)
+//
+// The Hadamard H_R = (H4/2)^{(x)k}, R = 4^k, acts on each base-4 digit of the
+// in-block index with the radix-4 butterfly y_i = s/2 - x_{3-i}, s = sum(x).
+// A tile of 4096 positions is spread as 16 contiguous elements per thread
+// (digits 0-1 in registers); digits 2-3 are reached through one LDS transpose
+// among 16 threads, digits 4-5 through a second transpose among 256 threads.
+#include "ic_common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kTile = 4096;       // positions per tile (kThreads * 16)
+constexpr int kMaxTiles = 4;      // K_w <= 16384 for the fused single-pass kernel
+constexpr int kPadStride = 18;    // 16 doubles + 2 pad per 16-position row of the transpose buffer
+
+IC_DEV void h4(double& a, double& b, double& c, double& d) {
+  double s = (a + b) + (c + d);
+  double ya = __builtin_fma(s, 0.5, -d);
+  double yb = __builtin_fma(s, 0.5, -c);
+  double yc = __builtin_fma(s, 0.5, -b);
+  double yd = __builtin_fma(s, 0.5, -a);
+  a = ya; b = yb; c = yc; d = yd;
+}
+// radix-4 stage on the low / high 2-bit digit of a 16-element register array
+IC_DEV void stage_lo(double* v) {
+#pragma unroll
+  for (int a = 0; a < 4; ++a) h4(v[4 * a + 0], v[4 * a + 1], v[4 * a + 2], v[4 * a + 3]);
+}
+IC_DEV void stage_hi(double* v) {
+#pragma unroll
+  for (int a = 0; a < 4; ++a) h4(v[a], v[4 + a], v[8 + a], v[12 + a]);
+}
+// physical slot of logical position p in the padded transpose buffer
+IC_DEV int tslot(int p) { return p + 2 * (p >> 4); }
+
+template <int DT> IC_DEV u16 f32_bits16(float v) {
+  if constexpr (DT == IC_DTYPE_F16) return f32_to_f16(v);
+  else return f32_to_bf16(v);
+}
+template <int DT> IC_DEV float bits16_f32(u16 b) {
+  if constexpr (DT == IC_DTYPE_F16) return f16_to_f32(b);
+  else return bf16_to_f32(b);
+}
+
+// Load 16 consecutive values starting at element p0 (zero past n) as f32.
+// Whole in-bounds 16-element runs use 16-byte loads when the base is aligned.
+template <int DT> IC_DEV void load16(const void* base, int p0, int n, bool vec_ok, float* out) {
+  constexpr int ESZ = DT == IC_DTYPE_F32 ? 4 : 2;
+  if (vec_ok && p0 + 16 <= n && ((((uintptr_t)base) & 15) == 0)) {
+    const v4u* src = (const v4u*)((const char*)base + (int64_t)p0 * ESZ);
+    if constexpr (ESZ == 2) {
+      v4u a = src[0], b = src[1];
+      uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        out[2 * i] = bits16_f32<DT>((u16)(w[i] & 0xffffu));
+        out[2 * i + 1] = bits16_f32<DT>((u16)(w[i] >> 16));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v4u a = src[i];
+        out[4 * i] = __uint_as_float(a.x);
+        out[4 * i + 1] = __uint_as_float(a.y);
+        out[4 * i + 2] = __uint_as_float(a.z);
+        out[4 * i + 3] = __uint_as_float(a.w);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) out[j] = (p0 + j < n) ? ld_as_f32<DT>(base, p0 + j) : 0.0f;
+  }
+}
+IC_DEV void load16i(const int32_t* base, int p0, int n, int* out) {
+  if (p0 + 16 <= n && ((((uintptr_t)base) & 15) == 0)) {
+    const v4u* src = (const v4u*)(base + p0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v4u a = src[i];
+      out[4 * i] = (int)a.x; out[4 * i + 1] = (int)a.y; out[4 * i + 2] = (int)a.z; out[4 * i + 3] = (int)a.w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) out[j] = (p0 + j < n) ? base[p0 + j] : 0;
+  }
+}
+
+// Layout of register element j of thread t after the rotation phases for rot
+// size class RC (0: none/16, 1: 64/256, 2: 1024/4096), tile-local position.
+template <int RC> IC_DEV int tile_pos(int t, int j) {
+  if constexpr (RC == 0) return 16 * t + j;
+  else if constexpr (RC == 1) return 256 * (t >> 4) + 16 * j + (t & 15);
+  else return 256 * j + t;
+}
+
+// LOG4R: 0 = no rotation, 2..6 = rot size 16..4096.  QUANT: write INT8 codes and
+// scales; otherwise write the prepared activation in the input type.
+template <int DT, int LOG4R, bool QUANT>
+__global__ __launch_bounds__(kThreads) void rotate_quant_kernel(
+    const void* __restrict__ x, int64_t ldx, int K_in,
+    const float* __restrict__ sr_rcp, const float* __restrict__ sr_f,
+    int K_w, const int32_t* __restrict__ perm,
+    const float* __restrict__ sm_rcp, const float* __restrict__ sm_f,
+    int8_t* __restrict__ q_out, int64_t ldq, float* __restrict__ s_out,
+    void* __restrict__ y_out, int64_t ldy) {
+  constexpr int R = LOG4R == 0 ? 1 : (1 << (2 * LOG4R));
+  constexpr int RC = LOG4R <= 2 ? 0 : (LOG4R <= 4 ? 1 : 2);
+  constexpr int ESZ = DT == IC_DTYPE_F32 ? 4 : 2;
+
+  __shared__ double tbuf[kTile / 16 * kPadStride];  // 36 KB; reused as the row buffer
+  __shared__ float red[kThreads / 64];
+
+  const int t = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const char* xrow = (const char*)x + row * ldx * ESZ;
+  const int K_r = LOG4R == 0 ? K_in : ((K_in + R - 1) / R) * R;  // rotated width
+  const bool xvec = ((((uintptr_t)xrow) & 15) == 0);
+  const bool fvec = (sr_rcp == nullptr || (((uintptr_t)sr_rcp) & 15) == 0) &&
+                    (sm_rcp == nullptr || (((uintptr_t)sm_rcp) & 15) == 0);
+  const int ntiles = (K_w + kTile - 1) / kTile;
+
+  // Rotated, rounded values of this thread (exact values of type DT) per tile.
+  float val[kMaxTiles][16];
+
+#pragma unroll
+  for (int tile = 0; tile < kMaxTiles; ++tile) {
+    if (tile >= ntiles) break;
+    const int base = tile * kTile;
+    double v[16];
+    // ---- load + SmoothRot divide (digits 0-1 layout: 16 contiguous positions)
+    const int p0 = base + 16 * t;
+    float xs[16];
+    load16<DT>(xrow, p0, K_in, xvec, xs);
+    if (sr_rcp != nullptr) {
+      float rc[16];
+      load16<IC_DTYPE_F32>(sr_rcp, p0, K_in, fvec, rc);
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (p0 + j < K_in) xs[j] = div_round_dt<DT>(xs[j], rc[j], sr_f, p0 + j);
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = (double)xs[j];
+    if constexpr (LOG4R >= 2) { stage_lo(v); stage_hi(v); }
+    if constexpr (LOG4R >= 3) {
+      __syncthreads();  // previous users of tbuf are done
+#pragma unroll
+      for (int j = 0; j < 16; ++j) tbuf[tslot(16 * t + j)] = v[j];
+      __syncthreads();
+      const int g = t >> 4, l = t & 15;
+#pragma unroll
+      for (int h = 0; h < 16; ++h) v[h] = tbuf[tslot(256 * g + 16 * h + l)];
+      stage_lo(v);
+      if constexpr (LOG4R >= 4) stage_hi(v);
+      if constexpr (LOG4R >= 5) {
+#pragma unroll
+        for (int h = 0; h < 16; ++h) tbuf[tslot(256 * g + 16 * h + l)] = v[h];
+        __syncthreads();
+#pragma unroll
+        for (int gg = 0; gg < 16; ++gg) v[gg] = tbuf[tslot(256 * gg + t)];
+        stage_lo(v);
+        if constexpr (LOG4R >= 6) stage_hi(v);
+      }
+    }
+    // ---- round once to the activation type; positions past the rotated
+    // width are the zero pad to K_w.
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int p = base + tile_pos<(LOG4R == 0 ? 0 : RC)>(t, j);
+      val[tile][j] = p < K_r ? round_f64_to_dt<DT>(v[j]) : 0.0f;
+    }
+  }
+
+  // ---- publish the prepared row (natural order) to LDS for the gather
+  __syncthreads();
+  char* rowbuf = (char*)tbuf;
+#pragma unroll
+  for (int tile = 0; tile < kMaxTiles; ++tile) {
+    if (tile >= ntiles) break;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int p = tile * kTile + tile_pos<(LOG4R == 0 ? 0 : RC)>(t, j);
+      if (p < K_w) {
+        if constexpr (ESZ == 2) ((u16*)rowbuf)[p] = f32_bits16<DT>(val[tile][j]);
+        else ((float*)rowbuf)[p] = val[tile][j];
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- gather (perm), old-smooth divide, abs-max.  Thread t owns output
+  // positions o = 16*(t + 256*c) + j.
+  float m = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kMaxTiles; ++c) {
+    if (c >= ntiles) break;
+    const int o0 = 16 * (t + kThreads * c);
+    int src[16];
+    if (perm != nullptr) {
+      load16i(perm, o0, K_w, src);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) src[j] = o0 + j;
+    }
+    float smr[16];
+    if (sm_rcp != nullptr) load16<IC_DTYPE_F32>(sm_rcp, o0, K_w, fvec, smr);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int o = o0 + j;
+      float vv = 0.0f;
+      if (o < K_w) {
+        // a malformed perm entry reads position 0 instead of leaving the row
+        const int sidx = (unsigned)src[j] < (unsigned)K_w ? src[j] : 0;
+        if constexpr (ESZ == 2) vv = bits16_f32<DT>(((const u16*)rowbuf)[sidx]);
+        else vv = ((const float*)rowbuf)[sidx];
+        if (sm_rcp != nullptr) vv = div_round_dt<DT>(vv, smr[j], sm_f, o);
+      }
+      val[c][j] = vv;
+      m = __builtin_fmaxf(m, __builtin_fabsf(vv));
+    }
+  }
+
+  if constexpr (!QUANT) {
+#pragma unroll
+    for (int c = 0; c < kMaxTiles; ++c) {
+      if (c >= ntiles) break;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int o = 16 * (t + kThreads * c) + j;
+        if (o < K_w) st_from_f32<DT>((char*)y_out + row * ldy * ESZ, o, val[c][j]);
+      }
+    }
+    return;
+  } else {
+    m = wave_max(m);
+    if ((t & 63) == 0) red[t >> 6] = m;
+    __syncthreads();
+    m = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+    const float s = quant_scale(m);
+    const double rs = 1.0 / (double)s;
+    if (t == 0) s_out[row] = s;
+    int8_t* qrow = q_out + row * ldq;
+#pragma unroll
+    for (int c = 0; c < kMaxTiles; ++c) {
+      if (c >= ntiles) break;
+      const int o0 = 16 * (t + kThreads * c);
+      if (o0 >= K_w) break;
+      uint32_t w[4];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const int code = quant_code(val[c][4 * d + b], rs);
+          packed |= ((uint32_t)code & 0xffu) << (8 * b);
+        }
+        w[d] = packed;
+      }
+      if (o0 + 16 <= K_w && ((((uintptr_t)(qrow + o0)) & 15) == 0)) {
+        *(v4u*)(qrow + o0) = v4u{w[0], w[1], w[2], w[3]};
+      } else {
+        for (int j = 0; j < 16 && o0 + j < K_w; ++j) qrow[o0 + j] = (int8_t)(w[j >> 2] >> (8 * (j & 3)));
+      }
+    }
+  }
+}
+
+// Row-streaming two-pass quantizer for rows wider than the fused kernel holds
+// (dynamic_quantize_activation semantics, triton_quantize.py:109-146).
+template <int DT>
+__global__ __launch_bounds__(kThreads) void quant_rows_kernel(
+    const void* __restrict__ x, int64_t ldx, int K, int8_t* __restrict__ q_out, int64_t ldq,
+    float* __restrict__ s_out) {
+  constexpr int ESZ = DT == IC_DTYPE_F32 ? 4 : 2;
+  __shared__ float red[kThreads / 64];
+  const int t = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const char* xrow = (const char*)x + row * ldx * ESZ;
+  float m = 0.0f;
+  for (int k = t; k < K; k += kThreads) m = __builtin_fmaxf(m, __builtin_fabsf(ld_as_f32<DT>(xrow, k)));
+  m = wave_max(m);
+  if ((t & 63) == 0) red[t >> 6] = m;
+  __syncthreads();
+  m = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+  const float s = quant_scale(m);
+  const double rs = 1.0 / (double)s;
+  if (t == 0) s_out[row] = s;
+  for (int k = t; k < K; k += kThreads) q_out[row * ldq + k] = (int8_t)quant_code(ld_as_f32<DT>(xrow, k), rs);
+}
+
+// SmoothRot / SmoothQuant factor preparation: fdt[k] = RN_dt(f[k]) as f32 and
+// rcp[k] = RN32(1 / fdt[k]) (IEEE divide).
+template <int DT>
+__global__ void factor_prep_kernel(const float* __restrict__ f, int K, float* __restrict__ fdt,
+                                   float* __restrict__ rcp) {
+  const int k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= K) return;
+  const float v = round_to_dt<DT>(f[k]);
+  fdt[k] = v;
+  rcp[k] = 1.0f / v;
+}
+
+template <int DT, int LOG4R, bool QUANT>
+hipError_t launch_rq(const ic_rotq_args& a, hipStream_t st) {
+  rotate_quant_kernel<DT, LOG4R, QUANT><<<dim3((unsigned)a.M), dim3(kThreads), 0, st>>>(
+      a.x, a.ldx, (int)a.K_in, a.sr_rcp, a.sr_f, (int)a.K_w, a.perm, a.sm_rcp, a.sm_f, a.q_out,
+      a.ldq, a.s_out, a.y_out, a.ldy);
+  return hipGetLastError();
+}
+
+template <int DT, bool QUANT>
+hipError_t dispatch_rot(const ic_rotq_args& a, hipStream_t st) {
+  switch (a.rot_size) {
+    case 0: return launch_rq<DT, 0, QUANT>(a, st);
+    case 16: return launch_rq<DT, 2, QUANT>(a, st);
+    case 64: return launch_rq<DT, 3, QUANT>(a, st);
+    case 256: return launch_rq<DT, 4, QUANT>(a, st);
+    case 1024: return launch_rq<DT, 5, QUANT>(a, st);
+    case 4096: return launch_rq<DT, 6, QUANT>(a, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ic_smoothrot_prepare(const float* factors, int64_t K, int dtype, float* fdt_out,
+                         float* rcp_out, void* stream) {
+  if (K < 0 || (K > 0 && (!factors || !fdt_out || !rcp_out)))
+    return ic_set_error(IC_ERR_INVALID_ARG, "ic_smoothrot_prepare: bad arguments");
+  if (K == 0) return IC_OK;
+  hipStream_t st = (hipStream_t)stream;
+  dim3 grid((unsigned)((K + 255) / 256)), block(256);
+  switch (dtype) {
+    case IC_DTYPE_F16: factor_prep_kernel<IC_DTYPE_F16><<<grid, block, 0, st>>>(factors, (int)K, fdt_out, rcp_out); break;
+    case IC_DTYPE_BF16: factor_prep_kernel<IC_DTYPE_BF16><<<grid, block, 0, st>>>(factors, (int)K, fdt_out, rcp_out); break;
+    case IC_DTYPE_F32: factor_prep_kernel<IC_DTYPE_F32><<<grid, block, 0, st>>>(factors, (int)K, fdt_out, rcp_out); break;
+    default: return ic_set_error(IC_ERR_INVALID_ARG, "ic_smoothrot_prepare: dtype must be f16/bf16/f32");
+  }
+  return ic_check_launch("ic_smoothrot_prepare");
+}
+
+static int check_rotq(const ic_rotq_args* a, bool quant, const char* who) {
+  if (!a) return ic_set_error(IC_ERR_INVALID_ARG, "%s: null args", who);
+  if (a->dtype != IC_DTYPE_F16 && a->dtype != IC_DTYPE_BF16 && a->dtype != IC_DTYPE_F32)
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: dtype must be f16/bf16/f32", who);
+  if (a->M < 0 || a->K_in <= 0 || a->K_w <= 0 || a->ldx < a->K_in)
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: bad shape M=%lld K_in=%lld K_w=%lld ldx=%lld", who,
+                        (long long)a->M, (long long)a->K_in, (long long)a->K_w, (long long)a->ldx);
+  const int R = a->rot_size;
+  if (!(R == 0 || R == 16 || R == 64 || R == 256 || R == 1024 || R == 4096))
+    return ic_set_error(IC_ERR_UNSUPPORTED,
+                        "%s: rot_size %d unsupported (regular Hadamard sizes 16/64/256/1024/4096 or 0)",
+                        who, R);
+  const int64_t K_r = R == 0 ? a->K_in : ((a->K_in + R - 1) / R) * R;
+  if (a->K_w < K_r)
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: K_w=%lld smaller than the rotated width %lld", who,
+                        (long long)a->K_w, (long long)K_r);
+  if (a->K_w > (int64_t)kTile * kMaxTiles)
+    return ic_set_error(IC_ERR_UNSUPPORTED, "%s: K_w=%lld exceeds the fused row limit %d", who,
+                        (long long)a->K_w, kTile * kMaxTiles);
+  if (a->dtype == IC_DTYPE_F32 && a->K_w > kTile * kMaxTiles / 2)
+    return ic_set_error(IC_ERR_UNSUPPORTED, "%s: f32 rows are limited to %d", who, kTile * kMaxTiles / 2);
+  if (a->M > 0 && !a->x) return ic_set_error(IC_ERR_INVALID_ARG, "%s: null x", who);
+  if ((a->sr_rcp == nullptr) != (a->sr_f == nullptr) || (a->sm_rcp == nullptr) != (a->sm_f == nullptr))
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: factor arrays come in (rcp, f) pairs", who);
+  if (a->dtype == IC_DTYPE_F32 && ((a->sr_f && !a->sr_rcp) || (a->sm_f && !a->sm_rcp)))
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: factor arrays come in (rcp, f) pairs", who);
+  if (quant) {
+    if (a->M > 0 && (!a->q_out || !a->s_out || a->ldq < a->K_w))
+      return ic_set_error(IC_ERR_INVALID_ARG, "%s: bad quantized output", who);
+  } else {
+    if (a->M > 0 && (!a->y_out || a->ldy < a->K_w))
+      return ic_set_error(IC_ERR_INVALID_ARG, "%s: bad prepared output", who);
+  }
+  if (a->M > 0x7fffffffLL) return ic_set_error(IC_ERR_UNSUPPORTED, "%s: M too large", who);
+  return IC_OK;
+}
+
+static int run_rotq(const ic_rotq_args* a, bool quant, void* stream) {
+  const char* who = quant ? "ic_rotate_quantize" : "ic_prepare_activation";
+  int rc = check_rotq(a, quant, who);
+  if (rc) return rc;
+  if (a->M == 0) return IC_OK;
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e = hipErrorInvalidValue;
+  switch (a->dtype) {
+    case IC_DTYPE_F16: e = quant ? dispatch_rot<IC_DTYPE_F16, true>(*a, st) : dispatch_rot<IC_DTYPE_F16, false>(*a, st); break;
+    case IC_DTYPE_BF16: e = quant ? dispatch_rot<IC_DTYPE_BF16, true>(*a, st) : dispatch_rot<IC_DTYPE_BF16, false>(*a, st); break;
+    case IC_DTYPE_F32: e = quant ? dispatch_rot<IC_DTYPE_F32, true>(*a, st) : dispatch_rot<IC_DTYPE_F32, false>(*a, st); break;
+  }
+  if (e != hipSuccess) return ic_set_error(IC_ERR_LAUNCH, "%s: %s", who, hipGetErrorString(e));
+  return IC_OK;
+}
+
+int ic_rotate_quantize(const void* x, int dtype, int64_t M, int64_t K_in, int64_t ldx,
+                       const float* sr_rcp, const float* sr_f, int rot_size, int64_t K_w,
+                       const int32_t* perm, const float* sm_rcp, const float* sm_f, int8_t* q_out,
+                       int64_t ldq, float* s_out, void* stream) {
+  ic_rotq_args a{x, dtype, M, K_in, ldx, sr_rcp, sr_f, rot_size, K_w, perm, sm_rcp, sm_f,
+                 q_out, ldq, s_out, nullptr, 0};
+  return run_rotq(&a, true, stream);
+}
+
+int ic_prepare_activation(const void* x, int dtype, int64_t M, int64_t K_in, int64_t ldx,
+                          const float* sr_rcp, const float* sr_f, int rot_size, int64_t K_w,
+                          const int32_t* perm, const float* sm_rcp, const float* sm_f,
+                          void* y_out, int64_t ldy, void* stream) {
+  ic_rotq_args a{x, dtype, M, K_in, ldx, sr_rcp, sr_f, rot_size, K_w, perm, sm_rcp, sm_f,
+                 nullptr, 0, nullptr, y_out, ldy};
+  return run_rotq(&a, false, stream);
+}
+
+int64_t ic_max_fused_row(void) { return (int64_t)kTile * kMaxTiles; }
+
+int ic_dynamic_quantize(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, int8_t* q_out,
+                        int64_t ldq, float* s_out, void* stream) {
+  if (M < 0 || K <= 0 || ldx < K || ldq < K || (M > 0 && (!x || !q_out || !s_out)))
+    return ic_set_error(IC_ERR_INVALID_ARG, "ic_dynamic_quantize: bad arguments");
+  if (dtype != IC_DTYPE_F16 && dtype != IC_DTYPE_BF16 && dtype != IC_DTYPE_F32)
+    return ic_set_error(IC_ERR_INVALID_ARG, "ic_dynamic_quantize: dtype must be f16/bf16/f32");
+  if (M == 0) return IC_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t lim = dtype == IC_DTYPE_F32 ? kTile * kMaxTiles / 2 : kTile * kMaxTiles;
+  if (K <= lim)
+    return ic_rotate_quantize(x, dtype, M, K, ldx, nullptr, nullptr, 0, K, nullptr, nullptr, nullptr,
+                              q_out, ldq, s_out, stream);
+  switch (dtype) {
+    case IC_DTYPE_F16: quant_rows_kernel<IC_DTYPE_F16><<<dim3((unsigned)M), dim3(kThreads), 0, st>>>(x, ldx, (int)K, q_out, ldq, s_out); break;
+    case IC_DTYPE_BF16: quant_rows_kernel<IC_DTYPE_BF16><<<dim3((unsigned)M), dim3(kThreads), 0, st>>>(x, ldx, (int)K, q_out, ldq, s_out); break;
+    default: quant_rows_kernel<IC_DTYPE_F32><<<dim3((unsigned)M), dim3(kThreads), 0, st>>>(x, ldx, (int)K, q_out, ldq, s_out); break;
+  }
+  return ic_check_launch("ic_dynamic_quantize");
+}
+
+}  // extern "C"

@@ -1,0 +1,137 @@
+/*
+ * intcrush.h - C ABI of libintcrush_gfx950.so, the MI355X (gfx950) kernels of
+ * the INT-Crush quantized-linear forward.
+ *
+ * Conventions
+ *   - Every pointer argument is a device pointer owned by the caller (the host
+ *     side allocates every output; no entry point allocates device memory).
+ *   - Matrices are row-major; ld* arguments are row strides in elements
+ *     (in bytes for packed INT4 weights).
+ *   - Work is enqueued on `stream` (a hipStream_t, NULL = the legacy default
+ *     stream) with no host synchronisation, so every entry point may be
+ *     recorded into a hipGraph.
+ *   - Return value: IC_OK (0) or an IC_ERR_* code; ic_last_error() returns a
+ *     thread-local message describing the last failure.
+ *   - dtype codes: IC_DTYPE_F16, IC_DTYPE_BF16, IC_DTYPE_F32.
+ *
+ * Reference citations are file:line in ThunderFun/ComfyUI-INT-Crush.
+ */
+#ifndef INTCRUSH_H
+#define INTCRUSH_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { IC_DTYPE_F16 = 0, IC_DTYPE_BF16 = 1, IC_DTYPE_F32 = 2 };
+enum { IC_OK = 0, IC_ERR_INVALID_ARG = 1, IC_ERR_UNSUPPORTED = 2, IC_ERR_LAUNCH = 3 };
+
+/* Library identification and diagnostics. */
+const char* ic_version(void);
+const char* ic_last_error(void);
+/* Largest K_w the single-pass ic_rotate_quantize / ic_prepare_activation handle
+ * for 16-bit activations (f32 rows are limited to half of it). */
+int64_t ic_max_fused_row(void);
+
+/*
+ * SmoothRot / SmoothQuant factor preparation (once per layer and activation
+ * dtype): fdt[k] = RN_dtype(factors[k]) held as f32, rcp[k] = RN32(1/fdt[k]).
+ * Replaces the per-call `factors.to(x.dtype)` of _ops.py:350 and :533.
+ */
+int ic_smoothrot_prepare(const float* factors, int64_t K, int dtype, float* fdt_out,
+                         float* rcp_out, void* stream);
+
+/*
+ * Fused activation prep + per-token dynamic INT8 quantization, one HBM pass.
+ * Replaces _ops.py:337-365 (_prep_activation: SmoothRot divide, rotate_activations
+ * of _quant_utils.py:117-147, pad to w_in, PermuQuant gather), the old
+ * SmoothQuant divide of _ops.py:529-533, and dynamic_quantize_activation of
+ * kernels/triton_quantize.py:151-198.
+ *   x        [M, K_in] activations (dtype), row stride ldx
+ *   sr_rcp/sr_f  SmoothRot factors prepared by ic_smoothrot_prepare, or both NULL
+ *   rot_size 0 (no rotation) or 16, 64, 256, 1024, 4096
+ *   K_w      prepared width (weight K); >= K_in rounded up to rot_size
+ *   perm     [K_w] int32 gather indices, or NULL
+ *   sm_rcp/sm_f  old-SmoothQuant factors applied after the gather, or both NULL
+ *   q_out    [M, K_w] int8 codes, row stride ldq; s_out [M] f32 scales
+ */
+int ic_rotate_quantize(const void* x, int dtype, int64_t M, int64_t K_in, int64_t ldx,
+                       const float* sr_rcp, const float* sr_f, int rot_size, int64_t K_w,
+                       const int32_t* perm, const float* sm_rcp, const float* sm_f, int8_t* q_out,
+                       int64_t ldq, float* s_out, void* stream);
+
+/* Same preparation without quantization: y_out [M, K_w] in dtype.  Replaces
+ * _prep_activation (_ops.py:337-365) for the W4A16 path. */
+int ic_prepare_activation(const void* x, int dtype, int64_t M, int64_t K_in, int64_t ldx,
+                          const float* sr_rcp, const float* sr_f, int rot_size, int64_t K_w,
+                          const int32_t* perm, const float* sm_rcp, const float* sm_f,
+                          void* y_out, int64_t ldy, void* stream);
+
+/* Per-token dynamic INT8 quantization of any width.
+ * Replaces dynamic_quantize_activation, kernels/triton_quantize.py:151-198. */
+int ic_dynamic_quantize(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, int8_t* q_out,
+                        int64_t ldq, float* s_out, void* stream);
+
+/*
+ * W8A8: out[M,N] = f32(xq . w^T) * (s_a[m] * s_w[n]) + bias[n].
+ * Replaces fused_int8_gemm_dequant, kernels/triton_int8_gemm.py:135-205.
+ *   xq [M,K] int8, w [N,K] int8, s_a [M] f32, s_w [N] f32, bias [N] (bias_dtype) or NULL.
+ */
+int ic_gemm_w8a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8_t* w, int64_t N,
+                 int64_t ldw, const float* s_a, const float* s_w, const void* bias, int bias_dtype,
+                 void* out, int out_dtype, int64_t ldo, void* stream);
+
+/*
+ * W4A8 with packed INT4 weights (two's complement nibbles, low nibble = even k)
+ * unpacked inside the GEMM.  Replaces unpack_int4_to_int8
+ * (kernels/triton_int4_to_int8_unpack.py:55-81) + fused_w4a8_gemm_dequant
+ * (kernels/triton_w4a8_gemm.py:111-169) as called by _ops.py:443-464.
+ *   w_packed [N, K/2] uint8 (row stride ldw bytes); s_w [N, num_groups] f32.
+ *   num_groups == 1: out = f32(acc) * (s_a[m] * s_w[n]) + bias[n]
+ *   num_groups  > 1: out = (sum_g f32(acc_g) * s_w[n,g]) * s_a[m] + bias[n],
+ *                    the sum an fma chain in g order, groups of K/num_groups.
+ */
+int ic_gemm_w4a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed,
+                 int64_t N, int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a,
+                 const void* bias, int bias_dtype, void* out, int out_dtype, int64_t ldo,
+                 void* stream);
+
+/*
+ * W4A16: out = x . RN_dt(q * RN_dt(s))^T (+ bias), fp32 accumulation, dtype f16/bf16.
+ * Replaces unpack_int4_to_float16 (kernels/triton_int4_unpack.py:62-88) + F.linear
+ * of _ops.py:466-481.
+ */
+int ic_gemm_w4a16(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed,
+                  int64_t N, int64_t ldw, const float* s_w, int64_t num_groups, const void* bias,
+                  int bias_dtype, void* out, int64_t ldo, void* stream);
+
+/* INT4 -> int8 unpack (no scale).  kernels/triton_int4_to_int8_unpack.py:55-81. */
+int ic_unpack_int4_to_int8(const uint8_t* packed, int64_t N, int64_t K, int64_t ldp, int8_t* out,
+                           int64_t ldo, void* stream);
+/* INT4 -> fp16/bf16 with scale, w = RN_dt(q * RN_dt(s[n, k/gs])).
+ * kernels/triton_int4_unpack.py:62-88 (per-row scale there; [N, G] here). */
+int ic_unpack_int4_to_float(const uint8_t* packed, const float* s_w, int64_t num_groups, int64_t N,
+                            int64_t K, int64_t ldp, void* out, int out_dtype, int64_t ldo, void* stream);
+
+/* Debug: raw int32 accumulators of the production GEMM kernels (generic != 0
+ * selects the shape-generic kernel instead).  W8A8: acc [M,N].  W4A8: acc
+ * [num_groups, M, N], one slab per group.  Pins the integer stage of
+ * triton_int8_gemm.py:96-103 / triton_w4a8_gemm.py:84-91 bit-exactly. */
+int ic_gemm_w8a8_acc_i32(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8_t* w,
+                         int64_t N, int64_t ldw, int32_t* acc, int generic, void* stream);
+int ic_gemm_w4a8_acc_i32(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed,
+                         int64_t N, int64_t ldw, const float* s_w, int64_t num_groups, int32_t* acc,
+                         int generic, void* stream);
+/* Shape-generic W8A8 kernel (any K/alignment); same arithmetic as ic_gemm_w8a8. */
+int ic_gemm_w8a8_generic(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8_t* w,
+                         int64_t N, int64_t ldw, const float* s_a, const float* s_w,
+                         const void* bias, int bias_dtype, void* out, int out_dtype, int64_t ldo,
+                         void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* INTCRUSH_H */

@@ -1,0 +1,308 @@
+"""CPU oracle for the INT-Crush quantized-linear forward.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py as the checker.  The product package never
+imports anything from here.
+
+The heavy lifting is the C restatement in intcrush_oracle.c (built by
+oracle/Makefile into liboracle_intcrush.so); this module wraps it with numpy,
+adds an exact big-integer fallback for Hadamard blocks whose double sum is not
+provably exact (wide-range bf16/f32 rows), and provides the reference PyTorch
+fallback (fp32 dequant -> F.linear) that the fp16/bf16 outputs are judged
+against.
+
+Reference citations are file:line in ThunderFun/ComfyUI-INT-Crush.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from fractions import Fraction
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle_intcrush.so")
+_lib = None
+
+DT_F16, DT_BF16, DT_F32 = 0, 1, 2
+
+
+def build(force: bool = False) -> str:
+    """Compile the C oracle with gcc (oracle/Makefile)."""
+    if force or not os.path.exists(_LIB_PATH):
+        subprocess.check_call(["make", "-s", "-B" if force else "all"], cwd=_HERE)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        build()
+        L = ctypes.CDLL(_LIB_PATH)
+        P = ctypes.c_void_p
+        i64 = ctypes.c_int64
+        L.oc_round.argtypes = [ctypes.c_double, ctypes.c_int]
+        L.oc_round.restype = ctypes.c_double
+        L.oc_prepare.argtypes = [P, ctypes.c_int, i64, i64, P, ctypes.c_int, i64, P, P, P,
+                                 ctypes.POINTER(i64), ctypes.c_int]
+        L.oc_prepare.restype = ctypes.c_int
+        L.oc_quantize.argtypes = [P, i64, i64, P, P]
+        L.oc_quantize.restype = None
+        L.oc_quantize_rne.argtypes = [P, i64, i64, P, P]
+        L.oc_quantize_rne.restype = None
+        L.oc_unpack_int4.argtypes = [P, i64, i64, i64, P]
+        L.oc_pack_int4.argtypes = [P, i64, i64, P]
+        L.oc_dequant_w4a16.argtypes = [P, P, i64, i64, i64, i64, ctypes.c_int, P]
+        L.oc_gemm_acc.argtypes = [P, i64, i64, P, i64, i64, P]
+        L.oc_gemm_acc.restype = i64
+        L.oc_epilogue.argtypes = [P, i64, i64, i64, P, P, P, ctypes.c_int, P]
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dtype):
+    return None if a is None else np.ascontiguousarray(a, dtype=dtype)
+
+
+# ---------------------------------------------------------------- rounding
+def round_dtype(values, dtype: int) -> np.ndarray:
+    """RN-even of float64 values to fp16/bf16/f32, returned as float32 values."""
+    v = np.asarray(values, dtype=np.float64)
+    if dtype == DT_F16:
+        return v.astype(np.float16).astype(np.float32)  # numpy's cast is RN-even
+    if dtype == DT_F32:
+        return v.astype(np.float32)
+    L = lib()
+    flat = v.reshape(-1)
+    out = np.array([L.oc_round(float(d), DT_BF16) for d in flat], dtype=np.float32)
+    return out.reshape(v.shape)
+
+
+def to_dtype_values(x, dtype: int) -> np.ndarray:
+    """Exact values of a torch/numpy array of the given dtype as float32."""
+    try:
+        import torch
+
+        if isinstance(x, torch.Tensor):
+            return x.detach().to("cpu", torch.float32).numpy()
+    except ImportError:  # pragma: no cover
+        pass
+    return np.asarray(x, dtype=np.float32)
+
+
+# ---------------------------------------------------------------- prep
+def _exact_hadamard_block(vals: np.ndarray, k: int) -> list[Fraction]:
+    """y = H x with Python rationals (no rounding at all)."""
+    R = len(vals)
+    ys: list[Fraction] = [Fraction(float(v)) for v in vals]
+    for d in range(k):
+        st = 1 << (2 * d)
+        for base in range(R):
+            if (base >> (2 * d)) & 3:
+                continue
+            a, b, c, e = (ys[base + i * st] for i in range(4))
+            s = (a + b + c + e) / 2
+            ys[base], ys[base + st], ys[base + 2 * st], ys[base + 3 * st] = s - e, s - c, s - b, s - a
+    return ys
+
+
+def _round_fraction(q: Fraction, dtype: int) -> float:
+    """Exact RN-even of a rational to fp16/bf16/f32."""
+    if q == 0:
+        return 0.0
+    p, emin, maxv = {DT_F16: (11, -14, 65504.0), DT_BF16: (8, -126, 3.3895313892515355e38),
+                     DT_F32: (24, -126, 3.4028234663852886e38)}[dtype]
+    sign = -1 if q < 0 else 1
+    a = abs(q)
+    E = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** E > a:
+        E -= 1
+    E = max(E, emin)
+    quantum = Fraction(2) ** (E - (p - 1))
+    n = a / quantum
+    fl = n.numerator // n.denominator
+    rem = n - fl
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and fl % 2 == 1):
+        fl += 1
+    r = float(fl * quantum)
+    if r > maxv:
+        r = float("inf")
+    return sign * r
+
+
+def prepare(x, dtype: int, *, smoothrot=None, rot_size: int = 0, w_in: int | None = None,
+            perm=None, smooth=None, fast: bool = True) -> np.ndarray:
+    """Reference _prep_activation (+ old SmoothQuant divide) of a 2-D row block.
+
+    x: [M, K_in] values of `dtype` (float32 array or tensor).  smoothrot /
+    smooth: raw fp32 factors (rounded to dtype here, as `.to(x.dtype)` does,
+    _ops.py:350, :533).  Returns float32 [M, K_w] holding exact dtype values.
+    """
+    L = lib()
+    xv = np.ascontiguousarray(to_dtype_values(x, dtype), dtype=np.float32)
+    M, K_in = xv.shape
+    R = int(rot_size)
+    K_r = ((K_in + R - 1) // R) * R if R else K_in
+    K_w = int(w_in) if w_in is not None else K_r
+    K_w = max(K_w, K_r)
+    srf = None if smoothrot is None else round_dtype(np.asarray(to_dtype_values(smoothrot, DT_F32), np.float64), dtype)
+    smf = None if smooth is None else round_dtype(np.asarray(to_dtype_values(smooth, DT_F32), np.float64), dtype)
+    pm = None if perm is None else np.ascontiguousarray(np.asarray(perm).astype(np.int32))
+    out = np.zeros((M, K_w), np.float32)
+    n_inexact = ctypes.c_int64(0)
+    rc = L.oc_prepare(_p(xv), dtype, M, K_in, _p(srf), R, K_w, _p(pm), _p(smf), _p(out),
+                      ctypes.byref(n_inexact), 1 if fast else 0)
+    if rc != 0:
+        raise ValueError(f"oc_prepare rejected arguments (rot_size={R}, K_in={K_in}, w_in={K_w})")
+    if n_inexact.value:
+        out = _prepare_exact_rows(xv, dtype, srf, R, K_w, pm, smf, out)
+    return out
+
+
+def _prepare_exact_rows(xv, dtype, srf, R, K_w, pm, smf, out):
+    """Recompute rows containing a block whose double sum is not provably exact."""
+    L = lib()
+    k = (R.bit_length() - 1) // 2
+    M, K_in = xv.shape
+    K_r = ((K_in + R - 1) // R) * R
+    p = {DT_F16: 11, DT_BF16: 8, DT_F32: 24}[dtype]
+    for m in range(M):
+        a = np.zeros(K_r, np.float64)
+        a[:K_in] = xv[m]
+        if srf is not None:
+            a[:K_in] = [L.oc_round(float(v) / float(f), dtype) for v, f in zip(xv[m], srf)]
+        y = np.zeros(K_w, np.float64)
+        redo = False
+        for b0 in range(0, K_r, R):
+            blk = a[b0:b0 + R]
+            nz = blk[blk != 0]
+            if nz.size:
+                emax = int(np.max(np.frexp(np.abs(nz))[1])) - 1
+                qmin = int(np.min(np.frexp(np.abs(nz))[1])) - p
+                if (emax + 1 + 2 * k) - qmin > 53:
+                    redo = True
+            ys = _exact_hadamard_block(blk, k)
+            y[b0:b0 + R] = [_round_fraction(v, dtype) for v in ys]
+        if not redo:
+            continue
+        row = y[pm] if pm is not None else y
+        if smf is not None:
+            row = np.array([L.oc_round(float(v) / float(f), dtype) for v, f in zip(row, smf)])
+        out[m] = row.astype(np.float32)
+    return out
+
+
+def quantize(v, *, rule: str = "gpu"):
+    """Per-token dynamic INT8 quantization (kernels/triton_quantize.py:109-146).
+
+    rule="gpu": q = trunc(f32(v/s) +- 0.5) (the Triton kernel rule, the canonical one);
+    rule="rne": torch.round half-to-even (the reference CPU fallback, :43-54).
+    Returns (int8 [M, K], float32 [M]).
+    """
+    L = lib()
+    xv = np.ascontiguousarray(v, dtype=np.float32)
+    M, K = xv.shape
+    q = np.zeros((M, K), np.int8)
+    s = np.zeros(M, np.float32)
+    (L.oc_quantize if rule == "gpu" else L.oc_quantize_rne)(_p(xv), M, K, _p(q), _p(s))
+    return q, s
+
+
+def rotate_quantize(x, dtype: int, **kw):
+    """prepare() followed by quantize(): the fused kernel's full contract."""
+    return quantize(prepare(x, dtype, **kw))
+
+
+# ---------------------------------------------------------------- weights
+def unpack_int4(packed, K: int) -> np.ndarray:
+    """_quant_utils.py:185-197."""
+    L = lib()
+    p = np.ascontiguousarray(packed, dtype=np.uint8)
+    N, Kp = p.shape
+    out = np.zeros((N, K), np.int8)
+    L.oc_unpack_int4(_p(p), N, K, Kp, _p(out))
+    return out
+
+
+def pack_int4(vals) -> np.ndarray:
+    """_quant_utils.py:170-182."""
+    L = lib()
+    v = np.ascontiguousarray(vals, dtype=np.int8)
+    if v.ndim == 1:
+        return pack_int4(v[None])[0]
+    if v.size and (v.min() < -8 or v.max() > 7):
+        raise ValueError("Values must be in [-8, 7]")
+    N, K = v.shape
+    out = np.zeros((N, (K + 1) // 2), np.uint8)
+    L.oc_pack_int4(_p(v), N, K, _p(out))
+    return out
+
+
+def dequant_w4a16(packed, s_w, K: int, dtype: int) -> np.ndarray:
+    """W4A16 weight RN_dt(q * RN_dt(s)) (triton_int4_unpack.py:49-56, group scales)."""
+    L = lib()
+    p = np.ascontiguousarray(packed, dtype=np.uint8)
+    s = np.ascontiguousarray(np.asarray(s_w, np.float32).reshape(p.shape[0], -1))
+    N, G = s.shape
+    out = np.zeros((N, K), np.float32)
+    L.oc_dequant_w4a16(_p(p), _p(s), G, N, K, p.shape[1], dtype, _p(out))
+    return out
+
+
+# ---------------------------------------------------------------- GEMM
+def gemm_acc(a_q, w_q, num_groups: int = 1) -> np.ndarray:
+    """Exact int32 accumulators [G, M, N] (G=1 -> [M, N])."""
+    L = lib()
+    A = np.ascontiguousarray(a_q, dtype=np.int8)
+    W = np.ascontiguousarray(w_q, dtype=np.int8)
+    M, K = A.shape
+    N = W.shape[0]
+    acc = np.zeros((num_groups, M, N), np.int32)
+    ovf = L.oc_gemm_acc(_p(A), M, K, _p(W), N, num_groups, _p(acc))
+    if ovf:
+        raise OverflowError(f"{ovf} accumulators exceed int32")
+    return acc[0] if num_groups == 1 else acc
+
+
+def epilogue(acc, s_a, s_w, bias=None, out_dtype: int = DT_F16) -> np.ndarray:
+    """Dequant epilogue (triton_int8_gemm.py:105-117 and the group layout)."""
+    L = lib()
+    acc = np.ascontiguousarray(acc, dtype=np.int32)
+    G = 1 if acc.ndim == 2 else acc.shape[0]
+    M, N = acc.shape[-2:]
+    sa = np.ascontiguousarray(s_a, dtype=np.float32)
+    sw = np.ascontiguousarray(np.asarray(s_w, np.float32).reshape(N, -1))
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    out = np.zeros((M, N), np.float32)
+    L.oc_epilogue(_p(acc), M, N, G, _p(sa), _p(sw), _p(b), out_dtype, _p(out))
+    return out
+
+
+# ---------------------------------------------------------------- fp32 fallback
+def dequant_weight_fp32(w, s_w, K: int, int4: bool):
+    """IntCrushInt{4,8}Layout.dequantize (quant_layout.py:80-87, :163-168) with
+    the [N, G] group layout of _quant_utils.py:237-270: W = q * s[n, k // gs]."""
+    import torch
+
+    q = torch.as_tensor(unpack_int4(w, K) if int4 else np.asarray(w), dtype=torch.float32)
+    s = torch.as_tensor(np.asarray(s_w, np.float32)).reshape(q.shape[0], -1)
+    G = s.shape[1]
+    return q * s.repeat_interleave(K // G, dim=1)
+
+
+def linear_fallback_fp32(x_prep, w, s_w, K: int, int4: bool, bias=None):
+    """Reference PyTorch fallback (_ops.py:483-491, :538-545) in fp32:
+    F.linear(x_prep, dequant(W), bias)."""
+    import torch
+    import torch.nn.functional as F
+
+    W = dequant_weight_fp32(w, s_w, K, int4)
+    xp = torch.as_tensor(np.asarray(x_prep, np.float32))
+    b = None if bias is None else torch.as_tensor(np.asarray(bias, np.float32))
+    return F.linear(xp, W, b).numpy()

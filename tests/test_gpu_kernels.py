@@ -1,0 +1,301 @@
+"""GPU parity of the gfx950 kernels against the CPU oracle.
+
+Integer stages (INT8 activation codes, unpacked weights, int32 accumulators)
+and the restated fp32 epilogue formula must be bit-exact; fp16/bf16 linear
+outputs must also sit within rtol 1e-2 / cosine >= 0.9999 of the reference
+fp32 dequant -> F.linear fallback.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DT = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _acts(M, K, dtype, seed, outliers=0.0, student_t=False):
+    g = _gen(seed)
+    if student_t:
+        x = torch.distributions.StudentT(4.0).sample((M, K))
+    else:
+        x = torch.randn(M, K, generator=g)
+    if outliers:
+        idx = torch.randperm(K, generator=g)[: max(1, int(K * outliers))]
+        x[:, idx] *= 20.0
+    return x.to(dtype)
+
+
+# ------------------------------------------------------------------ unpack
+def test_unpack_int4_known_answers(rt, oracle, dev):
+    # tests/test_quant_utils.py:65-99 of the reference
+    cases = [
+        np.array([[-8, -1, 0, 1, 7, -3, 5, 0]], np.int8),
+        np.array([[-8, 0, 7]], np.int8),
+        np.full((2, 16), -8, np.int8),
+        np.full((2, 16), 7, np.int8),
+    ]
+    for v in cases:
+        packed = oracle.pack_int4(v)
+        got = rt.unpack_int4_to_int8(torch.from_numpy(packed).to(dev), v.shape[1]).cpu().numpy()
+        assert np.array_equal(got, v)
+
+
+def test_unpack_int4_all_bytes(rt, oracle, dev):
+    packed = np.arange(256, dtype=np.uint8).reshape(4, 64)
+    got = rt.unpack_int4_to_int8(torch.from_numpy(packed).to(dev), 128).cpu().numpy()
+    assert np.array_equal(got, oracle.unpack_int4(packed, 128))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("G", [1, 4])
+def test_unpack_int4_to_float(rt, oracle, dev, dtype, G):
+    g = _gen(1)
+    N, K = 64, 512
+    packed = torch.randint(0, 256, (N, K // 2), generator=g, dtype=torch.uint8)
+    s = (torch.rand(N, G, generator=g) * 2e-2 + 1e-3).to(torch.float16).float()
+    got = rt.unpack_int4_to_float(packed.to(dev), s.to(dev), K, dtype).float().cpu().numpy()
+    ref = oracle.dequant_w4a16(packed.numpy(), s.numpy(), K, DT[dtype])
+    assert np.array_equal(got, ref)
+
+
+# ------------------------------------------------------------------ quantize
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("K", [64, 1000, 4096, 12288, 20480])
+def test_dynamic_quantize(rt, oracle, dev, dtype, K):
+    if dtype == torch.float32 and K > 8192 and K < 16384:
+        K = 8192
+    x = _acts(24, K, dtype, seed=K)
+    x[3] = 0  # all-zero row: s = 1e-8/127, codes 0
+    q, s = rt.dynamic_quantize_activation(x.to(dev))
+    q_ref, s_ref = oracle.quantize(oracle.to_dtype_values(x, DT[dtype]))
+    assert np.array_equal(s.cpu().numpy(), s_ref)
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+
+
+def test_dynamic_quantize_3d_and_prealloc(rt, dev):
+    x = torch.randn(2, 8, 128, device=dev, dtype=torch.float16)
+    q, s = rt.dynamic_quantize_activation(x)
+    assert q.shape == (2, 8, 128) and s.shape == (2, 8)
+    s_buf = torch.empty(16, device=dev)
+    q_buf = torch.empty(16, 128, dtype=torch.int8, device=dev)
+    q2, s2 = rt.dynamic_quantize_activation(x.reshape(16, 128), s_a_out=s_buf, x_int8_out=q_buf)
+    assert q2.data_ptr() == q_buf.data_ptr() and s2.data_ptr() == s_buf.data_ptr()
+    assert torch.equal(q2, q.reshape(16, 128)) and torch.equal(s2, s.reshape(16))
+
+
+def test_quantize_round_half_away_quirk(rt, dev):
+    # q = 0.49999997 + 0.5 rounds to 1.0 in f32, so trunc gives 1 (triton_quantize.py:142-145)
+    s = np.float32(127.0) / np.float32(127.0)  # row max 127 -> s = 1
+    row = torch.tensor([[127.0, 0.49999997, -0.49999997, 2.5, -2.5, 0.5]], dtype=torch.float32)
+    q, sc = rt.dynamic_quantize_activation(row.to(dev))
+    assert float(sc[0]) == float(s)
+    assert q.cpu().tolist() == [[127, 1, -1, 3, -3, 1]]
+
+
+# ------------------------------------------------------------------ fused prep
+ROT_CASES = [
+    # (K_in, R, w_in, smoothrot, perm, smooth)
+    (512, 16, None, False, False, False),
+    (512, 64, None, True, False, False),
+    (768, 256, None, True, True, False),
+    (3072, 256, None, True, True, False),
+    (2048, 1024, None, False, True, False),
+    (4096, 4096, None, False, False, False),
+    (8192, 4096, None, True, True, False),
+    (1000, 256, None, False, False, False),     # rotation pad 1000 -> 1024
+    (1000, 0, 1024, True, True, False),         # w_in pad, no rotation
+    (1536, 1024, 2304, False, True, False),     # rotation pad 1536 -> 2048, then w_in pad
+    (640, 64, None, False, True, True),         # old SmoothQuant after the gather
+    (13824, 1024, 14336, False, False, False),  # Wan FFN-down pad path
+    (12288, 256, None, True, True, False),      # Flux MLP down-proj (C3 prep)
+]
+
+
+def _prep_inputs(K_in, R, w_in, use_sr, use_perm, use_sm, seed):
+    g = _gen(seed)
+    K_r = ((K_in + R - 1) // R) * R if R else K_in
+    K_w = max(w_in or K_r, K_r)
+    sr = torch.exp(torch.randn(K_in, generator=g) * 0.5) if use_sr else None
+    perm = torch.randperm(K_w, generator=g) if use_perm else None
+    sm = torch.exp(torch.randn(K_w, generator=g) * 0.3) if use_sm else None
+    return K_w, sr, perm, sm
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("case", ROT_CASES)
+def test_rotate_quantize_bit_exact(rt, oracle, dev, dtype, case):
+    K_in, R, w_in, use_sr, use_perm, use_sm = case
+    K_w, sr, perm, sm = _prep_inputs(K_in, R, w_in, use_sr, use_perm, use_sm, seed=K_in + R)
+    x = _acts(6, K_in, dtype, seed=R + 7, outliers=0.01)
+    x[2] = 0
+    srp = rt.prepare_factors(sr.to(dev), dtype) if sr is not None else None
+    smp = rt.prepare_factors(sm.to(dev), dtype) if sm is not None else None
+    pp = rt.prepare_perm(perm.to(dev), K_w) if perm is not None else None
+    q, s = rt.rotate_quantize(x.to(dev), rot_size=R, w_in=K_w, smoothrot=srp, perm=pp, smooth=smp)
+    y = rt.prepare_activation(x.to(dev), rot_size=R, w_in=K_w, smoothrot=srp, perm=pp, smooth=smp)
+    y_ref = oracle.prepare(x, DT[dtype], smoothrot=sr, rot_size=R, w_in=K_w, perm=perm, smooth=sm)
+    q_ref, s_ref = oracle.quantize(y_ref)
+    assert np.array_equal(y.float().cpu().numpy(), y_ref)
+    assert np.array_equal(s.cpu().numpy(), s_ref)
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+
+
+def test_rotate_quantize_f32(rt, oracle, dev):
+    x = _acts(4, 2048, torch.float32, seed=3)
+    fac = torch.exp(torch.randn(2048, generator=_gen(4)) * 0.5)
+    srp = rt.prepare_factors(fac.to(dev), torch.float32)
+    q, s = rt.rotate_quantize(x.to(dev), rot_size=256, smoothrot=srp)
+    q_ref, s_ref = oracle.rotate_quantize(x, 2, smoothrot=fac, rot_size=256)
+    # f32 rows are exact whenever the oracle reports every block sum exact;
+    # allow +-1 code where a block is not (documented fp64 limitation)
+    assert np.array_equal(s.cpu().numpy(), s_ref) or np.allclose(s.cpu().numpy(), s_ref, rtol=1e-6)
+    assert np.abs(q.cpu().numpy().astype(int) - q_ref.astype(int)).max() <= 1
+
+
+def test_rotate_quantize_determinism(rt, dev):
+    x = torch.randn(64, 3072, device=dev, dtype=torch.float16)
+    a = rt.rotate_quantize(x, rot_size=256)
+    b = rt.rotate_quantize(x, rot_size=256)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+# ------------------------------------------------------------------ GEMMs
+GEMM_SHAPES = [(256, 256, 256), (300, 200, 192), (512, 384, 1024), (16, 1024, 512), (1, 96, 128)]
+
+
+def _int8(shape, seed, lo=-128, hi=128):
+    return torch.randint(lo, hi, shape, generator=_gen(seed), dtype=torch.int8)
+
+
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
+def test_w8a8_accumulators(rt, oracle, dev, M, N, K):
+    a = _int8((M, K), 1)
+    w = _int8((N, K), 2)
+    acc = rt.gemm_acc_i32(a.to(dev), w.to(dev)).cpu().numpy()
+    assert np.array_equal(acc, oracle.gemm_acc(a.numpy(), w.numpy()))
+
+
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
+@pytest.mark.parametrize("G", [1, "g128"])
+def test_w4a8_accumulators(rt, oracle, dev, M, N, K, G):
+    G = K // 128 if G == "g128" and K % 128 == 0 else 1
+    a = _int8((M, K), 3)
+    packed = torch.randint(0, 256, (N, K // 2), generator=_gen(4), dtype=torch.uint8)
+    s_w = torch.rand(N, G, generator=_gen(5)) * 1e-2 + 1e-3
+    acc = rt.gemm_acc_i32(a.to(dev), packed.to(dev), int4=True, s_w=s_w.to(dev)).cpu().numpy()
+    ref = oracle.gemm_acc(a.numpy(), oracle.unpack_int4(packed.numpy(), K), G)
+    assert np.array_equal(acc, ref)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("with_bias", [False, True])
+@pytest.mark.parametrize("M,N,K", [(256, 256, 512), (130, 320, 192)])
+def test_w8a8_output_formula(rt, oracle, dev, out_dtype, with_bias, M, N, K):
+    a = _int8((M, K), 6)
+    w = _int8((N, K), 7, -127, 128)
+    s_a = torch.rand(M, generator=_gen(8)) * 0.05 + 1e-3
+    s_w = (torch.rand(N, generator=_gen(9)) * 2e-3 + 1e-4).to(torch.float16).float()
+    bias = (torch.randn(N, generator=_gen(10))).to(out_dtype) if with_bias else None
+    out = rt.fused_int8_gemm_dequant(a.to(dev), w.to(dev), s_w.to(dev), s_a.to(dev),
+                                     bias=None if bias is None else bias.to(dev), out_dtype=out_dtype)
+    acc = oracle.gemm_acc(a.numpy(), w.numpy())
+    ref = oracle.epilogue(acc, s_a.numpy(), s_w.numpy(), None if bias is None else bias.float().numpy(),
+                          DT[out_dtype])
+    assert np.array_equal(out.float().cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("grouped", [False, True])
+@pytest.mark.parametrize("M,N,K", [(256, 256, 512), (260, 136, 384)])
+def test_w4a8_output_formula(rt, oracle, dev, out_dtype, grouped, M, N, K):
+    G = K // 128 if grouped else 1
+    a = _int8((M, K), 11)
+    packed = torch.randint(0, 256, (N, K // 2), generator=_gen(12), dtype=torch.uint8)
+    s_a = torch.rand(M, generator=_gen(13)) * 0.05 + 1e-3
+    s_w = (torch.rand(N, G, generator=_gen(14)) * 2e-2 + 1e-3).to(torch.float16).float()
+    bias = torch.randn(N, generator=_gen(15)).to(out_dtype)
+    out = rt.gemm_w4a8(a.to(dev), packed.to(dev), s_w.to(dev), s_a.to(dev), bias=bias.to(dev),
+                       out_dtype=out_dtype)
+    acc = oracle.gemm_acc(a.numpy(), oracle.unpack_int4(packed.numpy(), K), G)
+    ref = oracle.epilogue(acc, s_a.numpy(), s_w.numpy(), bias.float().numpy(), DT[out_dtype])
+    assert np.array_equal(out.float().cpu().numpy(), ref)
+
+
+def test_w8a8_generic_kernel_matches(rt, dev):
+    M, N, K = 64, 96, 200  # K not a multiple of 64 -> generic kernel
+    a = _int8((M, K), 16).to(dev)
+    w = _int8((N, K), 17).to(dev)
+    s_a = torch.rand(M, device=dev) * 0.01 + 1e-3
+    s_w = torch.rand(N, device=dev) * 0.01 + 1e-3
+    out = rt.fused_int8_gemm_dequant(a, w, s_w, s_a, out_dtype=torch.float32)
+    ref = (a.float() @ w.float().t()) * (s_a[:, None] * s_w[None, :])
+    assert torch.allclose(out, ref, rtol=1e-6, atol=1e-6)
+
+
+def _cos(a, b):
+    a = a.reshape(-1).double()
+    b = b.reshape(-1).double()
+    return float((a @ b) / (a.norm() * b.norm()))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("G", [1, 24])
+def test_w4a16_vs_fp32(rt, oracle, dev, dtype, G):
+    M, N, K = 300, 512, 3072
+    x = _acts(M, K, dtype, seed=20)
+    packed = torch.randint(0, 256, (N, K // 2), generator=_gen(21), dtype=torch.uint8)
+    s_w = (torch.rand(N, G, generator=_gen(22)) * 2e-2 + 1e-3).to(torch.float16).float()
+    bias = torch.randn(N, generator=_gen(23)).to(dtype)
+    out = rt.gemm_w4a16(x.to(dev), packed.to(dev), s_w.to(dev), bias=bias.to(dev)).float().cpu()
+    w = torch.from_numpy(oracle.dequant_w4a16(packed.numpy(), s_w.numpy(), K, DT[dtype]))
+    ref = x.float() @ w.t() + bias.float()
+    # fp32 accumulation order differs from the CPU; the output is one rounding of it
+    tol = 1e-2 if dtype == torch.float16 else 2e-2
+    assert torch.allclose(out, ref, rtol=tol, atol=tol * ref.abs().max().item() * 1e-2)
+    assert _cos(out, ref) >= 0.9999
+
+
+# ------------------------------------------------------------------ linear accuracy gate
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_w4a8_linear_vs_fp32_fallback(rt, oracle, dev, dtype):
+    """C3-style layer at reduced M: fused prep + W4A8 vs the fp32 dequant->F.linear fallback."""
+    M, K, N, R = 128, 12288, 512, 256
+    g = _gen(30)
+    x = _acts(M, K, dtype, seed=31, outliers=0.01)
+    sr = torch.exp(torch.randn(K, generator=g) * 0.5)
+    perm = torch.randperm(K, generator=g)
+    W = torch.randn(N, K, generator=g)
+    # converter-side group quantization (_quant_utils.py:237-270) in permuted space
+    Wg = W.reshape(N, K // 128, 128)
+    s_w = (Wg.abs().amax(-1) / 7.0).clamp(min=1e-8).to(torch.float16).float()
+    qw = (Wg / s_w[..., None]).round().clamp(-8, 7).to(torch.int8).reshape(N, K)
+    packed = torch.from_numpy(oracle.pack_int4(qw.numpy()))
+    bias = torch.randn(N, generator=g).to(dtype)
+    srp = rt.prepare_factors(sr.to(dev), dtype)
+    q, s = rt.rotate_quantize(x.to(dev), rot_size=R, w_in=K, smoothrot=srp, perm=rt.prepare_perm(perm.to(dev), K))
+    out = rt.gemm_w4a8(q, packed.to(dev), s_w.to(dev), s, bias=bias.to(dev), out_dtype=dtype).float().cpu()
+    x_prep = oracle.prepare(x, DT[dtype], smoothrot=sr, rot_size=R, w_in=K, perm=perm)
+    ref = torch.from_numpy(oracle.linear_fallback_fp32(x_prep, packed.numpy(), s_w.numpy(), K, True,
+                                                        bias.float().numpy()))
+    rel = (out - ref).norm() / ref.norm()
+    assert _cos(out, ref) >= 0.9999, f"cosine {_cos(out, ref)} rel {rel}"
+
+
+def test_w8a8_linear_vs_fp32_fallback(rt, oracle, dev):
+    """C1-style layer at reduced M (rot_size 0, per-channel scales)."""
+    M, K, N = 256, 3072, 768
+    g = _gen(40)
+    x = torch.randn(M, K, generator=g).to(torch.float16)
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    s_w = (torch.rand(N, generator=g) * (2e-3 - 1e-4) + 1e-4).to(torch.float16).float()
+    q, s = rt.dynamic_quantize_activation(x.to(dev))
+    out = rt.fused_int8_gemm_dequant(q, w.to(dev), s_w.to(dev), s, out_dtype=torch.float16).float().cpu()
+    ref = torch.from_numpy(oracle.linear_fallback_fp32(x.float().numpy(), w.numpy(), s_w.numpy(), K, False))
+    assert _cos(out, ref) >= 0.9999

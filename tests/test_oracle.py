@@ -1,0 +1,210 @@
+"""Pins the CPU oracle against the reference's own known answers and against
+closed forms / exact arithmetic (no GPU).
+
+Each check is chosen so that a plausible slip in the oracle (wrong sign in H4,
+transposed digit order, wrong rounding rule, dropped pad, wrong group index)
+fails it.
+"""
+from __future__ import annotations
+
+import math
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+
+# ---------------------------------------------------------------- INT4 pack / unpack
+# Known answers of the reference tests/test_quant_utils.py:65-99 and test_w4a8_gemm.py:49-57.
+def test_pack_unpack_known_answers(oracle):
+    v = np.array([-8, -1, 0, 1, 7, -3, 5, 0], np.int8)
+    packed = oracle.pack_int4(v)
+    # low nibble = even index, two's complement: -8 -> 0x8, -1 -> 0xF, 0, 1, 7, -3 -> 0xD, 5, 0
+    assert packed.tolist() == [0xF8, 0x10, 0xD7, 0x05]
+    assert oracle.unpack_int4(packed[None], 8)[0].tolist() == v.tolist()
+    odd = np.array([-8, 0, 7], np.int8)
+    assert oracle.unpack_int4(oracle.pack_int4(odd)[None], 3)[0].tolist() == odd.tolist()
+    for fill in (-8, 7):
+        vals = np.full((2, 16), fill, np.int8)
+        assert np.array_equal(oracle.unpack_int4(oracle.pack_int4(vals), 16), vals)
+    assert oracle.pack_int4(np.zeros((4, 33), np.int8)).shape == (4, 17)
+    with pytest.raises(ValueError):
+        oracle.pack_int4(np.array([8], np.int8))
+
+
+def test_unpack_brute_force_all_bytes(oracle):
+    packed = np.arange(256, dtype=np.uint8)[None]
+    out = oracle.unpack_int4(packed, 512)[0]
+    for b in range(256):
+        lo, hi = b & 15, b >> 4
+        assert out[2 * b] == (lo - 16 if lo >= 8 else lo)
+        assert out[2 * b + 1] == (hi - 16 if hi >= 8 else hi)
+
+
+def test_pack_unpack_roundtrip(oracle):
+    rng = np.random.default_rng(0)
+    v = rng.integers(-8, 8, size=(7, 130)).astype(np.int8)
+    assert np.array_equal(oracle.unpack_int4(oracle.pack_int4(v), 130), v)
+
+
+# ---------------------------------------------------------------- Hadamard
+def _kron_h(R):
+    """_quant_utils.py:81-93 construction, independently: kron of H4/2."""
+    h4 = np.array([[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]], np.float64) / 2
+    H = h4
+    while H.shape[0] < R:
+        H = np.kron(H, h4)
+    return H
+
+
+@pytest.mark.parametrize("R", [4, 16, 64, 256])
+def test_hadamard_properties(R):
+    H = _kron_h(R)
+    assert np.allclose(np.abs(H), 1 / math.sqrt(R))
+    assert np.array_equal(H @ H.T, np.eye(R))  # exact: entries are powers of two
+    assert np.array_equal(H, H.T)
+    assert np.array_equal(H @ H, np.eye(R))    # symmetric + orthogonal -> involution
+
+
+@pytest.mark.parametrize("R", [16, 64, 256])
+@pytest.mark.parametrize("dtype", [0, 1])
+def test_prepare_rotation_matches_kron_matmul(oracle, R, dtype):
+    torch_dt = torch.float16 if dtype == 0 else torch.bfloat16
+    x = torch.randn(5, 3 * R, generator=torch.Generator().manual_seed(R)).to(torch_dt)
+    xv = x.float().numpy().astype(np.float64)
+    H = _kron_h(R)
+    # x @ H^T per block in float64 is exact for 16-bit inputs; then one rounding
+    ref = (xv.reshape(5, 3, R) @ H.T).reshape(5, 3 * R)
+    ref = oracle.round_dtype(ref, dtype)
+    for fast in (False, True):
+        got = oracle.prepare(x, dtype, rot_size=R, fast=fast)
+        assert np.array_equal(got, ref)
+
+
+def test_prepare_rotation_pad_and_perm(oracle):
+    R, K_in, K_w = 64, 100, 192  # rotation pad 100 -> 128, then w_in pad to 192
+    x = torch.randn(3, K_in, generator=torch.Generator().manual_seed(1)).to(torch.float16)
+    perm = torch.randperm(K_w, generator=torch.Generator().manual_seed(2))
+    xp = np.zeros((3, 128))
+    xp[:, :K_in] = x.float().numpy()
+    H = _kron_h(R)
+    rot = oracle.round_dtype((xp.reshape(3, 2, R) @ H.T).reshape(3, 128), 0)
+    full = np.zeros((3, K_w), np.float32)
+    full[:, :128] = rot
+    got = oracle.prepare(x, 0, rot_size=R, w_in=K_w, perm=perm)
+    assert np.array_equal(got, full[:, perm.numpy()])
+
+
+def test_prepare_inverse_perm_roundtrip(oracle):
+    K = 256
+    x = torch.randn(2, K, generator=torch.Generator().manual_seed(3)).to(torch.float16)
+    perm = torch.randperm(K, generator=torch.Generator().manual_seed(4))
+    inv = torch.argsort(perm)
+    y = oracle.prepare(x, 0, perm=perm)
+    assert np.array_equal(y[:, inv.numpy()], x.float().numpy())
+
+
+def test_prepare_smoothrot_divide_exact(oracle):
+    """x / RN16(f) rounded once (torch half division), checked with rationals."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(2, 64, generator=g).to(torch.float16)
+    x[0, :8] = torch.tensor([6e-8, -6e-8, 1e-5, 65504, -65504, 0.0, 3.0, 1.0], dtype=torch.float16)
+    f = torch.exp(torch.randn(64, generator=g)) * 3
+    f[:8] = torch.tensor([3.0, 7.0, 11.0, 0.5, 2.0, 5.0, 1e-3, 1e4])
+    got = oracle.prepare(x, 0, smoothrot=f)
+    fd = f.to(torch.float16).double().numpy()
+    for i in range(2):
+        for j in range(64):
+            q = Fraction(float(x[i, j])) / Fraction(float(fd[j]))
+            assert got[i, j] == oracle._round_fraction(q, 0), (i, j)
+
+
+def test_bf16_wide_block_uses_exact_path(oracle):
+    """A bf16 block spanning 2^-100..2^60 is not exact in double: the oracle
+    must fall back to rationals and agree with an exact direct sum."""
+    R = 16
+    vals = torch.tensor([[2.0 ** 60, 2.0 ** -100, -3.0, 2.0 ** -90] + [1.0] * 12], dtype=torch.bfloat16)
+    got = oracle.prepare(vals, 1, rot_size=R)
+    H = _kron_h(R)
+    xv = [Fraction(float(v)) for v in vals[0].float()]
+    for i in range(R):
+        exact = sum((Fraction(H[i, j]) * xv[j] for j in range(R)), Fraction(0))
+        assert got[0, i] == oracle._round_fraction(exact, 1)
+
+
+# ---------------------------------------------------------------- quantization
+@pytest.mark.parametrize("M,K", [(1, 64), (4, 256), (16, 1024), (256, 4096)])
+def test_quantize_reference_cpu_vectors(oracle, M, K):
+    """tests/test_w8a8_fused_kernels.py:479-492 of the reference: seed 0 inputs,
+    torch.round reference.  The GPU rule (round half away from zero) agrees
+    everywhere except where the f32 quotient is exactly k + 1/2, and there it
+    is one code further from zero."""
+    torch.manual_seed(0)
+    x = torch.randn(M, K)
+    ref_s = x.float().abs().amax(dim=1).clamp(min=1e-8) / 127.0
+    quot = x.float() / ref_s.unsqueeze(1)
+    ref_q = quot.round().clamp(-128, 127).to(torch.int8)
+    q_rne, s_rne = oracle.quantize(x.numpy(), rule="rne")
+    q_gpu, s_gpu = oracle.quantize(x.numpy(), rule="gpu")
+    assert np.array_equal(q_rne, ref_q.numpy())
+    assert np.array_equal(s_rne, ref_s.numpy())
+    assert np.array_equal(s_gpu, ref_s.numpy())
+    diff = q_gpu.astype(int) - ref_q.numpy().astype(int)
+    qn = quot.numpy()
+    ties = (np.abs(qn) - np.floor(np.abs(qn))) == 0.5
+    assert np.array_equal(diff != 0, ties & (np.floor(np.abs(qn)) % 2 == 0))
+    assert np.array_equal(np.sign(diff[diff != 0]), np.sign(qn[diff != 0]).astype(int))
+
+
+def test_quantize_rounding_rules_on_ties(oracle):
+    x = np.array([[127.0, 0.5, 1.5, 2.5, -0.5, -2.5, 0.49999997, 0.0]], np.float32)
+    q_gpu, s = oracle.quantize(x, rule="gpu")
+    q_rne, _ = oracle.quantize(x, rule="rne")
+    assert s[0] == np.float32(1.0)
+    assert q_gpu[0].tolist() == [127, 1, 2, 3, -1, -3, 1, 0]  # half away from zero (+ f32 quirk)
+    assert q_rne[0].tolist() == [127, 0, 2, 2, 0, -2, 0, 0]   # half to even
+
+
+def test_quantize_zero_row_and_floor(oracle):
+    q, s = oracle.quantize(np.zeros((1, 8), np.float32))
+    assert s[0] == np.float32(np.float32(1e-8) / np.float32(127.0))
+    assert not q.any()
+
+
+# ---------------------------------------------------------------- GEMM pieces
+def test_gemm_acc_exact_and_groups(oracle):
+    rng = np.random.default_rng(1)
+    a = rng.integers(-128, 128, (9, 384)).astype(np.int8)
+    w = rng.integers(-8, 8, (11, 384)).astype(np.int8)
+    full = a.astype(np.int64) @ w.astype(np.int64).T
+    assert np.array_equal(oracle.gemm_acc(a, w), full)
+    g = oracle.gemm_acc(a, w, 3)
+    assert np.array_equal(g.sum(0), full)
+    assert np.array_equal(g[1], a[:, 128:256].astype(np.int64) @ w[:, 128:256].astype(np.int64).T)
+
+
+def test_epilogue_matches_fp32_fallback(oracle):
+    """The restated integer+epilogue path agrees with the independent fp32
+    dequant -> F.linear fallback on the same integer inputs."""
+    rng = np.random.default_rng(2)
+    M, N, K, G = 16, 24, 512, 4
+    a = rng.integers(-128, 128, (M, K)).astype(np.int8)
+    q = rng.integers(-8, 8, (N, K)).astype(np.int8)
+    packed = oracle.pack_int4(q)
+    s_a = (rng.random(M) * 0.01 + 1e-3).astype(np.float32)
+    s_w = (rng.random((N, G)) * 0.02 + 1e-3).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    acc = oracle.gemm_acc(a, oracle.unpack_int4(packed, K), G)
+    out = oracle.epilogue(acc, s_a, s_w, bias, out_dtype=2)
+    ref = oracle.linear_fallback_fp32(a.astype(np.float32) * s_a[:, None], packed, s_w, K, True, bias)
+    assert np.allclose(out, ref, rtol=1e-5, atol=1e-4)
+
+
+def test_dequant_w4a16_exact(oracle):
+    rng = np.random.default_rng(3)
+    q = rng.integers(-8, 8, (6, 256)).astype(np.int8)
+    s = (rng.random((6, 2)) * 0.02 + 1e-3).astype(np.float16).astype(np.float32)
+    w = oracle.dequant_w4a16(oracle.pack_int4(q), s, 256, 0)
+    exact = q.astype(np.float64) * np.repeat(s.astype(np.float64), 128, axis=1)
+    assert np.array_equal(w, exact.astype(np.float16).astype(np.float32))
