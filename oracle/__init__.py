@@ -306,3 +306,35 @@ def linear_fallback_fp32(x_prep, w, s_w, K: int, int4: bool, bias=None):
     xp = torch.as_tensor(np.asarray(x_prep, np.float32))
     b = None if bias is None else torch.as_tensor(np.asarray(bias, np.float32))
     return F.linear(xp, W, b).numpy()
+
+
+def reference_fallback_forward(x, w, s_w, K: int, *, int4: bool, smoothrot=None, rot_size: int = 0,
+                               perm=None, bias=None):
+    """CPU restatement of the reference PyTorch fallback forward in fp32
+    (_forward_int4_pytorch _ops.py:483-491 / no-kernel INT8 path :538-545):
+    dequantize W = q * s (group layout), prep the activation (SmoothRot divide,
+    block Hadamard via matmul, pad, perm; _ops.py:337-365) and F.linear.
+    Used as the timed CPU baseline; runs on whatever torch threads are set."""
+    import torch
+    import torch.nn.functional as F
+
+    W = dequant_weight_fp32(w, s_w, K, int4)
+    x2 = x.reshape(-1, x.shape[-1]).to(torch.float32)
+    if smoothrot is not None:
+        x2 = x2 / smoothrot.to(torch.float32)
+    if rot_size:
+        R = int(rot_size)
+        pad = (-x2.shape[-1]) % R
+        if pad:
+            x2 = F.pad(x2, (0, pad))
+        h4 = torch.tensor([[1., 1., 1., -1.], [1., 1., -1., 1.], [1., -1., 1., 1.], [-1., 1., 1., 1.]]) / 2
+        H = h4
+        while H.shape[0] < R:
+            H = torch.kron(H, h4)
+        x2 = torch.matmul(x2.reshape(x2.shape[0], -1, R), H.T).reshape(x2.shape[0], -1)
+    if x2.shape[-1] < K:
+        x2 = F.pad(x2, (0, K - x2.shape[-1]))
+    if perm is not None:
+        x2 = x2[..., perm]
+    b = None if bias is None else bias.to(torch.float32)
+    return F.linear(x2, W, b)
