@@ -7,6 +7,9 @@ numerics:
   -fhip-fp32-correctly-rounded-divide-sqrt  IEEE f32 division
   -Xclang -target-feature -Xclang -packed-fp32-ops
                                             no packed-FP32 VALU instructions
+  -mllvm -amdgpu-mfma-vgpr-form=1           MFMA accumulators in architectural
+                                            VGPRs, so epilogue/fold VALU reads
+                                            them without v_accvgpr_read copies
 """
 from __future__ import annotations
 
@@ -26,6 +29,7 @@ HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-ffp-contract=off",
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
 ]
 HOST_FLAGS = ["-O2", "-fPIC", "-std=c++17", "-Wall"]

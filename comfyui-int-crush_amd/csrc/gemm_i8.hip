@@ -6,24 +6,51 @@
 // A = activation codes [M, K] int8, K-major.  B = weights [N, K], K-major, as
 // int8 (W8A8, triton_int8_gemm.py:46-132) or as packed INT4 nibbles (W4A8,
 // triton_w4a8_gemm.py:40-108 plus the unpack of triton_int4_to_int8_unpack.py:26-52,
-// here fused into the global->LDS copy so the unpacked weight never reaches HBM).
+// here fused into the weight staging so the unpacked weight never reaches HBM).
 //
-// Tiling: 256 threads = 4 waves in a 2x2 grid; each wave owns a (BM/2)x(BN/2)
-// sub-tile built from v_mfma_i32_32x32x32_i8 tiles.  K advances 64 bytes per
-// stage through a double-buffered LDS ring whose 16-byte chunks are XOR
-// swizzled by row to keep ds_read_b128 fragment loads free of bank conflicts.
-// INT4 nibbles are expanded to 16*q (int8) with two masks and a byte permute;
-// the factor 16 is removed exactly in the epilogue (power-of-two scaling).
+// Work decomposition (one 512-thread workgroup per CU, two waves per SIMD):
+//   * a BM x BN output tile per workgroup, 8 waves in a WGM x (8/WGM) grid, each
+//     wave owning (BM/WGM) x (BN*WGM/8) built from v_mfma_i32_32x32x32_i8 tiles
+//     whose int32 accumulators stay in architectural VGPRs;
+//   * K advances 64 bytes per stage through a 4-deep LDS ring.  Activation rows
+//     (and int8 weight rows) travel HBM -> LDS with global_load_lds_dwordx4, so
+//     they never occupy VGPRs; the issuing lane is chosen so that the 16-byte
+//     chunks land XOR-swizzled by row, which keeps the ds_read_b128 fragment
+//     loads free of bank conflicts;
+//   * packed INT4 weights are loaded into VGPRs two stages ahead, expanded to
+//     16*q (int8) with two masks and a byte permute, and written to LDS once per
+//     workgroup; the factor 16 is removed exactly in the epilogue;
+//   * per-group scales (group = 128 = two stages) fold the int32 partials into
+//     an fp32 accumulator with one convert + FMA per element and group.  Two
+//     int32 accumulator sets alternate between groups so the fold of one group
+//     overlaps the MFMAs of the next.
 #include <type_traits>
 
 #include "ic_common.h"
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kRowBytes = 64;  // bytes of K per LDS row per stage
+constexpr int kNT = 512;  // threads per workgroup
 
-IC_DEV int lds_off(int row, int chunk) { return row * kRowBytes + ((chunk ^ ((row >> 1) & 3)) << 4); }
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// LDS rows hold BK bytes of K (BK/16 chunks of 16 bytes), the chunk index
+// XOR-swizzled by row.  With these swizzles the MFMA fragment reads (32
+// consecutive rows at chunk c and c+1) run at the full ds_read_b128 rate on
+// gfx950 (~232 B/clk/CU measured); unswizzled rows are 4-way (64 B) or 8-way
+// (128 B) bank-conflicted.
+template <int BK> IC_DEV int swz(int row) {
+  if constexpr (BK == 64) return (row >> 2) & 3;
+  else return (row >> 1) & 7;
+}
+template <int BK> IC_DEV int lds_off(int row, int chunk) { return row * BK + ((chunk ^ swz<BK>(row)) << 4); }
+
+// Block until at most N vector-memory operations of this wave are outstanding
+// (they retire in issue order).
+template <int N> IC_DEV void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
 // 8 INT4 nibbles (low nibble = even k) -> 8 int8 values 16*q in natural k order.
 IC_DEV void unpack8_x16(uint32_t P, uint32_t& w0, uint32_t& w1) {
@@ -51,123 +78,175 @@ IC_DEV void tile_coords(int b, int nb, int tiles_m, int tiles_n, int& tm, int& t
   tn = r / gsize;
 }
 
-template <int BM, int BN, bool INT4, int GS, int OUT_DT, bool ACC_OUT>
-__global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(
+// Tile configuration: BM x BN output tile, WGM wave rows, BK K-bytes per LDS
+// stage, NS-deep LDS ring.
+template <int BM_, int BN_, int WGM_, int BK_, int NS_>
+struct Tile {
+  static constexpr int BM = BM_, BN = BN_, WGM = WGM_, BK = BK_, NS = NS_;
+  static constexpr size_t lds_bytes() { return (size_t)NS * (BM + BN) * BK; }
+};
+
+template <class TL, bool INT4, int GS, int OUT_DT, bool ACC_OUT>
+__global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
     const int8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
     const float* __restrict__ s_a, const float* __restrict__ s_w, int G,
     const void* __restrict__ bias, int bias_dt, void* __restrict__ C, int64_t ldc, int M, int N,
     int K, int32_t* __restrict__ acc_out) {
-  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int BM = TL::BM, BN = TL::BN, WGM = TL::WGM, BK = TL::BK, NS = TL::NS;
+  constexpr int WGN = 8 / WGM;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int A_CH = BM * 4 / kThreads;                      // 16-byte A chunks per thread
-  constexpr int B_CH = INT4 ? BN * 2 / kThreads : BN * 4 / kThreads;
-  constexpr int STAGE = (BM + BN) * kRowBytes;
-  static_assert(TM >= 1 && TN >= 1 && A_CH >= 1 && B_CH >= 1, "tile too small");
-  static_assert(GS == 0 || GS == 128, "group size");
+  constexpr int NC = BK / 16;                     // 16-byte chunks per LDS row
+  constexpr int RPB = 1024 / BK;                  // rows per 1 KB DMA block
+  constexpr int A_DMA = BM / RPB / 8;             // DMA blocks of A per wave per stage
+  constexpr int B_DMA = INT4 ? 0 : BN / RPB / 8;  // same for int8 weights
+  constexpr int PK = INT4 ? BN * BK / 2 / kNT : 0;  // packed weight bytes per thread per stage
+  constexpr int B_LD = INT4 ? (PK + 15) / 16 : 0;   // packed-weight load instructions per stage
+  constexpr int D = A_DMA + B_DMA;                // DMA instructions per thread per stage
+  constexpr int STAGE = (BM + BN) * BK;
+  constexpr int KS = BK / 32;                     // MFMA K-steps per stage
+  constexpr int SPG = GS == 0 ? 1 : GS / BK;      // stages per scale group
+  static_assert(TM >= 1 && TN >= 1 && A_DMA >= 1 && (INT4 || B_DMA >= 1), "tile too small");
+  static_assert(!INT4 || PK == 8 || PK == 16 || PK == 32, "packed weight staging");
+  static_assert(GS == 0 || (GS == 128 && (BK == 64 || BK == 128)), "group size");
+  static_assert(NS >= 2, "ring depth");
 
   extern __shared__ __attribute__((aligned(16))) char smem[];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int wr = wave >> 1, wc = wave & 1;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (DMA bases live in M0)
+  const int wr = wave / WGN, wc = wave % WGN;
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   int tm, tn;
   tile_coords(blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int KT = K / 64;
+  const int KT = K / BK;
 
-  v4u ra[A_CH], rb[B_CH];
-  auto gload = [&](int kt) {
-    const int k0 = kt * 64;
+  // ---- staging: DMA of A (and int8 B) rows into the LDS ring.  Lane L of DMA
+  // block b covers LDS slot (row RPB*b + L/NC, chunk slot L%NC) and so loads
+  // global chunk (L%NC) ^ swz(row) of that row; every row segment is a whole
+  // number of 128-byte lines when BK = 128.
+  const int dma_row = lane / NC, dma_slot = lane % NC;
+  auto issue_dma = [&](int kt) {
+    char* st = smem + (kt % NS) * STAGE;
+    const int k0 = kt * BK;
 #pragma unroll
-    for (int c = 0; c < A_CH; ++c) {
-      const int q = tid + kThreads * c;
-      const int row = min(m0 + (q >> 2), M - 1);
-      ra[c] = *(const v4u*)(A + (int64_t)row * lda + k0 + (q & 3) * 16);
+    for (int c = 0; c < A_DMA; ++c) {
+      const int blk = wave + 8 * c;
+      const int row = RPB * blk + dma_row;
+      const int chunk = dma_slot ^ swz<BK>(row);
+      const int gr = min(m0 + row, M - 1);
+      __builtin_amdgcn_global_load_lds(A + (int64_t)gr * lda + k0 + chunk * 16,
+                                       (lds_ptr_t)(st + blk * 1024), 16, 0, 0);
     }
+    if constexpr (!INT4) {
+      char* sb = st + BM * BK;
 #pragma unroll
-    for (int c = 0; c < B_CH; ++c) {
-      const int q = tid + kThreads * c;
-      if constexpr (INT4) {
-        const int row = min(n0 + (q >> 1), N - 1);
-        rb[c] = *(const v4u*)(B + (int64_t)row * ldb + (k0 >> 1) + (q & 1) * 16);
-      } else {
-        const int row = min(n0 + (q >> 2), N - 1);
-        rb[c] = *(const v4u*)(B + (int64_t)row * ldb + k0 + (q & 3) * 16);
-      }
-    }
-  };
-  auto sstore = [&](int buf) {
-    char* sA = smem + buf * STAGE;
-    char* sB = sA + BM * kRowBytes;
-#pragma unroll
-    for (int c = 0; c < A_CH; ++c) {
-      const int q = tid + kThreads * c;
-      *(v4u*)(sA + lds_off(q >> 2, q & 3)) = ra[c];
-    }
-#pragma unroll
-    for (int c = 0; c < B_CH; ++c) {
-      const int q = tid + kThreads * c;
-      if constexpr (INT4) {
-        const int row = q >> 1, h = q & 1;
-        uint32_t w[8];
-        unpack8_x16(rb[c].x, w[0], w[1]);
-        unpack8_x16(rb[c].y, w[2], w[3]);
-        unpack8_x16(rb[c].z, w[4], w[5]);
-        unpack8_x16(rb[c].w, w[6], w[7]);
-        *(v4u*)(sB + lds_off(row, 2 * h)) = v4u{w[0], w[1], w[2], w[3]};
-        *(v4u*)(sB + lds_off(row, 2 * h + 1)) = v4u{w[4], w[5], w[6], w[7]};
-      } else {
-        *(v4u*)(sB + lds_off(q >> 2, q & 3)) = rb[c];
+      for (int c = 0; c < B_DMA; ++c) {
+        const int blk = wave + 8 * c;
+        const int row = RPB * blk + dma_row;
+        const int chunk = dma_slot ^ swz<BK>(row);
+        const int gr = min(n0 + row, N - 1);
+        __builtin_amdgcn_global_load_lds(B + (int64_t)gr * ldb + k0 + chunk * 16,
+                                         (lds_ptr_t)(sb + blk * 1024), 16, 0, 0);
       }
     }
   };
 
-  v16i acc[TM][TN];
-  v16f facc[TM][TN];
-  (void)facc;
-  if constexpr (GS == 0) {
+  // ---- packed INT4 weights: global -> VGPR (two stages ahead) -> unpack -> LDS.
+  // Thread t owns PK packed bytes (2*PK k values) of one weight row per stage.
+  constexpr int PPR = INT4 ? (BK / 2) / PK : 1;   // threads per weight row
+  typedef uint32_t pk_t __attribute__((ext_vector_type(PK >= 16 ? 4 : 2)));
+  struct PkRegs { pk_t v[B_LD > 0 ? B_LD : 1]; };
+  const int pk_row = tid / PPR;
+  const int pk_part = tid % PPR;
+  const uint8_t* pk_src = B + (int64_t)min(n0 + pk_row, N - 1) * ldb + pk_part * PK;
+  auto load_pk = [&](int kt) -> PkRegs {
+    PkRegs r{};
+    if constexpr (INT4) {
+#pragma unroll
+      for (int i = 0; i < B_LD; ++i) r.v[i] = *(const pk_t*)(pk_src + kt * (BK / 2) + 16 * i);
+    }
+    return r;
+  };
+  auto store_pk = [&](int kt, const PkRegs& p) {
+    if constexpr (INT4) {
+      char* sb = smem + (kt % NS) * STAGE + BM * BK;
+      const int c0 = pk_part * (PK / 8);  // first unpacked 16-byte chunk of this thread
+#pragma unroll
+      for (int i = 0; i < B_LD; ++i) {
+        uint32_t w[4];
+        unpack8_x16(p.v[i][0], w[0], w[1]);
+        unpack8_x16(p.v[i][1], w[2], w[3]);
+        *(v4u*)(sb + lds_off<BK>(pk_row, c0 + 2 * i)) = v4u{w[0], w[1], w[2], w[3]};
+        if constexpr (PK >= 16) {
+          unpack8_x16(p.v[i][2], w[0], w[1]);
+          unpack8_x16(p.v[i][3], w[2], w[3]);
+          *(v4u*)(sb + lds_off<BK>(pk_row, c0 + 2 * i + 1)) = v4u{w[0], w[1], w[2], w[3]};
+        }
+      }
+    }
+  };
+
+  // In steady state (ring full, no refill skipped) exactly NS-2 iterations,
+  // each issuing its packed loads and then one stage of DMA, separate the DMA
+  // of stage s from the top of iteration s; near the ends of the K loop wait
+  // for everything instead.
+  constexpr int kSteadyAfter = (NS - 2) * (D + B_LD);
+
+  typedef int v4i_t __attribute__((ext_vector_type(4)));
+  // Two alternating int32 accumulator sets let the fold of one group overlap
+  // the MFMAs of the next; they only fit the register file for small wave tiles.
+  constexpr bool kPingPong = GS == 128 && TM * TN <= 2;
+  constexpr int NSET = kPingPong ? 2 : 1;
+  v16i acc[NSET][TM][TN];
+  v16f facc[GS == 128 ? TM : 1][GS == 128 ? TN : 1];
+#pragma unroll
+  for (int s = 0; s < NSET; ++s)
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = v16i{};
-  } else {
+      for (int j = 0; j < TN; ++j) acc[s][i][j] = v16i{};
+  if constexpr (GS == 128) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) { facc[i][j] = v16f{}; acc[i][j] = v16i{}; }
+      for (int j = 0; j < TN; ++j) facc[i][j] = v16f{};
   }
 
-  // One 64-byte stage: two K-steps of 32.  ZERO_FIRST starts a fresh group
-  // accumulator (MFMA with a zero addend) instead of accumulating.
-  auto compute = [&](int buf, auto zero_first) {
-    constexpr bool ZF = decltype(zero_first)::value;
-    const char* sA = smem + buf * STAGE;
-    const char* sB = sA + BM * kRowBytes;
+  auto out_row = [&](int i, int r) { return m0 + wr * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); };
+  auto out_col = [&](int j) { return n0 + wc * WN + j * 32 + (lane & 31); };
+
+  // One stage (KS K-steps of 32) into accumulator set SET; ZF starts the set
+  // afresh (MFMA with a zero addend) on the first K-step.
+  auto mfma_stage = [&](int kt, auto set_c, auto zero_c) {
+    constexpr int SET = decltype(set_c)::value;
+    constexpr bool ZF = decltype(zero_c)::value;
+    const char* sA = smem + (kt % NS) * STAGE;
+    const char* sB = sA + BM * BK;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      v4i a[TM], b[TN];
+    for (int ks = 0; ks < KS; ++ks) {
+      v4i_t a[TM], b[TN];
       const int ch = 2 * ks + (lane >> 5);
 #pragma unroll
-      for (int i = 0; i < TM; ++i) a[i] = *(const v4i*)(sA + lds_off(wr * WM + i * 32 + (lane & 31), ch));
+      for (int i = 0; i < TM; ++i) a[i] = *(const v4i_t*)(sA + lds_off<BK>(wr * WM + i * 32 + (lane & 31), ch));
 #pragma unroll
-      for (int j = 0; j < TN; ++j) b[j] = *(const v4i*)(sB + lds_off(wc * WN + j * 32 + (lane & 31), ch));
+      for (int j = 0; j < TN; ++j) b[j] = *(const v4i_t*)(sB + lds_off<BK>(wc * WN + j * 32 + (lane & 31), ch));
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-          if (ZF && ks == 0) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], v16i{}, 0, 0, 0);
-          else acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+          if (ZF && ks == 0) acc[SET][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], v16i{}, 0, 0, 0);
+          else acc[SET][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[SET][i][j], 0, 0, 0);
         }
     }
   };
 
-  // Output coordinates of accumulator element r of tile (i, j) for this lane.
-  auto out_row = [&](int i, int r) { return m0 + wr * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); };
-  auto out_col = [&](int j) { return n0 + wc * WN + j * 32 + (lane & 31); };
-
-  // Per-group fold: facc += f32(acc_g) * s_w[n, g] (16*acc_g with s_w/16 for INT4).
-  auto fold = [&](int g) {
+  // Per-group fold of set SET (group g): facc += f32(acc_g) * s_w[n, g]
+  // (16*acc_g with s_w/16 for INT4, which is exactly the same product).
+  auto fold = [&](int g, auto set_c) {
+    constexpr int SET = decltype(set_c)::value;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int n = min(out_col(j), N - 1);
@@ -179,28 +258,119 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int m = out_row(i, r), nn = out_col(j);
-            if (m < M && nn < N) acc_out[((int64_t)g * M + m) * N + nn] = INT4 ? (acc[i][j][r] >> 4) : acc[i][j][r];
+            if (m < M && nn < N)
+              acc_out[((int64_t)g * M + m) * N + nn] = INT4 ? (acc[SET][i][j][r] >> 4) : acc[SET][i][j][r];
           }
         }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) facc[i][j][r] = __builtin_fmaf((float)acc[i][j][r], sw, facc[i][j][r]);
+        for (int r = 0; r < 16; ++r)
+          facc[i][j][r] = __builtin_fmaf((float)acc[SET][i][j][r], sw, facc[i][j][r]);
       }
     }
   };
 
-  gload(0);
-  sstore(0);
-  __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    if (kt + 1 < KT) gload(kt + 1);
-    if constexpr (GS == 128) {
-      if ((kt & 1) == 0) compute(kt & 1, std::true_type{});
-      else { compute(kt & 1, std::false_type{}); fold(kt >> 1); }
-    } else {
-      compute(kt & 1, std::false_type{});
+  // ---- prologue: packed loads of stages 0 and 1 first, then NS-1 stages of DMA
+  PkRegs pk0{}, pk1{};
+  if constexpr (INT4) {
+    pk0 = load_pk(0);
+    if (KT > 1) pk1 = load_pk(1);
+  }
+#pragma unroll
+  for (int t = 0; t < NS - 1; ++t)
+    if (t < KT) issue_dma(t);
+  if constexpr (INT4) store_pk(0, pk0);
+
+  // One pipeline step: make stage s resident, refill the ring, stage the
+  // packed weights of s+1, then run the MFMAs of stage s.
+  auto step = [&](int s, auto set_c, auto zero_c, PkRegs& pk_next, PkRegs& pk_free) {
+    if (s >= NS - 1 && s + NS - 1 < KT) wait_vm<kSteadyAfter>();
+    else wait_vm<0>();
+    // every wave's DMA into stage s has landed and its LDS writes of stage s
+    // (packed weights) have completed; no wave still reads the slot refilled below
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if constexpr (INT4) {
+      if (s + 2 < KT) pk_free = load_pk(s + 2);
     }
-    if (kt + 1 < KT) sstore((kt + 1) & 1);
-    __syncthreads();
+    if (s + NS - 1 < KT) issue_dma(s + NS - 1);
+    if constexpr (INT4) {
+      if (s + 1 < KT) store_pk(s + 1, pk_next);
+    }
+    mfma_stage(s, set_c, zero_c);
+  };
+
+  using T0 = std::integral_constant<int, 0>;
+  using T1 = std::integral_constant<int, 1>;
+  using ZF = std::true_type;
+  using NZ = std::false_type;
+  // Stage s reads its packed weights from pk1 when s is even (pk0 when odd)
+  // and refills the other register set with stage s+2.
+  if constexpr (GS == 0) {
+    int s = 0;
+    for (; s + 1 < KT; s += 2) {
+      step(s, T0{}, NZ{}, pk1, pk0);
+      step(s + 1, T0{}, NZ{}, pk0, pk1);
+    }
+    if (s < KT) step(s, T0{}, NZ{}, pk1, pk0);
+  } else if constexpr (SPG == 2) {
+    const int NG = KT / 2;
+    if constexpr (kPingPong) {
+      int g = 0;
+      for (; g + 1 < NG; g += 2) {
+        const int s = 2 * g;
+        step(s, T0{}, ZF{}, pk1, pk0);
+        if (g > 0) fold(g - 1, T1{});
+        step(s + 1, T0{}, NZ{}, pk0, pk1);
+        step(s + 2, T1{}, ZF{}, pk1, pk0);
+        fold(g, T0{});
+        step(s + 3, T1{}, NZ{}, pk0, pk1);
+      }
+      if (g < NG) {
+        const int s = 2 * g;
+        step(s, T0{}, ZF{}, pk1, pk0);
+        if (g > 0) fold(g - 1, T1{});
+        step(s + 1, T0{}, NZ{}, pk0, pk1);
+        fold(g, T0{});
+      } else {
+        fold(g - 1, T1{});
+      }
+    } else {
+      for (int g = 0; g < NG; ++g) {
+        step(2 * g, T0{}, ZF{}, pk1, pk0);
+        step(2 * g + 1, T0{}, NZ{}, pk0, pk1);
+        fold(g, T0{});
+      }
+    }
+  } else {
+    // one stage per group
+    const int NG = KT;
+    if constexpr (kPingPong) {
+      int g = 0;
+      for (; g + 1 < NG; g += 2) {
+        step(g, T0{}, ZF{}, pk1, pk0);
+        if (g > 0) fold(g - 1, T1{});
+        step(g + 1, T1{}, ZF{}, pk0, pk1);
+        fold(g, T0{});
+      }
+      if (g < NG) {
+        step(g, T0{}, ZF{}, pk1, pk0);
+        if (g > 0) fold(g - 1, T1{});
+        fold(g, T0{});
+      } else {
+        fold(g - 1, T1{});
+      }
+    } else {
+      int g = 0;
+      for (; g + 1 < NG; g += 2) {
+        step(g, T0{}, ZF{}, pk1, pk0);
+        fold(g, T0{});
+        step(g + 1, T0{}, ZF{}, pk0, pk1);
+        fold(g + 1, T0{});
+      }
+      if (g < NG) {
+        step(g, T0{}, ZF{}, pk1, pk0);
+        fold(g, T0{});
+      }
+    }
   }
 
   // ---- epilogue
@@ -212,10 +382,14 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int m = out_row(i, r), n = out_col(j);
-          if (m < M && n < N) acc_out[(int64_t)m * N + n] = INT4 ? (acc[i][j][r] >> 4) : acc[i][j][r];
+          if (m < M && n < N) acc_out[(int64_t)m * N + n] = INT4 ? (acc[0][i][j][r] >> 4) : acc[0][i][j][r];
         }
   }
   if (C == nullptr) return;
+  // Each lane stores 16 rows of one column per 32x32 tile; row offsets within
+  // a tile stay in 32-bit arithmetic (the host bounds ldc).
+  constexpr int ESZ = OUT_DT == IC_DTYPE_F32 ? 4 : 2;
+  const bool full = m0 + BM <= M && n0 + BN <= N;
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int n = out_col(j);
@@ -223,22 +397,28 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_kernel(
     const float b = bias != nullptr ? ld_any_f32(bias, bias_dt, nc) : 0.0f;
     const float sw = GS == 0 ? s_w[nc] : 0.0f;
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i) {
+      const int mr0 = m0 + wr * WM + i * 32 + 4 * (lane >> 5);
+      char* cb = (char*)C + ((int64_t)mr0 * ldc + n) * ESZ;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = out_row(i, r);
-        if (m >= M || n >= N) continue;
+        const int dr = 8 * (r >> 2) + (r & 3);
+        const int m = mr0 + dr;
+        if (!full && (m >= M || n >= N)) continue;
         float v;
         if constexpr (GS == 0) {
-          float a = (float)acc[i][j][r];
+          float a = (float)acc[0][i][j][r];
           if constexpr (INT4) a *= 0.0625f;
           v = a * (s_a[m] * sw);
         } else {
           v = facc[i][j][r] * s_a[m];
         }
         if (bias != nullptr) v = v + b;
-        st_from_f32<OUT_DT>(C, (int64_t)m * ldc + n, v);
+        st_from_f32<OUT_DT>(cb + dr * (int)ldc * ESZ, 0, v);
       }
+      // keep the scale loads of one 32x32 tile from being hoisted over all tiles
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 }
 
@@ -287,29 +467,38 @@ struct GemmArgs {
   int32_t* acc_out; bool int4;
 };
 
-template <int BM, int BN, bool INT4, int GS, int OUT_DT, bool ACC>
+template <class TL, bool INT4, int GS, int OUT_DT, bool ACC>
 hipError_t launch_mfma(const GemmArgs& g, hipStream_t st) {
-  const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-  const size_t shm = 2 * (BM + BN) * kRowBytes;
-  auto kern = gemm_i8_kernel<BM, BN, INT4, GS, OUT_DT, ACC>;
+  const int tiles = ((g.M + TL::BM - 1) / TL::BM) * ((g.N + TL::BN - 1) / TL::BN);
+  const size_t shm = TL::lds_bytes();
+  auto kern = gemm_i8_kernel<TL, INT4, GS, OUT_DT, ACC>;
   static bool attr_set = false;  // idempotent attribute; benign if raced
   if (!attr_set) {
-    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+    if (e != hipSuccess) return e;
     attr_set = true;
   }
-  kern<<<dim3(tiles), dim3(kThreads), shm, st>>>(g.A, g.lda, g.B, g.ldb, g.s_a, g.s_w, g.G, g.bias,
-                                                  g.bias_dt, g.C, g.ldc, g.M, g.N, g.K, g.acc_out);
+  kern<<<dim3(tiles), dim3(kNT), shm, st>>>(g.A, g.lda, g.B, g.ldb, g.s_a, g.s_w, g.G, g.bias,
+                                             g.bias_dt, g.C, g.ldc, g.M, g.N, g.K, g.acc_out);
   return hipGetLastError();
 }
 
+// Tile choices: large tiles when both dimensions fill them, 128-byte K stages
+// (whole cache lines per row) whenever K allows.
 template <bool INT4, int GS, int OUT_DT, bool ACC>
 hipError_t pick_tile(const GemmArgs& g, hipStream_t st) {
+  const bool k128 = g.K % 128 == 0;
   if constexpr (GS == 0) {
-    if (g.M >= 256 && g.N >= 256) return launch_mfma<256, 256, INT4, GS, OUT_DT, ACC>(g, st);
-    return launch_mfma<128, 128, INT4, GS, OUT_DT, ACC>(g, st);
+    if (g.M > 128 && g.N > 128) {
+      if (k128) return launch_mfma<Tile<256, 256, 2, 128, 2>, INT4, GS, OUT_DT, ACC>(g, st);
+      return launch_mfma<Tile<256, 256, 2, 64, 4>, INT4, GS, OUT_DT, ACC>(g, st);
+    }
+    if (k128) return launch_mfma<Tile<128, 128, 2, 128, 4>, INT4, GS, OUT_DT, ACC>(g, st);
+    return launch_mfma<Tile<128, 128, 2, 64, 4>, INT4, GS, OUT_DT, ACC>(g, st);
   } else {
-    if (g.M >= 256 && g.N >= 128) return launch_mfma<256, 128, INT4, GS, OUT_DT, ACC>(g, st);
-    return launch_mfma<128, 128, INT4, GS, OUT_DT, ACC>(g, st);
+    // grouped scales need K % 128 == 0
+    if (g.M > 128) return launch_mfma<Tile<256, 128, 4, 128, 3>, INT4, GS, OUT_DT, ACC>(g, st);
+    return launch_mfma<Tile<128, 128, 2, 128, 4>, INT4, GS, OUT_DT, ACC>(g, st);
   }
 }
 
@@ -342,6 +531,8 @@ hipError_t launch_generic(const GemmArgs& g, int gsize, hipStream_t st) {
 bool mfma_shape_ok(const GemmArgs& g, int gsize) {
   if (g.K % 64 != 0) return false;
   if (g.G > 1 && gsize != 128) return false;
+  // 16-byte DMA / vector loads need aligned bases and strides; packed INT4
+  // rows are read 8 or 16 bytes at a time
   if (((uintptr_t)g.A & 15) || ((uintptr_t)g.B & 15) || (g.lda & 15) || (g.ldb & 15)) return false;
   return true;
 }
@@ -353,6 +544,8 @@ int run_gemm(GemmArgs g, hipStream_t st, const char* who, bool force_generic) {
   if (g.int4 ? (g.ldb * 2 < g.K) : (g.ldb < g.K))
     return ic_set_error(IC_ERR_INVALID_ARG, "%s: weight row stride %lld too small for K=%d", who,
                         (long long)g.ldb, g.K);
+  if (g.ldc >= (1LL << 24))
+    return ic_set_error(IC_ERR_UNSUPPORTED, "%s: output row stride %lld too large", who, (long long)g.ldc);
   if (g.G < 1) return ic_set_error(IC_ERR_INVALID_ARG, "%s: num_groups must be >= 1", who);
   if (g.G > 1 && (g.K % g.G != 0))
     return ic_set_error(IC_ERR_INVALID_ARG, "%s: K=%d not divisible by num_groups=%d", who, g.K, g.G);
@@ -404,8 +597,6 @@ int ic_gemm_w4a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint
 
 int ic_gemm_w8a8_acc_i32(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8_t* w,
                          int64_t N, int64_t ldw, int32_t* acc, int generic, void* stream) {
-  static const float one = 1.0f;
-  (void)one;
   GemmArgs g{xq, ldx, (const uint8_t*)w, ldw, nullptr, nullptr, 1, nullptr, 0, nullptr,
              IC_DTYPE_F32, N, (int)M, (int)N, (int)K, acc, false};
   // scales are not read when no output is requested; pass the accumulator as a dummy

@@ -21,7 +21,9 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kRowBytes = 64;  // 32 fp16 K values per LDS row per stage
 
-IC_DEV int lds_off(int row, int chunk) { return row * kRowBytes + ((chunk ^ ((row >> 1) & 3)) << 4); }
+// 16-byte chunks XOR-swizzled by (row >> 2): conflict-free ds_read_b128 for
+// 32-row MFMA fragments on gfx950.
+IC_DEV int lds_off(int row, int chunk) { return row * kRowBytes + ((chunk ^ ((row >> 2) & 3)) << 4); }
 
 IC_DEV void tile_coords(int b, int nb, int tiles_m, int tiles_n, int& tm, int& tn) {
   const int xcd = b & 7, local = b >> 3;
