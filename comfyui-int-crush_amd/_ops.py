@@ -1,0 +1,589 @@
+"""INT-Crush ops factory: the ComfyUI `custom_operations` class whose Linear
+runs the gfx950 kernels.
+
+Drop-in counterpart of the reference's _ops.py:146-883.  `make_intcrush_ops`
+keeps its signature and memoisation, the returned class derives from
+ComfyUI's `manual_cast`, and its Linear keeps every `_intcrush_*` attribute
+that LoRA attach (`_lora.py`), graph replay (`_cuda_graph.py`) and the
+loaders read.  The weight format, state-dict keys and per-layer rotation
+rule are unchanged, so existing INT-Crush .safetensors files load as before.
+
+Forward dispatch (reference _ops.py:817-862):
+  INT4, rotated layer        -> W4A8: one fused prep+quantize kernel
+                                (SmoothRot divide, Hadamard, pad, PermuQuant
+                                gather, per-token INT8) + INT4xINT8 MFMA GEMM
+                                with the nibble unpack and the per-row or
+                                per-group dequant fused in
+  INT4, not rotated / use_w4a16 -> W4A16: fused prep kernel + INT4->fp16/bf16
+                                MFMA GEMM
+  INT4, use_pytorch          -> fp32 dequant -> F.linear (reference fallback)
+  INT8                       -> hipGraph replay of prep+quantize+GEMM, or the
+                                same kernels eagerly (zero-point, casting hooks)
+  M <= 16 tokens             -> the bandwidth-bound GEMV kernels
+
+Device tensors never fall back to PyTorch silently: if the HIP library is
+missing the forward raises, unless INTCRUSH_ALLOW_TORCH_FALLBACK=1 (or
+use_pytorch=True) asks for the PyTorch path explicitly.  CPU tensors use the
+PyTorch path, as the reference does without kernels.
+
+Reference behaviours kept on purpose (documented quirks):
+  * the W4A16 and PyTorch INT4 paths ignore the bias (_ops.py:474, :488);
+    INTCRUSH_W4A16_BIAS=1 adds it;
+  * the INT8 paths feed the raw (unrotated) input to the SVD low-rank
+    residual (_ops.py:567, :577).
+"""
+from __future__ import annotations
+
+import logging
+import os
+from typing import Any, Callable
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _hip_runtime as _rt
+from ._cuda_graph import CudaGraphRunner
+from ._quant_utils import expand_group_scales, rotate_activations
+from .quant_layout import IntCrushInt4Layout, IntCrushInt8Layout
+
+_log = logging.getLogger(__name__)
+
+# Layer-name substrings that disable rotation (_ops.py:30-32).
+_NO_ROTATION_NAME_SUBSTRINGS: tuple[str, ...] = (
+    "embed", "norm", "modulation", "output", "lm_head", "proj_out",
+)
+
+# State-dict key suffixes (_ops.py:36-45).
+_SD_KEY_WEIGHT = "weight"
+_SD_KEY_SCALE = "weight_scale"
+_SD_KEY_ZP = "weight_zp"
+_SD_KEY_PERM = "weight_perm"
+_SD_KEY_SMOOTH = "weight_smooth"
+_SD_KEY_SMOOTHROT = "weight_smoothrot_factors"
+_SD_KEY_L1 = "weight_L1"
+_SD_KEY_L2 = "weight_L2"
+_SD_KEY_QUANT = "comfy_quant"
+_SD_KEY_BIAS = "bias"
+_KNOWN_SUFFIXES = (_SD_KEY_WEIGHT, _SD_KEY_SCALE, _SD_KEY_ZP, _SD_KEY_PERM, _SD_KEY_SMOOTH,
+                   _SD_KEY_SMOOTHROT, _SD_KEY_L1, _SD_KEY_L2, _SD_KEY_BIAS, _SD_KEY_QUANT)
+_VALID_SCALE_DTYPES = (torch.float16, torch.float32)
+
+
+def _env_flag(name: str) -> bool:
+    return os.environ.get(name, "0") == "1"
+
+
+# ── lazy ComfyUI imports (_ops.py:53-72) ──────────────────────────────────
+_QuantizedTensor = None
+_cast_fns = None
+
+
+def _get_qt():
+    global _QuantizedTensor
+    if _QuantizedTensor is None:
+        from comfy.quant_ops import QuantizedTensor
+
+        _QuantizedTensor = QuantizedTensor
+    return _QuantizedTensor
+
+
+def _get_cast():
+    global _cast_fns
+    if _cast_fns is None:
+        from comfy.ops import cast_bias_weight, uncast_bias_weight
+
+        _cast_fns = (cast_bias_weight, uncast_bias_weight)
+    return _cast_fns
+
+
+def _move_adapter_weights(adapter: Any, device: torch.device, dtype: torch.dtype) -> None:
+    moved = [w.to(device=device, dtype=dtype) if isinstance(w, torch.Tensor) else w for w in adapter.weights]
+    adapter.weights = type(adapter.weights)(moved)
+
+
+def _hip_ready(x: torch.Tensor) -> bool:
+    """Whether the gfx950 kernels serve this input; raises for device tensors
+    when the library is missing and no PyTorch fallback was requested."""
+    if not x.is_cuda:
+        return False
+    if _rt.KERNELS_AVAILABLE:
+        return True
+    if _env_flag("INTCRUSH_ALLOW_TORCH_FALLBACK"):
+        return False
+    raise RuntimeError(
+        f"INT-Crush gfx950 kernels are not loaded ({_rt.LOAD_ERROR}); refusing a silent PyTorch "
+        "fallback on the GPU (set INTCRUSH_ALLOW_TORCH_FALLBACK=1 to allow it)")
+
+
+class _DeviceState:
+    """Per (device, activation dtype) kernel-side copies of a layer's
+    preparation tensors: rounded SmoothRot / SmoothQuant factors with their
+    reciprocals, and the int32 PermuQuant indices."""
+
+    __slots__ = ("smoothrot", "smooth", "perm")
+
+    def __init__(self, layer, device: torch.device, dtype: torch.dtype):
+        f = layer._intcrush_smoothrot_factors
+        self.smoothrot = _rt.prepare_factors(f.to(device), dtype) if f is not None else None
+        sm = layer._intcrush_smooth if f is None else None  # old SmoothQuant only without SmoothRot
+        self.smooth = _rt.prepare_factors(sm.to(device), dtype) if sm is not None else None
+        p = layer._intcrush_perm
+        self.perm = _rt.prepare_perm(p.to(device), layer._intcrush_w_in) if p is not None else None
+
+
+# ── ops factory ───────────────────────────────────────────────────────────
+_ops_cache: dict[tuple, type] = {}
+
+
+def make_intcrush_ops(quant_format: str, rot_size: int, use_pytorch: bool = False,
+                      use_w4a16: bool = False) -> type:
+    """Build (once per argument tuple) the manual_cast ops class with the
+    INT-Crush Linear (_ops.py:146-163).
+
+    quant_format: "int4_crush" or "int8_crush"; rot_size: Hadamard block
+    size (0, 16, 64, 256, 1024, 4096); use_pytorch: force the PyTorch
+    dequant path; use_w4a16: never take the W4A8 path for INT4 layers."""
+    key = (quant_format, rot_size, use_pytorch, use_w4a16)
+    cls = _ops_cache.get(key)
+    if cls is not None:
+        return cls
+    from comfy.ops import manual_cast
+
+    class IntCrushOps(manual_cast):
+
+        class Linear(manual_cast.Linear):
+            """INT-Crush Linear: QuantizedTensor storage, gfx950 forward."""
+
+            def __init__(self, *args: Any, **kwargs: Any) -> None:
+                super().__init__(*args, **kwargs)
+                self._intcrush_is_quantized = False
+                self._intcrush_rot_need = True
+                self._intcrush_rot_size = rot_size
+                self._intcrush_perm = None
+                self._intcrush_smooth = None
+                self._intcrush_smoothrot_factors = None
+                self._intcrush_L1 = None
+                self._intcrush_L2 = None
+                self._intcrush_use_pytorch = use_pytorch
+                self._intcrush_use_w4a16 = use_w4a16
+                self._intcrush_w_in = None
+                self.quant_format = None
+                self.layout_type = None
+                self._intcrush_adapter = None
+                self._intcrush_lora_strength = None
+                self._intcrush_adapter_ready = False
+                self._intcrush_adapter_device = None
+                self._intcrush_dev_states = {}
+                self._graph_runner = None
+
+            # ── preparation state ─────────────────────────────────────
+            def _intcrush_state(self, x: torch.Tensor) -> _DeviceState:
+                key = (x.device, x.dtype)
+                st = self._intcrush_dev_states.get(key)
+                if st is None:
+                    if len(self._intcrush_dev_states) >= 4:
+                        self._intcrush_dev_states.clear()
+                    st = _DeviceState(self, x.device, x.dtype)
+                    self._intcrush_dev_states[key] = st
+                return st
+
+            def _intcrush_invalidate(self) -> None:
+                self._intcrush_dev_states = {}
+                self._graph_runner = None
+
+            def _kernel_rot(self) -> int:
+                return self._intcrush_rot_size if self._intcrush_rot_need else 0
+
+            # ── residuals (PyTorch, as in the reference) ──────────────
+            def _apply_adapter(self, x_raw: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+                """LoRA-family residual on the raw input (_ops.py:195-271).
+
+                Standard LoRA uses one [M, rank] intermediate and an in-place
+                addmm_; every other adapter type uses its own h() / g().
+                The graph runner is not invalidated here: the captured graph
+                covers only prep + quantize + GEMM, which an adapter does not
+                change (the reference drops the graph on every call, F12)."""
+                adapter = self._intcrush_adapter
+                if adapter is None:
+                    return out
+                if not self._intcrush_adapter_ready or self._intcrush_adapter_device != x_raw.device:
+                    _move_adapter_weights(adapter, x_raw.device, x_raw.dtype)
+                    self._intcrush_adapter_ready = True
+                    self._intcrush_adapter_device = x_raw.device
+                strength = self._intcrush_lora_strength
+                if adapter.name == "lora":
+                    up, down, alpha = adapter.weights[0], adapter.weights[1], adapter.weights[2]
+                    rank = down.shape[0]
+                    scale = (float(alpha) / rank if alpha else 1.0) * strength
+                    mid = F.linear(x_raw, down)
+                    out.addmm_(mid.to(out.dtype), up.t().to(out.dtype), beta=1, alpha=scale)
+                    return out
+                adapter.multiplier = strength
+                out.add_(adapter.h(x_raw, out).to(out.dtype))
+                return adapter.g(out)
+
+            def _apply_residuals(self, x: torch.Tensor, out: torch.Tensor,
+                                 x_prep: torch.Tensor | None = None) -> torch.Tensor:
+                """SVD low-rank residual, then the adapter (_ops.py:367-387)."""
+                L1, L2 = self._intcrush_L1, self._intcrush_L2
+                if L1 is not None and L2 is not None:
+                    if L1.device != x.device or L1.dtype != x.dtype:
+                        L1 = self._intcrush_L1 = L1.to(device=x.device, dtype=x.dtype)
+                    if L2.device != x.device or L2.dtype != x.dtype:
+                        L2 = self._intcrush_L2 = L2.to(device=x.device, dtype=x.dtype)
+                    src = x_prep if x_prep is not None else x.reshape(-1, x.shape[-1])
+                    mid = src.to(L1.dtype) @ L2.t()
+                    out.addmm_(mid.to(out.dtype), L1.t().to(out.dtype), beta=1, alpha=1)
+                self._apply_adapter(x.reshape(-1, x.shape[-1]), out)
+                return out
+
+            def _finish_forward(self, out: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+                return out.to(x.dtype).reshape(*x.shape[:-1], -1)
+
+            # ── activation preparation ───────────────────────────────
+            def _prep_activation(self, x: torch.Tensor, pad_to_w_in: bool = True,
+                                 apply_perm: bool = True) -> torch.Tensor:
+                """reshape -> SmoothRot divide -> Hadamard -> pad -> perm
+                (_ops.py:337-365).  Device tensors run the fused prep kernel;
+                CPU tensors the PyTorch ops of the reference."""
+                x2 = x.reshape(-1, x.shape[-1])
+                if _hip_ready(x2):
+                    st = self._intcrush_state(x2)
+                    R = self._kernel_rot()
+                    K_r = -(-x2.shape[-1] // R) * R if R else x2.shape[-1]
+                    w_in = max(self._intcrush_w_in, K_r) if pad_to_w_in else K_r
+                    perm = st.perm if (apply_perm and pad_to_w_in) else None
+                    if apply_perm and not pad_to_w_in and self._intcrush_perm is not None:
+                        return self._prep_activation_torch(x2, pad_to_w_in, apply_perm)
+                    return _rt.prepare_activation(x2, rot_size=R, w_in=w_in, smoothrot=st.smoothrot, perm=perm)
+                return self._prep_activation_torch(x2, pad_to_w_in, apply_perm)
+
+            def _prep_activation_torch(self, x2: torch.Tensor, pad_to_w_in: bool, apply_perm: bool):
+                f = self._intcrush_smoothrot_factors
+                if f is not None:
+                    x2 = x2 / f.to(device=x2.device, dtype=x2.dtype)
+                if self._intcrush_rot_need:
+                    x2 = rotate_activations(x2, self._intcrush_rot_size)
+                if pad_to_w_in and x2.shape[-1] < self._intcrush_w_in:
+                    x2 = F.pad(x2, (0, self._intcrush_w_in - x2.shape[-1]))
+                if apply_perm and self._intcrush_perm is not None:
+                    x2 = x2[..., self._intcrush_perm.to(x2.device)]
+                return x2
+
+            def _prep_int8_torch(self, x2: torch.Tensor) -> torch.Tensor:
+                """INT8 prep on CPU: _prep_activation then the old SmoothQuant
+                divide after the gather (_ops.py:529-533)."""
+                xp = self._prep_activation_torch(x2, True, True)
+                if self._intcrush_smoothrot_factors is None and self._intcrush_smooth is not None:
+                    xp = xp / self._intcrush_smooth.to(device=xp.device, dtype=xp.dtype)
+                return xp
+
+            # ── ComfyUI casting (VBAR / low-VRAM), _ops.py:401-433 ────
+            def _setup_casting(self, x: torch.Tensor):
+                QT = _get_qt()
+                need_cast = (
+                    self.comfy_cast_weights or self.weight_function or self.bias_function
+                    or getattr(self, "weight_lowvram_function", None) is not None
+                    or getattr(self, "bias_lowvram_function", None) is not None
+                )
+                if not need_cast:
+                    return self.weight, self.bias, None, QT
+                weight_dtype = self.weight._params.orig_dtype if isinstance(self.weight, QT) else x.dtype
+                cast, uncast_fn = _get_cast()
+                weight, bias, offload_stream = cast(self, input=None, dtype=weight_dtype, device=x.device,
+                                                    bias_dtype=x.dtype, offloadable=True)
+                return weight, bias, (lambda: uncast_fn(self, weight, bias, offload_stream)), QT
+
+            def _casting_hooks(self) -> bool:
+                return bool(self.comfy_cast_weights or self.weight_function or self.bias_function
+                            or getattr(self, "weight_lowvram_function", None)
+                            or getattr(self, "bias_lowvram_function", None))
+
+            # ── forward paths ────────────────────────────────────────
+            def _forward_predequant(self, weight, bias, x):
+                """Weight already dequantized by a wrapper (_ops.py:435-441)."""
+                x2 = self._prep_activation(x, pad_to_w_in=False, apply_perm=False)
+                out = F.linear(x2, weight.to(x2.dtype), None if bias is None else bias.to(x2.dtype))
+                out = self._apply_residuals(x, out, x_prep=x2)
+                return self._finish_forward(out, x)
+
+            @staticmethod
+            def _zp_correction(out, x_prep, scale, zp):
+                """out -= sum_k x_prep[m,k] * zp[n] * s[n, g(k)]: the zero-point
+                term of W = (q - zp) * s (_ops.py:449-461, group-aware)."""
+                N = out.shape[1]
+                s = scale.reshape(N, -1).float()
+                G = s.shape[1]
+                M, K = x_prep.shape
+                xs = x_prep.float().reshape(M, G, K // G).sum(-1)  # [M, G]
+                corr = xs @ (s * zp.reshape(-1, 1).float()).t()  # [M, N]
+                out.sub_(corr.to(out.dtype))
+
+            def _forward_int4_w4a8(self, qdata, weight, bias, x):
+                """W4A8 (_ops.py:443-464): fused prep+quantize, fused INT4 GEMM."""
+                x2 = x.reshape(-1, x.shape[-1])
+                st = self._intcrush_state(x2)
+                params = weight._params
+                R = self._intcrush_rot_size
+                need_prep = params.zp is not None or (self._intcrush_L1 is not None and self._intcrush_L2 is not None)
+                x_prep = (_rt.prepare_activation(x2, rot_size=R, w_in=self._intcrush_w_in, smoothrot=st.smoothrot,
+                                                 perm=st.perm) if need_prep else None)
+                q, s_a = _rt.rotate_quantize(x2, rot_size=R, w_in=self._intcrush_w_in, smoothrot=st.smoothrot,
+                                             perm=st.perm)
+                out = _rt.gemm_w4a8(q, qdata, params.scale, s_a, bias=bias, out_dtype=x.dtype)
+                if params.zp is not None:
+                    self._zp_correction(out, x_prep, params.scale, params.zp)
+                out = self._apply_residuals(x, out, x_prep=x_prep)
+                return self._finish_forward(out, x)
+
+            def _forward_int4_w4a16(self, qdata, weight, bias, x):
+                """W4A16 (_ops.py:466-481): fused prep, INT4->fp16/bf16 MFMA GEMM."""
+                x2 = x.reshape(-1, x.shape[-1])
+                st = self._intcrush_state(x2)
+                params = weight._params
+                x_prep = _rt.prepare_activation(x2, rot_size=self._kernel_rot(), w_in=self._intcrush_w_in,
+                                                smoothrot=st.smoothrot, perm=st.perm)
+                b = bias if _env_flag("INTCRUSH_W4A16_BIAS") else None
+                out = _rt.gemm_w4a16(x_prep, qdata, params.scale, bias=b)
+                if params.zp is not None:
+                    self._zp_correction(out, x_prep, params.scale, params.zp)
+                out = self._apply_residuals(x, out, x_prep=x_prep)
+                return self._finish_forward(out, x)
+
+            def _forward_int4_pytorch(self, qdata, weight, x):
+                """fp32 dequant -> F.linear (_ops.py:483-491)."""
+                w = IntCrushInt4Layout.dequantize(qdata, weight._params).to(x.device, x.dtype)
+                x2 = self._prep_activation_torch(x.reshape(-1, x.shape[-1]), True, True)
+                out = F.linear(x2, w)
+                out = self._apply_residuals(x, out, x_prep=x2)
+                return self._finish_forward(out, x)
+
+            def _forward_int8(self, qdata, weight, bias, x):
+                """INT8 (_ops.py:493-579): graph replay or eager kernels."""
+                params = weight._params
+                zp = params.zp
+                compute_dtype = x.dtype if x.dtype in (torch.float16, torch.bfloat16) else torch.bfloat16
+                x2 = x.reshape(-1, x.shape[-1])
+                if not _hip_ready(x2):
+                    # dequantize in compute_dtype, as the reference does (_ops.py:538-545)
+                    xp = self._prep_int8_torch(x2).to(compute_dtype)
+                    s = expand_group_scales(params.scale, qdata.shape[0], qdata.shape[1]).to(xp.device)
+                    s = s.to(compute_dtype)
+                    w = qdata.to(device=xp.device, dtype=compute_dtype) * s
+                    if zp is not None:
+                        w = w - zp.reshape(-1, 1).to(device=xp.device, dtype=compute_dtype) * s
+                    out = F.linear(xp, w, None if bias is None else bias.to(compute_dtype))
+                    out = self._apply_residuals(x, out)
+                    return self._finish_forward(out, x)
+                if zp is None and not self._casting_hooks() and _rt.USE_CUDA_GRAPHS:
+                    if self._graph_runner is None:
+                        self._graph_runner = CudaGraphRunner(self, safe_no_clone=True)
+                    out = self._graph_runner.run(x, bias, compute_dtype)
+                    out = self._apply_residuals(x, out)
+                    return self._finish_forward(out, x)
+                st = self._intcrush_state(x2)
+                R = self._kernel_rot()
+                fused = _rt.USE_FUSED_W8A8 and x2.dtype in (torch.float16, torch.bfloat16)
+                x_prep = None
+                if zp is not None or fused:
+                    x_prep = _rt.prepare_activation(x2, rot_size=R, w_in=self._intcrush_w_in, smoothrot=st.smoothrot,
+                                                    perm=st.perm, smooth=st.smooth)
+                if fused:
+                    out = _rt.fused_quant_int8_gemm_dequant(x_prep, qdata, params.scale, bias=bias,
+                                                            out_dtype=compute_dtype)
+                else:
+                    q, s_a = _rt.rotate_quantize(x2, rot_size=R, w_in=self._intcrush_w_in, smoothrot=st.smoothrot,
+                                                 perm=st.perm, smooth=st.smooth)
+                    out = _rt.fused_int8_gemm_dequant(q, qdata, params.scale, s_a, bias=bias, out_dtype=compute_dtype)
+                if zp is not None:
+                    self._zp_correction(out, x_prep, params.scale, zp)
+                out = self._apply_residuals(x, out)
+                return self._finish_forward(out, x)
+
+            # ── state-dict loading (_ops.py:583-761) ─────────────────
+            @staticmethod
+            def _detect_weight_format(weight, scale):
+                if weight is None or scale is None or scale.dtype not in _VALID_SCALE_DTYPES:
+                    return None
+                if weight.dtype == torch.uint8:
+                    return "int4_crush"
+                if weight.dtype == torch.int8:
+                    return "int8_crush"
+                return None
+
+            def _pop_intcrush_tensors(self, state_dict: dict, prefix: str) -> dict:
+                t = {
+                    "weight": state_dict.pop(prefix + _SD_KEY_WEIGHT),
+                    "scale": state_dict.pop(prefix + _SD_KEY_SCALE),
+                    "zp": state_dict.pop(prefix + _SD_KEY_ZP, None),
+                    "perm": state_dict.pop(prefix + _SD_KEY_PERM, None),
+                    "smooth": state_dict.pop(prefix + _SD_KEY_SMOOTH, None),
+                    "smoothrot_factors": state_dict.pop(prefix + _SD_KEY_SMOOTHROT, None),
+                    "L1": state_dict.pop(prefix + _SD_KEY_L1, None),
+                    "L2": state_dict.pop(prefix + _SD_KEY_L2, None),
+                    "bias": state_dict.pop(prefix + _SD_KEY_BIAS, None),
+                }
+                state_dict.pop(prefix + _SD_KEY_QUANT, None)
+                return t
+
+            def _store_intcrush_attrs(self, tensors: dict, params, device) -> None:
+                self._intcrush_perm = params.perm
+                self._intcrush_w_in = self.in_features
+                self._intcrush_smooth = (tensors["smooth"].float().to(device)
+                                         if tensors["smooth"] is not None else None)
+                self._intcrush_smoothrot_factors = (tensors["smoothrot_factors"].float().to(device)
+                                                    if tensors["smoothrot_factors"] is not None else None)
+                self._intcrush_L1 = (tensors["L1"].to(device=device, dtype=torch.float16)
+                                     if tensors["L1"] is not None else None)
+                self._intcrush_L2 = (tensors["L2"].to(device=device, dtype=torch.float16)
+                                     if tensors["L2"] is not None else None)
+                self._intcrush_invalidate()
+
+            @staticmethod
+            def _clear_known_missing_keys(missing_keys: list, prefix: str) -> None:
+                for suffix in _KNOWN_SUFFIXES:
+                    if prefix + suffix in missing_keys:
+                        missing_keys.remove(prefix + suffix)
+
+            def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
+                                      unexpected_keys, error_msgs):
+                from comfy.quant_ops import QUANT_ALGOS, QuantizedTensor, get_layout_class
+
+                fmt = self._detect_weight_format(state_dict.get(prefix + _SD_KEY_WEIGHT),
+                                                 state_dict.get(prefix + _SD_KEY_SCALE))
+                if fmt is None:
+                    super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys,
+                                                  unexpected_keys, error_msgs)
+                    return
+                qconfig = QUANT_ALGOS[fmt]
+                layout_type = qconfig["comfy_tensor_layout"]
+                layout_cls = get_layout_class(layout_type)
+                tensors = self._pop_intcrush_tensors(state_dict, prefix)
+                w0 = getattr(self, "weight", None)
+                device = w0.device if w0 is not None else torch.device("cpu")
+                name = prefix.lower()
+                rot_need = rot_size > 0 and not any(s in name for s in _NO_ROTATION_NAME_SUBSTRINGS)
+                self._intcrush_rot_need = rot_need
+                self._intcrush_rot_size = rot_size
+                self._intcrush_is_quantized = True
+                perm, zp = tensors["perm"], tensors["zp"]
+                scale = tensors["scale"].float()
+                if fmt == "int8_crush":
+                    scale = scale.reshape(-1)
+                params = layout_cls.Params(
+                    scale=scale.to(device=device), orig_dtype=torch.float16,
+                    orig_shape=(self.out_features, self.in_features), rot_need=rot_need, rot_size=rot_size,
+                    perm=perm.to(device=device) if perm is not None else None,
+                    zp=zp.to(device=device) if zp is not None else None,
+                )
+                self._store_intcrush_attrs(tensors, params, device)
+                self.weight = nn.Parameter(
+                    QuantizedTensor(tensors["weight"].to(device=device, dtype=qconfig["storage_t"]),
+                                    layout_type, params),
+                    requires_grad=False)
+                self.quant_format = fmt
+                self.layout_type = layout_type
+                b = tensors["bias"]
+                self.bias = nn.Parameter(b.to(device=device), requires_grad=False) if b is not None else None
+                if perm is not None:
+                    self.register_parameter("weight_perm", nn.Parameter(perm.to(device=device), requires_grad=False))
+                if zp is not None:
+                    self.register_parameter("weight_zp", nn.Parameter(zp.to(device=device), requires_grad=False))
+                self._clear_known_missing_keys(missing_keys, prefix)
+
+            def convert_weight(self, weight, inplace: bool = False):
+                """Keep QuantizedTensor weights as they are (_ops.py:763-768)."""
+                QT = _get_qt()
+                if self._intcrush_is_quantized and isinstance(weight, QT):
+                    return weight
+                return super().convert_weight(weight, inplace)
+
+            def set_weight(self, out_weight, inplace_update=False, seed=0, return_weight=False, **kwargs):
+                """Requantize patched float weights, keeping rotation and
+                permutation (_ops.py:770-807)."""
+                import dataclasses
+
+                self._intcrush_invalidate()
+                if not self._intcrush_is_quantized:
+                    w = out_weight.to(self.weight.dtype)
+                    if return_weight:
+                        return w
+                    self.weight = nn.Parameter(w, requires_grad=False)
+                    return None
+                from comfy.quant_ops import QuantizedTensor, get_layout_class
+
+                if isinstance(out_weight, QuantizedTensor):
+                    if return_weight:
+                        return out_weight
+                    self.weight = nn.Parameter(out_weight, requires_grad=False)
+                    return None
+                layout_cls = get_layout_class(self.layout_type)
+                packed, params = layout_cls.quantize(out_weight.float(), scale="recalculate",
+                                                     stochastic_rounding=seed)
+                params = dataclasses.replace(params, rot_need=self._intcrush_rot_need,
+                                             rot_size=self._intcrush_rot_size, perm=self._intcrush_perm)
+                qt = QuantizedTensor(packed, self.layout_type, params)
+                if return_weight:
+                    return qt
+                self.weight = nn.Parameter(qt, requires_grad=False)
+                return None
+
+            def set_bias(self, out_bias, inplace_update=False, seed=0, return_weight=False, **kwargs):
+                if out_bias is None:
+                    return None
+                if return_weight:
+                    return out_bias
+                self._graph_runner = None
+                self.bias = nn.Parameter(out_bias, requires_grad=False)
+                return None
+
+            # ── forward (_ops.py:817-862) ────────────────────────────
+            @torch.no_grad()
+            def forward(self, x: torch.Tensor) -> torch.Tensor:
+                if not self._intcrush_is_quantized:
+                    return super().forward(x)
+                weight, bias, uncast, QT = self._setup_casting(x)
+                try:
+                    if not isinstance(weight, QT):
+                        return self._forward_predequant(weight, bias, x)
+                    qdata = weight._qdata
+                    if isinstance(weight._params, IntCrushInt4Layout.Params):
+                        if self._intcrush_use_pytorch or not _hip_ready(x):
+                            return self._forward_int4_pytorch(qdata, weight, x)
+                        if (not self._intcrush_use_w4a16 and self._intcrush_rot_need
+                                and _rt.HIP_W4A8_GEMM and _rt.HIP_ROTATE_QUANT):
+                            return self._forward_int4_w4a8(qdata, weight, bias, x)
+                        if x.dtype in (torch.float16, torch.bfloat16) and _rt.HIP_W4A16_GEMM:
+                            return self._forward_int4_w4a16(qdata, weight, bias, x)
+                        return self._forward_int4_pytorch(qdata, weight, x)
+                    if isinstance(weight._params, IntCrushInt8Layout.Params):
+                        return self._forward_int8(qdata, weight, bias, x)
+                    return super().forward(x)
+                finally:
+                    if uncast is not None:
+                        uncast()
+
+        class GroupNorm(manual_cast.GroupNorm):
+            pass
+
+        class LayerNorm(manual_cast.LayerNorm):
+            pass
+
+        class Conv2d(manual_cast.Conv2d):
+            pass
+
+        class Conv3d(manual_cast.Conv3d):
+            pass
+
+        class ConvTranspose2d(manual_cast.ConvTranspose2d):
+            pass
+
+        class Embedding(manual_cast.Embedding):
+            pass
+
+    _ops_cache[key] = IntCrushOps
+    return IntCrushOps
+
+
+__all__ = ["make_intcrush_ops"]

@@ -12,6 +12,10 @@ if ROOT not in sys.path:
 TESTS = os.path.dirname(os.path.abspath(__file__))
 if TESTS not in sys.path:
     sys.path.insert(0, TESTS)
+# ComfyUI is not installed: a minimal stand-in of the modules the plugin uses
+FAKE_COMFY = os.path.join(TESTS, "fake_comfy")
+if FAKE_COMFY not in sys.path:
+    sys.path.insert(0, FAKE_COMFY)
 
 import __graft_entry__  # noqa: E402
 
