@@ -21,6 +21,18 @@ int ic_check_launch(const char* who) {
   return IC_OK;
 }
 
+// Compute units of the current device (cached per device id).
+int ic_num_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < 64 && cache[dev] > 0) return cache[dev];
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+  if (dev < 64) cache[dev] = n;
+  return n;
+}
+
 extern "C" {
 const char* ic_version(void) { return "intcrush-gfx950 0.1.0"; }
 const char* ic_last_error(void) { return g_err; }

@@ -17,6 +17,7 @@
 // Thread-local error message + launch checking (defined in capi.cpp).
 int ic_set_error(int code, const char* fmt, ...);
 int ic_check_launch(const char* who);
+int ic_num_cus();  // compute units of the current device
 
 // Arguments of the fused preparation kernels (internal; the ABI is flat).
 struct ic_rotq_args {
@@ -132,6 +133,23 @@ IC_DEV int quant_code(float v, double rs) {
   c = c < -128 ? -128 : c;
   c = c > 127 ? 127 : c;
   return c;
+}
+
+// Same code without the clamp, for values v with |v| <= m (the row abs-max the
+// scale was built from): then |RN32(v/s)| <= RN32(127 * (1 + 2^-24)) < 127.5,
+// so trunc(q +- 0.5) already lies in [-127, 127]; infinite or NaN quotients
+// only arise with m = inf or v = NaN, where v_cvt_i32_f32 returns 0 and the
+// clamped form returns 0 as well.
+IC_DEV int quant_code_nc(float v, double rs) {
+  const float q = (float)((double)v * rs);
+  return (int)(q + __builtin_copysignf(0.5f, q));
+}
+
+// Low bytes of four ints packed little-endian into one dword.
+IC_DEV uint32_t pack4_lo_bytes(int c0, int c1, int c2, int c3) {
+  const uint32_t lo = __builtin_amdgcn_perm((uint32_t)c1, (uint32_t)c0, 0x0c0c0400u);
+  const uint32_t hi = __builtin_amdgcn_perm((uint32_t)c3, (uint32_t)c2, 0x04000c0cu);
+  return lo | hi;
 }
 
 // ------------------------------------------------------------ reductions

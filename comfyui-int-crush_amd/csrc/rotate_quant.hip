@@ -19,43 +19,11 @@
 // A tile of 4096 positions is spread as 16 contiguous elements per thread
 // (digits 0-1 in registers); digits 2-3 are reached through one LDS transpose
 // among 16 threads, digits 4-5 through a second transpose among 256 threads.
-#include "ic_common.h"
+#include "rq_common.h"
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kTile = 4096;       // positions per tile (kThreads * 16)
-constexpr int kMaxTiles = 4;      // K_w <= 16384 for the fused single-pass kernel
-constexpr int kPadStride = 18;    // 16 doubles + 2 pad per 16-position row of the transpose buffer
-
-IC_DEV void h4(double& a, double& b, double& c, double& d) {
-  double s = (a + b) + (c + d);
-  double ya = __builtin_fma(s, 0.5, -d);
-  double yb = __builtin_fma(s, 0.5, -c);
-  double yc = __builtin_fma(s, 0.5, -b);
-  double yd = __builtin_fma(s, 0.5, -a);
-  a = ya; b = yb; c = yc; d = yd;
-}
-// radix-4 stage on the low / high 2-bit digit of a 16-element register array
-IC_DEV void stage_lo(double* v) {
-#pragma unroll
-  for (int a = 0; a < 4; ++a) h4(v[4 * a + 0], v[4 * a + 1], v[4 * a + 2], v[4 * a + 3]);
-}
-IC_DEV void stage_hi(double* v) {
-#pragma unroll
-  for (int a = 0; a < 4; ++a) h4(v[a], v[4 + a], v[8 + a], v[12 + a]);
-}
-// physical slot of logical position p in the padded transpose buffer
-IC_DEV int tslot(int p) { return p + 2 * (p >> 4); }
-
-template <int DT> IC_DEV u16 f32_bits16(float v) {
-  if constexpr (DT == IC_DTYPE_F16) return f32_to_f16(v);
-  else return f32_to_bf16(v);
-}
-template <int DT> IC_DEV float bits16_f32(u16 b) {
-  if constexpr (DT == IC_DTYPE_F16) return f16_to_f32(b);
-  else return bf16_to_f32(b);
-}
+using namespace rq;
 
 // Load 16 consecutive values starting at element p0 (zero past n) as f32.
 // Whole in-bounds 16-element runs use 16-byte loads when the base is aligned.
@@ -98,14 +66,6 @@ IC_DEV void load16i(const int32_t* base, int p0, int n, int* out) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) out[j] = (p0 + j < n) ? base[p0 + j] : 0;
   }
-}
-
-// Layout of register element j of thread t after the rotation phases for rot
-// size class RC (0: none/16, 1: 64/256, 2: 1024/4096), tile-local position.
-template <int RC> IC_DEV int tile_pos(int t, int j) {
-  if constexpr (RC == 0) return 16 * t + j;
-  else if constexpr (RC == 1) return 256 * (t >> 4) + 16 * j + (t & 15);
-  else return 256 * j + t;
 }
 
 // LOG4R: 0 = no rotation, 2..6 = rot size 16..4096.  QUANT: write INT8 codes and
@@ -314,6 +274,16 @@ __global__ void factor_prep_kernel(const float* __restrict__ f, int K, float* __
   rcp[k] = 1.0f / v;
 }
 
+bool fast_path_ok(const ic_rotq_args& a) {
+  auto al16 = [](const void* p) { return (((uintptr_t)p) & 15) == 0; };
+  if (a.dtype != IC_DTYPE_F16 && a.dtype != IC_DTYPE_BF16) return false;
+  if (a.sm_rcp != nullptr || a.q_out == nullptr) return false;
+  if (a.K_in % 16 || a.K_w % 16 || a.K_w > (int64_t)kFastMaxTiles * kTile) return false;
+  if (a.ldx % 8 || a.ldq % 16 || !al16(a.x) || !al16(a.q_out)) return false;
+  if ((a.sr_rcp && !al16(a.sr_rcp)) || (a.perm && !al16(a.perm))) return false;
+  return true;
+}
+
 template <int DT, int LOG4R, bool QUANT>
 hipError_t launch_rq(const ic_rotq_args& a, hipStream_t st) {
   rotate_quant_kernel<DT, LOG4R, QUANT><<<dim3((unsigned)a.M), dim3(kThreads), 0, st>>>(
@@ -399,6 +369,11 @@ static int run_rotq(const ic_rotq_args* a, bool quant, void* stream) {
   if (a->M == 0) return IC_OK;
   hipStream_t st = (hipStream_t)stream;
   hipError_t e = hipErrorInvalidValue;
+  if (quant && fast_path_ok(*a)) {
+    e = a->dtype == IC_DTYPE_F16 ? ic_rq_fast_f16(*a, st) : ic_rq_fast_bf16(*a, st);
+    if (e != hipSuccess) return ic_set_error(IC_ERR_LAUNCH, "%s: %s", who, hipGetErrorString(e));
+    return IC_OK;
+  }
   switch (a->dtype) {
     case IC_DTYPE_F16: e = quant ? dispatch_rot<IC_DTYPE_F16, true>(*a, st) : dispatch_rot<IC_DTYPE_F16, false>(*a, st); break;
     case IC_DTYPE_BF16: e = quant ? dispatch_rot<IC_DTYPE_BF16, true>(*a, st) : dispatch_rot<IC_DTYPE_BF16, false>(*a, st); break;

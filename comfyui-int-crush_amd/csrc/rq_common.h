@@ -1,0 +1,57 @@
+// Device helpers shared by the fused prep + quantize kernels (generic path in
+// rotate_quant.hip, fast path in rq_fast.h).
+#pragma once
+#include "ic_common.h"
+
+namespace rq {
+
+constexpr int kThreads = 256;
+constexpr int kTile = 4096;       // positions per tile (kThreads * 16)
+constexpr int kMaxTiles = 4;      // K_w <= 16384 for the fused single-pass kernel
+constexpr int kPadStride = 18;    // 16 doubles + 2 pad per 16-position row of the transpose buffer
+
+IC_DEV void h4(double& a, double& b, double& c, double& d) {
+  double s = (a + b) + (c + d);
+  double ya = __builtin_fma(s, 0.5, -d);
+  double yb = __builtin_fma(s, 0.5, -c);
+  double yc = __builtin_fma(s, 0.5, -b);
+  double yd = __builtin_fma(s, 0.5, -a);
+  a = ya; b = yb; c = yc; d = yd;
+}
+// radix-4 stage on the low / high 2-bit digit of a 16-element register array
+IC_DEV void stage_lo(double* v) {
+#pragma unroll
+  for (int a = 0; a < 4; ++a) h4(v[4 * a + 0], v[4 * a + 1], v[4 * a + 2], v[4 * a + 3]);
+}
+IC_DEV void stage_hi(double* v) {
+#pragma unroll
+  for (int a = 0; a < 4; ++a) h4(v[a], v[4 + a], v[8 + a], v[12 + a]);
+}
+// physical slot of logical position p in the padded transpose buffer
+IC_DEV int tslot(int p) { return p + 2 * (p >> 4); }
+
+template <int DT> IC_DEV u16 f32_bits16(float v) {
+  if constexpr (DT == IC_DTYPE_F16) return f32_to_f16(v);
+  else return f32_to_bf16(v);
+}
+template <int DT> IC_DEV float bits16_f32(u16 b) {
+  if constexpr (DT == IC_DTYPE_F16) return f16_to_f32(b);
+  else return bf16_to_f32(b);
+}
+
+// Layout of register element j of thread t after the rotation phases for rot
+// size class RC (0: none/16, 1: 64/256, 2: 1024/4096), tile-local position.
+template <int RC> IC_DEV int tile_pos(int t, int j) {
+  if constexpr (RC == 0) return 16 * t + j;
+  else if constexpr (RC == 1) return 256 * (t >> 4) + 16 * j + (t & 15);
+  else return 256 * j + t;
+}
+
+constexpr int kFastMaxTiles = 4;  // fast path: K_w <= 16384
+
+}  // namespace rq
+
+// Fast-path launchers (rq_fast_f16.hip / rq_fast_bf16.hip); argument checks
+// and fast_path_ok() are done by the caller.
+hipError_t ic_rq_fast_f16(const ic_rotq_args& a, hipStream_t st);
+hipError_t ic_rq_fast_bf16(const ic_rotq_args& a, hipStream_t st);

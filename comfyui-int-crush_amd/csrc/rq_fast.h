@@ -1,0 +1,390 @@
+// Fast path of the fused prep + quantize (see the comment at the top of the
+// kernels).  Included once per activation dtype (rq_fast_f16.hip,
+// rq_fast_bf16.hip) so the two instantiation sets compile in parallel.
+#pragma once
+#include "rq_common.h"
+
+namespace {
+using namespace rq;
+
+// ===================================================================== fast path
+// 16-bit activations with K_in % 16 == 0, K_w % 16 == 0, 16-byte aligned rows,
+// factor and perm arrays, quantized output, no old-SmoothQuant divide.  Same
+// arithmetic as rotate_quant_kernel, arranged for throughput:
+//   * persistent workgroups walk rows r = blockIdx.x, +gridDim.x, ...; the
+//     SmoothRot reciprocals of a thread's input positions and the gather
+//     offsets of its output positions are loaded once into registers;
+//   * the next row's activations are loaded into registers as soon as the
+//     current row's values of that tile have been consumed, so HBM latency
+//     overlaps a whole row of work;
+//   * every 16-element run is entirely inside or outside the row, so the
+//     per-element work is branch-free; the divide takes the IEEE slow path
+//     only for a run holding a lane outside the proven fast-path range;
+//   * rotated values are rounded once and kept as 16-bit values in an LDS row
+//     buffer, which the gather reads directly (perm pre-scaled to byte offsets).
+constexpr int kFastMaxTiles = 4;  // K_w <= 16384
+
+template <int DT> IC_DEV void unpack8(v4u a, float* o) {
+  const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o[2 * i] = bits16_f32<DT>((u16)(w[i] & 0xffffu));
+    o[2 * i + 1] = bits16_f32<DT>((u16)(w[i] >> 16));
+  }
+}
+
+// quantize 16 values (|v| <= row abs-max) and pack the codes little-endian
+IC_DEV v4u quant16(const float* v, double rs) {
+  uint32_t w[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+    w[d] = pack4_lo_bytes(quant_code_nc(v[4 * d], rs), quant_code_nc(v[4 * d + 1], rs),
+                          quant_code_nc(v[4 * d + 2], rs), quant_code_nc(v[4 * d + 3], rs));
+  return v4u{w[0], w[1], w[2], w[3]};
+}
+
+// RN_dt(y) of an fp64 value through RN32: exact unless RN32(y) is itself a
+// rounding boundary of DT (a midpoint between neighbours, including the
+// overflow threshold) or lies below DT's normal range.  Boundary test on the
+// f32 bits: the bits below DT's precision are exactly 100...0.
+template <int DT> IC_DEV bool rn32_is_dt_boundary(float z) {
+  const uint32_t w = __float_as_uint(z);
+  if constexpr (DT == IC_DTYPE_F16) return (w & 0x1fffu) == 0x1000u;
+  else return (w & 0xffffu) == 0x8000u;
+}
+
+// Two workgroups per CU while the per-thread constants fit half the register
+// file (K_w <= 12288); wider rows keep one.
+// LDS layouts (doubles in the exchange buffer, 16-bit values in the row
+// buffer).  Exchange slot of tile position p: 2 doubles of padding per 16
+// positions and 16 per 256.  Then the b128 row writes of 16 lanes hit 16
+// distinct 4-bank groups (row stride 36 dwords) and the transposed b64 reads
+// of the four 16-lane groups of a wave land on alternate halves of the 64
+// banks.  Row-buffer address of position p: 16 values of padding per 256, so
+// the strided writes of the four 16-lane groups of a wave use distinct banks.
+IC_DEV int xslot(int p) { return p + 2 * (p >> 4) + 16 * (p >> 8); }
+constexpr int kXbufDoubles = kTile + 2 * (kTile / 16) + 16 * (kTile / 256);
+IC_DEV int rbaddr(int p) { return p + 16 * (p >> 8); }
+template <int NT> constexpr int rowbuf_len() { return NT * kTile + 16 * (NT * kTile / 256); }
+
+template <int DT, int LOG4R, int NT>
+__global__ __launch_bounds__(kThreads, NT <= 3 ? 2 : 1) void rq_fast_kernel(
+    const u16* __restrict__ x, int64_t ldx, int M, int K_in, int K_r,
+    const float* __restrict__ sr_rcp, const float* __restrict__ sr_f, int K_w,
+    const int32_t* __restrict__ perm, int8_t* __restrict__ q_out, int64_t ldq,
+    float* __restrict__ s_out) {
+  constexpr int RC = LOG4R <= 2 ? 0 : (LOG4R <= 4 ? 1 : 2);
+  constexpr bool XCH = LOG4R >= 3;
+  __shared__ double xbuf[XCH ? kXbufDoubles : 2];
+  __shared__ __attribute__((aligned(16))) u16 rowbuf[rowbuf_len<NT>()];
+  __shared__ float red[kThreads / 64];
+
+  const int t = threadIdx.x;
+  const bool has_sr = sr_rcp != nullptr;
+  const bool has_perm = perm != nullptr;
+
+  // ---- per-workgroup constants
+  float rc[NT][16];
+  uint32_t po[NT][8];
+#pragma unroll
+  for (int c = 0; c < NT; ++c) {
+    const int p0 = c * kTile + 16 * t;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) rc[c][j] = 1.0f;
+    if (has_sr && p0 < K_in) {
+      const v4f* src = (const v4f*)(sr_rcp + p0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const v4f r = src[i];
+        rc[c][4 * i] = r.x; rc[c][4 * i + 1] = r.y; rc[c][4 * i + 2] = r.z; rc[c][4 * i + 3] = r.w;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) po[c][i] = 0;
+    if (has_perm && p0 < K_w) {
+      const v4u* src = (const v4u*)(perm + p0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const v4u r = src[i];
+        const uint32_t e[4] = {r.x, r.y, r.z, r.w};
+        uint32_t off[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) off[k] = 2u * (uint32_t)rbaddr(e[k] < (uint32_t)K_w ? (int)e[k] : 0);  // malformed -> position 0
+        po[c][2 * i] = off[0] | (off[1] << 16);
+        po[c][2 * i + 1] = off[2] | (off[3] << 16);
+      }
+    }
+  }
+
+  // Activation runs are loaded from a clamped, always valid address; runs past
+  // K_in are zeroed after the load (only in the last, partial tiles).
+  v4u xr[NT][2];
+  auto load_x = [&](int r, int c) {
+    const int p0 = min(c * kTile + 16 * t, K_in - 16);
+    const v4u* src = (const v4u*)(x + (int64_t)r * ldx + p0);
+    xr[c][0] = src[0];
+    xr[c][1] = src[1];
+  };
+  int row = blockIdx.x;
+  if (row < M) {
+#pragma unroll
+    for (int c = 0; c < NT; ++c)
+      if (c * kTile < K_in) load_x(row, c);
+  }
+
+  for (; row < M; row += gridDim.x) {
+    const int next = row + gridDim.x;
+    __syncthreads();  // the previous row's gather is done with rowbuf and red
+    float amax = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NT; ++c) {
+      const int base = c * kTile;
+      if (base >= K_w) break;  // uniform
+      const int p0 = base + 16 * t;
+      double v[16];
+      if (base < K_in) {  // uniform: the tile holds input values
+        v4u xa = xr[c][0], xb = xr[c][1];
+        if (next < M) load_x(next, c);
+        if (base + kTile > K_in && p0 >= K_in) xa = xb = v4u{0, 0, 0, 0};
+        float xs[16];
+        unpack8<DT>(xa, xs);
+        unpack8<DT>(xb, xs + 8);
+        if (has_sr) {
+          // fast path valid for products in DT's normal range; zeros and
+          // pad runs take the exact path, which returns the same signed zero
+          float pmin = __builtin_huge_valf();
+          bool nonfinite = false;
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const float p = xs[j] * rc[c][j];
+            pmin = __builtin_fminf(pmin, __builtin_fabsf(p));
+            if constexpr (DT == IC_DTYPE_BF16) nonfinite |= !__builtin_isfinite(p);
+            xs[j] = round_to_dt<DT>(p);
+          }
+          if (__builtin_expect(!(pmin >= dt_min_normal<DT>()) || nonfinite, 0)) {
+            if (p0 < K_in) {
+              float xo[16];
+              unpack8<DT>(xa, xo);
+              unpack8<DT>(xb, xo + 8);
+#pragma unroll
+              for (int j = 0; j < 16; ++j) xs[j] = div_round_dt<DT>(xo[j], rc[c][j], sr_f, p0 + j);
+            } else {
+#pragma unroll
+              for (int j = 0; j < 16; ++j) xs[j] = 0.0f;
+            }
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = (double)xs[j];
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = 0.0;
+      }
+      // ---- block Hadamard (same digit layout as rotate_quant_kernel)
+      if constexpr (LOG4R >= 2) { stage_lo(v); stage_hi(v); }
+      if constexpr (XCH) {
+        // digits 2-3: transpose among 16 lanes of one wave (no workgroup barrier)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) xbuf[xslot(16 * t + j)] = v[j];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int g = t >> 4, l = t & 15;
+#pragma unroll
+        for (int h = 0; h < 16; ++h) v[h] = xbuf[xslot(256 * g + 16 * h + l)];
+        stage_lo(v);
+        if constexpr (LOG4R >= 4) stage_hi(v);
+        if constexpr (LOG4R >= 5) {
+          // digits 4-5 span all four waves
+#pragma unroll
+          for (int h = 0; h < 16; ++h) xbuf[xslot(256 * g + 16 * h + l)] = v[h];
+          __syncthreads();
+#pragma unroll
+          for (int gg = 0; gg < 16; ++gg) v[gg] = xbuf[xslot(256 * gg + t)];
+          stage_lo(v);
+          if constexpr (LOG4R >= 6) stage_hi(v);
+          __syncthreads();  // every wave has read xbuf before the next tile rewrites it
+        } else {
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+      }
+      // ---- round once to DT: RN32 first, exact round-to-odd for the rare runs
+      // holding a DT rounding boundary, a tiny value or a zero
+      float z[16];
+      float zmin = __builtin_huge_valf(), zmax = 0.0f;
+      bool boundary = false;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        z[j] = (float)v[j];
+        zmin = __builtin_fminf(zmin, __builtin_fabsf(z[j]));
+        zmax = __builtin_fmaxf(zmax, __builtin_fabsf(z[j]));
+        boundary |= rn32_is_dt_boundary<DT>(z[j]);
+      }
+      if (__builtin_expect(boundary || !(zmin >= dt_min_normal<DT>()), 0)) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) z[j] = rto24(v[j]);
+      }
+      if (base + kTile > K_r) {  // uniform: the tile reaches into the pad to K_w
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (base + tile_pos<(LOG4R == 0 ? 0 : RC)>(t, j) >= K_r) z[j] = 0.0f;
+      }
+      if (__builtin_expect(boundary || !(zmin >= dt_min_normal<DT>()) || base + kTile > K_r, 0)) {
+        zmax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) zmax = __builtin_fmaxf(zmax, __builtin_fabsf(z[j]));
+      }
+      amax = __builtin_fmaxf(amax, zmax);
+      if constexpr (LOG4R == 0 || RC == 0) {
+        // 16 contiguous positions per thread: two 16-byte stores
+        uint32_t w[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = (uint32_t)f32_bits16<DT>(z[2 * i]) | ((uint32_t)f32_bits16<DT>(z[2 * i + 1]) << 16);
+        v4u* dst = (v4u*)(rowbuf + rbaddr(base + 16 * t));
+        dst[0] = v4u{w[0], w[1], w[2], w[3]};
+        dst[1] = v4u{w[4], w[5], w[6], w[7]};
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) rowbuf[rbaddr(base + tile_pos<RC>(t, j))] = f32_bits16<DT>(z[j]);
+      }
+    }
+
+    // ---- row scale: RN_dt is monotone, so max |RN_dt(z)| = RN_dt(max |z|)
+    amax = wave_max(amax);
+    if ((t & 63) == 0) red[t >> 6] = amax;
+    __syncthreads();
+    const float m = round_to_dt<DT>(__builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3])));
+    const float s = quant_scale(m);
+    const double rs = 1.0 / (double)s;
+    if (t == 0) s_out[row] = s;
+
+    // ---- gather + quantize + store 16 codes per run
+    int8_t* qrow = q_out + (int64_t)row * ldq;
+#pragma unroll
+    for (int c = 0; c < NT; ++c) {
+      if (c * kTile >= K_w) break;  // uniform
+      const int o0 = 16 * (t + kThreads * c);
+      float vv[16];
+      if (has_perm) {
+        const char* rb = (const char*)rowbuf;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          vv[2 * i] = bits16_f32<DT>(*(const u16*)(rb + (po[c][i] & 0xffffu)));
+          vv[2 * i + 1] = bits16_f32<DT>(*(const u16*)(rb + (po[c][i] >> 16)));
+        }
+      } else {
+        unpack8<DT>(*(const v4u*)(rowbuf + rbaddr(o0)), vv);
+        unpack8<DT>(*(const v4u*)(rowbuf + rbaddr(o0) + 8), vv + 8);
+      }
+      const v4u codes = quant16(vv, rs);
+      if (o0 < K_w) *(v4u*)(qrow + o0) = codes;
+      __builtin_amdgcn_sched_barrier(0);  // one run at a time keeps the register footprint small
+    }
+  }
+}
+
+// Plain per-token quantization (no rotation, factors or perm), one wave per
+// row: the whole row is loaded at once (16 bytes per lane per 512 values),
+// unpacked, reduced to the abs-max across the wave, then quantized 8 codes per
+// lane per run.
+template <int DT, int MAXCH>
+__global__ __launch_bounds__(kThreads) void quant_wave_kernel(
+    const u16* __restrict__ x, int64_t ldx, int M, int K, int8_t* __restrict__ q_out, int64_t ldq,
+    float* __restrict__ s_out) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (row >= M) return;  // wave-uniform
+  const u16* xrow = x + (int64_t)row * ldx;
+  const int nch = (K + 511) >> 9;  // 512-value chunks (uniform); only the last may be partial
+  v4u a[MAXCH];
+#pragma unroll
+  for (int i = 0; i < MAXCH; ++i) {
+    if (i >= nch) break;
+    const int e = min((i * 64 + lane) * 8, K - 8);
+    a[i] = *(const v4u*)(xrow + e);
+  }
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < MAXCH; ++i) {
+    if (i >= nch) break;
+    float v[8];
+    unpack8<DT>(a[i], v);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) m = __builtin_fmaxf(m, __builtin_fabsf(v[k]));
+  }
+  m = wave_max(m);
+  const float s = quant_scale(m);
+  const double rs = 1.0 / (double)s;
+  if (lane == 0) s_out[row] = s;
+  int8_t* qrow = q_out + (int64_t)row * ldq;
+#pragma unroll
+  for (int i = 0; i < MAXCH; ++i) {
+    if (i >= nch) break;
+    const int e = (i * 64 + lane) * 8;
+    float v[8];
+    unpack8<DT>(a[i], v);
+    const uint32_t w0 = pack4_lo_bytes(quant_code_nc(v[0], rs), quant_code_nc(v[1], rs),
+                                       quant_code_nc(v[2], rs), quant_code_nc(v[3], rs));
+    const uint32_t w1 = pack4_lo_bytes(quant_code_nc(v[4], rs), quant_code_nc(v[5], rs),
+                                       quant_code_nc(v[6], rs), quant_code_nc(v[7], rs));
+    if (e < K) *(v2u*)(qrow + e) = v2u{w0, w1};
+  }
+}
+
+template <class Kern>
+int persistent_grid(Kern kern, int64_t M) {
+  static thread_local int per_cu = 0;  // resident workgroups per CU for this kernel
+  if (per_cu == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, kThreads, 0) != hipSuccess || n <= 0) n = 1;
+    per_cu = n;
+  }
+  const int64_t g = (int64_t)per_cu * ic_num_cus();
+  return (int)(M < g ? M : g);
+}
+
+template <int DT, int LOG4R, int NT>
+hipError_t launch_fast_t(const ic_rotq_args& a, hipStream_t st) {
+  auto kern = rq_fast_kernel<DT, LOG4R, NT>;
+  const int64_t K_r = LOG4R == 0 ? a.K_in : ((a.K_in + a.rot_size - 1) / a.rot_size) * a.rot_size;
+  kern<<<dim3(persistent_grid(kern, a.M)), dim3(kThreads), 0, st>>>(
+      (const u16*)a.x, a.ldx, (int)a.M, (int)a.K_in, (int)K_r, a.sr_rcp, a.sr_f, (int)a.K_w, a.perm,
+      a.q_out, a.ldq, a.s_out);
+  return hipGetLastError();
+}
+
+template <int DT, int LOG4R>
+hipError_t launch_fast_nt(const ic_rotq_args& a, hipStream_t st) {
+  if (a.K_w <= kTile) return launch_fast_t<DT, LOG4R, 1>(a, st);
+  if (a.K_w <= 2 * kTile) return launch_fast_t<DT, LOG4R, 2>(a, st);
+  if (a.K_w <= 3 * kTile) return launch_fast_t<DT, LOG4R, 3>(a, st);
+  return launch_fast_t<DT, LOG4R, 4>(a, st);
+}
+
+template <int DT>
+hipError_t launch_fast(const ic_rotq_args& a, hipStream_t st) {
+  if (a.rot_size == 0 && a.sr_rcp == nullptr && a.perm == nullptr && a.K_w == a.K_in &&
+      a.K_in <= 32 * 512) {
+    const unsigned grid = (unsigned)((a.M + 3) / 4);
+    if (a.K_in <= 8 * 512)
+      quant_wave_kernel<DT, 8><<<grid, kThreads, 0, st>>>((const u16*)a.x, a.ldx, (int)a.M, (int)a.K_in, a.q_out, a.ldq, a.s_out);
+    else if (a.K_in <= 16 * 512)
+      quant_wave_kernel<DT, 16><<<grid, kThreads, 0, st>>>((const u16*)a.x, a.ldx, (int)a.M, (int)a.K_in, a.q_out, a.ldq, a.s_out);
+    else
+      quant_wave_kernel<DT, 32><<<grid, kThreads, 0, st>>>((const u16*)a.x, a.ldx, (int)a.M, (int)a.K_in, a.q_out, a.ldq, a.s_out);
+    return hipGetLastError();
+  }
+  switch (a.rot_size) {
+    case 0: return launch_fast_nt<DT, 0>(a, st);
+    case 16: return launch_fast_nt<DT, 2>(a, st);
+    case 64: return launch_fast_nt<DT, 3>(a, st);
+    case 256: return launch_fast_nt<DT, 4>(a, st);
+    case 1024: return launch_fast_nt<DT, 5>(a, st);
+    case 4096: return launch_fast_nt<DT, 6>(a, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
