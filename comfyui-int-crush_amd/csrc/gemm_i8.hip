@@ -12,18 +12,23 @@
 //   * a BM x BN output tile per workgroup, 8 waves in a WGM x (8/WGM) grid, each
 //     wave owning (BM/WGM) x (BN*WGM/8) built from v_mfma_i32_32x32x32_i8 tiles
 //     whose int32 accumulators stay in architectural VGPRs;
-//   * K advances 64 bytes per stage through a 4-deep LDS ring.  Activation rows
-//     (and int8 weight rows) travel HBM -> LDS with global_load_lds_dwordx4, so
-//     they never occupy VGPRs; the issuing lane is chosen so that the 16-byte
-//     chunks land XOR-swizzled by row, which keeps the ds_read_b128 fragment
-//     loads free of bank conflicts;
-//   * packed INT4 weights are loaded into VGPRs two stages ahead, expanded to
-//     16*q (int8) with two masks and a byte permute, and written to LDS once per
-//     workgroup; the factor 16 is removed exactly in the epilogue;
-//   * per-group scales (group = 128 = two stages) fold the int32 partials into
-//     an fp32 accumulator with one convert + FMA per element and group.  Two
-//     int32 accumulator sets alternate between groups so the fold of one group
-//     overlaps the MFMAs of the next.
+//   * K advances 128 bytes per stage (one 128-wide scale group) through an
+//     NS-deep LDS ring.  Every global read of the main loop -- activation
+//     rows, int8 or packed INT4 weight rows, per-group scales -- is a direct
+//     global->LDS DMA (global_load_lds) issued from inline assembly, so no
+//     VGPR holds staged data and the only memory waits are the explicit,
+//     static vmcnt waits of the pipeline (the compiler cannot see these DMAs
+//     and so does not serialise LDS accesses behind them);
+//   * activation and int8 weight chunks land XOR-swizzled by row (the issuing
+//     lane picks the global chunk), so the ds_read_b128 fragment loads are
+//     bank-conflict free;
+//   * packed INT4 weights are expanded once per workgroup and stage from the
+//     ring into a double-buffered LDS tile as 16*q (int8): two masks and a byte
+//     permute per 8 nibbles; the factor 16 is removed exactly in the epilogue;
+//   * per-group scales (group 128 = one stage) fold the int32 partials into an
+//     fp32 accumulator with one convert + FMA per element and group; two int32
+//     accumulator sets alternate between groups so the fold of group g runs
+//     while the MFMAs of group g+1 execute.
 #include <type_traits>
 
 #include "ic_common.h"
@@ -31,19 +36,30 @@
 namespace {
 
 constexpr int kNT = 512;  // threads per workgroup
+constexpr int kBK = 128;  // K bytes per stage
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef __attribute__((address_space(3))) char lds_char;
 
-// LDS rows hold BK bytes of K (BK/16 chunks of 16 bytes), the chunk index
-// XOR-swizzled by row.  With these swizzles the MFMA fragment reads (32
-// consecutive rows at chunk c and c+1) run at the full ds_read_b128 rate on
-// gfx950 (~232 B/clk/CU measured); unswizzled rows are 4-way (64 B) or 8-way
-// (128 B) bank-conflicted.
-template <int BK> IC_DEV int swz(int row) {
-  if constexpr (BK == 64) return (row >> 2) & 3;
-  else return (row >> 1) & 7;
+// LDS rows of 128 bytes hold 8 chunks of 16 bytes, the chunk index XOR-swizzled
+// by row: the MFMA fragment reads (32 consecutive rows at chunk c and c+1) then
+// run at the full ds_read_b128 rate on gfx950.
+IC_DEV int swz(int row) { return (row >> 1) & 7; }
+IC_DEV int lds_off(int row, int chunk) { return row * kBK + ((chunk ^ swz(row)) << 4); }
+
+// Global -> LDS DMA of 16 (or 4) bytes per lane, from sbase + voff (a
+// wave-uniform 64-bit base and a per-lane 32-bit byte offset) to M0 + 16*lane
+// (4*lane).  Issued from inline assembly so that the compiler neither tracks
+// it nor orders LDS accesses behind it; completion is waited for explicitly
+// with wait_vm before the workgroup barrier that publishes the stage.  M0 holds
+// no compiler value in these kernels (gfx950 LDS instructions do not use it).
+IC_DEV void dma16(uint32_t voff, const void* sbase, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(sbase)
+               : "memory", "m0");
 }
-template <int BK> IC_DEV int lds_off(int row, int chunk) { return row * BK + ((chunk ^ swz<BK>(row)) << 4); }
+IC_DEV void dma4(uint32_t voff, const void* sbase, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(voff), "s"(sbase)
+               : "memory", "m0");
+}
 
 // Block until at most N vector-memory operations of this wave are outstanding
 // (they retire in issue order).
@@ -51,6 +67,7 @@ template <int N> IC_DEV void wait_vm() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
+IC_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // 8 INT4 nibbles (low nibble = even k) -> 8 int8 values 16*q in natural k order.
 IC_DEV void unpack8_x16(uint32_t P, uint32_t& w0, uint32_t& w1) {
@@ -78,127 +95,134 @@ IC_DEV void tile_coords(int b, int nb, int tiles_m, int tiles_n, int& tm, int& t
   tn = r / gsize;
 }
 
-// Tile configuration: BM x BN output tile, WGM wave rows, BK K-bytes per LDS
-// stage, NS-deep LDS ring.
-template <int BM_, int BN_, int WGM_, int BK_, int NS_>
+// Tile configuration: BM x BN output tile, WGM wave rows, NS-deep LDS ring.
+template <int BM_, int BN_, int WGM_, int NS_, bool INT4_, int GS_>
 struct Tile {
-  static constexpr int BM = BM_, BN = BN_, WGM = WGM_, BK = BK_, NS = NS_;
-  static constexpr size_t lds_bytes() { return (size_t)NS * (BM + BN) * BK; }
+  static constexpr int BM = BM_, BN = BN_, WGM = WGM_, NS = NS_;
+  static constexpr bool INT4 = INT4_;
+  static constexpr int GS = GS_;
+  static constexpr int A_BYTES = BM * kBK;
+  static constexpr int B_BYTES = INT4 ? BN * kBK / 2 : BN * kBK;  // packed for INT4
+  static constexpr int S_BYTES = GS ? BN * 4 : 0;
+  static constexpr int SLOT = A_BYTES + B_BYTES + S_BYTES;
+  static constexpr int BU_BYTES = INT4 ? BN * kBK : 0;  // one unpacked INT4 tile
+  static constexpr int EPI_RS = BN + 8;  // 16-bit output staging row stride (elements)
+  static constexpr size_t epi_bytes() { return (size_t)BM * EPI_RS * 2 + (size_t)(BM + 2 * BN) * 4; }
+  static constexpr size_t ring_bytes() { return (size_t)NS * SLOT + 2 * (size_t)BU_BYTES; }
+  static constexpr size_t lds_bytes() { return ring_bytes() > epi_bytes() ? ring_bytes() : epi_bytes(); }
 };
 
-template <class TL, bool INT4, int GS, int OUT_DT, bool ACC_OUT>
+template <class TL, int OUT_DT, bool ACC_OUT>
 __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
     const int8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
     const float* __restrict__ s_a, const float* __restrict__ s_w, int G,
     const void* __restrict__ bias, int bias_dt, void* __restrict__ C, int64_t ldc, int M, int N,
     int K, int32_t* __restrict__ acc_out) {
-  constexpr int BM = TL::BM, BN = TL::BN, WGM = TL::WGM, BK = TL::BK, NS = TL::NS;
+  constexpr int BM = TL::BM, BN = TL::BN, WGM = TL::WGM, NS = TL::NS, GS = TL::GS;
+  constexpr bool INT4 = TL::INT4;
   constexpr int WGN = 8 / WGM;
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int NC = BK / 16;                     // 16-byte chunks per LDS row
-  constexpr int RPB = 1024 / BK;                  // rows per 1 KB DMA block
-  constexpr int A_DMA = BM / RPB / 8;             // DMA blocks of A per wave per stage
-  constexpr int B_DMA = INT4 ? 0 : BN / RPB / 8;  // same for int8 weights
-  constexpr int PK = INT4 ? BN * BK / 2 / kNT : 0;  // packed weight bytes per thread per stage
-  constexpr int B_LD = INT4 ? (PK + 15) / 16 : 0;   // packed-weight load instructions per stage
-  constexpr int D = A_DMA + B_DMA;                // DMA instructions per thread per stage
-  constexpr int STAGE = (BM + BN) * BK;
-  constexpr int KS = BK / 32;                     // MFMA K-steps per stage
-  constexpr int SPG = GS == 0 ? 1 : GS / BK;      // stages per scale group
-  static_assert(TM >= 1 && TN >= 1 && A_DMA >= 1 && (INT4 || B_DMA >= 1), "tile too small");
-  static_assert(!INT4 || PK == 8 || PK == 16 || PK == 32, "packed weight staging");
-  static_assert(GS == 0 || (GS == 128 && (BK == 64 || BK == 128)), "group size");
-  static_assert(NS >= 2, "ring depth");
+  constexpr int A_DMA = BM / 64;                  // 1 KB DMA blocks of A per wave per stage
+  constexpr int B_DMA = INT4 ? BN / 128 : BN / 64;  // same for (packed) weights
+  constexpr int S_WAVES = GS ? BN / 64 : 0;       // waves issuing one scale DMA per stage
+  constexpr int D = A_DMA + B_DMA;
+  constexpr int PK = INT4 ? BN * (kBK / 2) / kNT : 0;  // packed weight bytes unpacked per thread
+  static_assert(TM >= 1 && TN >= 1 && A_DMA >= 1 && B_DMA >= 1, "tile too small");
+  static_assert(!INT4 || PK == 16 || PK == 32, "INT4 unpack split");
+  static_assert(GS == 0 || GS == 128, "group size");
+  static_assert(NS >= 2 && S_WAVES <= 8, "ring depth");
 
   extern __shared__ __attribute__((aligned(16))) char smem[];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_char*)smem;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (DMA bases live in M0)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wr = wave / WGN, wc = wave % WGN;
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   int tm, tn;
   tile_coords(blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int KT = K / BK;
+  const int KT = K / kBK;
+  const bool s_wave = wave < S_WAVES;
 
-  // ---- staging: DMA of A (and int8 B) rows into the LDS ring.  Lane L of DMA
-  // block b covers LDS slot (row RPB*b + L/NC, chunk slot L%NC) and so loads
-  // global chunk (L%NC) ^ swz(row) of that row; every row segment is a whole
-  // number of 128-byte lines when BK = 128.
-  const int dma_row = lane / NC, dma_slot = lane % NC;
+  // ---- DMA addressing.  A / int8 B: lane L of a 1 KB block covers LDS row
+  // 8*blk + L/8, chunk slot L%8, and loads global chunk (L%8) ^ swz(row).
+  // Packed B: 16 rows of 64 bytes per block, unswizzled.  Scales: one dword
+  // per lane, column n0 + 64*wave + lane of group kt.
+  const int dma_row = lane >> 3;
+  uint32_t a_off[A_DMA];
+#pragma unroll
+  for (int c = 0; c < A_DMA; ++c) {
+    const int row = 8 * (wave + 8 * c) + dma_row;
+    a_off[c] = (uint32_t)(min(row, M - 1 - m0) * lda + (((lane & 7) ^ swz(row)) << 4));
+  }
+  uint32_t b_off[B_DMA];
+#pragma unroll
+  for (int c = 0; c < B_DMA; ++c) {
+    if constexpr (INT4) {
+      const int row = 16 * (wave + 8 * c) + (lane >> 2);
+      b_off[c] = (uint32_t)(min(row, N - 1 - n0) * ldb + ((lane & 3) << 4));
+    } else {
+      const int row = 8 * (wave + 8 * c) + dma_row;
+      b_off[c] = (uint32_t)(min(row, N - 1 - n0) * ldb + (((lane & 7) ^ swz(row)) << 4));
+    }
+  }
+  const uint32_t s_off = GS ? (uint32_t)(min(64 * wave + lane, N - 1 - n0) * G * 4) : 0u;
+  const int8_t* a_base = A + (int64_t)m0 * lda;
+  const uint8_t* b_base = B + (int64_t)n0 * ldb;
+  const float* s_base = GS ? s_w + (int64_t)n0 * G : nullptr;
+
   auto issue_dma = [&](int kt) {
-    char* st = smem + (kt % NS) * STAGE;
-    const int k0 = kt * BK;
+    const uint32_t slot = lds0 + (uint32_t)((kt % NS) * TL::SLOT);
+    const int8_t* ab = a_base + (int64_t)kt * kBK;
 #pragma unroll
-    for (int c = 0; c < A_DMA; ++c) {
-      const int blk = wave + 8 * c;
-      const int row = RPB * blk + dma_row;
-      const int chunk = dma_slot ^ swz<BK>(row);
-      const int gr = min(m0 + row, M - 1);
-      __builtin_amdgcn_global_load_lds(A + (int64_t)gr * lda + k0 + chunk * 16,
-                                       (lds_ptr_t)(st + blk * 1024), 16, 0, 0);
+    for (int c = 0; c < A_DMA; ++c) dma16(a_off[c], ab, slot + (uint32_t)((wave + 8 * c) * 1024));
+    const uint8_t* bb = b_base + (int64_t)kt * (INT4 ? kBK / 2 : kBK);
+#pragma unroll
+    for (int c = 0; c < B_DMA; ++c) dma16(b_off[c], bb, slot + (uint32_t)(TL::A_BYTES + (wave + 8 * c) * 1024));
+    if constexpr (GS != 0) {
+      if (s_wave) dma4(s_off, s_base + kt, slot + (uint32_t)(TL::A_BYTES + TL::B_BYTES + wave * 256));
     }
-    if constexpr (!INT4) {
-      char* sb = st + BM * BK;
+  };
+  // Top of step s: stages s+1 .. s+NS-2 may stay in flight (D DMA
+  // instructions each, one more on the waves that also fetch scales); near the
+  // end of K, wait for everything.
+  auto wait_stage = [&](int s) {
+    if constexpr (NS > 2) {
+      if (s + NS - 2 < KT) {
+        if (s_wave) wait_vm<(D + 1) * (NS - 2)>();
+        else wait_vm<D * (NS - 2)>();
+        return;
+      }
+    }
+    wait_vm<0>();
+  };
+
+  // ---- packed INT4 -> 16*q int8 tile in LDS (double buffered)
+  auto unpack = [&](int kt) {
+    if constexpr (INT4) {
+      const char* bp = smem + (kt % NS) * TL::SLOT + TL::A_BYTES;
+      char* bu = smem + NS * TL::SLOT + (kt & 1) * TL::BU_BYTES;
 #pragma unroll
-      for (int c = 0; c < B_DMA; ++c) {
-        const int blk = wave + 8 * c;
-        const int row = RPB * blk + dma_row;
-        const int chunk = dma_slot ^ swz<BK>(row);
-        const int gr = min(n0 + row, N - 1);
-        __builtin_amdgcn_global_load_lds(B + (int64_t)gr * ldb + k0 + chunk * 16,
-                                         (lds_ptr_t)(sb + blk * 1024), 16, 0, 0);
+      for (int h = 0; h < PK / 16; ++h) {
+        const int idx = tid + kNT * h;      // 16-byte packed chunk index
+        const int row = idx >> 2, part = idx & 3;
+        const v4u p = *(const v4u*)(bp + idx * 16);
+        uint32_t w[8];
+        unpack8_x16(p.x, w[0], w[1]);
+        unpack8_x16(p.y, w[2], w[3]);
+        unpack8_x16(p.z, w[4], w[5]);
+        unpack8_x16(p.w, w[6], w[7]);
+        *(v4u*)(bu + lds_off(row, 2 * part)) = v4u{w[0], w[1], w[2], w[3]};
+        *(v4u*)(bu + lds_off(row, 2 * part + 1)) = v4u{w[4], w[5], w[6], w[7]};
       }
     }
   };
-
-  // ---- packed INT4 weights: global -> VGPR (two stages ahead) -> unpack -> LDS.
-  // Thread t owns PK packed bytes (2*PK k values) of one weight row per stage.
-  constexpr int PPR = INT4 ? (BK / 2) / PK : 1;   // threads per weight row
-  typedef uint32_t pk_t __attribute__((ext_vector_type(PK >= 16 ? 4 : 2)));
-  struct PkRegs { pk_t v[B_LD > 0 ? B_LD : 1]; };
-  const int pk_row = tid / PPR;
-  const int pk_part = tid % PPR;
-  const uint8_t* pk_src = B + (int64_t)min(n0 + pk_row, N - 1) * ldb + pk_part * PK;
-  auto load_pk = [&](int kt) -> PkRegs {
-    PkRegs r{};
-    if constexpr (INT4) {
-#pragma unroll
-      for (int i = 0; i < B_LD; ++i) r.v[i] = *(const pk_t*)(pk_src + kt * (BK / 2) + 16 * i);
-    }
-    return r;
-  };
-  auto store_pk = [&](int kt, const PkRegs& p) {
-    if constexpr (INT4) {
-      char* sb = smem + (kt % NS) * STAGE + BM * BK;
-      const int c0 = pk_part * (PK / 8);  // first unpacked 16-byte chunk of this thread
-#pragma unroll
-      for (int i = 0; i < B_LD; ++i) {
-        uint32_t w[4];
-        unpack8_x16(p.v[i][0], w[0], w[1]);
-        unpack8_x16(p.v[i][1], w[2], w[3]);
-        *(v4u*)(sb + lds_off<BK>(pk_row, c0 + 2 * i)) = v4u{w[0], w[1], w[2], w[3]};
-        if constexpr (PK >= 16) {
-          unpack8_x16(p.v[i][2], w[0], w[1]);
-          unpack8_x16(p.v[i][3], w[2], w[3]);
-          *(v4u*)(sb + lds_off<BK>(pk_row, c0 + 2 * i + 1)) = v4u{w[0], w[1], w[2], w[3]};
-        }
-      }
-    }
-  };
-
-  // In steady state (ring full, no refill skipped) exactly NS-2 iterations,
-  // each issuing its packed loads and then one stage of DMA, separate the DMA
-  // of stage s from the top of iteration s; near the ends of the K loop wait
-  // for everything instead.
-  constexpr int kSteadyAfter = (NS - 2) * (D + B_LD);
 
   typedef int v4i_t __attribute__((ext_vector_type(4)));
-  // Two alternating int32 accumulator sets let the fold of one group overlap
-  // the MFMAs of the next; they only fit the register file for small wave tiles.
-  constexpr bool kPingPong = GS == 128 && TM * TN <= 2;
+  constexpr bool kPingPong = GS == 128 && TM * TN <= 2 * 2;
   constexpr int NSET = kPingPong ? 2 : 1;
   v16i acc[NSET][TM][TN];
   v16f facc[GS == 128 ? TM : 1][GS == 128 ? TN : 1];
@@ -218,21 +242,64 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
   auto out_row = [&](int i, int r) { return m0 + wr * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); };
   auto out_col = [&](int j) { return n0 + wc * WN + j * 32 + (lane & 31); };
 
-  // One stage (KS K-steps of 32) into accumulator set SET; ZF starts the set
-  // afresh (MFMA with a zero addend) on the first K-step.
-  auto mfma_stage = [&](int kt, auto set_c, auto zero_c) {
+  // Scales of group kt for this lane's columns, from the stage's LDS slot.
+  auto read_scales = [&](int kt, float* sw) {
+    if constexpr (GS == 128) {
+      const float* sS = (const float*)(smem + (kt % NS) * TL::SLOT + TL::A_BYTES + TL::B_BYTES);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        sw[j] = sS[wc * WN + j * 32 + (lane & 31)];
+        if constexpr (INT4) sw[j] *= 0.0625f;  // acc holds 16 * the true sum
+      }
+    }
+  };
+
+  // Fold of one 32x32 tile t of accumulator set FS (group g) into facc:
+  // facc += f32(acc_g) * s_w[n, g] (16 converts + 16 FMAs per lane).
+  auto fold_tile = [&](int g, auto fs_c, int t, const float* sw) {
+    constexpr int FS = decltype(fs_c)::value;
+    const int i = t / TN, j = t % TN;
+    // Anchors: empty volatile asm statements on the tile before and on its
+    // fp32 accumulator after the fold keep the register-only fold between the
+    // stage's barriers (volatile asm stays ordered), so it can neither be
+    // hoisted nor sunk out of the MFMA region it is interleaved with.
+    asm volatile("" : "+v"(acc[FS][i][j]));
+    if constexpr (ACC_OUT) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = out_row(i, r), nn = out_col(j);
+        if (m < M && nn < N)
+          acc_out[((int64_t)g * M + m) * N + nn] = INT4 ? (acc[FS][i][j][r] >> 4) : acc[FS][i][j][r];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) facc[i][j][r] = __builtin_fmaf((float)acc[FS][i][j][r], sw[j], facc[i][j][r]);
+    asm volatile("" : "+v"(facc[i][j]));  // nor sunk past the next barrier
+  };
+  auto fold = [&](int g, auto fs_c, const float* sw) {
+#pragma unroll
+    for (int t = 0; t < TM * TN; ++t) fold_tile(g, fs_c, t, sw);
+  };
+
+  // One stage (4 K-steps of 32) into accumulator set SET; ZF starts the set
+  // afresh (MFMA with a zero addend) on the first K-step.  With FOLD, the fold
+  // of the previous group (set FS, scales sw_f) is spread over the stage, one
+  // 32x32 tile per K-step, and its VALU work is interleaved between the MFMAs
+  // so that each wave converts and accumulates while its MFMAs execute.
+  auto mfma_stage = [&](int kt, auto set_c, auto zero_c, auto fold_c, auto fs_c, int g_f, const float* sw_f) {
     constexpr int SET = decltype(set_c)::value;
     constexpr bool ZF = decltype(zero_c)::value;
-    const char* sA = smem + (kt % NS) * STAGE;
-    const char* sB = sA + BM * BK;
+    constexpr bool FOLD = decltype(fold_c)::value;
+    const char* sA = smem + (kt % NS) * TL::SLOT;
+    const char* sB = INT4 ? smem + NS * TL::SLOT + (kt & 1) * TL::BU_BYTES : sA + TL::A_BYTES;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
+    for (int ks = 0; ks < kBK / 32; ++ks) {
       v4i_t a[TM], b[TN];
       const int ch = 2 * ks + (lane >> 5);
 #pragma unroll
-      for (int i = 0; i < TM; ++i) a[i] = *(const v4i_t*)(sA + lds_off<BK>(wr * WM + i * 32 + (lane & 31), ch));
+      for (int i = 0; i < TM; ++i) a[i] = *(const v4i_t*)(sA + lds_off(wr * WM + i * 32 + (lane & 31), ch));
 #pragma unroll
-      for (int j = 0; j < TN; ++j) b[j] = *(const v4i_t*)(sB + lds_off<BK>(wc * WN + j * 32 + (lane & 31), ch));
+      for (int j = 0; j < TN; ++j) b[j] = *(const v4i_t*)(sB + lds_off(wc * WN + j * 32 + (lane & 31), ch));
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -240,136 +307,74 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
           if (ZF && ks == 0) acc[SET][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], v16i{}, 0, 0, 0);
           else acc[SET][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[SET][i][j], 0, 0, 0);
         }
-    }
-  };
-
-  // Per-group fold of set SET (group g): facc += f32(acc_g) * s_w[n, g]
-  // (16*acc_g with s_w/16 for INT4, which is exactly the same product).
-  auto fold = [&](int g, auto set_c) {
-    constexpr int SET = decltype(set_c)::value;
+      if constexpr (FOLD) {
+        if (ks < TM * TN) fold_tile(g_f, fs_c, ks, sw_f);
+        if constexpr (!ACC_OUT) {
+          // per MFMA of this K-step: 32 / (TM*TN) fold instructions
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int n = min(out_col(j), N - 1);
-      float sw = s_w[(int64_t)n * G + g];
-      if constexpr (INT4) sw *= 0.0625f;
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        if constexpr (ACC_OUT) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int m = out_row(i, r), nn = out_col(j);
-            if (m < M && nn < N)
-              acc_out[((int64_t)g * M + m) * N + nn] = INT4 ? (acc[SET][i][j][r] >> 4) : acc[SET][i][j][r];
+          for (int q = 0; q < TM * TN; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);              // 1 MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 32 / (TM * TN), 0); // VALU
           }
         }
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          facc[i][j][r] = __builtin_fmaf((float)acc[SET][i][j][r], sw, facc[i][j][r]);
       }
+    }
+    if constexpr (FOLD && TM * TN > kBK / 32) {
+#pragma unroll
+      for (int t = kBK / 32; t < TM * TN; ++t) fold_tile(g_f, fs_c, t, sw_f);
     }
   };
 
-  // ---- prologue: packed loads of stages 0 and 1 first, then NS-1 stages of DMA
-  PkRegs pk0{}, pk1{};
-  if constexpr (INT4) {
-    pk0 = load_pk(0);
-    if (KT > 1) pk1 = load_pk(1);
-  }
+  // ---- prologue: NS-1 stages in flight
 #pragma unroll
   for (int t = 0; t < NS - 1; ++t)
     if (t < KT) issue_dma(t);
-  if constexpr (INT4) store_pk(0, pk0);
 
-  // One pipeline step: make stage s resident, refill the ring, stage the
-  // packed weights of s+1, then run the MFMAs of stage s.
-  auto step = [&](int s, auto set_c, auto zero_c, PkRegs& pk_next, PkRegs& pk_free) {
-    if (s >= NS - 1 && s + NS - 1 < KT) wait_vm<kSteadyAfter>();
-    else wait_vm<0>();
-    // every wave's DMA into stage s has landed and its LDS writes of stage s
-    // (packed weights) have completed; no wave still reads the slot refilled below
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if constexpr (INT4) {
-      if (s + 2 < KT) pk_free = load_pk(s + 2);
-    }
-    if (s + NS - 1 < KT) issue_dma(s + NS - 1);
-    if constexpr (INT4) {
-      if (s + 1 < KT) store_pk(s + 1, pk_next);
-    }
-    mfma_stage(s, set_c, zero_c);
-  };
-
+  // One pipeline step: make stage s resident (this wave's DMAs, then the
+  // barrier for everyone's), refill the ring slot freed by step s-1, expand
+  // packed weights (second barrier), then run the MFMAs of stage s.
   using T0 = std::integral_constant<int, 0>;
   using T1 = std::integral_constant<int, 1>;
   using ZF = std::true_type;
   using NZ = std::false_type;
-  // Stage s reads its packed weights from pk1 when s is even (pk0 when odd)
-  // and refills the other register set with stage s+2.
-  if constexpr (GS == 0) {
-    int s = 0;
-    for (; s + 1 < KT; s += 2) {
-      step(s, T0{}, NZ{}, pk1, pk0);
-      step(s + 1, T0{}, NZ{}, pk0, pk1);
+  float sw_a[TN], sw_b[TN];
+  auto step = [&](int s, auto set_c, auto zero_c, float* sw_read, auto fold_c, auto fs_c, int g_f,
+                  const float* sw_f) {
+    wait_stage(s);
+    lds_barrier();
+    if (s + NS - 1 < KT) issue_dma(s + NS - 1);
+    if constexpr (INT4) {
+      unpack(s);
+      lds_barrier();
     }
-    if (s < KT) step(s, T0{}, NZ{}, pk1, pk0);
-  } else if constexpr (SPG == 2) {
-    const int NG = KT / 2;
-    if constexpr (kPingPong) {
-      int g = 0;
-      for (; g + 1 < NG; g += 2) {
-        const int s = 2 * g;
-        step(s, T0{}, ZF{}, pk1, pk0);
-        if (g > 0) fold(g - 1, T1{});
-        step(s + 1, T0{}, NZ{}, pk0, pk1);
-        step(s + 2, T1{}, ZF{}, pk1, pk0);
-        fold(g, T0{});
-        step(s + 3, T1{}, NZ{}, pk0, pk1);
-      }
-      if (g < NG) {
-        const int s = 2 * g;
-        step(s, T0{}, ZF{}, pk1, pk0);
-        if (g > 0) fold(g - 1, T1{});
-        step(s + 1, T0{}, NZ{}, pk0, pk1);
-        fold(g, T0{});
-      } else {
-        fold(g - 1, T1{});
-      }
+    read_scales(s, sw_read);
+    // keep the (register-only) fold inside the MFMA region instead of letting
+    // it be hoisted above the barriers
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_stage(s, set_c, zero_c, fold_c, fs_c, g_f, sw_f);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  if constexpr (GS == 0) {
+    for (int s = 0; s < KT; ++s) step(s, T0{}, NZ{}, sw_a, NZ{}, T0{}, 0, sw_a);
+  } else if constexpr (kPingPong) {
+    // set g&1 accumulates group g while set (g-1)&1 (group g-1) is folded
+    step(0, T0{}, ZF{}, sw_a, NZ{}, T1{}, 0, sw_b);
+    int g = 1;
+    for (; g + 1 < KT; g += 2) {
+      step(g, T1{}, ZF{}, sw_b, ZF{}, T0{}, g - 1, sw_a);
+      step(g + 1, T0{}, ZF{}, sw_a, ZF{}, T1{}, g, sw_b);
+    }
+    if (g < KT) {
+      step(g, T1{}, ZF{}, sw_b, ZF{}, T0{}, g - 1, sw_a);
+      fold(g, T1{}, sw_b);
     } else {
-      for (int g = 0; g < NG; ++g) {
-        step(2 * g, T0{}, ZF{}, pk1, pk0);
-        step(2 * g + 1, T0{}, NZ{}, pk0, pk1);
-        fold(g, T0{});
-      }
+      fold(g - 1, T0{}, sw_a);
     }
   } else {
-    // one stage per group
-    const int NG = KT;
-    if constexpr (kPingPong) {
-      int g = 0;
-      for (; g + 1 < NG; g += 2) {
-        step(g, T0{}, ZF{}, pk1, pk0);
-        if (g > 0) fold(g - 1, T1{});
-        step(g + 1, T1{}, ZF{}, pk0, pk1);
-        fold(g, T0{});
-      }
-      if (g < NG) {
-        step(g, T0{}, ZF{}, pk1, pk0);
-        if (g > 0) fold(g - 1, T1{});
-        fold(g, T0{});
-      } else {
-        fold(g - 1, T1{});
-      }
-    } else {
-      int g = 0;
-      for (; g + 1 < NG; g += 2) {
-        step(g, T0{}, ZF{}, pk1, pk0);
-        fold(g, T0{});
-        step(g + 1, T0{}, ZF{}, pk0, pk1);
-        fold(g + 1, T0{});
-      }
-      if (g < NG) {
-        step(g, T0{}, ZF{}, pk1, pk0);
-        fold(g, T0{});
-      }
+    for (int g = 0; g < KT; ++g) {
+      step(g, T0{}, ZF{}, sw_a, NZ{}, T0{}, 0, sw_a);
+      fold(g, T0{}, sw_a);
     }
   }
 
@@ -386,6 +391,61 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
         }
   }
   if (C == nullptr) return;
+  if constexpr (OUT_DT != IC_DTYPE_F32) {
+    // 16-bit outputs: finish each value in registers, stage the tile through
+    // LDS row-major, then write whole rows with 16-byte stores.  s_a, bias and
+    // the per-row weight scales are staged once per tile.
+    if ((((uintptr_t)C) & 15) == 0 && (ldc & 7) == 0 && (N & 7) == 0) {
+      constexpr int RS = TL::EPI_RS;
+      lds_barrier();  // every wave is done with the last stage
+      u16* ot = (u16*)smem;
+      float* sa_l = (float*)(smem + BM * RS * 2);
+      float* b_l = sa_l + BM;
+      float* sw_l = b_l + BN;
+      for (int t = tid; t < BM; t += kNT) sa_l[t] = s_a[min(m0 + t, M - 1)];
+      for (int t = tid; t < BN; t += kNT) {
+        const int n = min(n0 + t, N - 1);
+        b_l[t] = bias != nullptr ? ld_any_f32(bias, bias_dt, n) : 0.0f;
+        if constexpr (GS == 0) sw_l[t] = s_w[n];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int nl = wc * WN + j * 32 + (lane & 31);
+        const float b = b_l[nl];
+        const float sw = GS == 0 ? sw_l[nl] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int ml = wr * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            float v;
+            if constexpr (GS == 0) {
+              float a = (float)acc[0][i][j][r];
+              if constexpr (INT4) a *= 0.0625f;
+              v = a * (sa_l[ml] * sw);
+            } else {
+              v = facc[i][j][r] * sa_l[ml];
+            }
+            if (bias != nullptr) v = v + b;
+            u16 h;
+            if constexpr (OUT_DT == IC_DTYPE_F16) h = f32_to_f16(v);
+            else h = f32_to_bf16(v);
+            ot[ml * RS + nl] = h;
+          }
+        }
+      }
+      __syncthreads();
+      constexpr int CPR = BN / 8;  // 16-byte chunks per tile row
+#pragma unroll 4
+      for (int c = tid; c < BM * CPR; c += kNT) {
+        const int row = c / CPR, col = (c % CPR) * 8;
+        const int m = m0 + row, n = n0 + col;
+        if (m < M && n < N) *(v4u*)((u16*)C + (int64_t)m * ldc + n) = *(const v4u*)(ot + row * RS + col);
+      }
+      return;
+    }
+  }
   // Each lane stores 16 rows of one column per 32x32 tile; row offsets within
   // a tile stay in 32-bit arithmetic (the host bounds ldc).
   constexpr int ESZ = OUT_DT == IC_DTYPE_F32 ? 4 : 2;
@@ -467,11 +527,12 @@ struct GemmArgs {
   int32_t* acc_out; bool int4;
 };
 
-template <class TL, bool INT4, int GS, int OUT_DT, bool ACC>
+template <class TL, int OUT_DT, bool ACC>
 hipError_t launch_mfma(const GemmArgs& g, hipStream_t st) {
   const int tiles = ((g.M + TL::BM - 1) / TL::BM) * ((g.N + TL::BN - 1) / TL::BN);
   const size_t shm = TL::lds_bytes();
-  auto kern = gemm_i8_kernel<TL, INT4, GS, OUT_DT, ACC>;
+  static_assert(TL::lds_bytes() <= 160 * 1024, "LDS budget");
+  auto kern = gemm_i8_kernel<TL, OUT_DT, ACC>;
   static bool attr_set = false;  // idempotent attribute; benign if raced
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
@@ -483,22 +544,15 @@ hipError_t launch_mfma(const GemmArgs& g, hipStream_t st) {
   return hipGetLastError();
 }
 
-// Tile choices: large tiles when both dimensions fill them, 128-byte K stages
-// (whole cache lines per row) whenever K allows.
+// Tile choices: 256-row tiles when M fills them, else 128 x 128.
 template <bool INT4, int GS, int OUT_DT, bool ACC>
 hipError_t pick_tile(const GemmArgs& g, hipStream_t st) {
-  const bool k128 = g.K % 128 == 0;
-  if constexpr (GS == 0) {
-    if (g.M > 128 && g.N > 128) {
-      if (k128) return launch_mfma<Tile<256, 256, 2, 128, 2>, INT4, GS, OUT_DT, ACC>(g, st);
-      return launch_mfma<Tile<256, 256, 2, 64, 4>, INT4, GS, OUT_DT, ACC>(g, st);
-    }
-    if (k128) return launch_mfma<Tile<128, 128, 2, 128, 4>, INT4, GS, OUT_DT, ACC>(g, st);
-    return launch_mfma<Tile<128, 128, 2, 64, 4>, INT4, GS, OUT_DT, ACC>(g, st);
+  if constexpr (!INT4 && GS == 0) {
+    if (g.M > 128 && g.N > 128) return launch_mfma<Tile<256, 256, 2, 2, false, 0>, OUT_DT, ACC>(g, st);
+    return launch_mfma<Tile<128, 128, 2, 4, false, 0>, OUT_DT, ACC>(g, st);
   } else {
-    // grouped scales need K % 128 == 0
-    if (g.M > 128) return launch_mfma<Tile<256, 128, 4, 128, 3>, INT4, GS, OUT_DT, ACC>(g, st);
-    return launch_mfma<Tile<128, 128, 2, 128, 4>, INT4, GS, OUT_DT, ACC>(g, st);
+    if (g.M > 128) return launch_mfma<Tile<256, 128, 4, 3, INT4, GS>, OUT_DT, ACC>(g, st);
+    return launch_mfma<Tile<128, 128, 2, 4, INT4, GS>, OUT_DT, ACC>(g, st);
   }
 }
 
@@ -529,7 +583,7 @@ hipError_t launch_generic(const GemmArgs& g, int gsize, hipStream_t st) {
 }
 
 bool mfma_shape_ok(const GemmArgs& g, int gsize) {
-  if (g.K % 64 != 0) return false;
+  if (g.K % kBK != 0) return false;
   if (g.G > 1 && gsize != 128) return false;
   // 16-byte DMA / vector loads need aligned bases and strides; packed INT4
   // rows are read 8 or 16 bytes at a time
