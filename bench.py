@@ -7,18 +7,25 @@ BASELINE config 3, the Flux MLP down-projection as an INT4 W4A8 linear:
   lognormal(0, 0.5), PermuQuant perm, rot_size 256, INT4 weights [3072, 12288]
   packed with fp16 group-128 scales.
 One step = fused prep+quantize kernel + W4A8 GEMM (one linear forward).
-Inputs rotate over several HBM-resident copies so the 256 MB Infinity Cache
-cannot serve repeated reads.
+Other --config values are the remaining BASELINE shapes (C1 W8A8, C2 W4A16)
+and the M = 1 modulation linears of the Flux step (C4), which run the
+bandwidth-bound GEMV kernels.
 
-Prints ONE JSON line with the driver's contract fields plus "roofline" (the
-W4A8 GEMM against the dense INT8 MFMA peak, timed with HIP events on the
-launch stream) and "cpu_baseline" (the reference fp32 PyTorch fallback,
-restated under oracle/, timed on this host's cores).
+Timing: inputs are resident in HBM before the timed region; weights and
+activations rotate over enough copies that the 256 MB Infinity Cache cannot
+serve repeats.  `value` is whole-step throughput from HIP events around K
+steps; the dominant kernel is also timed alone (back-to-back launches between
+two events on the launch stream) for the roofline entry.
+
+Prints ONE JSON line with the driver's contract fields plus "roofline" and
+"cpu_baseline" (the reference fp32 PyTorch fallback, restated under oracle/,
+timed on this host's cores).
 """
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import statistics
 import sys
@@ -39,6 +46,12 @@ CONFIGS = {
                rot=0, smoothrot=False, perm=False, G=24, act="fp16"),
     "c3": dict(name="C3 W4A8 linear 12288->3072 (Flux MLP down-proj), M=4608, g128, R=256",
                fmt="int4", M=4608, K=12288, N=3072, rot=256, smoothrot=True, perm=True, G=96, act="fp16"),
+    "c4mod_w4a8": dict(name="C4 modulation GEMV W4A8 3072->18432, M=1, g128, R=256 (double-block img_mod/txt_mod)",
+                       fmt="int4", M=1, K=3072, N=18432, rot=256, smoothrot=True, perm=True, G=24, act="bf16"),
+    "c4mod_w4a16": dict(name="C4 modulation GEMV W4A16 3072->18432, M=1, g128 (single-block modulation)",
+                        fmt="w4a16", M=1, K=3072, N=18432, rot=0, smoothrot=False, perm=False, G=24, act="bf16"),
+    "c4mod_w8a8": dict(name="C4 modulation GEMV W8A8 3072->18432, M=1 (INT8 checkpoint)",
+                       fmt="int8", M=1, K=3072, N=18432, rot=0, smoothrot=False, perm=False, G=1, act="bf16"),
 }
 
 
@@ -48,28 +61,21 @@ def _parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
-    ap.add_argument("--copies", type=int, default=4, help="input copies rotated across steps")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (PMC calibration)")
     return ap.parse_args()
 
 
-def _gen(seed):
+def make_inputs(cfg, seed=0):
+    """Seeded synthetic inputs of BASELINE.json's config (host tensors)."""
     import torch
 
-    return torch.Generator().manual_seed(seed)
-
-
-def make_inputs(cfg, dev, seed=0):
-    """Seeded synthetic inputs of BASELINE.json's config (host + device)."""
-    import torch
-
-    g = _gen(seed)
+    g = torch.Generator().manual_seed(seed)
     M, K, N, G = cfg["M"], cfg["K"], cfg["N"], cfg["G"]
     act = torch.float16 if cfg["act"] == "fp16" else torch.bfloat16
     x = torch.randn(M, K, generator=g)
-    if cfg["fmt"] == "int4":
+    if cfg["fmt"] == "int4" and cfg["name"].startswith("C3"):
         idx = torch.randperm(K, generator=g)[: K // 100]
         x[:, idx] *= 20.0
     x = x.to(act)
@@ -85,12 +91,48 @@ def make_inputs(cfg, dev, seed=0):
     return inp
 
 
-def gpu_bench(cfg, inp, steps, warmup, copies, rt):
+def algorithmic(cfg):
+    """(ops per GEMM launch, HBM bytes per GEMV launch, bytes per prep launch)."""
+    M, K, N, G = cfg["M"], cfg["K"], cfg["N"], cfg["G"]
+    ops = 2.0 * M * N * K
+    wbytes = N * K if cfg["fmt"] == "int8" else N * K // 2
+    gemv_bytes = wbytes + 2 * N * G + 2 * M * K + 2 * M * N  # fp16 scales, 16-bit x and out
+    prep_bytes = M * K * 2 + M * K + 4 * M
+    return ops, gemv_bytes, prep_bytes
+
+
+def _time_loop(fn, n):
+    """Average ms of n calls, captured once into a hipGraph (torch.cuda.CUDAGraph)
+    and replayed between two events, so host launch latency does not hide the
+    kernels (the reference replays CUDA graphs too, _cuda_graph.py:252-297).
+    The kernels never allocate, synchronise or clear memory, so the graph holds
+    kernel nodes only; outputs are checked against eager runs in the tests."""
+    import torch
+
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n):
+            fn(i)
+    g.replay()  # warm-up replay
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record()
+    g.replay()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) / n
+
+
+def gpu_bench(cfg, inp, steps, warmup, rt):
     import torch
 
     dev = torch.device("cuda:0")
     M, K, N = cfg["M"], cfg["K"], cfg["N"]
     act = inp["x"].dtype
+    # enough copies that weights + activations exceed the 256 MB Infinity Cache
+    per_copy = inp["x"].numel() * inp["x"].element_size() + inp["w"].numel() * inp["w"].element_size()
+    copies = max(2, min(64, math.ceil(640e6 / per_copy)))
     xs = [inp["x"].to(dev) for _ in range(copies)]
     ws = [inp["w"].to(dev) for _ in range(copies)]
     s_w = inp["s_w"].to(dev)
@@ -100,39 +142,33 @@ def gpu_bench(cfg, inp, steps, warmup, copies, rt):
     s_a = torch.empty(M, dtype=torch.float32, device=dev)
     out = torch.empty(M, N, dtype=act, device=dev)
 
-    def step(i, ev=None):
-        x, w = xs[i % copies], ws[i % copies]
+    def prep(i):
+        rt.rotate_quantize(xs[i % copies], rot_size=cfg["rot"], w_in=K, smoothrot=sr, perm=perm,
+                           s_a_out=s_a, x_int8_out=q)
+
+    def gemm(i):
+        w = ws[i % copies]
         if cfg["fmt"] == "w4a16":
-            if ev:
-                ev[0].record()
-            rt.gemm_w4a16(x, w, s_w, out=out)
-            if ev:
-                ev[1].record()
-            return
-        if ev:
-            ev[2].record()
-        rt.rotate_quantize(x, rot_size=cfg["rot"], w_in=K, smoothrot=sr, perm=perm, s_a_out=s_a, x_int8_out=q)
-        if ev:
-            ev[0].record()
-        if cfg["fmt"] == "int8":
+            rt.gemm_w4a16(xs[i % copies], w, s_w, out=out)
+        elif cfg["fmt"] == "int8":
             rt.fused_int8_gemm_dequant(q, w, s_w, s_a, out_dtype=act, out=out)
         else:
             rt.gemm_w4a8(q, w, s_w, s_a, out_dtype=act, out=out)
-        if ev:
-            ev[1].record()
+
+    def step(i):
+        if cfg["fmt"] != "w4a16":
+            prep(i)
+        gemm(i)
 
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
     t0 = time.perf_counter()
-    for i in range(steps):
-        step(i, events[i])
-    torch.cuda.synchronize()
+    step_ms = _time_loop(step, steps)
     wall = time.perf_counter() - t0
-    gemm_ms = [e[0].elapsed_time(e[1]) for e in events]
-    prep_ms = [e[2].elapsed_time(e[0]) for e in events] if cfg["fmt"] != "w4a16" else []
-    return wall, gemm_ms, prep_ms
+    gemm_ms = _time_loop(gemm, steps)
+    prep_ms = _time_loop(prep, steps) if cfg["fmt"] != "w4a16" else None
+    return step_ms, wall, gemm_ms, prep_ms, copies
 
 
 def cpu_baseline(cfg, inp):
@@ -144,8 +180,7 @@ def cpu_baseline(cfg, inp):
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     M, K, N = cfg["M"], cfg["K"], cfg["N"]
-    rows = M  # full shape; a C3 call is a few seconds of host work
-    x = inp["x"][:rows]
+    x = inp["x"]
     kw = dict(int4=cfg["fmt"] != "int8", smoothrot=inp["smoothrot"], rot_size=cfg["rot"], perm=inp["perm"])
     w = inp["w"].numpy()
     s_w = inp["s_w"].numpy()
@@ -156,24 +191,26 @@ def cpu_baseline(cfg, inp):
         oracle.reference_fallback_forward(x, w, s_w, K, **kw)
         ts.append(time.perf_counter() - t0)
     t = statistics.median(ts)
-    return {"value": round(2.0 * rows * N * K / t / 1e12, 5), "unit": "TOPS", "cores": cores,
-            "kind": "port", "seconds_per_call": round(t, 4),
-            "sample": f"{rows}x{K} -> {N}, full shape, fp32 dequant + prep + F.linear, median of 3 after 1 warm-up"}
+    return {"value": round(2.0 * M * N * K / t / 1e12, 5), "unit": "TOPS", "cores": cores,
+            "kind": "port", "seconds_per_call": round(t, 5),
+            "sample": f"{M}x{K} -> {N}, full shape, fp32 dequant + prep + F.linear per call "
+                      f"(the reference fallback re-dequantizes every forward), median of 3 after 1 warm-up"}
 
 
 def traffic_for(workload_key):
-    path = os.path.join(ROOT, "profiles", f"traffic_{workload_key}.json")
+    """HBM bytes per launch of the dominant kernel from committed rocprofv3 counters."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        return json.load(f).get("gemm_hbm_bytes_per_launch")
+        return json.load(f).get(workload_key, {}).get("hbm_bytes_per_launch")
 
 
 def main():
     args = _parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "the multi-GPU sharding is a design note, not a measured path.", file=sys.stderr)
+              "multi-GPU sharding is a design note (token split), not a measured path.", file=sys.stderr)
         sys.exit(2)
     import torch
 
@@ -184,42 +221,47 @@ def main():
         print(f"bench.py needs an MI355X and the built kernels ({rt.LOAD_ERROR})", file=sys.stderr)
         sys.exit(1)
     cfg = CONFIGS[args.config]
-    inp = make_inputs(cfg, "cuda:0")
+    inp = make_inputs(cfg)
     if args.calib_copy:
         a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda:0")
         b = torch.empty_like(a)
         b.copy_(a)
         torch.cuda.synchronize()
         del a, b
-    wall, gemm_ms, prep_ms = gpu_bench(cfg, inp, args.steps, args.warmup, args.copies, rt)
+    step_ms, wall, g_ms, p_ms, copies = gpu_bench(cfg, inp, args.steps, args.warmup, rt)
     M, K, N = cfg["M"], cfg["K"], cfg["N"]
-    ops = 2.0 * M * N * K
-    ms_step = wall * 1e3 / args.steps
-    g_ms = statistics.mean(gemm_ms)
+    ops, gemv_bytes, prep_bytes = algorithmic(cfg)
     is_fp = cfg["fmt"] == "w4a16"
-    peak = PEAK_FP16_TFLOPS if is_fp else PEAK_INT8_TOPS
-    achieved = ops / (g_ms * 1e-3) / 1e12
-    roof = {"bound": "mfma", "kernel": "gemm_w4a16" if is_fp else ("gemm_w8a8" if cfg["fmt"] == "int8" else "gemm_w4a8"),
-            "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s" if is_fp else "TOPS",
-            "frac": round(achieved / peak, 4), "kernel_ms": round(g_ms, 5),
-            "algorithmic_ops_per_launch": ops, "traffic": traffic_for(args.config)}
+    kname = "gemm_w4a16" if is_fp else ("gemm_w8a8" if cfg["fmt"] == "int8" else "gemm_w4a8")
+    if M <= rt.GEMV_MAX_M:
+        kname = kname.replace("gemm", "gemv")
+        achieved = gemv_bytes / (g_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "kernel": kname, "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS,
+                "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4), "kernel_ms": round(g_ms, 5),
+                "algorithmic_bytes_per_launch": gemv_bytes, "traffic": traffic_for(args.config)}
+    else:
+        peak = PEAK_FP16_TFLOPS if is_fp else PEAK_INT8_TOPS
+        achieved = ops / (g_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "kernel": kname, "achieved": round(achieved, 2), "peak": peak,
+                "unit": "TFLOP/s" if is_fp else "TOPS", "frac": round(achieved / peak, 4),
+                "kernel_ms": round(g_ms, 5), "algorithmic_ops_per_launch": ops,
+                "traffic": traffic_for(args.config)}
     line = {
-        "metric": METRIC, "value": round(ops / (ms_step * 1e-3) / 1e12, 2), "unit": "TOPS",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
+        "metric": METRIC, "value": round(ops / (step_ms * 1e-3) / 1e12, 3), "unit": "TOPS",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(step_ms, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "fp16xint8" if not is_fp else "fp16", "data": "synthetic",
+        "dtype": cfg["act"] if is_fp else "int8", "data": "synthetic",
         "config": {"workload": cfg["name"], "M": M, "K": K, "N": N, "group_size": K // cfg["G"],
                    "rot_size": cfg["rot"], "smoothrot": cfg["smoothrot"], "perm": cfg["perm"],
-                   "activation": cfg["act"], "parallelism": "single GPU"},
+                   "activation": cfg["act"], "input_copies": copies, "parallelism": "single GPU"},
         "roofline": roof,
+        "host_wall_ms_per_step": round(wall * 1e3 / args.steps, 5),
     }
-    if prep_ms:
-        p_ms = statistics.mean(prep_ms)
-        qbytes = M * K * 2 + M * K + 4 * M
+    if p_ms is not None:
+        pach = prep_bytes / (p_ms * 1e-3) / 1e9
         line["prep_quant"] = {"kernel": "rotate_quantize", "bound": "hbm", "kernel_ms": round(p_ms, 5),
-                              "algorithmic_bytes": qbytes, "achieved": round(qbytes / (p_ms * 1e-3) / 1e9, 1),
-                              "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                              "frac": round(qbytes / (p_ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
+                              "algorithmic_bytes": prep_bytes, "achieved": round(pach, 1),
+                              "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(pach / PEAK_HBM_GBPS, 4)}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(cfg, inp)
     print(json.dumps(line), flush=True)

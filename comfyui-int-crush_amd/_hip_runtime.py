@@ -73,6 +73,9 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "ic_gemm_w8a8_acc_i32": ([_P, _L, _L, _L, _P, _L, _L, _P, _I, _P], _I),
     "ic_gemm_w4a8_acc_i32": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _I, _P], _I),
     "ic_gemm_w8a8_generic": ([_P, _L, _L, _L, _P, _L, _L, _P, _P, _P, _I, _P, _I, _L, _P], _I),
+    "ic_gemv_w8a8": ([_P, _L, _L, _L, _P, _L, _L, _P, _P, _P, _I, _P, _I, _L, _P], _I),
+    "ic_gemv_w4a8": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _P, _I, _P, _I, _L, _P], _I),
+    "ic_gemv_w4a16": ([_P, _I, _L, _L, _L, _P, _L, _L, _P, _L, _P, _I, _P, _L, _P], _I),
 }
 
 _lib = None
@@ -429,6 +432,47 @@ def gemm_w4a16(x: torch.Tensor, w_packed: torch.Tensor, s_w: torch.Tensor,
     return c
 
 
+# ── small-batch GEMV (M <= 16; the GEMM callables route there by themselves) ──
+GEMV_MAX_M = 16
+
+
+def gemv(x: torch.Tensor, w: torch.Tensor, s_w: torch.Tensor, s_a: torch.Tensor | None = None,
+         bias: torch.Tensor | None = None, out_dtype: torch.dtype | None = None, *,
+         kind: str) -> torch.Tensor:
+    """Explicit GEMV entry points (ic_gemv_w8a8 / ic_gemv_w4a8 / ic_gemv_w4a16).
+
+    kind "w8a8": x int8 codes [M, K], w int8 [N, K], s_w [N], s_a [M].
+    kind "w4a8": x int8 codes, w packed uint8 [N, K/2], s_w [N, G] (G = 1 or K/128), s_a [M].
+    kind "w4a16": x fp16/bf16 [M, K], w packed uint8, s_w [N, G]; out in x.dtype.
+    """
+    _need_cuda(x, w, s_w, s_a, bias)
+    x2 = _rows(x)
+    M, K = x2.shape
+    wr = _rows(w)
+    N = wr.shape[0]
+    bp, bdt, _keep = _bias_args(bias, N)
+    with torch.cuda.device(x2.device):
+        if kind == "w4a16":
+            sw = s_w.detach().reshape(N, -1).to(torch.float32).contiguous()
+            c = torch.empty((M, N), dtype=x2.dtype, device=x2.device)
+            _call("ic_gemv_w4a16", _ptr(x2), _dt(x2.dtype, "gemv"), M, K, x2.stride(0), _ptr(wr), N,
+                  wr.stride(0), _ptr(sw), sw.shape[1], bp, bdt, _ptr(c), c.stride(0), _stream(x2))
+            return c
+        sa = s_a.detach().reshape(-1).to(torch.float32).contiguous()
+        c = torch.empty((M, N), dtype=out_dtype or torch.bfloat16, device=x2.device)
+        if kind == "w8a8":
+            sw = s_w.detach().reshape(-1).to(torch.float32).contiguous()
+            _call("ic_gemv_w8a8", _ptr(x2), M, K, x2.stride(0), _ptr(wr), N, wr.stride(0), _ptr(sa),
+                  _ptr(sw), bp, bdt, _ptr(c), _dt(c.dtype, "out"), c.stride(0), _stream(x2))
+        elif kind == "w4a8":
+            sw = s_w.detach().reshape(N, -1).to(torch.float32).contiguous()
+            _call("ic_gemv_w4a8", _ptr(x2), M, K, x2.stride(0), _ptr(wr), N, wr.stride(0), _ptr(sw),
+                  sw.shape[1], _ptr(sa), bp, bdt, _ptr(c), _dt(c.dtype, "out"), c.stride(0), _stream(x2))
+        else:
+            raise ValueError(f"unknown GEMV kind {kind!r}")
+    return c
+
+
 def fused_quant_int8_gemm_dequant(x: torch.Tensor, w_int8: torch.Tensor, s_w: torch.Tensor,
                                   bias: torch.Tensor | None = None,
                                   out_dtype: torch.dtype = torch.bfloat16,
@@ -512,5 +556,6 @@ __all__ = [
     "fused_quant_int8_gemm_dequant", "fused_w4a8_gemm_dequant", "unpack_int4_to_int8",
     "unpack_int4_to_float16", "rotate_quantize", "prepare_activation", "gemm_w4a8", "gemm_w4a16",
     "unpack_int4_to_float", "prepare_factors", "prepare_perm", "PreparedFactors", "gemm_acc_i32",
+    "gemv", "GEMV_MAX_M",
     "load_library",
 ]

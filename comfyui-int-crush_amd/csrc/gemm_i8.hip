@@ -635,6 +635,8 @@ extern "C" {
 int ic_gemm_w8a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8_t* w, int64_t N,
                  int64_t ldw, const float* s_a, const float* s_w, const void* bias, int bias_dtype,
                  void* out, int out_dtype, int64_t ldo, void* stream) {
+  if (ic_gemv_applicable(M, K, xq, ldx, w, ldw) && ldw >= K && N > 0 && ldo >= N && ldx >= K)
+    return ic_gemv_w8a8(xq, M, K, ldx, w, N, ldw, s_a, s_w, bias, bias_dtype, out, out_dtype, ldo, stream);
   GemmArgs g{xq, ldx, (const uint8_t*)w, ldw, s_a, s_w, 1, bias, bias_dtype, out, out_dtype, ldo,
              (int)M, (int)N, (int)K, nullptr, false};
   return run_gemm(g, (hipStream_t)stream, "ic_gemm_w8a8", false);
@@ -644,6 +646,10 @@ int ic_gemm_w4a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint
                  int64_t N, int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a,
                  const void* bias, int bias_dtype, void* out, int out_dtype, int64_t ldo,
                  void* stream) {
+  if (ic_gemv_applicable(M, K, xq, ldx, w_packed, ldw) && ldw * 2 >= K && N > 0 && ldo >= N && ldx >= K &&
+      (num_groups == 1 || num_groups * 128 == K))
+    return ic_gemv_w4a8(xq, M, K, ldx, w_packed, N, ldw, s_w, num_groups, s_a, bias, bias_dtype, out, out_dtype,
+                        ldo, stream);
   GemmArgs g{xq, ldx, w_packed, ldw, s_a, s_w, (int)num_groups, bias, bias_dtype, out, out_dtype,
              ldo, (int)M, (int)N, (int)K, nullptr, true};
   return run_gemm(g, (hipStream_t)stream, "ic_gemm_w4a8", false);

@@ -264,6 +264,8 @@ int ic_gemm_w4a16(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, c
     return ic_set_error(IC_ERR_INVALID_ARG, "%s: bias dtype must be f16/bf16/f32", who);
   if (M == 0) return IC_OK;
   if (!x || !w_packed || !s_w || !out) return ic_set_error(IC_ERR_INVALID_ARG, "%s: null pointer", who);
+  if (ic_gemv_applicable(M, K, x, ldx * 2, w_packed, ldw) && (num_groups == 1 || (K / num_groups) % 32 == 0))
+    return ic_gemv_w4a16(x, dtype, M, K, ldx, w_packed, N, ldw, s_w, num_groups, bias, bias_dtype, out, ldo, stream);
   const int G = (int)num_groups, gsize = (int)(K / num_groups);
   const bool mfma_ok = (K % 32 == 0) && (G == 1 || gsize % 32 == 0) && !((uintptr_t)x & 15) &&
                        !((uintptr_t)w_packed & 15) && !((ldx * 2) & 15) && !(ldw & 15);

@@ -1,0 +1,347 @@
+// Small-batch (M <= 16 tokens) quantized linears on gfx950: bandwidth-bound
+// GEMV kernels that read every packed weight byte once.
+//
+// The reference runs every batch size through the tiled GEMM (_ops.py:493-579,
+// triton_w4a8_gemm.py:111-169); a 256-row GEMM tile is >90% padding at M = 1
+// (Flux modulation layers, CFG batch 2).  Here one 256-thread workgroup owns
+// 16 output columns and its four waves split K in blocks of 128:
+//
+//   W8A8 / W4A8:  two v_mfma_i32_16x16x64_i8 per block (rows = tokens, padded
+//                 to 16; columns = outputs); INT4 weights are expanded in
+//                 registers to 16*q (two masks and a byte permute per 8
+//                 nibbles), the factor 16 removed exactly at the end.  Block
+//                 sums are exact int32; grouped scales are folded afterwards in
+//                 group order, so every output equals the tiled GEMM's
+//                 (same formula, same rounding steps):
+//                   G == 1: f32(sum) * (s_a[m] * s_w[n]) (+ bias)
+//                   G  > 1: (fma chain over g of f32(acc_g) * s_w[n,g]) * s_a[m] (+ bias)
+//   W4A16:        four v_mfma_f32_16x16x32_{f16,bf16} per block on weights
+//                 dequantized exactly as RN_dt(q * RN_dt(s)); fp32 partials of
+//                 the four waves are added in wave order.
+//
+// Every lane of a wave reads 16 packed bytes (32 values) of one weight row per
+// block, so a wave-wide load covers 16 rows x 64 bytes.
+#include "ic_common.h"
+
+namespace {
+
+constexpr int kGT = 256;  // threads per workgroup (4 waves)
+constexpr int kGBK = 128; // K per block
+
+typedef _Float16 v8h_t __attribute__((ext_vector_type(8)));
+typedef __bf16 v8bf_t __attribute__((ext_vector_type(8)));
+
+// 8 INT4 nibbles (low nibble = even k) -> 8 int8 values 16*q in natural k order.
+IC_DEV void unpack8_x16(uint32_t P, uint32_t& w0, uint32_t& w1) {
+  const uint32_t lo = (P << 4) & 0xf0f0f0f0u;
+  const uint32_t hi = P & 0xf0f0f0f0u;
+  w0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+  w1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+}
+
+template <bool INT4, int GS, int OUT_DT>
+__global__ __launch_bounds__(kGT) void gemv_i8_kernel(
+    const int8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
+    const float* __restrict__ s_a, const float* __restrict__ s_w, int G,
+    const void* __restrict__ bias, int bias_dt, void* __restrict__ C, int64_t ldc, int M, int N, int K) {
+  // GS == 128: block sums [KB][M][16]; otherwise per-wave totals [4][M][16]
+  extern __shared__ int32_t sacc[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n0 = blockIdx.x * 16;
+  const int c = lane >> 4, col = lane & 15;
+  const int n = min(n0 + col, N - 1);
+  const int am = min(col, M - 1);  // token row fed by this lane (rows >= M repeat the last one)
+  const int KB = K / kGBK;
+  const int8_t* arow = A + (int64_t)am * lda + 32 * c;
+  const uint8_t* brow = B + (int64_t)n * ldb + (INT4 ? 16 * c : 32 * c);
+
+  // Loads of up to kBatch blocks are issued before any of them is used, so a
+  // wave keeps kBatch weight loads (plus activation loads) in flight.
+  constexpr int kBatch = 8;
+  v4i tot = {0, 0, 0, 0};
+  for (int b0 = wave; b0 < KB; b0 += 4 * kBatch) {
+    v4u pw[kBatch];
+    v4i a0[kBatch], a1[kBatch], w1[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int b = b0 + 4 * u;
+      if (b < KB) {  // uniform across the wave
+        a0[u] = *(const v4i*)(arow + kGBK * b);
+        a1[u] = *(const v4i*)(arow + kGBK * b + 16);
+        if constexpr (INT4) {
+          pw[u] = *(const v4u*)(brow + (kGBK / 2) * b);
+        } else {
+          pw[u] = *(const v4u*)(brow + kGBK * b);
+          w1[u] = *(const v4i*)(brow + kGBK * b + 16);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int b = b0 + 4 * u;
+      if (b >= KB) break;
+      v4i b0v, b1v;
+      if constexpr (INT4) {
+        uint32_t w[8];
+        unpack8_x16(pw[u].x, w[0], w[1]);
+        unpack8_x16(pw[u].y, w[2], w[3]);
+        unpack8_x16(pw[u].z, w[4], w[5]);
+        unpack8_x16(pw[u].w, w[6], w[7]);
+        b0v = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+        b1v = v4i{(int)w[4], (int)w[5], (int)w[6], (int)w[7]};
+      } else {
+        b0v = __builtin_bit_cast(v4i, pw[u]);
+        b1v = w1[u];
+      }
+      if constexpr (GS == 128) {
+        v4i s = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[u], b0v, v4i{0, 0, 0, 0}, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[u], b1v, s, 0, 0, 0);
+        // D layout: lane holds rows 4*(lane/16) + i of column lane%16
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 4 * c + i;
+          if (r < M) sacc[(b * M + r) * 16 + col] = s[i];
+        }
+      } else {
+        tot = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[u], b0v, tot, 0, 0, 0);
+        tot = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[u], b1v, tot, 0, 0, 0);
+      }
+    }
+  }
+  if constexpr (GS != 128) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * c + i;
+      if (r < M) sacc[(wave * M + r) * 16 + col] = tot[i];
+    }
+  }
+  __syncthreads();
+
+  if (tid >= 16 * M) return;
+  const int m = tid >> 4, nl = tid & 15, no = n0 + nl;
+  if (no >= N) return;
+  float v;
+  if constexpr (GS == 128) {
+    const float* sw = s_w + (int64_t)no * G;
+    float facc = 0.0f;
+    for (int g = 0; g < KB; ++g) {
+      float s = sw[g];
+      if constexpr (INT4) s *= 0.0625f;  // block sums hold 16 * the true sum
+      facc = __builtin_fmaf((float)sacc[(g * M + m) * 16 + nl], s, facc);
+    }
+    v = facc * s_a[m];
+  } else {
+    const int t = ((sacc[(0 * M + m) * 16 + nl] + sacc[(1 * M + m) * 16 + nl]) +
+                   sacc[(2 * M + m) * 16 + nl]) + sacc[(3 * M + m) * 16 + nl];
+    float a = (float)t;
+    if constexpr (INT4) a *= 0.0625f;
+    v = a * (s_a[m] * s_w[no]);
+  }
+  if (bias != nullptr) v = v + ld_any_f32(bias, bias_dt, no);
+  st_from_f32<OUT_DT>(C, (int64_t)m * ldc + no, v);
+}
+
+// W4A16 weight dequantization RN_dt(q * RN_dt(s)) of 8 nibbles.
+template <int DT> IC_DEV void deq8(uint32_t P, float s, u16* out) {
+  if constexpr (DT == IC_DTYPE_F16) {
+    const _Float16 sh = (_Float16)s;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int q = (int)(P << (28 - 4 * i)) >> 28;
+      out[i] = __builtin_bit_cast(u16, (_Float16)((_Float16)q * sh));
+    }
+  } else {
+    const float sb = bf16_to_f32(f32_to_bf16(s));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int q = (int)(P << (28 - 4 * i)) >> 28;
+      out[i] = f32_to_bf16((float)q * sb);  // |q| <= 8 and 8-bit s: the product is exact
+    }
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(kGT) void gemv_w4a16_kernel(
+    const u16* __restrict__ X, int64_t ldx, const uint8_t* __restrict__ B, int64_t ldb,
+    const float* __restrict__ s_w, int G, int gsize, const void* __restrict__ bias, int bias_dt,
+    u16* __restrict__ C, int64_t ldc, int M, int N, int K) {
+  __shared__ float sacc[4 * 16 * 16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n0 = blockIdx.x * 16;
+  const int c = lane >> 4, col = lane & 15;
+  const int n = min(n0 + col, N - 1);
+  const int am = min(col, M - 1);
+  const int KB = K / kGBK;
+  const u16* xrow = X + (int64_t)am * ldx + 32 * c;
+  const uint8_t* brow = B + (int64_t)n * ldb + 16 * c;
+  const float* swrow = s_w + (int64_t)n * G;
+
+  constexpr int kBatch = 4;
+  v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int b0 = wave; b0 < KB; b0 += 4 * kBatch) {
+    v4u xv[kBatch][4], pw[kBatch];
+    float sv[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int b = b0 + 4 * u;
+      if (b < KB) {  // uniform across the wave
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xv[u][j] = *(const v4u*)(xrow + kGBK * b + 8 * j);
+        pw[u] = *(const v4u*)(brow + (kGBK / 2) * b);
+        sv[u] = swrow[G > 1 ? (kGBK * b + 32 * c) / gsize : 0];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int b = b0 + 4 * u;
+      if (b >= KB) break;
+      const uint32_t p4[4] = {pw[u].x, pw[u].y, pw[u].z, pw[u].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        u16 h[8];
+        deq8<DT>(p4[j], sv[u], h);
+        const v4u wv = {h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16),
+                        h[4] | ((uint32_t)h[5] << 16), h[6] | ((uint32_t)h[7] << 16)};
+        if constexpr (DT == IC_DTYPE_F16)
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h_t, xv[u][j]), __builtin_bit_cast(v8h_t, wv), acc, 0, 0, 0);
+        else
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf_t, xv[u][j]), __builtin_bit_cast(v8bf_t, wv), acc, 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sacc[(wave * 16 + 4 * c + i) * 16 + col] = acc[i];
+  __syncthreads();
+  if (tid >= 16 * M) return;
+  const int m = tid >> 4, nl = tid & 15, no = n0 + nl;
+  if (no >= N) return;
+  float v = ((sacc[(0 * 16 + m) * 16 + nl] + sacc[(1 * 16 + m) * 16 + nl]) + sacc[(2 * 16 + m) * 16 + nl]) +
+            sacc[(3 * 16 + m) * 16 + nl];
+  if (bias != nullptr) v = v + ld_any_f32(bias, bias_dt, no);
+  st_from_f32<DT>(C, (int64_t)m * ldc + no, v);
+}
+
+template <bool INT4, int GS, int OUT_DT>
+hipError_t launch_gemv_i8(const int8_t* A, int64_t lda, const uint8_t* B, int64_t ldb, const float* s_a,
+                          const float* s_w, int G, const void* bias, int bias_dt, void* C, int64_t ldc,
+                          int M, int N, int K, hipStream_t st) {
+  auto kern = gemv_i8_kernel<INT4, GS, OUT_DT>;
+  const size_t shm = (size_t)(GS == 128 ? K / kGBK : 4) * M * 16 * 4;
+  static bool attr_set = false;  // idempotent attribute; benign if raced
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  kern<<<dim3((unsigned)((N + 15) / 16)), dim3(kGT), shm, st>>>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C,
+                                                                ldc, M, N, K);
+  return hipGetLastError();
+}
+
+template <bool INT4, int GS>
+hipError_t pick_gemv_out(int out_dt, const int8_t* A, int64_t lda, const uint8_t* B, int64_t ldb,
+                         const float* s_a, const float* s_w, int G, const void* bias, int bias_dt, void* C,
+                         int64_t ldc, int M, int N, int K, hipStream_t st) {
+  switch (out_dt) {
+    case IC_DTYPE_F16:
+      return launch_gemv_i8<INT4, GS, IC_DTYPE_F16>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
+    case IC_DTYPE_BF16:
+      return launch_gemv_i8<INT4, GS, IC_DTYPE_BF16>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
+    default:
+      return launch_gemv_i8<INT4, GS, IC_DTYPE_F32>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
+  }
+}
+
+int check_gemv_common(const char* who, int64_t M, int64_t K, int64_t N, int64_t ldx, int64_t ldo,
+                      const void* bias, int bias_dtype) {
+  if (M < 0 || M > IC_GEMV_MAX_M)
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: M=%lld outside [0, %d]", who, (long long)M, IC_GEMV_MAX_M);
+  if (N <= 0 || K <= 0 || ldx < K || ldo < N)
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: bad shape N=%lld K=%lld", who, (long long)N, (long long)K);
+  if (K % kGBK != 0 || K > IC_GEMV_MAX_K)
+    return ic_set_error(IC_ERR_UNSUPPORTED, "%s: K=%lld must be a multiple of %d and <= %d", who, (long long)K,
+                        kGBK, IC_GEMV_MAX_K);
+  if (bias && bias_dtype != IC_DTYPE_F16 && bias_dtype != IC_DTYPE_BF16 && bias_dtype != IC_DTYPE_F32)
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: bias dtype must be f16/bf16/f32", who);
+  return IC_OK;
+}
+
+}  // namespace
+
+// Shared by the GEMM entry points, which route M <= 16 here.
+bool ic_gemv_applicable(int64_t M, int64_t K, const void* x, int64_t ldx_bytes, const void* w, int64_t ldw_bytes) {
+  return M >= 1 && M <= IC_GEMV_MAX_M && K % kGBK == 0 && K <= IC_GEMV_MAX_K && ((uintptr_t)x & 15) == 0 &&
+         ((uintptr_t)w & 15) == 0 && (ldx_bytes & 15) == 0 && (ldw_bytes & 15) == 0;
+}
+
+extern "C" {
+
+int ic_gemv_w8a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8_t* w, int64_t N, int64_t ldw,
+                 const float* s_a, const float* s_w, const void* bias, int bias_dtype, void* out, int out_dtype,
+                 int64_t ldo, void* stream) {
+  const char* who = "ic_gemv_w8a8";
+  int rc = check_gemv_common(who, M, K, N, ldx, ldo, bias, bias_dtype);
+  if (rc) return rc;
+  if (M == 0) return IC_OK;
+  if (!xq || !w || !s_a || !s_w || !out) return ic_set_error(IC_ERR_INVALID_ARG, "%s: null pointer", who);
+  if (!ic_gemv_applicable(M, K, xq, ldx, w, ldw) || ldw < K)
+    return ic_set_error(IC_ERR_UNSUPPORTED, "%s: operands must be 16-byte aligned", who);
+  if (out_dtype != IC_DTYPE_F16 && out_dtype != IC_DTYPE_BF16 && out_dtype != IC_DTYPE_F32)
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: out dtype must be f16/bf16/f32", who);
+  hipError_t e = pick_gemv_out<false, 0>(out_dtype, xq, ldx, (const uint8_t*)w, ldw, s_a, s_w, 1, bias, bias_dtype,
+                                         out, ldo, (int)M, (int)N, (int)K, (hipStream_t)stream);
+  if (e != hipSuccess) return ic_set_error(IC_ERR_LAUNCH, "%s: %s", who, hipGetErrorString(e));
+  return IC_OK;
+}
+
+int ic_gemv_w4a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed, int64_t N,
+                 int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a, const void* bias,
+                 int bias_dtype, void* out, int out_dtype, int64_t ldo, void* stream) {
+  const char* who = "ic_gemv_w4a8";
+  int rc = check_gemv_common(who, M, K, N, ldx, ldo, bias, bias_dtype);
+  if (rc) return rc;
+  if (num_groups < 1 || (num_groups > 1 && num_groups * kGBK != K))
+    return ic_set_error(IC_ERR_UNSUPPORTED, "%s: num_groups must be 1 or K/128", who);
+  if (M == 0) return IC_OK;
+  if (!xq || !w_packed || !s_a || !s_w || !out) return ic_set_error(IC_ERR_INVALID_ARG, "%s: null pointer", who);
+  if (!ic_gemv_applicable(M, K, xq, ldx, w_packed, ldw) || ldw * 2 < K)
+    return ic_set_error(IC_ERR_UNSUPPORTED, "%s: operands must be 16-byte aligned", who);
+  if (out_dtype != IC_DTYPE_F16 && out_dtype != IC_DTYPE_BF16 && out_dtype != IC_DTYPE_F32)
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: out dtype must be f16/bf16/f32", who);
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e = num_groups > 1
+                     ? pick_gemv_out<true, 128>(out_dtype, xq, ldx, w_packed, ldw, s_a, s_w, (int)num_groups, bias,
+                                                bias_dtype, out, ldo, (int)M, (int)N, (int)K, st)
+                     : pick_gemv_out<true, 0>(out_dtype, xq, ldx, w_packed, ldw, s_a, s_w, 1, bias, bias_dtype, out,
+                                              ldo, (int)M, (int)N, (int)K, st);
+  if (e != hipSuccess) return ic_set_error(IC_ERR_LAUNCH, "%s: %s", who, hipGetErrorString(e));
+  return IC_OK;
+}
+
+int ic_gemv_w4a16(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed, int64_t N,
+                  int64_t ldw, const float* s_w, int64_t num_groups, const void* bias, int bias_dtype, void* out,
+                  int64_t ldo, void* stream) {
+  const char* who = "ic_gemv_w4a16";
+  if (dtype != IC_DTYPE_F16 && dtype != IC_DTYPE_BF16)
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: activation dtype must be f16/bf16", who);
+  int rc = check_gemv_common(who, M, K, N, ldx, ldo, bias, bias_dtype);
+  if (rc) return rc;
+  if (num_groups < 1 || K % num_groups != 0 || (num_groups > 1 && (K / num_groups) % 32 != 0))
+    return ic_set_error(IC_ERR_UNSUPPORTED, "%s: groups must span multiples of 32 values", who);
+  if (M == 0) return IC_OK;
+  if (!x || !w_packed || !s_w || !out) return ic_set_error(IC_ERR_INVALID_ARG, "%s: null pointer", who);
+  if (!ic_gemv_applicable(M, K, x, ldx * 2, w_packed, ldw) || ldw * 2 < K)
+    return ic_set_error(IC_ERR_UNSUPPORTED, "%s: operands must be 16-byte aligned", who);
+  const int G = (int)num_groups, gsize = (int)(K / num_groups);
+  const dim3 grid((unsigned)((N + 15) / 16));
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == IC_DTYPE_F16)
+    gemv_w4a16_kernel<IC_DTYPE_F16><<<grid, kGT, 0, st>>>((const u16*)x, ldx, w_packed, ldw, s_w, G, gsize, bias,
+                                                         bias_dtype, (u16*)out, ldo, (int)M, (int)N, (int)K);
+  else
+    gemv_w4a16_kernel<IC_DTYPE_BF16><<<grid, kGT, 0, st>>>((const u16*)x, ldx, w_packed, ldw, s_w, G, gsize, bias,
+                                                          bias_dtype, (u16*)out, ldo, (int)M, (int)N, (int)K);
+  return ic_check_launch(who);
+}
+
+}  // extern "C"

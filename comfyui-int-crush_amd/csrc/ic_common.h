@@ -18,6 +18,8 @@
 int ic_set_error(int code, const char* fmt, ...);
 int ic_check_launch(const char* who);
 int ic_num_cus();  // compute units of the current device
+// GEMV routing test shared by the GEMM entry points (gemv.hip); strides in bytes.
+bool ic_gemv_applicable(int64_t M, int64_t K, const void* x, int64_t ldx_bytes, const void* w, int64_t ldw_bytes);
 
 // Arguments of the fused preparation kernels (internal; the ABI is flat).
 struct ic_rotq_args {

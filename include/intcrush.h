@@ -107,6 +107,29 @@ int ic_gemm_w4a16(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, c
                   int64_t N, int64_t ldw, const float* s_w, int64_t num_groups, const void* bias,
                   int bias_dtype, void* out, int64_t ldo, void* stream);
 
+/*
+ * Small-batch GEMV forms (1 <= M <= IC_GEMV_MAX_M tokens, K a multiple of 128
+ * and <= IC_GEMV_MAX_K, 16-byte aligned operands): same arguments, same
+ * arithmetic and same results as ic_gemm_w8a8 / ic_gemm_w4a8 (bit-identical)
+ * and ic_gemm_w4a16 (fp32 accumulation, tolerance-equal), reading each packed
+ * weight byte once.  The GEMM entry points route such calls here themselves.
+ * Replace the M <= 16 use of fused_int8_gemm_dequant / fused_w4a8_gemm_dequant
+ * (kernels/triton_int8_gemm.py:135-205, triton_w4a8_gemm.py:111-169) and of
+ * F.linear on unpacked weights (_ops.py:466-481), e.g. Flux modulation linears.
+ */
+#define IC_GEMV_MAX_M 16
+#define IC_GEMV_MAX_K 16384
+int ic_gemv_w8a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8_t* w, int64_t N,
+                 int64_t ldw, const float* s_a, const float* s_w, const void* bias, int bias_dtype,
+                 void* out, int out_dtype, int64_t ldo, void* stream);
+int ic_gemv_w4a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed,
+                 int64_t N, int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a,
+                 const void* bias, int bias_dtype, void* out, int out_dtype, int64_t ldo,
+                 void* stream);
+int ic_gemv_w4a16(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed,
+                  int64_t N, int64_t ldw, const float* s_w, int64_t num_groups, const void* bias,
+                  int bias_dtype, void* out, int64_t ldo, void* stream);
+
 /* INT4 -> int8 unpack (no scale).  kernels/triton_int4_to_int8_unpack.py:55-81. */
 int ic_unpack_int4_to_int8(const uint8_t* packed, int64_t N, int64_t K, int64_t ldp, int8_t* out,
                            int64_t ldo, void* stream);
