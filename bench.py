@@ -64,6 +64,8 @@ def _parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (PMC calibration)")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch eagerly instead of replaying a captured graph (for counter collection)")
     return ap.parse_args()
 
 
@@ -101,6 +103,9 @@ def algorithmic(cfg):
     return ops, gemv_bytes, prep_bytes
 
 
+EAGER = False
+
+
 def _time_loop(fn, n):
     """Average ms of n calls, captured once into a hipGraph (torch.cuda.CUDAGraph)
     and replayed between two events, so host launch latency does not hide the
@@ -109,6 +114,15 @@ def _time_loop(fn, n):
     kernel nodes only; outputs are checked against eager runs in the tests."""
     import torch
 
+    if EAGER:
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        for i in range(n):
+            fn(i)
+        e.record()
+        e.synchronize()
+        return s.elapsed_time(e) / n
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         for i in range(n):
@@ -220,6 +234,8 @@ def main():
     if not torch.cuda.is_available() or not rt.KERNELS_AVAILABLE:
         print(f"bench.py needs an MI355X and the built kernels ({rt.LOAD_ERROR})", file=sys.stderr)
         sys.exit(1)
+    global EAGER
+    EAGER = args.eager
     cfg = CONFIGS[args.config]
     inp = make_inputs(cfg)
     if args.calib_copy:
