@@ -18,13 +18,15 @@
 //     global->LDS DMA (global_load_lds) issued from inline assembly, so no
 //     VGPR holds staged data and the only memory waits are the explicit,
 //     static vmcnt waits of the pipeline (the compiler cannot see these DMAs
-//     and so does not serialise LDS accesses behind them);
+//     and so does not serialise LDS accesses behind them).  A stage's DMAs
+//     are issued in slices between the MFMA K-steps of the stage before, so
+//     no wave stalls at a burst of DMA issues before its MFMAs;
 //   * activation and int8 weight chunks land XOR-swizzled by row (the issuing
 //     lane picks the global chunk), so the ds_read_b128 fragment loads are
 //     bank-conflict free;
 //   * packed INT4 weights are expanded once per workgroup and stage from the
-//     ring into a double-buffered LDS tile as 16*q (int8): two masks and a byte
-//     permute per 8 nibbles; the factor 16 is removed exactly in the epilogue;
+//     ring into an LDS tile as 16*q (int8): two masks and a byte permute per
+//     8 nibbles; the factor 16 is removed exactly in the epilogue;
 //   * per-group scales (group 128 = one stage) fold the int32 partials into an
 //     fp32 accumulator with one convert + FMA per element and group; two int32
 //     accumulator sets alternate between groups so the fold of group g runs
@@ -108,7 +110,7 @@ struct Tile {
   static constexpr int BU_BYTES = INT4 ? BN * kBK : 0;  // one unpacked INT4 tile
   static constexpr int EPI_RS = BN + 8;  // 16-bit output staging row stride (elements)
   static constexpr size_t epi_bytes() { return (size_t)BM * EPI_RS * 2 + (size_t)(BM + 2 * BN) * 4; }
-  static constexpr size_t ring_bytes() { return (size_t)NS * SLOT + 2 * (size_t)BU_BYTES; }
+  static constexpr size_t ring_bytes() { return (size_t)NS * SLOT + (size_t)BU_BYTES; }
   static constexpr size_t lds_bytes() { return ring_bytes() > epi_bytes() ? ring_bytes() : epi_bytes(); }
 };
 
@@ -174,17 +176,28 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
   const uint8_t* b_base = B + (int64_t)n0 * ldb;
   const float* s_base = GS ? s_w + (int64_t)n0 * G : nullptr;
 
-  auto issue_dma = [&](int kt) {
+  // The D DMA instructions of one stage are issued in kParts slices, one per
+  // K-step of the MFMA loop: a wave that issued a whole stage at once stalled
+  // at issue instead of starting its MFMAs.  Slice p holds the blocks d with
+  // d % kParts == p (A blocks first, then B); the scale DMA goes last.
+  constexpr int kParts = kBK / 32;
+  auto issue_dma_part = [&](int kt, int part) {
     const uint32_t slot = lds0 + (uint32_t)((kt % NS) * TL::SLOT);
     const int8_t* ab = a_base + (int64_t)kt * kBK;
 #pragma unroll
-    for (int c = 0; c < A_DMA; ++c) dma16(a_off[c], ab, slot + (uint32_t)((wave + 8 * c) * 1024));
+    for (int c = 0; c < A_DMA; ++c)
+      if (c % kParts == part) dma16(a_off[c], ab, slot + (uint32_t)((wave + 8 * c) * 1024));
     const uint8_t* bb = b_base + (int64_t)kt * (INT4 ? kBK / 2 : kBK);
 #pragma unroll
-    for (int c = 0; c < B_DMA; ++c) dma16(b_off[c], bb, slot + (uint32_t)(TL::A_BYTES + (wave + 8 * c) * 1024));
+    for (int c = 0; c < B_DMA; ++c)
+      if ((A_DMA + c) % kParts == part) dma16(b_off[c], bb, slot + (uint32_t)(TL::A_BYTES + (wave + 8 * c) * 1024));
     if constexpr (GS != 0) {
-      if (s_wave) dma4(s_off, s_base + kt, slot + (uint32_t)(TL::A_BYTES + TL::B_BYTES + wave * 256));
+      if (part == kParts - 1 && s_wave) dma4(s_off, s_base + kt, slot + (uint32_t)(TL::A_BYTES + TL::B_BYTES + wave * 256));
     }
+  };
+  auto issue_dma = [&](int kt) {
+#pragma unroll
+    for (int p = 0; p < kParts; ++p) issue_dma_part(kt, p);
   };
   // Top of step s: stages s+1 .. s+NS-2 may stay in flight (D DMA
   // instructions each, one more on the waves that also fetch scales); near the
@@ -200,11 +213,13 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
     wait_vm<0>();
   };
 
-  // ---- packed INT4 -> 16*q int8 tile in LDS (double buffered)
+  // ---- packed INT4 -> 16*q int8 tile in LDS.  One buffer suffices: the
+  // barrier at the top of each step orders the MFMA reads of step s-1 before
+  // the unpack of step s.
   auto unpack = [&](int kt) {
     if constexpr (INT4) {
       const char* bp = smem + (kt % NS) * TL::SLOT + TL::A_BYTES;
-      char* bu = smem + NS * TL::SLOT + (kt & 1) * TL::BU_BYTES;
+      char* bu = smem + NS * TL::SLOT;
 #pragma unroll
       for (int h = 0; h < PK / 16; ++h) {
         const int idx = tid + kNT * h;      // 16-byte packed chunk index
@@ -286,12 +301,13 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
   // of the previous group (set FS, scales sw_f) is spread over the stage, one
   // 32x32 tile per K-step, and its VALU work is interleaved between the MFMAs
   // so that each wave converts and accumulates while its MFMAs execute.
-  auto mfma_stage = [&](int kt, auto set_c, auto zero_c, auto fold_c, auto fs_c, int g_f, const float* sw_f) {
+  auto mfma_stage = [&](int kt, int dma_kt, auto set_c, auto zero_c, auto fold_c, auto fs_c, int g_f,
+                        const float* sw_f) {
     constexpr int SET = decltype(set_c)::value;
     constexpr bool ZF = decltype(zero_c)::value;
     constexpr bool FOLD = decltype(fold_c)::value;
     const char* sA = smem + (kt % NS) * TL::SLOT;
-    const char* sB = INT4 ? smem + NS * TL::SLOT + (kt & 1) * TL::BU_BYTES : sA + TL::A_BYTES;
+    const char* sB = INT4 ? smem + NS * TL::SLOT : sA + TL::A_BYTES;
 #pragma unroll
     for (int ks = 0; ks < kBK / 32; ++ks) {
       v4i_t a[TM], b[TN];
@@ -307,6 +323,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
           if (ZF && ks == 0) acc[SET][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], v16i{}, 0, 0, 0);
           else acc[SET][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[SET][i][j], 0, 0, 0);
         }
+      if (dma_kt < KT) issue_dma_part(dma_kt, ks);
       if constexpr (FOLD) {
         if (ks < TM * TN) fold_tile(g_f, fs_c, ks, sw_f);
         if constexpr (!ACC_OUT) {
@@ -331,8 +348,8 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
     if (t < KT) issue_dma(t);
 
   // One pipeline step: make stage s resident (this wave's DMAs, then the
-  // barrier for everyone's), refill the ring slot freed by step s-1, expand
-  // packed weights (second barrier), then run the MFMAs of stage s.
+  // barrier for everyone's), expand packed weights (second barrier), then run
+  // the MFMAs of stage s while refilling the ring slot freed by step s-1.
   using T0 = std::integral_constant<int, 0>;
   using T1 = std::integral_constant<int, 1>;
   using ZF = std::true_type;
@@ -342,7 +359,6 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
                   const float* sw_f) {
     wait_stage(s);
     lds_barrier();
-    if (s + NS - 1 < KT) issue_dma(s + NS - 1);
     if constexpr (INT4) {
       unpack(s);
       lds_barrier();
@@ -351,7 +367,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
     // keep the (register-only) fold inside the MFMA region instead of letting
     // it be hoisted above the barriers
     __builtin_amdgcn_sched_barrier(0);
-    mfma_stage(s, set_c, zero_c, fold_c, fs_c, g_f, sw_f);
+    mfma_stage(s, s + NS - 1, set_c, zero_c, fold_c, fs_c, g_f, sw_f);
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -544,11 +560,25 @@ hipError_t launch_mfma(const GemmArgs& g, hipStream_t st) {
   return hipGetLastError();
 }
 
-// Tile choices: 256-row tiles when M fills them, else 128 x 128.
+// Workgroup rounds of a BM x BN tiling on the device's CUs times the tile
+// area: proportional to the run time of an MFMA-bound launch.
+int64_t tiling_cost(const GemmArgs& g, int bm, int bn) {
+  const int64_t tiles = (int64_t)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn);
+  const int64_t cus = ic_num_cus();
+  return (tiles + cus - 1) / cus * bm * bn;
+}
+
+// Tile choices: 256-row tiles when M fills them, else 128 x 128.  Per-row
+// W8A8 takes 256 x 192 where that fills the CUs in fewer tile-area rounds
+// than 256 x 256 (4096 x 3072: 256 tiles instead of 192 on 256 CUs).
 template <bool INT4, int GS, int OUT_DT, bool ACC>
 hipError_t pick_tile(const GemmArgs& g, hipStream_t st) {
   if constexpr (!INT4 && GS == 0) {
-    if (g.M > 128 && g.N > 128) return launch_mfma<Tile<256, 256, 2, 2, false, 0>, OUT_DT, ACC>(g, st);
+    if (g.M > 128 && g.N > 128) {
+      if (tiling_cost(g, 256, 192) < tiling_cost(g, 256, 256))
+        return launch_mfma<Tile<256, 192, 4, 2, false, 0>, OUT_DT, ACC>(g, st);
+      return launch_mfma<Tile<256, 256, 2, 2, false, 0>, OUT_DT, ACC>(g, st);
+    }
     return launch_mfma<Tile<128, 128, 2, 4, false, 0>, OUT_DT, ACC>(g, st);
   } else {
     if (g.M > 128) return launch_mfma<Tile<256, 128, 4, 3, INT4, GS>, OUT_DT, ACC>(g, st);

@@ -182,6 +182,18 @@ def test_w8a8_accumulators(rt, oracle, dev, M, N, K):
     assert np.array_equal(acc, oracle.gemm_acc(a.numpy(), w.numpy()))
 
 
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 256), (4096, 3072, 256), (4000, 3000, 384)])
+def test_w8a8_accumulators_full_grid(rt, dev, M, N, K):
+    """Shapes that fill the CUs with 256 x 256 tiles (4096^2) or 256 x 192
+    tiles (4096 x 3072, and ragged edges): int32 accumulators equal the exact
+    integer matmul, computed in float64 on the CPU (|acc| < 2^53)."""
+    a = _int8((M, K), 21)
+    w = _int8((N, K), 22)
+    acc = rt.gemm_acc_i32(a.to(dev), w.to(dev)).cpu()
+    ref = (a.double() @ w.double().T).to(torch.int64)
+    assert torch.equal(acc.to(torch.int64), ref)
+
+
 @pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
 @pytest.mark.parametrize("G", [1, "g128"])
 def test_w4a8_accumulators(rt, oracle, dev, M, N, K, G):
