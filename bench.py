@@ -52,6 +52,14 @@ CONFIGS = {
                         fmt="w4a16", M=1, K=3072, N=18432, rot=0, smoothrot=False, perm=False, G=24, act="bf16"),
     "c4mod_w8a8": dict(name="C4 modulation GEMV W8A8 3072->18432, M=1 (INT8 checkpoint)",
                        fmt="int8", M=1, K=3072, N=18432, rot=0, smoothrot=False, perm=False, G=1, act="bf16"),
+    # C5, Wan2.1-14B FFN down-projection: K 13824 rotated in 1024-blocks and
+    # padded to 14336 (the weights were quantized in the padded space)
+    "c5down_w4a8": dict(name="C5 Wan FFN-down W4A8 13824(->14336)->5120, M=32760, g128, R=1024",
+                        fmt="int4", M=32760, K_in=13824, K=14336, N=5120, rot=1024, smoothrot=False,
+                        perm=False, G=112, act="fp16", dist="student_t", cpu_rows=2048),
+    "c5down_w8a8": dict(name="C5 Wan FFN-down W8A8 13824(->14336)->5120, M=32760, R=1024",
+                        fmt="int8", M=32760, K_in=13824, K=14336, N=5120, rot=1024, smoothrot=False,
+                        perm=False, G=1, act="fp16", dist="student_t", cpu_rows=2048),
 }
 
 
@@ -75,8 +83,13 @@ def make_inputs(cfg, seed=0):
 
     g = torch.Generator().manual_seed(seed)
     M, K, N, G = cfg["M"], cfg["K"], cfg["N"], cfg["G"]
+    K_in = cfg.get("K_in", K)
     act = torch.float16 if cfg["act"] == "fp16" else torch.bfloat16
-    x = torch.randn(M, K, generator=g)
+    if cfg.get("dist") == "student_t":
+        torch.manual_seed(seed)  # torch.distributions draws from the global generator
+        x = torch.distributions.StudentT(4.0).sample((M, K_in))
+    else:
+        x = torch.randn(M, K_in, generator=g)
     if cfg["fmt"] == "int4" and cfg["name"].startswith("C3"):
         idx = torch.randperm(K, generator=g)[: K // 100]
         x[:, idx] *= 20.0
@@ -88,7 +101,7 @@ def make_inputs(cfg, seed=0):
     else:
         inp["w"] = torch.randint(0, 256, (N, K // 2), generator=g, dtype=torch.uint8)
         inp["s_w"] = (torch.rand(N, G, generator=g) * (2e-2 - 1e-3) + 1e-3).to(torch.float16).float()
-    inp["smoothrot"] = torch.exp(torch.randn(K, generator=g) * 0.5) if cfg["smoothrot"] else None
+    inp["smoothrot"] = torch.exp(torch.randn(K_in, generator=g) * 0.5) if cfg["smoothrot"] else None
     inp["perm"] = torch.randperm(K, generator=g) if cfg["perm"] else None
     return inp
 
@@ -96,10 +109,11 @@ def make_inputs(cfg, seed=0):
 def algorithmic(cfg):
     """(ops per GEMM launch, HBM bytes per GEMV launch, bytes per prep launch)."""
     M, K, N, G = cfg["M"], cfg["K"], cfg["N"], cfg["G"]
-    ops = 2.0 * M * N * K
+    K_in = cfg.get("K_in", K)
+    ops = 2.0 * M * N * K  # K = padded weight K (pad columns carry rotated data)
     wbytes = N * K if cfg["fmt"] == "int8" else N * K // 2
-    gemv_bytes = wbytes + 2 * N * G + 2 * M * K + 2 * M * N  # fp16 scales, 16-bit x and out
-    prep_bytes = M * K * 2 + M * K + 4 * M
+    gemv_bytes = wbytes + 2 * N * G + 2 * M * K_in + 2 * M * N  # fp16 scales, 16-bit x and out
+    prep_bytes = M * K_in * 2 + M * K + 4 * M
     return ops, gemv_bytes, prep_bytes
 
 
@@ -143,6 +157,7 @@ def gpu_bench(cfg, inp, steps, warmup, rt):
 
     dev = torch.device("cuda:0")
     M, K, N = cfg["M"], cfg["K"], cfg["N"]
+    K_in = cfg.get("K_in", K)
     act = inp["x"].dtype
     # enough copies that weights + activations exceed the 256 MB Infinity Cache
     per_copy = inp["x"].numel() * inp["x"].element_size() + inp["w"].numel() * inp["w"].element_size()
@@ -194,7 +209,8 @@ def cpu_baseline(cfg, inp):
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     M, K, N = cfg["M"], cfg["K"], cfg["N"]
-    x = inp["x"]
+    rows = min(M, cfg.get("cpu_rows", M))  # bounded sample: the first `rows` tokens
+    x = inp["x"][:rows]
     kw = dict(int4=cfg["fmt"] != "int8", smoothrot=inp["smoothrot"], rot_size=cfg["rot"], perm=inp["perm"])
     w = inp["w"].numpy()
     s_w = inp["s_w"].numpy()
@@ -205,9 +221,10 @@ def cpu_baseline(cfg, inp):
         oracle.reference_fallback_forward(x, w, s_w, K, **kw)
         ts.append(time.perf_counter() - t0)
     t = statistics.median(ts)
-    return {"value": round(2.0 * M * N * K / t / 1e12, 5), "unit": "TOPS", "cores": cores,
+    shape = "full shape" if rows == M else f"first {rows} of {M} tokens (throughput of the slice)"
+    return {"value": round(2.0 * rows * N * K / t / 1e12, 5), "unit": "TOPS", "cores": cores,
             "kind": "port", "seconds_per_call": round(t, 5),
-            "sample": f"{M}x{K} -> {N}, full shape, fp32 dequant + prep + F.linear per call "
+            "sample": f"{rows}x{cfg.get('K_in', K)} -> {N}, {shape}, fp32 dequant + prep + F.linear per call "
                       f"(the reference fallback re-dequantizes every forward), median of 3 after 1 warm-up"}
 
 
@@ -267,7 +284,8 @@ def main():
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(step_ms, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": cfg["act"] if is_fp else "int8", "data": "synthetic",
-        "config": {"workload": cfg["name"], "M": M, "K": K, "N": N, "group_size": K // cfg["G"],
+        "config": {"workload": cfg["name"], "M": M, "K_in": cfg.get("K_in", K), "K": K, "N": N,
+                   "group_size": K // cfg["G"],
                    "rot_size": cfg["rot"], "smoothrot": cfg["smoothrot"], "perm": cfg["perm"],
                    "activation": cfg["act"], "input_copies": copies, "parallelism": "single GPU"},
         "roofline": roof,

@@ -23,6 +23,7 @@ def _gen(seed):
 def _acts(M, K, dtype, seed, outliers=0.0, student_t=False):
     g = _gen(seed)
     if student_t:
+        torch.manual_seed(seed)  # torch.distributions samples from the global generator
         x = torch.distributions.StudentT(4.0).sample((M, K))
     else:
         x = torch.randn(M, K, generator=g)
@@ -238,6 +239,53 @@ def test_w4a8_output_formula(rt, oracle, dev, out_dtype, grouped, M, N, K):
     acc = oracle.gemm_acc(a.numpy(), oracle.unpack_int4(packed.numpy(), K), G)
     ref = oracle.epilogue(acc, s_a.numpy(), s_w.numpy(), bias.float().numpy(), DT[out_dtype])
     assert np.array_equal(out.float().cpu().numpy(), ref)
+
+
+C5_ROWS = [0, 1, 255, 256, 12345, 32511, 32512, 32759]  # tile edges and the last, partial tile
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_c5_full_size_prep_sampled_rows(rt, oracle, dev, dtype):
+    """Wan FFN-down activation prep at full size: 32760 rows of 13824 (1% of
+    channels x20), rotated in 1024-blocks and padded to 14336.  Rows are
+    independent, so sampled rows (first, last, tile edges) must equal the
+    oracle's prep and quantization bit for bit.  (Student-t rows are covered
+    at small M; sampling 4.5e8 of them on the CPU would dominate the test.)"""
+    M, K_in, K_w = 32760, 13824, 14336
+    x = _acts(M, K_in, dtype, seed=41, outliers=0.01)
+    q, s = rt.rotate_quantize(x.to(dev), rot_size=1024, w_in=K_w)
+    rows = torch.tensor(C5_ROWS)
+    y_ref = oracle.prepare(x[rows], DT[dtype], smoothrot=None, rot_size=1024, w_in=K_w, perm=None, smooth=None)
+    q_ref, s_ref = oracle.quantize(y_ref)
+    assert np.array_equal(s[rows.to(dev)].cpu().numpy(), s_ref)
+    assert np.array_equal(q[rows.to(dev)].cpu().numpy(), q_ref)
+
+
+@pytest.mark.parametrize("fmt", ["int4_g128", "int8"])
+def test_c5_full_size_gemm_sampled_rows(rt, oracle, dev, fmt):
+    """Wan FFN-down at its full size (M=32760, K_w=14336, N=5120; G=112 for
+    INT4): one launch of the production kernel, and the output rows at tile
+    edges and in the last partial M-tile equal the oracle's accumulators and
+    epilogue formula bit for bit."""
+    M, K, N = 32760, 14336, 5120
+    a = _int8((M, K), 31, -127, 128)
+    s_a = torch.rand(M, generator=_gen(32)) * 0.05 + 1e-3
+    if fmt == "int8":
+        w = _int8((N, K), 33, -127, 128)
+        s_w = (torch.rand(N, generator=_gen(34)) * 2e-3 + 1e-4).to(torch.float16).float()
+        out = rt.fused_int8_gemm_dequant(a.to(dev), w.to(dev), s_w.to(dev), s_a.to(dev),
+                                         out_dtype=torch.float16)
+        w_q, G = w.numpy(), 1
+    else:
+        G = K // 128
+        w = torch.randint(0, 256, (N, K // 2), generator=_gen(35), dtype=torch.uint8)
+        s_w = (torch.rand(N, G, generator=_gen(36)) * 2e-2 + 1e-3).to(torch.float16).float()
+        out = rt.gemm_w4a8(a.to(dev), w.to(dev), s_w.to(dev), s_a.to(dev), out_dtype=torch.float16)
+        w_q = oracle.unpack_int4(w.numpy(), K)
+    rows = torch.tensor(C5_ROWS)
+    acc = oracle.gemm_acc(a[rows].numpy(), w_q, G)
+    ref = oracle.epilogue(acc, s_a[rows].numpy(), s_w.numpy(), None, DT[torch.float16])
+    assert np.array_equal(out[rows.to(dev)].float().cpu().numpy(), ref)
 
 
 def test_w8a8_generic_kernel_matches(rt, dev):
