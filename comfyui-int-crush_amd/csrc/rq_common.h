@@ -55,3 +55,6 @@ constexpr int kFastMaxTiles = 4;  // fast path: K_w <= 16384
 // and fast_path_ok() are done by the caller.
 hipError_t ic_rq_fast_f16(const ic_rotq_args& a, hipStream_t st);
 hipError_t ic_rq_fast_bf16(const ic_rotq_args& a, hipStream_t st);
+// without SmoothRot factors or perm
+hipError_t ic_rq_fast_f16_plain(const ic_rotq_args& a, hipStream_t st);
+hipError_t ic_rq_fast_bf16_plain(const ic_rotq_args& a, hipStream_t st);

@@ -54,7 +54,10 @@ template <int DT> IC_DEV bool rn32_is_dt_boundary(float z) {
 }
 
 // Two workgroups per CU while the per-thread constants fit half the register
-// file (K_w <= 12288); wider rows keep one.
+// file (K_w <= 12288, or any width without SmoothRot factors and perm); wider
+// rows with factors or a perm keep one.  PLAIN kernels (no SmoothRot, no perm)
+// are separate instantiations: besides the registers, they drop the per-run
+// divide, its range checks and the gather's per-element LDS addressing.
 // LDS layouts (doubles in the exchange buffer, 16-bit values in the row
 // buffer).  Exchange slot of tile position p: 2 doubles of padding per 16
 // positions and 16 per 256.  Then the b128 row writes of 16 lanes hit 16
@@ -67,8 +70,8 @@ constexpr int kXbufDoubles = kTile + 2 * (kTile / 16) + 16 * (kTile / 256);
 IC_DEV int rbaddr(int p) { return p + 16 * (p >> 8); }
 template <int NT> constexpr int rowbuf_len() { return NT * kTile + 16 * (NT * kTile / 256); }
 
-template <int DT, int LOG4R, int NT>
-__global__ __launch_bounds__(kThreads, NT <= 3 ? 2 : 1) void rq_fast_kernel(
+template <int DT, int LOG4R, int NT, bool PLAIN>
+__global__ __launch_bounds__(kThreads, (NT <= 3 || PLAIN) ? 2 : 1) void rq_fast_kernel(
     const u16* __restrict__ x, int64_t ldx, int M, int K_in, int K_r,
     const float* __restrict__ sr_rcp, const float* __restrict__ sr_f, int K_w,
     const int32_t* __restrict__ perm, int8_t* __restrict__ q_out, int64_t ldq,
@@ -80,14 +83,16 @@ __global__ __launch_bounds__(kThreads, NT <= 3 ? 2 : 1) void rq_fast_kernel(
   __shared__ float red[kThreads / 64];
 
   const int t = threadIdx.x;
-  const bool has_sr = sr_rcp != nullptr;
-  const bool has_perm = perm != nullptr;
+  const bool has_sr = !PLAIN && sr_rcp != nullptr;
+  const bool has_perm = !PLAIN && perm != nullptr;
 
-  // ---- per-workgroup constants
-  float rc[NT][16];
-  uint32_t po[NT][8];
+  // ---- per-workgroup constants (not allocated by PLAIN kernels)
+  constexpr int NTC = PLAIN ? 1 : NT;
+  float rc[NTC][16];
+  uint32_t po[NTC][8];
 #pragma unroll
-  for (int c = 0; c < NT; ++c) {
+  for (int c = 0; c < NTC; ++c) {
+    if constexpr (PLAIN) break;
     const int p0 = c * kTile + 16 * t;
 #pragma unroll
     for (int j = 0; j < 16; ++j) rc[c][j] = 1.0f;
@@ -156,7 +161,7 @@ __global__ __launch_bounds__(kThreads, NT <= 3 ? 2 : 1) void rq_fast_kernel(
           bool nonfinite = false;
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
-            const float p = xs[j] * rc[c][j];
+            const float p = xs[j] * rc[PLAIN ? 0 : c][j];
             pmin = __builtin_fminf(pmin, __builtin_fabsf(p));
             if constexpr (DT == IC_DTYPE_BF16) nonfinite |= !__builtin_isfinite(p);
             xs[j] = round_to_dt<DT>(p);
@@ -167,7 +172,7 @@ __global__ __launch_bounds__(kThreads, NT <= 3 ? 2 : 1) void rq_fast_kernel(
               unpack8<DT>(xa, xo);
               unpack8<DT>(xb, xo + 8);
 #pragma unroll
-              for (int j = 0; j < 16; ++j) xs[j] = div_round_dt<DT>(xo[j], rc[c][j], sr_f, p0 + j);
+              for (int j = 0; j < 16; ++j) xs[j] = div_round_dt<DT>(xo[j], rc[PLAIN ? 0 : c][j], sr_f, p0 + j);
             } else {
 #pragma unroll
               for (int j = 0; j < 16; ++j) xs[j] = 0.0f;
@@ -271,8 +276,8 @@ __global__ __launch_bounds__(kThreads, NT <= 3 ? 2 : 1) void rq_fast_kernel(
         const char* rb = (const char*)rowbuf;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          vv[2 * i] = bits16_f32<DT>(*(const u16*)(rb + (po[c][i] & 0xffffu)));
-          vv[2 * i + 1] = bits16_f32<DT>(*(const u16*)(rb + (po[c][i] >> 16)));
+          vv[2 * i] = bits16_f32<DT>(*(const u16*)(rb + (po[PLAIN ? 0 : c][i] & 0xffffu)));
+          vv[2 * i + 1] = bits16_f32<DT>(*(const u16*)(rb + (po[PLAIN ? 0 : c][i] >> 16)));
         }
       } else {
         unpack8<DT>(*(const v4u*)(rowbuf + rbaddr(o0)), vv);
@@ -345,9 +350,9 @@ int persistent_grid(Kern kern, int64_t M) {
   return (int)(M < g ? M : g);
 }
 
-template <int DT, int LOG4R, int NT>
+template <int DT, int LOG4R, int NT, bool PLAIN>
 hipError_t launch_fast_t(const ic_rotq_args& a, hipStream_t st) {
-  auto kern = rq_fast_kernel<DT, LOG4R, NT>;
+  auto kern = rq_fast_kernel<DT, LOG4R, NT, PLAIN>;
   const int64_t K_r = LOG4R == 0 ? a.K_in : ((a.K_in + a.rot_size - 1) / a.rot_size) * a.rot_size;
   kern<<<dim3(persistent_grid(kern, a.M)), dim3(kThreads), 0, st>>>(
       (const u16*)a.x, a.ldx, (int)a.M, (int)a.K_in, (int)K_r, a.sr_rcp, a.sr_f, (int)a.K_w, a.perm,
@@ -355,18 +360,19 @@ hipError_t launch_fast_t(const ic_rotq_args& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <int DT, int LOG4R>
+template <int DT, int LOG4R, bool PLAIN>
 hipError_t launch_fast_nt(const ic_rotq_args& a, hipStream_t st) {
-  if (a.K_w <= kTile) return launch_fast_t<DT, LOG4R, 1>(a, st);
-  if (a.K_w <= 2 * kTile) return launch_fast_t<DT, LOG4R, 2>(a, st);
-  if (a.K_w <= 3 * kTile) return launch_fast_t<DT, LOG4R, 3>(a, st);
-  return launch_fast_t<DT, LOG4R, 4>(a, st);
+  if (a.K_w <= kTile) return launch_fast_t<DT, LOG4R, 1, PLAIN>(a, st);
+  if (a.K_w <= 2 * kTile) return launch_fast_t<DT, LOG4R, 2, PLAIN>(a, st);
+  if (a.K_w <= 3 * kTile) return launch_fast_t<DT, LOG4R, 3, PLAIN>(a, st);
+  return launch_fast_t<DT, LOG4R, 4, PLAIN>(a, st);
 }
 
-template <int DT>
+// PLAIN: no SmoothRot factors and no perm (the caller routes on that);
+// otherwise the kernels read both flags at run time.
+template <int DT, bool PLAIN>
 hipError_t launch_fast(const ic_rotq_args& a, hipStream_t st) {
-  if (a.rot_size == 0 && a.sr_rcp == nullptr && a.perm == nullptr && a.K_w == a.K_in &&
-      a.K_in <= 32 * 512) {
+  if (PLAIN && a.rot_size == 0 && a.K_w == a.K_in && a.K_in <= 32 * 512) {
     const unsigned grid = (unsigned)((a.M + 3) / 4);
     if (a.K_in <= 8 * 512)
       quant_wave_kernel<DT, 8><<<grid, kThreads, 0, st>>>((const u16*)a.x, a.ldx, (int)a.M, (int)a.K_in, a.q_out, a.ldq, a.s_out);
@@ -377,12 +383,12 @@ hipError_t launch_fast(const ic_rotq_args& a, hipStream_t st) {
     return hipGetLastError();
   }
   switch (a.rot_size) {
-    case 0: return launch_fast_nt<DT, 0>(a, st);
-    case 16: return launch_fast_nt<DT, 2>(a, st);
-    case 64: return launch_fast_nt<DT, 3>(a, st);
-    case 256: return launch_fast_nt<DT, 4>(a, st);
-    case 1024: return launch_fast_nt<DT, 5>(a, st);
-    case 4096: return launch_fast_nt<DT, 6>(a, st);
+    case 0: return launch_fast_nt<DT, 0, PLAIN>(a, st);
+    case 16: return launch_fast_nt<DT, 2, PLAIN>(a, st);
+    case 64: return launch_fast_nt<DT, 3, PLAIN>(a, st);
+    case 256: return launch_fast_nt<DT, 4, PLAIN>(a, st);
+    case 1024: return launch_fast_nt<DT, 5, PLAIN>(a, st);
+    case 4096: return launch_fast_nt<DT, 6, PLAIN>(a, st);
   }
   return hipErrorInvalidValue;
 }

@@ -1,0 +1,7 @@
+// Fast-path prep + quantize kernels for bf16 activations without SmoothRot
+// factors or perm (rotation, pad and quantization only).
+#include "rq_fast.h"
+
+hipError_t ic_rq_fast_bf16_plain(const ic_rotq_args& a, hipStream_t st) {
+  return launch_fast<IC_DTYPE_BF16, true>(a, st);
+}
