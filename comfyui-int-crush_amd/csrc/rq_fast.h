@@ -303,30 +303,51 @@ __global__ __launch_bounds__(kThreads) void quant_wave_kernel(
   if (row >= M) return;  // wave-uniform
   const u16* xrow = x + (int64_t)row * ldx;
   const int nch = (K + 511) >> 9;  // 512-value chunks (uniform); only the last may be partial
+  // Up to 8 chunks the early-exit loops keep the row in a few registers;
+  // wider rows use uniform guards instead, so every array index stays a
+  // compile-time constant and the row is not demoted to scratch memory.
   v4u a[MAXCH];
-#pragma unroll
-  for (int i = 0; i < MAXCH; ++i) {
-    if (i >= nch) break;
-    const int e = min((i * 64 + lane) * 8, K - 8);
-    a[i] = *(const v4u*)(xrow + e);
-  }
   float m = 0.0f;
+  if constexpr (MAXCH <= 8) {
 #pragma unroll
-  for (int i = 0; i < MAXCH; ++i) {
-    if (i >= nch) break;
-    float v[8];
-    unpack8<DT>(a[i], v);
+    for (int i = 0; i < MAXCH; ++i) {
+      if (i >= nch) break;
+      const int e = min((i * 64 + lane) * 8, K - 8);
+      a[i] = *(const v4u*)(xrow + e);
+    }
 #pragma unroll
-    for (int k = 0; k < 8; ++k) m = __builtin_fmaxf(m, __builtin_fabsf(v[k]));
+    for (int i = 0; i < MAXCH; ++i) {
+      if (i >= nch) break;
+      float v[8];
+      unpack8<DT>(a[i], v);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) m = __builtin_fmaxf(m, __builtin_fabsf(v[k]));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < MAXCH; ++i) {
+      a[i] = v4u{0, 0, 0, 0};
+      if (i < nch) {
+        const int e = min((i * 64 + lane) * 8, K - 8);
+        a[i] = *(const v4u*)(xrow + e);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < MAXCH; ++i) {
+      if (i < nch) {
+        float v[8];
+        unpack8<DT>(a[i], v);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) m = __builtin_fmaxf(m, __builtin_fabsf(v[k]));
+      }
+    }
   }
   m = wave_max(m);
   const float s = quant_scale(m);
   const double rs = 1.0 / (double)s;
   if (lane == 0) s_out[row] = s;
   int8_t* qrow = q_out + (int64_t)row * ldq;
-#pragma unroll
-  for (int i = 0; i < MAXCH; ++i) {
-    if (i >= nch) break;
+  auto quant_chunk = [&](int i) {
     const int e = (i * 64 + lane) * 8;
     float v[8];
     unpack8<DT>(a[i], v);
@@ -335,6 +356,17 @@ __global__ __launch_bounds__(kThreads) void quant_wave_kernel(
     const uint32_t w1 = pack4_lo_bytes(quant_code_nc(v[4], rs), quant_code_nc(v[5], rs),
                                        quant_code_nc(v[6], rs), quant_code_nc(v[7], rs));
     if (e < K) *(v2u*)(qrow + e) = v2u{w0, w1};
+  };
+  if constexpr (MAXCH <= 8) {
+#pragma unroll
+    for (int i = 0; i < MAXCH; ++i) {
+      if (i >= nch) break;
+      quant_chunk(i);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < MAXCH; ++i)
+      if (i < nch) quant_chunk(i);
   }
 }
 

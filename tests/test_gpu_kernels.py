@@ -68,7 +68,7 @@ def test_unpack_int4_to_float(rt, oracle, dev, dtype, G):
 
 # ------------------------------------------------------------------ quantize
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("K", [64, 1000, 4096, 12288, 20480])
+@pytest.mark.parametrize("K", [64, 1000, 4096, 6144, 12288, 20480])
 def test_dynamic_quantize(rt, oracle, dev, dtype, K):
     if dtype == torch.float32 and K > 8192 and K < 16384:
         K = 8192
