@@ -33,69 +33,9 @@
 //     while the MFMAs of group g+1 execute.
 #include <type_traits>
 
-#include "ic_common.h"
+#include "gemm_common.h"
 
 namespace {
-
-constexpr int kNT = 512;  // threads per workgroup
-constexpr int kBK = 128;  // K bytes per stage
-
-typedef __attribute__((address_space(3))) char lds_char;
-
-// LDS rows of 128 bytes hold 8 chunks of 16 bytes, the chunk index XOR-swizzled
-// by row: the MFMA fragment reads (32 consecutive rows at chunk c and c+1) then
-// run at the full ds_read_b128 rate on gfx950.
-IC_DEV int swz(int row) { return (row >> 1) & 7; }
-IC_DEV int lds_off(int row, int chunk) { return row * kBK + ((chunk ^ swz(row)) << 4); }
-
-// Global -> LDS DMA of 16 (or 4) bytes per lane, from sbase + voff (a
-// wave-uniform 64-bit base and a per-lane 32-bit byte offset) to M0 + 16*lane
-// (4*lane).  Issued from inline assembly so that the compiler neither tracks
-// it nor orders LDS accesses behind it; completion is waited for explicitly
-// with wait_vm before the workgroup barrier that publishes the stage.  M0 holds
-// no compiler value in these kernels (gfx950 LDS instructions do not use it).
-IC_DEV void dma16(uint32_t voff, const void* sbase, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(sbase)
-               : "memory", "m0");
-}
-IC_DEV void dma4(uint32_t voff, const void* sbase, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(voff), "s"(sbase)
-               : "memory", "m0");
-}
-
-// Block until at most N vector-memory operations of this wave are outstanding
-// (they retire in issue order).
-template <int N> IC_DEV void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-IC_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
-// 8 INT4 nibbles (low nibble = even k) -> 8 int8 values 16*q in natural k order.
-IC_DEV void unpack8_x16(uint32_t P, uint32_t& w0, uint32_t& w1) {
-  const uint32_t lo = (P << 4) & 0xf0f0f0f0u;  // bytes: 16*q[k=0,2,4,6]
-  const uint32_t hi = P & 0xf0f0f0f0u;         // bytes: 16*q[k=1,3,5,7]
-  w0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);  // q0 q1 q2 q3
-  w1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // q4 q5 q6 q7
-}
-
-// Logical tile id for hardware block id b.  Consecutive block ids are spread
-// round-robin over the 8 XCDs; renumber so each XCD works on a contiguous run
-// of logical tiles, then walk the run in GROUP_M-row bands so neighbouring
-// tiles share A rows and B columns in that XCD's L2.
-IC_DEV void tile_coords(int b, int nb, int tiles_m, int tiles_n, int& tm, int& tn) {
-  const int xcd = b & 7, local = b >> 3;
-  const int per = nb >> 3, rem = nb & 7;
-  const int L = xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
-  constexpr int GM = 8;
-  const int in_group = GM * tiles_n;
-  const int group = L / in_group;
-  const int first_m = group * GM;
-  const int gsize = min(tiles_m - first_m, GM);
-  const int r = L - group * in_group;
-  tm = first_m + r % gsize;
-  tn = r / gsize;
-}
 
 // Tile configuration: BM x BN output tile, WGM wave rows, NS-deep LDS ring.
 template <int BM_, int BN_, int WGM_, int NS_, bool INT4_, int GS_>

@@ -2,42 +2,33 @@
 //
 // Replaces unpack_int4_to_float16 (triton_int4_unpack.py:25-88) followed by the
 // cuBLAS F.linear of _forward_int4_w4a16 (_ops.py:466-481): the dequantized
-// weight w[n,k] = RN_dt(q[n,k] * RN_dt(s[n, k/gs])) is produced in the
-// global->LDS copy and consumed by v_mfma_f32_32x32x16_{f16,bf16}; it is never
-// written to HBM.  For fp16 this is bit-identical to the reference unpack
-// (an fp16 product of two fp16 values); the reference rejects bf16 here and
-// its PyTorch fallback rounds q*s to the activation type, which is what bf16
-// does.  Accumulation is fp32 in the MFMA; the epilogue adds the bias (the
-// reference drops it on this path) and rounds to the activation type.
+// weight w[n,k] = RN_dt(q[n,k] * RN_dt(s[n, k/gs])) is produced in LDS and
+// consumed by v_mfma_f32_32x32x16_{f16,bf16}; it is never written to HBM.  For
+// fp16 this is bit-identical to the reference unpack (an fp16 product of two
+// fp16 values); the reference rejects bf16 here and its PyTorch fallback
+// rounds q*s to the activation type, which is what bf16 does.  Accumulation is
+// fp32 in the MFMA; the epilogue adds the bias (the reference drops it on this
+// path) and rounds to the activation type.
+//
+// The pipeline is the one of the INT8 GEMM (gemm_i8.hip, shared pieces in
+// gemm_common.h): 512-thread workgroups, a 256 x 256 output tile, an NS-deep
+// LDS ring filled by inline-assembly global->LDS DMAs issued in slices between
+// the MFMA K-steps, explicit vmcnt waits.  One stage is 64 K values: a 128-byte
+// row of 16-bit activations, 32 bytes of packed weights per output column and
+// the fp32 scale of the stage's group per column.  Once per stage the
+// workgroup dequantizes the packed tile into a 16-bit LDS tile with the same
+// swizzled row layout as the activations (two or three VALU instructions per
+// weight with packed 16-bit math), then every wave runs its MFMAs from LDS.
 //
 // Also provides the standalone unpack kernels (INT4->int8 and INT4->fp16/bf16),
 // triton_int4_to_int8_unpack.py:26-81 and triton_int4_unpack.py:25-88.
-#include <type_traits>
-
-#include "ic_common.h"
+#include "gemm_common.h"
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kRowBytes = 64;  // 32 fp16 K values per LDS row per stage
-
-// 16-byte chunks XOR-swizzled by (row >> 2): conflict-free ds_read_b128 for
-// 32-row MFMA fragments on gfx950.
-IC_DEV int lds_off(int row, int chunk) { return row * kRowBytes + ((chunk ^ ((row >> 2) & 3)) << 4); }
-
-IC_DEV void tile_coords(int b, int nb, int tiles_m, int tiles_n, int& tm, int& tn) {
-  const int xcd = b & 7, local = b >> 3;
-  const int per = nb >> 3, rem = nb & 7;
-  const int L = xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
-  constexpr int GM = 8;
-  const int in_group = GM * tiles_n;
-  const int group = L / in_group;
-  const int first_m = group * GM;
-  const int gsize = min(tiles_m - first_m, GM);
-  const int r = L - group * in_group;
-  tm = first_m + r % gsize;
-  tn = r / gsize;
-}
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef float v2f __attribute__((ext_vector_type(2)));
 
 IC_DEV int nib(uint32_t w, int i) {  // i-th nibble (low nibble first), two's complement
   const int v = (w >> (4 * i)) & 0xf;
@@ -53,74 +44,175 @@ template <int DT> IC_DEV u16 deq1_bits(int q, float s) {
   if constexpr (DT == IC_DTYPE_F16) return __builtin_bit_cast(u16, (_Float16)((_Float16)q * (_Float16)s));
   else return f32_to_bf16((float)q * bf16_to_f32(f32_to_bf16(s)));
 }
-// Dequantize 8 nibbles of one packed dword to 8 values of type DT (bits).
-template <int DT> IC_DEV void deq8(uint32_t P, float s, u16* out) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) out[i] = deq1_bits<DT>(nib(P, i), s);
+
+// Per-column dequantization constants of one stage: f16 keeps the pair
+// (RN_f16(s), RN_f16(s)); bf16 keeps sb = RN_bf16(s) and -8 * sb (exact).
+struct DeqScale {
+  uint32_t s2;    // f16: two copies of RN_f16(s)
+  float sb, m8s;  // bf16
+};
+template <int DT> IC_DEV DeqScale deq_scale(float s) {
+  DeqScale d;
+  if constexpr (DT == IC_DTYPE_F16) {
+    const uint32_t h = __builtin_bit_cast(u16, (_Float16)s);
+    d.s2 = h | (h << 16);
+    d.sb = d.m8s = 0.0f;
+  } else {
+    d.s2 = 0;
+    d.sb = bf16_to_f32(f32_to_bf16(s));
+    d.m8s = -8.0f * d.sb;
+  }
+  return d;
 }
 
-template <int BM, int BN, int DT>
-__global__ __launch_bounds__(kThreads, 1) void gemm_w4a16_kernel(
+// Dequantize 8 INT4 values (one packed dword, low nibble = even k) to 8 16-bit
+// values of type DT in natural k order (4 dwords, two values each).
+//   u = q + 8 in [0, 15] is the nibble with its sign bit flipped.
+//   f16:  the halves 0x6400 | u are the f16 numbers 1024 + u; subtracting 1032
+//         gives q exactly, and one f16 multiply by RN_f16(s) rounds q*s once.
+//   bf16: u as f32, fma(u, sb, -8*sb) = q*sb exactly (12 significant bits),
+//         then one RN-even conversion to bf16.
+template <int DT> IC_DEV void deq8(uint32_t P, const DeqScale& d, uint32_t* o) {
+  const uint32_t t = (P & 0x0f0f0f0fu) ^ 0x08080808u;         // u of k = 0, 2, 4, 6
+  const uint32_t h = ((P >> 4) & 0x0f0f0f0fu) ^ 0x08080808u;  // u of k = 1, 3, 5, 7
+  const uint32_t e = __builtin_amdgcn_perm(h, t, 0x05010400u);  // u0 u1 u2 u3
+  const uint32_t f = __builtin_amdgcn_perm(h, t, 0x07030602u);  // u4 u5 u6 u7
+  if constexpr (DT == IC_DTYPE_F16) {
+    const uint32_t c64 = 0x64646464u;
+    const uint32_t w[4] = {__builtin_amdgcn_perm(c64, e, 0x04010400u), __builtin_amdgcn_perm(c64, e, 0x04030402u),
+                           __builtin_amdgcn_perm(c64, f, 0x04010400u), __builtin_amdgcn_perm(c64, f, 0x04030402u)};
+    const v2h sc = __builtin_bit_cast(v2h, d.s2);
+    const v2h off = {(_Float16)1032.0f, (_Float16)1032.0f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(v2h, w[i]) - off) * sc);
+  } else {
+    const uint32_t u[2] = {e, f};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float a = __builtin_fmaf((float)((u[i] >> (16 * j)) & 0xffu), d.sb, d.m8s);
+        const float b = __builtin_fmaf((float)((u[i] >> (16 * j + 8)) & 0xffu), d.sb, d.m8s);
+        o[2 * i + j] = __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f){a, b}, v2bf));
+      }
+    }
+  }
+}
+
+// W4A16 tile: BM x BN outputs, WGM wave rows, NS-deep ring of 64-K stages.
+template <int BM_, int BN_, int WGM_, int NS_>
+struct WTile {
+  static constexpr int BM = BM_, BN = BN_, WGM = WGM_, NS = NS_;
+  static constexpr int A_BYTES = BM * kBK;  // 64 16-bit activations per row
+  static constexpr int B_BYTES = BN * 32;   // 64 packed INT4 weights per column
+  static constexpr int S_BYTES = BN * 4;    // fp32 scale of the stage's group per column
+  static constexpr int SLOT = A_BYTES + B_BYTES + S_BYTES;
+  static constexpr int BU_BYTES = BN * kBK;  // dequantized 16-bit weights
+  static constexpr int EPI_RS = BN + 8;      // output staging row stride (elements)
+  static constexpr size_t epi_bytes() { return (size_t)BM * EPI_RS * 2 + (size_t)BN * 4; }
+  static constexpr size_t ring_bytes() { return (size_t)NS * SLOT + (size_t)BU_BYTES; }
+  static constexpr size_t lds_bytes() { return ring_bytes() > epi_bytes() ? ring_bytes() : epi_bytes(); }
+};
+
+template <class TL, int DT>
+__global__ __launch_bounds__(kNT, 1) void gemm_w4a16_kernel(
     const u16* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
     const float* __restrict__ s_w, int G, int gsize, const void* __restrict__ bias, int bias_dt,
     u16* __restrict__ C, int64_t ldc, int M, int N, int K) {
-  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int BM = TL::BM, BN = TL::BN, WGM = TL::WGM, NS = TL::NS;
+  constexpr int WGN = 8 / WGM;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int A_CH = BM * 4 / kThreads;  // 16-byte chunks (8 values) per thread
-  constexpr int B_CH = BN / kThreads;      // one packed 16-byte chunk (32 values) per B row
-  constexpr int STAGE = (BM + BN) * kRowBytes;
-  static_assert(TM >= 1 && TN >= 1 && A_CH >= 1 && B_CH >= 1, "tile too small");
+  constexpr int A_DMA = BM / 64;         // 1 KB DMA blocks of A per wave per stage
+  constexpr int B_DMA = BN * 32 / 8192;  // same for the packed weights
+  constexpr int S_WAVES = BN / 64;       // waves issuing one scale DMA per stage
+  constexpr int D = A_DMA + B_DMA;
+  constexpr int kParts = 4;              // DMA slices per stage (one per MFMA K-step)
+  static_assert(TM >= 1 && TN >= 1 && A_DMA >= 1 && B_DMA >= 1 && BN * 32 % 8192 == 0, "tile shape");
+  static_assert(BN * 32 == kNT * 16, "one packed 16-byte chunk per thread and stage");
+  static_assert(NS >= 2 && S_WAVES <= 8, "ring depth");
+
   extern __shared__ __attribute__((aligned(16))) char smem[];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_char*)smem;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int wr = wave >> 1, wc = wave & 1;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = wave / WGN, wc = wave % WGN;
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   int tm, tn;
   tile_coords(blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int KT = K / 32;
+  const int KT = K / 64;
+  const bool s_wave = wave < S_WAVES;
 
-  v4u ra[A_CH], rb[B_CH];
-  float rs[B_CH];
-  auto gload = [&](int kt) {
-    const int k0 = kt * 32;
+  // ---- DMA addressing.  A: lane L of a 1 KB block covers LDS row 8*blk + L/8,
+  // chunk slot L%8, and loads global chunk (L%8) ^ swz(row).  Packed B: 32
+  // rows of 32 bytes per block.  Scales: one dword per lane, column
+  // n0 + 64*wave + lane of the stage's group.
+  const int64_t lda_b = lda * 2;
+  uint32_t a_off[A_DMA];
 #pragma unroll
-    for (int c = 0; c < A_CH; ++c) {
-      const int q = tid + kThreads * c;
-      const int row = min(m0 + (q >> 2), M - 1);
-      ra[c] = *(const v4u*)(A + (int64_t)row * lda + k0 + (q & 3) * 8);
-    }
+  for (int c = 0; c < A_DMA; ++c) {
+    const int row = 8 * (wave + 8 * c) + (lane >> 3);
+    a_off[c] = (uint32_t)(min(row, M - 1 - m0) * lda_b + (((lane & 7) ^ swz(row)) << 4));
+  }
+  uint32_t b_off[B_DMA];
 #pragma unroll
-    for (int c = 0; c < B_CH; ++c) {
-      const int row = min(n0 + tid + kThreads * c, N - 1);
-      rb[c] = *(const v4u*)(B + (int64_t)row * ldb + (k0 >> 1));
-      rs[c] = s_w[(int64_t)row * G + (G > 1 ? k0 / gsize : 0)];
+  for (int c = 0; c < B_DMA; ++c) {
+    const int row = 32 * (wave + 8 * c) + (lane >> 1);
+    b_off[c] = (uint32_t)(min(row, N - 1 - n0) * ldb + ((lane & 1) << 4));
+  }
+  const uint32_t s_off = (uint32_t)(min(64 * wave + lane, N - 1 - n0) * G * 4);
+  const char* a_base = (const char*)(A + (int64_t)m0 * lda);
+  const uint8_t* b_base = B + (int64_t)n0 * ldb;
+  const float* s_base = s_w + (int64_t)n0 * G;
+
+  auto issue_dma_part = [&](int kt, int part) {
+    const uint32_t slot = lds0 + (uint32_t)((kt % NS) * TL::SLOT);
+    const char* ab = a_base + (int64_t)kt * kBK;
+#pragma unroll
+    for (int c = 0; c < A_DMA; ++c)
+      if (c % kParts == part) dma16(a_off[c], ab, slot + (uint32_t)((wave + 8 * c) * 1024));
+    const uint8_t* bb = b_base + (int64_t)kt * 32;
+#pragma unroll
+    for (int c = 0; c < B_DMA; ++c)
+      if ((A_DMA + c) % kParts == part) dma16(b_off[c], bb, slot + (uint32_t)(TL::A_BYTES + (wave + 8 * c) * 1024));
+    if (part == kParts - 1 && s_wave) {
+      const int g = G > 1 ? (kt * 64) / gsize : 0;
+      dma4(s_off, s_base + g, slot + (uint32_t)(TL::A_BYTES + TL::B_BYTES + wave * 256));
     }
   };
-  auto sstore = [&](int buf) {
-    char* sA = smem + buf * STAGE;
-    char* sB = sA + BM * kRowBytes;
+  auto issue_dma = [&](int kt) {
 #pragma unroll
-    for (int c = 0; c < A_CH; ++c) {
-      const int q = tid + kThreads * c;
-      *(v4u*)(sA + lds_off(q >> 2, q & 3)) = ra[c];
-    }
-#pragma unroll
-    for (int c = 0; c < B_CH; ++c) {
-      const int row = tid + kThreads * c;
-      const uint32_t pw[4] = {rb[c].x, rb[c].y, rb[c].z, rb[c].w};
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        u16 h[8];
-        deq8<DT>(pw[d], rs[c], h);
-        v4u o;
-        o.x = h[0] | ((uint32_t)h[1] << 16);
-        o.y = h[2] | ((uint32_t)h[3] << 16);
-        o.z = h[4] | ((uint32_t)h[5] << 16);
-        o.w = h[6] | ((uint32_t)h[7] << 16);
-        *(v4u*)(sB + lds_off(row, d)) = o;
+    for (int p = 0; p < kParts; ++p) issue_dma_part(kt, p);
+  };
+  auto wait_stage = [&](int s) {
+    if constexpr (NS > 2) {
+      if (s + NS - 2 < KT) {
+        if (s_wave) wait_vm<(D + 1) * (NS - 2)>();
+        else wait_vm<D * (NS - 2)>();
+        return;
       }
+    }
+    wait_vm<0>();
+  };
+
+  // ---- packed INT4 -> 16-bit weights in LDS, 32 values per thread (one
+  // barrier at the top of each step orders the MFMA reads of step s-1 before
+  // the dequantization of step s)
+  auto dequant = [&](int kt) {
+    const char* slot = smem + (kt % NS) * TL::SLOT;
+    const int row = tid >> 1, part = tid & 1;
+    const v4u p = *(const v4u*)(slot + TL::A_BYTES + tid * 16);
+    const DeqScale d = deq_scale<DT>(((const float*)(slot + TL::A_BYTES + TL::B_BYTES))[row]);
+    char* bu = smem + NS * TL::SLOT;
+    const uint32_t pw[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t o[4];
+      deq8<DT>(pw[i], d, o);
+      *(v4u*)(bu + lds_off(row, 4 * part + i)) = v4u{o[0], o[1], o[2], o[3]};
     }
   };
 
@@ -130,13 +222,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_w4a16_kernel(
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = v16f{};
 
-  auto compute = [&](int buf) {
-    const char* sA = smem + buf * STAGE;
-    const char* sB = sA + BM * kRowBytes;
+  auto mfma_stage = [&](int kt, int dma_kt) {
+    const char* sA = smem + (kt % NS) * TL::SLOT;
+    const char* sB = smem + NS * TL::SLOT;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int ch = 2 * ks + (lane >> 5);
+    for (int ks = 0; ks < 4; ++ks) {
       v4u a[TM], b[TN];
+      const int ch = 2 * ks + (lane >> 5);
 #pragma unroll
       for (int i = 0; i < TM; ++i) a[i] = *(const v4u*)(sA + lds_off(wr * WM + i * 32 + (lane & 31), ch));
 #pragma unroll
@@ -152,19 +244,59 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_w4a16_kernel(
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a[i]),
                                                                 __builtin_bit_cast(v8bf, b[j]), acc[i][j], 0, 0, 0);
         }
+      if (dma_kt < KT) issue_dma_part(dma_kt, ks);
     }
   };
 
-  gload(0);
-  sstore(0);
-  __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    if (kt + 1 < KT) gload(kt + 1);
-    compute(kt & 1);
-    if (kt + 1 < KT) sstore((kt + 1) & 1);
-    __syncthreads();
+  // ---- prologue: NS-1 stages in flight; then one step per stage: make it
+  // resident, dequantize its weights, run its MFMAs while refilling the slot
+  // freed by the previous step
+#pragma unroll
+  for (int t = 0; t < NS - 1; ++t)
+    if (t < KT) issue_dma(t);
+  for (int s = 0; s < KT; ++s) {
+    wait_stage(s);
+    lds_barrier();
+    dequant(s);
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_stage(s, s + NS - 1);
+    __builtin_amdgcn_sched_barrier(0);
   }
 
+  // ---- epilogue: v = acc (+ bias), rounded once to DT
+  if ((((uintptr_t)C) & 15) == 0 && (ldc & 7) == 0 && (N & 7) == 0) {
+    // stage the tile through LDS row-major, then write whole rows with 16-byte stores
+    constexpr int RS = TL::EPI_RS;
+    lds_barrier();  // every wave is done with the last stage
+    u16* ot = (u16*)smem;
+    float* b_l = (float*)(smem + BM * RS * 2);
+    for (int t = tid; t < BN; t += kNT) b_l[t] = bias != nullptr ? ld_any_f32(bias, bias_dt, min(n0 + t, N - 1)) : 0.0f;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int nl = wc * WN + j * 32 + (lane & 31);
+      const float b = b_l[nl];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int ml = wr * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          float v = acc[i][j][r];
+          if (bias != nullptr) v = v + b;
+          ot[ml * RS + nl] = DT == IC_DTYPE_F16 ? f32_to_f16(v) : f32_to_bf16(v);
+        }
+    }
+    __syncthreads();
+    constexpr int CPR = BN / 8;  // 16-byte chunks per tile row
+#pragma unroll 4
+    for (int c = tid; c < BM * CPR; c += kNT) {
+      const int row = c / CPR, col = (c % CPR) * 8;
+      const int m = m0 + row, n = n0 + col;
+      if (m < M && n < N) *(v4u*)(C + (int64_t)m * ldc + n) = *(const v4u*)(ot + row * RS + col);
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int n = n0 + wc * WN + j * 32 + (lane & 31);
@@ -201,14 +333,21 @@ __global__ __launch_bounds__(256) void gemm_w4a16_generic_kernel(
   st_from_f32<DT>(C, (int64_t)m * ldc + n, acc);
 }
 
-template <int BM, int BN, int DT>
+template <class TL, int DT>
 hipError_t launch_w4a16(const u16* A, int64_t lda, const uint8_t* B, int64_t ldb, const float* s_w,
                         int G, int gsize, const void* bias, int bias_dt, u16* C, int64_t ldc, int M,
                         int N, int K, hipStream_t st) {
-  const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  const size_t shm = 2 * (BM + BN) * kRowBytes;
-  gemm_w4a16_kernel<BM, BN, DT><<<dim3(tiles), dim3(kThreads), shm, st>>>(A, lda, B, ldb, s_w, G, gsize,
-                                                                          bias, bias_dt, C, ldc, M, N, K);
+  const int tiles = ((M + TL::BM - 1) / TL::BM) * ((N + TL::BN - 1) / TL::BN);
+  const size_t shm = TL::lds_bytes();
+  static_assert(TL::lds_bytes() <= 160 * 1024, "LDS budget");
+  auto kern = gemm_w4a16_kernel<TL, DT>;
+  static bool attr_set = false;  // idempotent attribute; benign if raced
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  kern<<<dim3(tiles), dim3(kNT), shm, st>>>(A, lda, B, ldb, s_w, G, gsize, bias, bias_dt, C, ldc, M, N, K);
   return hipGetLastError();
 }
 
@@ -217,8 +356,8 @@ hipError_t run_w4a16(const u16* A, int64_t lda, const uint8_t* B, int64_t ldb, c
                      int gsize, const void* bias, int bias_dt, u16* C, int64_t ldc, int M, int N, int K,
                      bool mfma_ok, hipStream_t st) {
   if (mfma_ok) {
-    if (M >= 256 && N >= 256) return launch_w4a16<256, 256, DT>(A, lda, B, ldb, s_w, G, gsize, bias, bias_dt, C, ldc, M, N, K, st);
-    return launch_w4a16<128, 256, DT>(A, lda, B, ldb, s_w, G, gsize, bias, bias_dt, C, ldc, M, N, K, st);
+    if (M > 128) return launch_w4a16<WTile<256, 256, 2, 3>, DT>(A, lda, B, ldb, s_w, G, gsize, bias, bias_dt, C, ldc, M, N, K, st);
+    return launch_w4a16<WTile<128, 256, 2, 4>, DT>(A, lda, B, ldb, s_w, G, gsize, bias, bias_dt, C, ldc, M, N, K, st);
   }
   dim3 grid((unsigned)((N + 255) / 256), (unsigned)M);
   gemm_w4a16_generic_kernel<DT><<<grid, dim3(256), 0, st>>>(A, lda, B, ldb, s_w, G, gsize, bias, bias_dt, C, ldc, M, N, K);
@@ -267,8 +406,11 @@ int ic_gemm_w4a16(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, c
   if (ic_gemv_applicable(M, K, x, ldx * 2, w_packed, ldw) && (num_groups == 1 || (K / num_groups) % 32 == 0))
     return ic_gemv_w4a16(x, dtype, M, K, ldx, w_packed, N, ldw, s_w, num_groups, bias, bias_dtype, out, ldo, stream);
   const int G = (int)num_groups, gsize = (int)(K / num_groups);
-  const bool mfma_ok = (K % 32 == 0) && (G == 1 || gsize % 32 == 0) && !((uintptr_t)x & 15) &&
-                       !((uintptr_t)w_packed & 15) && !((ldx * 2) & 15) && !(ldw & 15);
+  // DMA pipeline: 64-K stages, scale groups of whole stages, 16-byte aligned
+  // rows; 32-bit DMA offsets within one tile
+  const bool mfma_ok = (K % 64 == 0) && (G == 1 || gsize % 64 == 0) && !((uintptr_t)x & 15) &&
+                       !((uintptr_t)w_packed & 15) && !((ldx * 2) & 15) && !(ldw & 15) &&
+                       256 * ldx * 2 < (1LL << 31) && 256 * ldw < (1LL << 31) && N * G * 4 < (1LL << 31);
   hipStream_t st = (hipStream_t)stream;
   hipError_t e = dtype == IC_DTYPE_F16
                      ? run_w4a16<IC_DTYPE_F16>((const u16*)x, ldx, w_packed, ldw, s_w, G, gsize, bias, bias_dtype,

@@ -322,6 +322,45 @@ def test_w4a16_vs_fp32(rt, oracle, dev, dtype, G):
     assert _cos(out, ref) >= 0.9999
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("grouped", [False, True])
+@pytest.mark.parametrize("M,N", [(512, 300), (512, 264), (100, 264)])
+def test_w4a16_dequant_bit_exact_one_hot(rt, oracle, dev, dtype, grouped, M, N):
+    """x = one-hot rows (row m selects k = m): each output is a single product
+    1 * w[n, m] accumulated in fp32 and rounded to the activation type, so the
+    GEMM output equals the kernel's in-LDS dequantized weight, which must be
+    RN_dt(q * RN_dt(s)) bit for bit.  N = 300 takes the direct epilogue, N = 264
+    the LDS-staged one; M = 100 the 128-row tile."""
+    K = 512
+    G = K // 128 if grouped else 1
+    x = torch.zeros(M, K, dtype=dtype)
+    x[torch.arange(M), torch.arange(M) % K] = 1
+    packed = torch.randint(0, 256, (N, K // 2), generator=_gen(24), dtype=torch.uint8)
+    s_w = (torch.rand(N, G, generator=_gen(25)) * 2e-2 + 1e-3).to(torch.float16).float()
+    out = rt.gemm_w4a16(x.to(dev), packed.to(dev), s_w.to(dev)).float().cpu().numpy()
+    w = oracle.dequant_w4a16(packed.numpy(), s_w.numpy(), K, DT[dtype])  # [N, K]
+    assert np.array_equal(out, w[:, np.arange(M) % K].T)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_w4a16_full_size_c2_sampled_rows(rt, oracle, dev, dtype):
+    """C2 at full size (M=4608, K=3072, N=12288, g128): one launch; sampled
+    rows (tile edges, last tile) within fp32-accumulation tolerance of the
+    dequantized-weight product computed on the CPU."""
+    M, K, N, G = 4608, 3072, 12288, 24
+    x = _acts(M, K, dtype, seed=26)
+    packed = torch.randint(0, 256, (N, K // 2), generator=_gen(27), dtype=torch.uint8)
+    s_w = (torch.rand(N, G, generator=_gen(28)) * 2e-2 + 1e-3).to(torch.float16).float()
+    out = rt.gemm_w4a16(x.to(dev), packed.to(dev), s_w.to(dev))
+    rows = torch.tensor([0, 1, 255, 256, 2000, 4351, 4352, 4607])
+    w = torch.from_numpy(oracle.dequant_w4a16(packed.numpy(), s_w.numpy(), K, DT[dtype]))
+    ref = x[rows].float() @ w.t()
+    got = out[rows.to(dev)].float().cpu()
+    tol = 1e-2 if dtype == torch.float16 else 2e-2
+    assert torch.allclose(got, ref, rtol=tol, atol=tol * ref.abs().max().item() * 1e-2)
+    assert _cos(got, ref) >= 0.9999
+
+
 # ------------------------------------------------------------------ linear accuracy gate
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_w4a8_linear_vs_fp32_fallback(rt, oracle, dev, dtype):
