@@ -21,7 +21,7 @@
 //
 // Every lane of a wave reads 16 packed bytes (32 values) of one weight row per
 // block, so a wave-wide load covers 16 rows x 64 bytes.
-#include "ic_common.h"
+#include "dequant4.h"
 
 namespace {
 
@@ -66,6 +66,8 @@ __global__ __launch_bounds__(kGT) void gemv_i8_kernel(
     for (int u = 0; u < kBatch; ++u) {
       const int b = b0 + 4 * u;
       if (b < KB) {  // uniform across the wave
+        // lanes of padding rows (col >= M) feed output rows that are never
+        // stored: they load nothing and multiply zeros
         a0[u] = *(const v4i*)(arow + kGBK * b);
         a1[u] = *(const v4i*)(arow + kGBK * b + 16);
         if constexpr (INT4) {
@@ -142,24 +144,6 @@ __global__ __launch_bounds__(kGT) void gemv_i8_kernel(
 }
 
 // W4A16 weight dequantization RN_dt(q * RN_dt(s)) of 8 nibbles.
-template <int DT> IC_DEV void deq8(uint32_t P, float s, u16* out) {
-  if constexpr (DT == IC_DTYPE_F16) {
-    const _Float16 sh = (_Float16)s;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int q = (int)(P << (28 - 4 * i)) >> 28;
-      out[i] = __builtin_bit_cast(u16, (_Float16)((_Float16)q * sh));
-    }
-  } else {
-    const float sb = bf16_to_f32(f32_to_bf16(s));
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int q = (int)(P << (28 - 4 * i)) >> 28;
-      out[i] = f32_to_bf16((float)q * sb);  // |q| <= 8 and 8-bit s: the product is exact
-    }
-  }
-}
-
 template <int DT>
 __global__ __launch_bounds__(kGT) void gemv_w4a16_kernel(
     const u16* __restrict__ X, int64_t ldx, const uint8_t* __restrict__ B, int64_t ldb,
@@ -176,7 +160,7 @@ __global__ __launch_bounds__(kGT) void gemv_w4a16_kernel(
   const uint8_t* brow = B + (int64_t)n * ldb + 16 * c;
   const float* swrow = s_w + (int64_t)n * G;
 
-  constexpr int kBatch = 4;
+  constexpr int kBatch = 8;
   v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int b0 = wave; b0 < KB; b0 += 4 * kBatch) {
     v4u xv[kBatch][4], pw[kBatch];
@@ -185,6 +169,7 @@ __global__ __launch_bounds__(kGT) void gemv_w4a16_kernel(
     for (int u = 0; u < kBatch; ++u) {
       const int b = b0 + 4 * u;
       if (b < KB) {  // uniform across the wave
+        // padding rows (col >= M): no loads, zeros (their outputs are not stored)
 #pragma unroll
         for (int j = 0; j < 4; ++j) xv[u][j] = *(const v4u*)(xrow + kGBK * b + 8 * j);
         pw[u] = *(const v4u*)(brow + (kGBK / 2) * b);
@@ -196,12 +181,12 @@ __global__ __launch_bounds__(kGT) void gemv_w4a16_kernel(
       const int b = b0 + 4 * u;
       if (b >= KB) break;
       const uint32_t p4[4] = {pw[u].x, pw[u].y, pw[u].z, pw[u].w};
+      const DeqScale d = deq_scale<DT>(sv[u]);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        u16 h[8];
-        deq8<DT>(p4[j], sv[u], h);
-        const v4u wv = {h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16),
-                        h[4] | ((uint32_t)h[5] << 16), h[6] | ((uint32_t)h[7] << 16)};
+        uint32_t o[4];
+        deq8<DT>(p4[j], d, o);
+        const v4u wv = {o[0], o[1], o[2], o[3]};
         if constexpr (DT == IC_DTYPE_F16)
           acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h_t, xv[u][j]), __builtin_bit_cast(v8h_t, wv), acc, 0, 0, 0);
         else
