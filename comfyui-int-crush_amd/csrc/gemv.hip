@@ -66,8 +66,6 @@ __global__ __launch_bounds__(kGT) void gemv_i8_kernel(
     for (int u = 0; u < kBatch; ++u) {
       const int b = b0 + 4 * u;
       if (b < KB) {  // uniform across the wave
-        // lanes of padding rows (col >= M) feed output rows that are never
-        // stored: they load nothing and multiply zeros
         a0[u] = *(const v4i*)(arow + kGBK * b);
         a1[u] = *(const v4i*)(arow + kGBK * b + 16);
         if constexpr (INT4) {
@@ -169,7 +167,6 @@ __global__ __launch_bounds__(kGT) void gemv_w4a16_kernel(
     for (int u = 0; u < kBatch; ++u) {
       const int b = b0 + 4 * u;
       if (b < KB) {  // uniform across the wave
-        // padding rows (col >= M): no loads, zeros (their outputs are not stored)
 #pragma unroll
         for (int j = 0; j < 4; ++j) xv[u][j] = *(const v4u*)(xrow + kGBK * b + 8 * j);
         pw[u] = *(const v4u*)(brow + (kGBK / 2) * b);
