@@ -68,7 +68,7 @@ def _parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS) + [STEP_CONFIG])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (PMC calibration)")
@@ -228,6 +228,185 @@ def cpu_baseline(cfg, inp):
                       f"(the reference fallback re-dequantizes every forward), median of 3 after 1 warm-up"}
 
 
+# ---------------------------------------------------------------- C4: Flux step
+# The quantized linears of one Flux-dev denoise step: 19
+# double blocks (image stream M=4096 and text stream M=512, each with its own
+# weights) and 38 single blocks (M=4608), each with qkv 3072->9216, proj
+# 3072->3072 and the MLP 3072->12288->3072 as INT4 W4A8 linears (R=256, g128,
+# SmoothRot + PermuQuant, bf16), plus the 76 M=1 modulation linears 3072->18432
+# (img_mod/txt_mod rotated W4A8, single-block modulation W4A16).  Every layer
+# has its own weights, so weights stream from HBM as in a real step.
+# Attention (torch's SDPA between qkv and proj) is not part of this path and
+# is not run: the step time is that of the quantized linears.
+STEP_CONFIG = "c4step"
+FLUX_LINEARS = (("qkv", 3072, 9216), ("proj", 3072, 3072), ("mlp_up", 3072, 12288), ("mlp_down", 12288, 3072))
+FLUX_BLOCKS = (("double", 19, (4096, 512)), ("single", 38, (4608,)))
+FLUX_MOD = (3072, 18432)
+
+
+def _time_graph(fn, reps):
+    """Average ms of fn() captured once into a hipGraph and replayed reps times."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    if EAGER:
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            fn()
+        e.record()
+        e.synchronize()
+        return s.elapsed_time(e) / reps
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    g.replay()
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        g.replay()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+def flux_step_bench(args, rt):
+    import torch
+
+    dev = torch.device("cuda:0")
+    act = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(0)
+    Ms = sorted({m for _, _, ms in FLUX_BLOCKS for m in ms})
+    Ks = sorted({k for _, k, _ in FLUX_LINEARS})
+    x = {(m, k): torch.randn(m, k, generator=g, device=dev).to(act) for m in Ms + [1] for k in Ks}
+    sr = {k: rt.prepare_factors(torch.exp(torch.randn(k, generator=g, device=dev) * 0.5), act) for k in Ks}
+    perm = {k: rt.prepare_perm(torch.randperm(k, generator=g, device=dev), k) for k in Ks}
+    q = {(m, k): torch.empty(m, k, dtype=torch.int8, device=dev) for m in Ms + [1] for k in Ks}
+    s_a = {m: torch.empty(m, dtype=torch.float32, device=dev) for m in Ms + [1]}
+
+    def weights(n, k):
+        w = torch.randint(0, 256, (n, k // 2), generator=g, device=dev, dtype=torch.uint8)
+        s = (torch.rand(n, k // 128, generator=g, device=dev) * (2e-2 - 1e-3) + 1e-3).to(torch.float16).float()
+        return w, s
+
+    layers = []  # (kind, M, K, N, w, s_w)
+    for _, nblk, ms in FLUX_BLOCKS:
+        for _ in range(nblk):
+            for m in ms:
+                for name, k, n in FLUX_LINEARS:
+                    layers.append((name, m, k, n) + weights(n, k))
+    kmod, nmod = FLUX_MOD
+    mods_w4a8 = [weights(nmod, kmod) for _ in range(2 * FLUX_BLOCKS[0][1])]
+    mods_w4a16 = [weights(nmod, kmod) for _ in range(FLUX_BLOCKS[1][1])]
+    out = {}
+    for _, m, _, n, _, _ in layers:
+        if (m, n) not in out:
+            out[(m, n)] = torch.empty(m, n, dtype=act, device=dev)
+    out_mod = torch.empty(1, nmod, dtype=act, device=dev)
+
+    def prep(m, k):
+        rt.rotate_quantize(x[(m, k)], rot_size=256, w_in=k, smoothrot=sr[k], perm=perm[k],
+                           s_a_out=s_a[m], x_int8_out=q[(m, k)])
+
+    def run(kinds=None, do_prep=True, do_gemm=True, do_mod=True):
+        def fn():
+            for name, m, k, n, w, sw in layers:
+                if kinds is not None and name not in kinds:
+                    continue
+                if do_prep:
+                    prep(m, k)
+                if do_gemm:
+                    rt.gemm_w4a8(q[(m, k)], w, sw, s_a[m], out_dtype=act, out=out[(m, n)])
+            if do_mod:
+                for w, sw in mods_w4a8:
+                    prep(1, kmod)
+                    rt.gemm_w4a8(q[(1, kmod)], w, sw, s_a[1], out_dtype=act, out=out_mod)
+                for w, sw in mods_w4a16:
+                    rt.gemm_w4a16(x[(1, kmod)], w, sw, out=out_mod)
+        return fn
+
+    reps = max(1, args.steps)
+    for _ in range(max(0, args.warmup)):
+        run()()
+    torch.cuda.synchronize()
+    step_ms = _time_graph(run(), reps)
+    gemm_ms = _time_graph(run(do_prep=False, do_mod=False), reps)
+    prep_ms = _time_graph(run(do_gemm=False, do_mod=False), reps)
+    mod_ms = _time_graph(run(kinds=(), do_mod=True), reps)
+    per_kind = {name: round(_time_graph(run(kinds=(name,), do_prep=False, do_mod=False), reps), 4)
+                for name, _, _ in FLUX_LINEARS}
+    lin_ops = sum(2.0 * m * k * n for _, m, k, n, _, _ in layers)
+    mod_ops = 2.0 * kmod * nmod * (len(mods_w4a8) + len(mods_w4a16))
+    wbytes = sum(w.numel() + 4 * sw.numel() for _, _, _, _, w, sw in layers)
+    return dict(step_ms=step_ms, gemm_ms=gemm_ms, prep_ms=prep_ms, mod_ms=mod_ms, per_kind=per_kind,
+                lin_ops=lin_ops, mod_ops=mod_ops, n_layers=len(layers), n_mods=len(mods_w4a8) + len(mods_w4a16),
+                weight_bytes=wbytes)
+
+
+def flux_step_cpu_baseline(rows=512):
+    """Reference fp32 fallback (oracle restatement) on one layer of each Flux
+    linear shape at `rows` tokens; the step estimate scales that throughput to
+    the step's operations (labelled as extrapolated)."""
+    import torch
+
+    import oracle
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    gen = torch.Generator().manual_seed(0)
+    ops, secs = 0.0, 0.0
+    for _, k, n in FLUX_LINEARS:
+        x = torch.randn(rows, k, generator=gen).to(torch.bfloat16)
+        w = torch.randint(0, 256, (n, k // 2), generator=gen, dtype=torch.uint8).numpy()
+        sw = (torch.rand(n, k // 128, generator=gen) * (2e-2 - 1e-3) + 1e-3).to(torch.float16).float().numpy()
+        kw = dict(int4=True, smoothrot=torch.exp(torch.randn(k, generator=gen) * 0.5), rot_size=256,
+                  perm=torch.randperm(k, generator=gen))
+        oracle.reference_fallback_forward(x, w, sw, k, **kw)  # warm-up
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            oracle.reference_fallback_forward(x, w, sw, k, **kw)
+            ts.append(time.perf_counter() - t0)
+        secs += statistics.median(ts)
+        ops += 2.0 * rows * k * n
+    return ops / secs, cores
+
+
+def flux_step_main(args, rt):
+    r = flux_step_bench(args, rt)
+    total_ops = r["lin_ops"] + r["mod_ops"]
+    gemm_tops = r["lin_ops"] / (r["gemm_ms"] * 1e-3) / 1e12
+    line = {
+        "metric": METRIC, "value": round(total_ops / (r["step_ms"] * 1e-3) / 1e12, 3), "unit": "TOPS",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(r["step_ms"], 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "C4 Flux-dev denoise step, quantized linears only (attention not run): "
+                               "19 double blocks (M=4096 + 512) + 38 single blocks (M=4608), "
+                               "qkv/proj/MLP W4A8 R=256 g128 SmoothRot+perm bf16, 76 M=1 modulation GEMVs",
+                   "layers": r["n_layers"], "modulation_gemvs": r["n_mods"],
+                   "weight_bytes": r["weight_bytes"], "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "kernel": "gemm_w4a8 (all linear launches of the step)",
+                     "achieved": round(gemm_tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TOPS",
+                     "frac": round(gemm_tops / PEAK_INT8_TOPS, 4), "kernel_ms": round(r["gemm_ms"], 4),
+                     "algorithmic_ops_per_step": r["lin_ops"], "traffic": None},
+        "breakdown_ms": {"step": round(r["step_ms"], 4), "gemm_w4a8": round(r["gemm_ms"], 4),
+                         "rotate_quantize": round(r["prep_ms"], 4), "modulation_gemvs": round(r["mod_ms"], 4),
+                         "gemm_by_layer": r["per_kind"]},
+    }
+    if not args.no_cpu:
+        tops, cores = flux_step_cpu_baseline()
+        line["cpu_baseline"] = {"value": round(tops / 1e12, 5), "unit": "TOPS", "cores": cores, "kind": "port",
+                                "extrapolated_step_s": round(total_ops / tops, 2),
+                                "sample": "one layer of each Flux linear shape (qkv, proj, mlp_up, mlp_down) at "
+                                          "512 tokens, fp32 dequant + prep + F.linear per call, median of 3; "
+                                          "step time extrapolated from that throughput"}
+    print(json.dumps(line), flush=True)
+
+
 def traffic_for(workload_key):
     """HBM bytes per launch of the dominant kernel from committed rocprofv3 counters."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
@@ -253,6 +432,9 @@ def main():
         sys.exit(1)
     global EAGER
     EAGER = args.eager
+    if args.config == STEP_CONFIG:
+        flux_step_main(args, rt)
+        return
     cfg = CONFIGS[args.config]
     inp = make_inputs(cfg)
     if args.calib_copy:
