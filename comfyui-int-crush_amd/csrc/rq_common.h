@@ -49,6 +49,11 @@ template <int RC> IC_DEV int tile_pos(int t, int j) {
 
 constexpr int kFastMaxTiles = 4;  // fast path: K_w <= 16384
 
+// Instantiation sets of the fast-path kernels (see rq_fast.h).
+constexpr int kRqPlain = 0;    // no SmoothRot factors, no perm
+constexpr int kRqGeneral = 1;  // either one; flags read at run time
+constexpr int kRqBoth = 2;     // both
+
 }  // namespace rq
 
 // Fast-path launchers (rq_fast_f16.hip / rq_fast_bf16.hip); argument checks
@@ -58,3 +63,6 @@ hipError_t ic_rq_fast_bf16(const ic_rotq_args& a, hipStream_t st);
 // without SmoothRot factors or perm
 hipError_t ic_rq_fast_f16_plain(const ic_rotq_args& a, hipStream_t st);
 hipError_t ic_rq_fast_bf16_plain(const ic_rotq_args& a, hipStream_t st);
+// with both SmoothRot factors and perm
+hipError_t ic_rq_fast_f16_both(const ic_rotq_args& a, hipStream_t st);
+hipError_t ic_rq_fast_bf16_both(const ic_rotq_args& a, hipStream_t st);

@@ -53,11 +53,15 @@ template <int DT> IC_DEV bool rn32_is_dt_boundary(float z) {
   else return (w & 0xffffu) == 0x8000u;
 }
 
-// Two workgroups per CU while the per-thread constants fit half the register
-// file (K_w <= 12288, or any width without SmoothRot factors and perm); wider
-// rows with factors or a perm keep one.  PLAIN kernels (no SmoothRot, no perm)
-// are separate instantiations: besides the registers, they drop the per-run
-// divide, its range checks and the gather's per-element LDS addressing.
+// Three instantiation sets (VAR): kRqPlain (no SmoothRot factors, no perm),
+// kRqBoth (both, known at compile time) and kRqGeneral (either one, read at
+// run time).  The plain kernels drop the per-run divide, its range checks,
+// the gather's per-element LDS addressing and their registers; the
+// compile-time flags of kRqBoth remove the unused gather path and the
+// run-time branches (~9 % at the Flux MLP down-projection).  Two workgroups
+// per CU while the per-thread constants fit half the register file (K_w <=
+// 12288, or any width for plain rows); wider rows with factors or a perm keep
+// one.
 // LDS layouts (doubles in the exchange buffer, 16-bit values in the row
 // buffer).  Exchange slot of tile position p: 2 doubles of padding per 16
 // positions and 16 per 256.  Then the b128 row writes of 16 lanes hit 16
@@ -70,8 +74,8 @@ constexpr int kXbufDoubles = kTile + 2 * (kTile / 16) + 16 * (kTile / 256);
 IC_DEV int rbaddr(int p) { return p + 16 * (p >> 8); }
 template <int NT> constexpr int rowbuf_len() { return NT * kTile + 16 * (NT * kTile / 256); }
 
-template <int DT, int LOG4R, int NT, bool PLAIN>
-__global__ __launch_bounds__(kThreads, (NT <= 3 || PLAIN) ? 2 : 1) void rq_fast_kernel(
+template <int DT, int LOG4R, int NT, int VAR>
+__global__ __launch_bounds__(kThreads, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_fast_kernel(
     const u16* __restrict__ x, int64_t ldx, int M, int K_in, int K_r,
     const float* __restrict__ sr_rcp, const float* __restrict__ sr_f, int K_w,
     const int32_t* __restrict__ perm, int8_t* __restrict__ q_out, int64_t ldq,
@@ -82,9 +86,10 @@ __global__ __launch_bounds__(kThreads, (NT <= 3 || PLAIN) ? 2 : 1) void rq_fast_
   __shared__ __attribute__((aligned(16))) u16 rowbuf[rowbuf_len<NT>()];
   __shared__ float red[kThreads / 64];
 
+  constexpr bool PLAIN = VAR == kRqPlain;
   const int t = threadIdx.x;
-  const bool has_sr = !PLAIN && sr_rcp != nullptr;
-  const bool has_perm = !PLAIN && perm != nullptr;
+  const bool has_sr = VAR == kRqBoth || (VAR == kRqGeneral && sr_rcp != nullptr);
+  const bool has_perm = VAR == kRqBoth || (VAR == kRqGeneral && perm != nullptr);
 
   // ---- per-workgroup constants (not allocated by PLAIN kernels)
   constexpr int NTC = PLAIN ? 1 : NT;
@@ -382,9 +387,9 @@ int persistent_grid(Kern kern, int64_t M) {
   return (int)(M < g ? M : g);
 }
 
-template <int DT, int LOG4R, int NT, bool PLAIN>
+template <int DT, int LOG4R, int NT, int VAR>
 hipError_t launch_fast_t(const ic_rotq_args& a, hipStream_t st) {
-  auto kern = rq_fast_kernel<DT, LOG4R, NT, PLAIN>;
+  auto kern = rq_fast_kernel<DT, LOG4R, NT, VAR>;
   const int64_t K_r = LOG4R == 0 ? a.K_in : ((a.K_in + a.rot_size - 1) / a.rot_size) * a.rot_size;
   kern<<<dim3(persistent_grid(kern, a.M)), dim3(kThreads), 0, st>>>(
       (const u16*)a.x, a.ldx, (int)a.M, (int)a.K_in, (int)K_r, a.sr_rcp, a.sr_f, (int)a.K_w, a.perm,
@@ -392,19 +397,18 @@ hipError_t launch_fast_t(const ic_rotq_args& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <int DT, int LOG4R, bool PLAIN>
+template <int DT, int LOG4R, int VAR>
 hipError_t launch_fast_nt(const ic_rotq_args& a, hipStream_t st) {
-  if (a.K_w <= kTile) return launch_fast_t<DT, LOG4R, 1, PLAIN>(a, st);
-  if (a.K_w <= 2 * kTile) return launch_fast_t<DT, LOG4R, 2, PLAIN>(a, st);
-  if (a.K_w <= 3 * kTile) return launch_fast_t<DT, LOG4R, 3, PLAIN>(a, st);
-  return launch_fast_t<DT, LOG4R, 4, PLAIN>(a, st);
+  if (a.K_w <= kTile) return launch_fast_t<DT, LOG4R, 1, VAR>(a, st);
+  if (a.K_w <= 2 * kTile) return launch_fast_t<DT, LOG4R, 2, VAR>(a, st);
+  if (a.K_w <= 3 * kTile) return launch_fast_t<DT, LOG4R, 3, VAR>(a, st);
+  return launch_fast_t<DT, LOG4R, 4, VAR>(a, st);
 }
 
-// PLAIN: no SmoothRot factors and no perm (the caller routes on that);
-// otherwise the kernels read both flags at run time.
-template <int DT, bool PLAIN>
+// VAR must match the arguments (the per-dtype dispatcher routes on them).
+template <int DT, int VAR>
 hipError_t launch_fast(const ic_rotq_args& a, hipStream_t st) {
-  if (PLAIN && a.rot_size == 0 && a.K_w == a.K_in && a.K_in <= 32 * 512) {
+  if (VAR == kRqPlain && a.rot_size == 0 && a.K_w == a.K_in && a.K_in <= 32 * 512) {
     const unsigned grid = (unsigned)((a.M + 3) / 4);
     if (a.K_in <= 8 * 512)
       quant_wave_kernel<DT, 8><<<grid, kThreads, 0, st>>>((const u16*)a.x, a.ldx, (int)a.M, (int)a.K_in, a.q_out, a.ldq, a.s_out);
@@ -415,12 +419,12 @@ hipError_t launch_fast(const ic_rotq_args& a, hipStream_t st) {
     return hipGetLastError();
   }
   switch (a.rot_size) {
-    case 0: return launch_fast_nt<DT, 0, PLAIN>(a, st);
-    case 16: return launch_fast_nt<DT, 2, PLAIN>(a, st);
-    case 64: return launch_fast_nt<DT, 3, PLAIN>(a, st);
-    case 256: return launch_fast_nt<DT, 4, PLAIN>(a, st);
-    case 1024: return launch_fast_nt<DT, 5, PLAIN>(a, st);
-    case 4096: return launch_fast_nt<DT, 6, PLAIN>(a, st);
+    case 0: return launch_fast_nt<DT, 0, VAR>(a, st);
+    case 16: return launch_fast_nt<DT, 2, VAR>(a, st);
+    case 64: return launch_fast_nt<DT, 3, VAR>(a, st);
+    case 256: return launch_fast_nt<DT, 4, VAR>(a, st);
+    case 1024: return launch_fast_nt<DT, 5, VAR>(a, st);
+    case 4096: return launch_fast_nt<DT, 6, VAR>(a, st);
   }
   return hipErrorInvalidValue;
 }

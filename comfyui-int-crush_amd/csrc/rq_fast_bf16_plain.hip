@@ -3,5 +3,5 @@
 #include "rq_fast.h"
 
 hipError_t ic_rq_fast_bf16_plain(const ic_rotq_args& a, hipStream_t st) {
-  return launch_fast<IC_DTYPE_BF16, true>(a, st);
+  return launch_fast<IC_DTYPE_BF16, kRqPlain>(a, st);
 }
