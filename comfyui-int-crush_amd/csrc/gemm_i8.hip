@@ -494,16 +494,17 @@ hipError_t launch_mfma(const GemmArgs& g, hipStream_t st) {
 }
 
 // Workgroup rounds of a BM x BN tiling on the device's CUs times the tile
-// area: proportional to the run time of an MFMA-bound launch.
-int64_t tiling_cost(const GemmArgs& g, int bm, int bn) {
+// area, times the tile's relative cost per output (percent): proportional to
+// the run time of an MFMA-bound launch.
+int64_t tiling_cost(const GemmArgs& g, int bm, int bn, int pct = 100) {
   const int64_t tiles = (int64_t)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn);
   const int64_t cus = ic_num_cus();
-  return (tiles + cus - 1) / cus * bm * bn;
+  return (tiles + cus - 1) / cus * bm * bn * pct;
 }
 
-// Tile choices: 256-row tiles when M fills them, else 128 x 128.  Per-row
-// W8A8 takes 256 x 192 where that fills the CUs in fewer tile-area rounds
-// than 256 x 256 (4096 x 3072: 256 tiles instead of 192 on 256 CUs).
+// Tile choices by tile-area rounds (tiling_cost).  Per-row W8A8 takes
+// 256 x 192 where that fills the CUs in fewer rounds than 256 x 256
+// (4096 x 3072: 256 tiles instead of 192 on 256 CUs).
 template <bool INT4, int GS, int OUT_DT, bool ACC>
 hipError_t pick_tile(const GemmArgs& g, hipStream_t st) {
   if constexpr (!INT4 && GS == 0) {
@@ -514,7 +515,12 @@ hipError_t pick_tile(const GemmArgs& g, hipStream_t st) {
     }
     return launch_mfma<Tile<128, 128, 2, 4, false, 0>, OUT_DT, ACC>(g, st);
   } else {
-    if (g.M > 128) return launch_mfma<Tile<256, 128, 4, 3, INT4, GS>, OUT_DT, ACC>(g, st);
+    // INT4 / grouped: 256 x 128 unless 128 x 128 is cheaper; a 128 x 128
+    // tile costs 1.44x more per output (measured on the Flux shapes), so it
+    // wins only when it fills CUs that 256 x 128 leaves idle (512 x 3072: 48
+    // tiles of 256 x 128, 96 of 128 x 128 on 256 CUs)
+    if (g.M > 128 && tiling_cost(g, 256, 128) <= tiling_cost(g, 128, 128, 144))
+      return launch_mfma<Tile<256, 128, 4, 3, INT4, GS>, OUT_DT, ACC>(g, st);
     return launch_mfma<Tile<128, 128, 2, 4, INT4, GS>, OUT_DT, ACC>(g, st);
   }
 }

@@ -195,6 +195,26 @@ def test_w8a8_accumulators_full_grid(rt, dev, M, N, K):
     assert torch.equal(acc.to(torch.int64), ref)
 
 
+@pytest.mark.parametrize("M,N,K", [(4096, 3072, 256), (4000, 3000, 384)])
+@pytest.mark.parametrize("grouped", [False, True])
+def test_w4a8_accumulators_full_grid(rt, oracle, dev, M, N, K, grouped):
+    """Shapes large enough for 256 x 128 tiles (small ones take 128 x 128):
+    int32 accumulators (per 128-group when grouped) equal the exact integer
+    matmul of the unpacked weights, computed in float64 on the CPU."""
+    G = K // 128 if grouped else 1
+    a = _int8((M, K), 23)
+    packed = torch.randint(0, 256, (N, K // 2), generator=_gen(24), dtype=torch.uint8)
+    s_w = torch.rand(N, G, generator=_gen(25)) * 1e-2 + 1e-3
+    acc = rt.gemm_acc_i32(a.to(dev), packed.to(dev), int4=True, s_w=s_w.to(dev)).cpu().to(torch.int64)
+    w = torch.from_numpy(oracle.unpack_int4(packed.numpy(), K)).double()
+    ad = a.double()
+    if G == 1:
+        ref = (ad @ w.T).to(torch.int64)
+    else:
+        ref = torch.stack([(ad[:, 128 * g:128 * g + 128] @ w[:, 128 * g:128 * g + 128].T) for g in range(G)]).to(torch.int64)
+    assert torch.equal(acc, ref)
+
+
 @pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
 @pytest.mark.parametrize("G", [1, "g128"])
 def test_w4a8_accumulators(rt, oracle, dev, M, N, K, G):
