@@ -44,13 +44,9 @@ typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 IC_DEV float f16_to_f32(u16 h) { return (float)__builtin_bit_cast(_Float16, h); }
 IC_DEV u16 f32_to_f16(float f) { return __builtin_bit_cast(u16, (_Float16)f); }
 IC_DEV float bf16_to_f32(u16 b) { return __uint_as_float((uint32_t)b << 16); }
-IC_DEV u16 f32_to_bf16(float f) {
-  // Round-to-nearest-even on the bit pattern; NaN stays a quiet NaN.
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u16)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (u16)(u >> 16);
-}
+// Round-to-nearest-even f32 -> bf16 with the gfx950 conversion instruction
+// (one VALU op; NaN stays a quiet NaN).
+IC_DEV u16 f32_to_bf16(float f) { return __builtin_bit_cast(u16, (__bf16)f); }
 
 template <int DT> IC_DEV float ld_as_f32(const void* p, int64_t i) {
   if constexpr (DT == IC_DTYPE_F16) return f16_to_f32(((const u16*)p)[i]);

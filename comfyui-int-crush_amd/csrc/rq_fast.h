@@ -70,21 +70,26 @@ template <int DT> IC_DEV bool rn32_is_dt_boundary(float z) {
 // banks.  Row-buffer address of position p: 16 values of padding per 256, so
 // the strided writes of the four 16-lane groups of a wave use distinct banks.
 IC_DEV int xslot(int p) { return p + 2 * (p >> 4) + 16 * (p >> 8); }
-constexpr int kXbufDoubles = kTile + 2 * (kTile / 16) + 16 * (kTile / 256);
+template <int TILE> constexpr int xbuf_doubles() { return TILE + 2 * (TILE / 16) + 16 * (TILE / 256); }
 IC_DEV int rbaddr(int p) { return p + 16 * (p >> 8); }
-template <int NT> constexpr int rowbuf_len() { return NT * kTile + 16 * (NT * kTile / 256); }
+template <int NT, int TILE> constexpr int rowbuf_len() { return NT * TILE + 16 * (NT * TILE / 256); }
 
-template <int DT, int LOG4R, int NT, int VAR>
-__global__ __launch_bounds__(kThreads, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_fast_kernel(
+// TH threads per workgroup (256, or 192 = three waves for rows of up to 3072
+// or 6144 values with R <= 256, whose Hadamard exchange stays inside a wave):
+// a tile is TH * 16 positions.
+template <int DT, int LOG4R, int NT, int VAR, int TH>
+__global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_fast_kernel(
     const u16* __restrict__ x, int64_t ldx, int M, int K_in, int K_r,
     const float* __restrict__ sr_rcp, const float* __restrict__ sr_f, int K_w,
     const int32_t* __restrict__ perm, int8_t* __restrict__ q_out, int64_t ldq,
     float* __restrict__ s_out) {
   constexpr int RC = LOG4R <= 2 ? 0 : (LOG4R <= 4 ? 1 : 2);
   constexpr bool XCH = LOG4R >= 3;
-  __shared__ double xbuf[XCH ? kXbufDoubles : 2];
-  __shared__ __attribute__((aligned(16))) u16 rowbuf[rowbuf_len<NT>()];
-  __shared__ float red[kThreads / 64];
+  constexpr int kTile = TH * 16;  // positions per tile
+  static_assert(TH == 256 || (TH % 64 == 0 && LOG4R <= 4), "cross-wave rotation needs four waves");
+  __shared__ double xbuf[XCH ? xbuf_doubles<kTile>() : 2];
+  __shared__ __attribute__((aligned(16))) u16 rowbuf[rowbuf_len<NT, kTile>()];
+  __shared__ float red[TH / 64];
 
   constexpr bool PLAIN = VAR == kRqPlain;
   const int t = threadIdx.x;
@@ -265,7 +270,10 @@ __global__ __launch_bounds__(kThreads, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) voi
     amax = wave_max(amax);
     if ((t & 63) == 0) red[t >> 6] = amax;
     __syncthreads();
-    const float m = round_to_dt<DT>(__builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3])));
+    float mr = red[0];
+#pragma unroll
+    for (int w = 1; w < TH / 64; ++w) mr = __builtin_fmaxf(mr, red[w]);
+    const float m = round_to_dt<DT>(mr);
     const float s = quant_scale(m);
     const double rs = 1.0 / (double)s;
     if (t == 0) s_out[row] = s;
@@ -275,7 +283,7 @@ __global__ __launch_bounds__(kThreads, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) voi
 #pragma unroll
     for (int c = 0; c < NT; ++c) {
       if (c * kTile >= K_w) break;  // uniform
-      const int o0 = 16 * (t + kThreads * c);
+      const int o0 = 16 * (t + TH * c);
       float vv[16];
       if (has_perm) {
         const char* rb = (const char*)rowbuf;
@@ -376,22 +384,22 @@ __global__ __launch_bounds__(kThreads) void quant_wave_kernel(
 }
 
 template <class Kern>
-int persistent_grid(Kern kern, int64_t M) {
+int persistent_grid(Kern kern, int threads, int64_t M) {
   static thread_local int per_cu = 0;  // resident workgroups per CU for this kernel
   if (per_cu == 0) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, kThreads, 0) != hipSuccess || n <= 0) n = 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, 0) != hipSuccess || n <= 0) n = 1;
     per_cu = n;
   }
   const int64_t g = (int64_t)per_cu * ic_num_cus();
   return (int)(M < g ? M : g);
 }
 
-template <int DT, int LOG4R, int NT, int VAR>
+template <int DT, int LOG4R, int NT, int VAR, int TH = kThreads>
 hipError_t launch_fast_t(const ic_rotq_args& a, hipStream_t st) {
-  auto kern = rq_fast_kernel<DT, LOG4R, NT, VAR>;
+  auto kern = rq_fast_kernel<DT, LOG4R, NT, VAR, TH>;
   const int64_t K_r = LOG4R == 0 ? a.K_in : ((a.K_in + a.rot_size - 1) / a.rot_size) * a.rot_size;
-  kern<<<dim3(persistent_grid(kern, a.M)), dim3(kThreads), 0, st>>>(
+  kern<<<dim3(persistent_grid(kern, TH, a.M)), dim3(TH), 0, st>>>(
       (const u16*)a.x, a.ldx, (int)a.M, (int)a.K_in, (int)K_r, a.sr_rcp, a.sr_f, (int)a.K_w, a.perm,
       a.q_out, a.ldq, a.s_out);
   return hipGetLastError();
@@ -399,6 +407,13 @@ hipError_t launch_fast_t(const ic_rotq_args& a, hipStream_t st) {
 
 template <int DT, int LOG4R, int VAR>
 hipError_t launch_fast_nt(const ic_rotq_args& a, hipStream_t st) {
+  if constexpr (LOG4R <= 4) {
+    // three-wave workgroups where their tile fits the row more tightly
+    // (3072: one full tile instead of 3/4 of one; 4097..6144: two)
+    constexpr int T3 = 192 * 16;
+    if (a.K_w <= T3 && a.K_w > kTile / 2) return launch_fast_t<DT, LOG4R, 1, VAR, 192>(a, st);
+    if (a.K_w > kTile && a.K_w <= 2 * T3) return launch_fast_t<DT, LOG4R, 2, VAR, 192>(a, st);
+  }
   if (a.K_w <= kTile) return launch_fast_t<DT, LOG4R, 1, VAR>(a, st);
   if (a.K_w <= 2 * kTile) return launch_fast_t<DT, LOG4R, 2, VAR>(a, st);
   if (a.K_w <= 3 * kTile) return launch_fast_t<DT, LOG4R, 3, VAR>(a, st);

@@ -116,6 +116,10 @@ ROT_CASES = [
     (640, 64, None, False, True, True),         # old SmoothQuant after the gather
     (13824, 1024, 14336, False, False, False),  # Wan FFN-down pad path
     (12288, 256, None, True, True, False),      # Flux MLP down-proj (C3 prep)
+    (5120, 256, None, False, False, False),     # three-wave workgroups, two tiles (Wan qkv/proj width)
+    (5120, 64, None, True, True, False),
+    (6144, 256, None, False, True, False),
+    (3072, 16, None, True, False, False),       # three-wave workgroups, one full tile
 ]
 
 
