@@ -1,6 +1,7 @@
-// Fast path of the fused prep + quantize (see the comment at the top of the
-// kernels).  Included once per activation dtype (rq_fast_f16.hip,
-// rq_fast_bf16.hip) so the two instantiation sets compile in parallel.
+// Fast path of the fused prep + quantize (the general kernel and the
+// arithmetic it shares with this one are described in rotate_quant.hip).
+// Included by one translation unit per activation dtype and instantiation set
+// (rq_fast_{f16,bf16}{,_plain,_both}.hip) so the sets compile in parallel.
 #pragma once
 #include "rq_common.h"
 
@@ -22,7 +23,6 @@ using namespace rq;
 //     only for a run holding a lane outside the proven fast-path range;
 //   * rotated values are rounded once and kept as 16-bit values in an LDS row
 //     buffer, which the gather reads directly (perm pre-scaled to byte offsets).
-constexpr int kFastMaxTiles = 4;  // K_w <= 16384
 
 template <int DT> IC_DEV void unpack8(v4u a, float* o) {
   const uint32_t w[4] = {a.x, a.y, a.z, a.w};
