@@ -397,6 +397,9 @@ def flux_step_main(args, rt):
                          "rotate_quantize": round(r["prep_ms"], 4), "modulation_gemvs": round(r["mod_ms"], 4),
                          "gemm_by_layer": r["per_kind"]},
     }
+    peaks = measure_peaks()
+    line["peak_measured"] = peaks
+    line["roofline"]["frac_of_measured_peak"] = round(gemm_tops / peaks["int8_tops"], 4)
     if not args.no_cpu:
         tops, cores = flux_step_cpu_baseline()
         line["cpu_baseline"] = {"value": round(tops / 1e12, 5), "unit": "TOPS", "cores": cores, "kind": "port",
@@ -405,6 +408,61 @@ def flux_step_main(args, rt):
                                           "512 tokens, fp32 dequant + prep + F.linear per call, median of 3; "
                                           "step time extrapolated from that throughput"}
     print(json.dumps(line), flush=True)
+
+
+def measure_peaks():
+    """Rates this GPU sustains at its loaded clock: dense INT8 and FP16 MFMA
+    from register-only loops (bench_peak.hip) and HBM from a 1 GiB
+    device-to-device copy (read + write bytes).  Reported beside the
+    published peaks the roofline fractions use."""
+    import ctypes
+
+    import torch
+
+    import __graft_entry__
+
+    if not os.path.exists(__graft_entry__.PEAK_LIB):
+        __graft_entry__.build_peak_probe()
+    lib = ctypes.CDLL(__graft_entry__.PEAK_LIB)
+    lib.bp_grid.restype = ctypes.c_int
+    lib.bp_ops_per_launch.restype = ctypes.c_double
+    lib.bp_ops_per_launch.argtypes = [ctypes.c_int, ctypes.c_int]
+    for f in (lib.bp_mfma_i8, lib.bp_mfma_f16):
+        f.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+        f.restype = ctypes.c_int
+    out = torch.empty(lib.bp_grid() * 256, dtype=torch.int32, device="cuda:0")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    iters = 4000
+    rates = {}
+    for kind, fn in ((0, lib.bp_mfma_i8), (1, lib.bp_mfma_f16)):
+        for _ in range(2):  # warm-up: clocks settle under load
+            if fn(iters, ctypes.c_void_p(out.data_ptr()), stream) != 0:
+                raise RuntimeError("peak probe launch failed")
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(5):
+            fn(iters, ctypes.c_void_p(out.data_ptr()), stream)
+        e.record()
+        e.synchronize()
+        rates[kind] = 5 * lib.bp_ops_per_launch(kind, iters) / (s.elapsed_time(e) * 1e-3) / 1e12
+    a = torch.empty(1 << 30, dtype=torch.uint8, device="cuda:0")
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(5):
+        b.copy_(a)
+    e.record()
+    e.synchronize()
+    hbm = 5 * 2 * a.numel() / (s.elapsed_time(e) * 1e-3) / 1e9
+    del a, b
+    return {"int8_tops": round(rates[0], 1), "fp16_tflops": round(rates[1], 1), "hbm_copy_gbps": round(hbm, 1),
+            "method": "register-only MFMA loops (v_mfma_i32_32x32x32_i8, v_mfma_f32_32x32x16_f16), "
+                      "2 workgroups of 4 waves per CU, 4 independent accumulator chains per wave; "
+                      "HBM: 1 GiB device copy, read + write bytes"}
 
 
 def traffic_for(workload_key):
@@ -473,6 +531,10 @@ def main():
         "roofline": roof,
         "host_wall_ms_per_step": round(wall * 1e3 / args.steps, 5),
     }
+    peaks = measure_peaks()
+    line["peak_measured"] = peaks
+    meas = peaks["hbm_copy_gbps"] if roof["bound"] == "hbm" else (peaks["fp16_tflops"] if is_fp else peaks["int8_tops"])
+    roof["frac_of_measured_peak"] = round(roof["achieved"] / meas, 4)
     if p_ms is not None:
         pach = prep_bytes / (p_ms * 1e-3) / 1e9
         line["prep_quant"] = {"kernel": "rotate_quantize", "bound": "hbm", "kernel_ms": round(p_ms, 5),
