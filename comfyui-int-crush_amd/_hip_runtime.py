@@ -67,6 +67,9 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "ic_dynamic_quantize": ([_P, _I, _L, _L, _L, _P, _L, _P, _P], _I),
     "ic_gemm_w8a8": ([_P, _L, _L, _L, _P, _L, _L, _P, _P, _P, _I, _P, _I, _L, _P], _I),
     "ic_gemm_w4a8": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _P, _I, _P, _I, _L, _P], _I),
+    "ic_gemm_splitk_bytes": ([_L, _L, _L, _L, _I], _L),
+    "ic_gemm_w8a8_ws": ([_P, _L, _L, _L, _P, _L, _L, _P, _P, _P, _I, _P, _I, _L, _P, _L, _P], _I),
+    "ic_gemm_w4a8_ws": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _P, _I, _P, _I, _L, _P, _L, _P], _I),
     "ic_gemm_w4a16": ([_P, _I, _L, _L, _L, _P, _L, _L, _P, _L, _P, _I, _P, _L, _P], _I),
     "ic_unpack_int4_to_int8": ([_P, _L, _L, _L, _P, _L, _P], _I),
     "ic_unpack_int4_to_float": ([_P, _P, _L, _L, _L, _L, _P, _I, _L, _P], _I),
@@ -338,6 +341,16 @@ def _out_buffer(out, M, N, out_dtype, device):
     return torch.empty((M, N), dtype=out_dtype, device=device)
 
 
+def _splitk_workspace(M: int, N: int, K: int, G: int, int4: bool, device) -> tuple[torch.Tensor | None, int]:
+    """Workspace for the split-K form of the GEMM when the library plans one
+    (small M: too few output tiles to occupy the GPU); (None, 0) otherwise.
+    Allocated from torch's caching allocator, so it is graph-capture safe."""
+    nb = int(lib().ic_gemm_splitk_bytes(M, N, K, G, 1 if int4 else 0))
+    if nb <= 0:
+        return None, 0
+    return torch.empty(nb, dtype=torch.uint8, device=device), nb
+
+
 def fused_int8_gemm_dequant(x_int8: torch.Tensor, w_int8: torch.Tensor, s_w: torch.Tensor,
                             s_a: torch.Tensor, bias: torch.Tensor | None = None,
                             out_dtype: torch.dtype = torch.bfloat16, activation: int = 0,
@@ -366,8 +379,9 @@ def fused_int8_gemm_dequant(x_int8: torch.Tensor, w_int8: torch.Tensor, s_w: tor
     bp, bdt, _keep = _bias_args(bias, N)
     c = _out_buffer(out, M, N, out_dtype, x_int8.device)
     with torch.cuda.device(xq.device):
-        _call("ic_gemm_w8a8", _ptr(xq), M, K, xq.stride(0), _ptr(w), N, w.stride(0), _ptr(sa),
-              _ptr(sw), bp, bdt, _ptr(c), _dt(c.dtype, "out"), c.stride(0), _stream(xq))
+        ws, nb = _splitk_workspace(M, N, K, 1, False, xq.device)
+        _call("ic_gemm_w8a8_ws", _ptr(xq), M, K, xq.stride(0), _ptr(w), N, w.stride(0), _ptr(sa),
+              _ptr(sw), bp, bdt, _ptr(c), _dt(c.dtype, "out"), c.stride(0), _ptr(ws), nb, _stream(xq))
     return c
 
 
@@ -402,8 +416,9 @@ def gemm_w4a8(x_int8: torch.Tensor, w_packed: torch.Tensor, s_w: torch.Tensor, s
     bp, bdt, _keep = _bias_args(bias, N)
     c = _out_buffer(out, M, N, out_dtype, xq.device)
     with torch.cuda.device(xq.device):
-        _call("ic_gemm_w4a8", _ptr(xq), M, K, xq.stride(0), _ptr(w), N, w.stride(0), _ptr(sw), G,
-              _ptr(sa), bp, bdt, _ptr(c), _dt(c.dtype, "out"), c.stride(0), _stream(xq))
+        ws, nb = _splitk_workspace(M, N, K, G, True, xq.device)
+        _call("ic_gemm_w4a8_ws", _ptr(xq), M, K, xq.stride(0), _ptr(w), N, w.stride(0), _ptr(sw), G,
+              _ptr(sa), bp, bdt, _ptr(c), _dt(c.dtype, "out"), c.stride(0), _ptr(ws), nb, _stream(xq))
     return c
 
 

@@ -54,7 +54,11 @@ struct Tile {
   static constexpr size_t lds_bytes() { return ring_bytes() > epi_bytes() ? ring_bytes() : epi_bytes(); }
 };
 
-template <class TL, int OUT_DT, bool ACC_OUT>
+// PART (split-K): workgroup (x, y) computes tile x over the K stages of
+// slice y of gridDim.y and writes its 4-byte partials -- the int32 sum
+// (per-row scales) or the fp32 group fold (grouped) -- to
+// acc_out[(y * M + m) * N + n]; splitk_reduce_kernel finishes them.
+template <class TL, int OUT_DT, bool ACC_OUT, bool PART = false>
 __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
     const int8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
     const float* __restrict__ s_a, const float* __restrict__ s_w, int G,
@@ -86,7 +90,9 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
   int tm, tn;
   tile_coords(blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int KT = K / kBK;
+  const int KT_all = K / kBK;
+  const int kt0 = PART ? (int)((int64_t)blockIdx.y * KT_all / gridDim.y) : 0;
+  const int KT = PART ? (int)((int64_t)(blockIdx.y + 1) * KT_all / gridDim.y) - kt0 : KT_all;
   const bool s_wave = wave < S_WAVES;
 
   // ---- DMA addressing.  A / int8 B: lane L of a 1 KB block covers LDS row
@@ -112,9 +118,9 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
     }
   }
   const uint32_t s_off = GS ? (uint32_t)(min(64 * wave + lane, N - 1 - n0) * G * 4) : 0u;
-  const int8_t* a_base = A + (int64_t)m0 * lda;
-  const uint8_t* b_base = B + (int64_t)n0 * ldb;
-  const float* s_base = GS ? s_w + (int64_t)n0 * G : nullptr;
+  const int8_t* a_base = A + (int64_t)m0 * lda + (int64_t)kt0 * kBK;
+  const uint8_t* b_base = B + (int64_t)n0 * ldb + (int64_t)kt0 * (INT4 ? kBK / 2 : kBK);
+  const float* s_base = GS ? s_w + (int64_t)n0 * G + kt0 : nullptr;
 
   // The D DMA instructions of one stage are issued in kParts slices, one per
   // K-step of the MFMA loop: a wave that issued a whole stage at once stalled
@@ -328,6 +334,24 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
   }
 
   // ---- epilogue
+  if constexpr (PART) {
+    // partials of this K slice: 32 lanes of one accumulator row write 32
+    // consecutive columns (128 bytes)
+    int32_t* ws = acc_out + (int64_t)blockIdx.y * M * N;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = out_row(i, r), n = out_col(j);
+          if (m < M && n < N) {
+            if constexpr (GS == 0) ws[(int64_t)m * N + n] = acc[0][i][j][r];
+            else ((float*)ws)[(int64_t)m * N + n] = facc[i][j][r];
+          }
+        }
+    return;
+  }
   if constexpr (ACC_OUT && GS == 0) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -469,29 +493,42 @@ __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(
   st_from_f32<OUT_DT>(C, (int64_t)m * ldc + n, v);
 }
 
+// Sum of the K-slice partials in slice order, then the operations of the
+// unsplit epilogue; per-row-scale outputs are therefore bit-identical to an
+// unsplit launch (exact int32 sums), grouped ones differ only in the order of
+// the fp32 group-fold additions.
+template <bool INT4, int GS, int OUT_DT>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(
+    const int32_t* __restrict__ ws, int S, const float* __restrict__ s_a, const float* __restrict__ s_w,
+    const void* __restrict__ bias, int bias_dt, void* __restrict__ C, int64_t ldc, int M, int N) {
+  const int64_t MN = (int64_t)M * N;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= MN) return;
+  const int m = (int)(i / N), n = (int)(i - (int64_t)m * N);
+  float v;
+  if constexpr (GS == 0) {
+    int t = 0;
+    for (int s = 0; s < S; ++s) t += ws[s * MN + i];
+    float a = (float)t;
+    if constexpr (INT4) a *= 0.0625f;
+    v = a * (s_a[m] * s_w[n]);
+  } else {
+    const float* f = (const float*)ws;
+    float t = f[i];
+    for (int s = 1; s < S; ++s) t = t + f[s * MN + i];
+    v = t * s_a[m];
+  }
+  if (bias != nullptr) v = v + ld_any_f32(bias, bias_dt, n);
+  st_from_f32<OUT_DT>(C, (int64_t)m * ldc + n, v);
+}
+
 struct GemmArgs {
   const int8_t* A; int64_t lda; const uint8_t* B; int64_t ldb;
   const float* s_a; const float* s_w; int G;
   const void* bias; int bias_dt; void* C; int out_dt; int64_t ldc; int M, N, K;
   int32_t* acc_out; bool int4;
+  void* ws = nullptr; int64_t ws_bytes = 0;  // split-K workspace (optional)
 };
-
-template <class TL, int OUT_DT, bool ACC>
-hipError_t launch_mfma(const GemmArgs& g, hipStream_t st) {
-  const int tiles = ((g.M + TL::BM - 1) / TL::BM) * ((g.N + TL::BN - 1) / TL::BN);
-  const size_t shm = TL::lds_bytes();
-  static_assert(TL::lds_bytes() <= 160 * 1024, "LDS budget");
-  auto kern = gemm_i8_kernel<TL, OUT_DT, ACC>;
-  static bool attr_set = false;  // idempotent attribute; benign if raced
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
-  kern<<<dim3(tiles), dim3(kNT), shm, st>>>(g.A, g.lda, g.B, g.ldb, g.s_a, g.s_w, g.G, g.bias,
-                                             g.bias_dt, g.C, g.ldc, g.M, g.N, g.K, g.acc_out);
-  return hipGetLastError();
-}
 
 // Workgroup rounds of a BM x BN tiling on the device's CUs times the tile
 // area, times the tile's relative cost per output (percent): proportional to
@@ -502,25 +539,88 @@ int64_t tiling_cost(const GemmArgs& g, int bm, int bn, int pct = 100) {
   return (tiles + cus - 1) / cus * bm * bn * pct;
 }
 
-// Tile choices by tile-area rounds (tiling_cost).  Per-row W8A8 takes
+// Tile choice by tile-area rounds (tiling_cost).  Per-row W8A8 takes
 // 256 x 192 where that fills the CUs in fewer rounds than 256 x 256
-// (4096 x 3072: 256 tiles instead of 192 on 256 CUs).
+// (4096 x 3072: 256 tiles instead of 192 on 256 CUs).  INT4 / grouped:
+// 256 x 128 unless 128 x 128 is cheaper; a 128 x 128 tile costs 1.44x more
+// per output (measured on the Flux shapes), so it wins only when it fills CUs
+// that 256 x 128 leaves idle (512 x 3072: 48 tiles of 256 x 128, 96 of
+// 128 x 128 on 256 CUs).
+struct TileShape { int bm, bn; };
+TileShape tile_choice(const GemmArgs& g, bool grouped) {
+  if (!g.int4 && !grouped) {
+    if (g.M > 128 && g.N > 128)
+      return tiling_cost(g, 256, 192) < tiling_cost(g, 256, 256) ? TileShape{256, 192} : TileShape{256, 256};
+    return {128, 128};
+  }
+  if (g.M > 128 && tiling_cost(g, 256, 128) <= tiling_cost(g, 128, 128, 144)) return {256, 128};
+  return {128, 128};
+}
+
+// K slices for `tiles` workgroups over KT stages: minimise rounds of
+// workgroups times stages per slice plus the partials' round trip through
+// HBM (8 bytes per output and slice; ~3.6 MB per stage time).  Only when the
+// unsplit launch would leave more than half the CUs idle; 1 = no split.
+int choose_splits(int64_t tiles, int KT, int64_t M, int64_t N) {
+  const int64_t cus = ic_num_cus();
+  if (tiles * 2 > cus || KT < 8) return 1;
+  double best = (double)((tiles + cus - 1) / cus) * KT;
+  int bs = 1;
+  for (int S = 2; S <= 16 && KT / S >= 4; ++S) {
+    const double c = (double)((tiles * S + cus - 1) / cus) * ((KT + S - 1) / S) + (double)S * M * N * 8.0 / 3.6e6;
+    if (c < best) { best = c; bs = S; }
+  }
+  return bs;
+}
+
+int splitk_plan(const GemmArgs& g, bool grouped) {
+  const TileShape t = tile_choice(g, grouped);
+  const int64_t tiles = (int64_t)((g.M + t.bm - 1) / t.bm) * ((g.N + t.bn - 1) / t.bn);
+  return choose_splits(tiles, g.K / kBK, g.M, g.N);
+}
+
+template <class TL, int OUT_DT, bool ACC, bool PART>
+hipError_t launch_kernel(const GemmArgs& g, int S, hipStream_t st) {
+  const int tiles = ((g.M + TL::BM - 1) / TL::BM) * ((g.N + TL::BN - 1) / TL::BN);
+  const size_t shm = TL::lds_bytes();
+  static_assert(TL::lds_bytes() <= 160 * 1024, "LDS budget");
+  auto kern = gemm_i8_kernel<TL, OUT_DT, ACC, PART>;
+  static bool attr_set = false;  // idempotent attribute; benign if raced
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  kern<<<dim3(tiles, S), dim3(kNT), shm, st>>>(g.A, g.lda, g.B, g.ldb, g.s_a, g.s_w, g.G, g.bias, g.bias_dt,
+                                               g.C, g.ldc, g.M, g.N, g.K, PART ? (int32_t*)g.ws : g.acc_out);
+  return hipGetLastError();
+}
+
+template <class TL, int OUT_DT, bool ACC>
+hipError_t launch_mfma(const GemmArgs& g, hipStream_t st) {
+  if constexpr (!ACC) {
+    const int S = g.ws != nullptr ? splitk_plan(g, TL::GS != 0) : 1;
+    if (S > 1 && g.C != nullptr && g.ws_bytes >= (int64_t)S * g.M * g.N * 4) {
+      hipError_t e = launch_kernel<TL, OUT_DT, false, true>(g, S, st);
+      if (e != hipSuccess) return e;
+      const int64_t MN = (int64_t)g.M * g.N;
+      splitk_reduce_kernel<TL::INT4, TL::GS, OUT_DT><<<dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, st>>>(
+          (const int32_t*)g.ws, S, g.s_a, g.s_w, g.bias, g.bias_dt, g.C, g.ldc, g.M, g.N);
+      return hipGetLastError();
+    }
+  }
+  return launch_kernel<TL, OUT_DT, ACC, false>(g, 1, st);
+}
+
 template <bool INT4, int GS, int OUT_DT, bool ACC>
 hipError_t pick_tile(const GemmArgs& g, hipStream_t st) {
+  const TileShape t = tile_choice(g, GS != 0);
   if constexpr (!INT4 && GS == 0) {
-    if (g.M > 128 && g.N > 128) {
-      if (tiling_cost(g, 256, 192) < tiling_cost(g, 256, 256))
-        return launch_mfma<Tile<256, 192, 4, 2, false, 0>, OUT_DT, ACC>(g, st);
-      return launch_mfma<Tile<256, 256, 2, 2, false, 0>, OUT_DT, ACC>(g, st);
-    }
+    if (t.bm == 256 && t.bn == 192) return launch_mfma<Tile<256, 192, 4, 2, false, 0>, OUT_DT, ACC>(g, st);
+    if (t.bm == 256) return launch_mfma<Tile<256, 256, 2, 2, false, 0>, OUT_DT, ACC>(g, st);
     return launch_mfma<Tile<128, 128, 2, 4, false, 0>, OUT_DT, ACC>(g, st);
   } else {
-    // INT4 / grouped: 256 x 128 unless 128 x 128 is cheaper; a 128 x 128
-    // tile costs 1.44x more per output (measured on the Flux shapes), so it
-    // wins only when it fills CUs that 256 x 128 leaves idle (512 x 3072: 48
-    // tiles of 256 x 128, 96 of 128 x 128 on 256 CUs)
-    if (g.M > 128 && tiling_cost(g, 256, 128) <= tiling_cost(g, 128, 128, 144))
-      return launch_mfma<Tile<256, 128, 4, 3, INT4, GS>, OUT_DT, ACC>(g, st);
+    if (t.bm == 256) return launch_mfma<Tile<256, 128, 4, 3, INT4, GS>, OUT_DT, ACC>(g, st);
     return launch_mfma<Tile<128, 128, 2, 4, INT4, GS>, OUT_DT, ACC>(g, st);
   }
 }
@@ -601,27 +701,53 @@ int run_gemm(GemmArgs g, hipStream_t st, const char* who, bool force_generic) {
 
 extern "C" {
 
-int ic_gemm_w8a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8_t* w, int64_t N,
-                 int64_t ldw, const float* s_a, const float* s_w, const void* bias, int bias_dtype,
-                 void* out, int out_dtype, int64_t ldo, void* stream) {
+int64_t ic_gemm_splitk_bytes(int64_t M, int64_t N, int64_t K, int64_t num_groups, int int4) {
+  if (M <= IC_GEMV_MAX_M || N <= 0 || K <= 0 || K % kBK != 0 || num_groups < 1) return 0;
+  if (num_groups > 1 && K / num_groups != 128) return 0;
+  if (M * N > (1LL << 31)) return 0;
+  GemmArgs g{nullptr, K, nullptr, K, nullptr, nullptr, (int)num_groups, nullptr, 0, nullptr, IC_DTYPE_F32,
+             N, (int)M, (int)N, (int)K, nullptr, int4 != 0};
+  const int S = splitk_plan(g, num_groups > 1);
+  return S > 1 ? (int64_t)S * M * N * 4 : 0;
+}
+
+int ic_gemm_w8a8_ws(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8_t* w, int64_t N,
+                    int64_t ldw, const float* s_a, const float* s_w, const void* bias, int bias_dtype,
+                    void* out, int out_dtype, int64_t ldo, void* workspace, int64_t workspace_bytes,
+                    void* stream) {
   if (ic_gemv_applicable(M, K, xq, ldx, w, ldw) && ldw >= K && N > 0 && ldo >= N && ldx >= K)
     return ic_gemv_w8a8(xq, M, K, ldx, w, N, ldw, s_a, s_w, bias, bias_dtype, out, out_dtype, ldo, stream);
   GemmArgs g{xq, ldx, (const uint8_t*)w, ldw, s_a, s_w, 1, bias, bias_dtype, out, out_dtype, ldo,
-             (int)M, (int)N, (int)K, nullptr, false};
+             (int)M, (int)N, (int)K, nullptr, false, workspace, workspace_bytes};
   return run_gemm(g, (hipStream_t)stream, "ic_gemm_w8a8", false);
+}
+
+int ic_gemm_w8a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8_t* w, int64_t N,
+                 int64_t ldw, const float* s_a, const float* s_w, const void* bias, int bias_dtype,
+                 void* out, int out_dtype, int64_t ldo, void* stream) {
+  return ic_gemm_w8a8_ws(xq, M, K, ldx, w, N, ldw, s_a, s_w, bias, bias_dtype, out, out_dtype, ldo, nullptr, 0,
+                         stream);
+}
+
+int ic_gemm_w4a8_ws(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed,
+                    int64_t N, int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a,
+                    const void* bias, int bias_dtype, void* out, int out_dtype, int64_t ldo,
+                    void* workspace, int64_t workspace_bytes, void* stream) {
+  if (ic_gemv_applicable(M, K, xq, ldx, w_packed, ldw) && ldw * 2 >= K && N > 0 && ldo >= N && ldx >= K &&
+      (num_groups == 1 || num_groups * 128 == K))
+    return ic_gemv_w4a8(xq, M, K, ldx, w_packed, N, ldw, s_w, num_groups, s_a, bias, bias_dtype, out, out_dtype,
+                        ldo, stream);
+  GemmArgs g{xq, ldx, w_packed, ldw, s_a, s_w, (int)num_groups, bias, bias_dtype, out, out_dtype,
+             ldo, (int)M, (int)N, (int)K, nullptr, true, workspace, workspace_bytes};
+  return run_gemm(g, (hipStream_t)stream, "ic_gemm_w4a8", false);
 }
 
 int ic_gemm_w4a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed,
                  int64_t N, int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a,
                  const void* bias, int bias_dtype, void* out, int out_dtype, int64_t ldo,
                  void* stream) {
-  if (ic_gemv_applicable(M, K, xq, ldx, w_packed, ldw) && ldw * 2 >= K && N > 0 && ldo >= N && ldx >= K &&
-      (num_groups == 1 || num_groups * 128 == K))
-    return ic_gemv_w4a8(xq, M, K, ldx, w_packed, N, ldw, s_w, num_groups, s_a, bias, bias_dtype, out, out_dtype,
-                        ldo, stream);
-  GemmArgs g{xq, ldx, w_packed, ldw, s_a, s_w, (int)num_groups, bias, bias_dtype, out, out_dtype,
-             ldo, (int)M, (int)N, (int)K, nullptr, true};
-  return run_gemm(g, (hipStream_t)stream, "ic_gemm_w4a8", false);
+  return ic_gemm_w4a8_ws(xq, M, K, ldx, w_packed, N, ldw, s_w, num_groups, s_a, bias, bias_dtype, out, out_dtype,
+                         ldo, nullptr, 0, stream);
 }
 
 int ic_gemm_w8a8_acc_i32(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8_t* w,

@@ -99,6 +99,29 @@ int ic_gemm_w4a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint
                  void* stream);
 
 /*
+ * Split-K forms of ic_gemm_w8a8 / ic_gemm_w4a8 (same kernels as the two entry
+ * points above, which the reference functions named there map to).  When the
+ * output has too few tiles to occupy the GPU (small M), K is cut into S slices
+ * computed in parallel; each slice writes 4-byte partials (exact int32 sums,
+ * or the fp32 group fold when num_groups > 1) to the caller's workspace and a
+ * second kernel adds them in slice order and applies the epilogue.  Per-row
+ * scale outputs are bit-identical to the unsplit GEMM; grouped outputs differ
+ * only in the order of the fp32 additions.  ic_gemm_splitk_bytes returns the
+ * workspace the launch will use (0: no split; then workspace may be null);
+ * a smaller workspace than that runs the unsplit GEMM.  The library itself
+ * never allocates.
+ */
+int64_t ic_gemm_splitk_bytes(int64_t M, int64_t N, int64_t K, int64_t num_groups, int int4);
+int ic_gemm_w8a8_ws(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8_t* w, int64_t N,
+                    int64_t ldw, const float* s_a, const float* s_w, const void* bias, int bias_dtype,
+                    void* out, int out_dtype, int64_t ldo, void* workspace, int64_t workspace_bytes,
+                    void* stream);
+int ic_gemm_w4a8_ws(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed,
+                    int64_t N, int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a,
+                    const void* bias, int bias_dtype, void* out, int out_dtype, int64_t ldo,
+                    void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * W4A16: out = x . RN_dt(q * RN_dt(s))^T (+ bias), fp32 accumulation, dtype f16/bf16.
  * Replaces unpack_int4_to_float16 (kernels/triton_int4_unpack.py:62-88) + F.linear
  * of _ops.py:466-481.

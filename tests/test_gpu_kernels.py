@@ -265,6 +265,65 @@ def test_w4a8_output_formula(rt, oracle, dev, out_dtype, grouped, M, N, K):
     assert np.array_equal(out.float().cpu().numpy(), ref)
 
 
+SPLITK_SHAPES = [(64, 3072, 12288), (512, 3072, 12288), (100, 1000, 3072)]
+
+
+@pytest.mark.parametrize("M,N,K", SPLITK_SHAPES)
+@pytest.mark.parametrize("fmt", ["int8", "int4"])
+def test_splitk_per_row_bit_exact(rt, oracle, dev, M, N, K, fmt):
+    """Small M: the library splits K over workgroups (the size query says
+    so); with per-row scales the int32 partials add exactly, so the output
+    equals the oracle's unsplit epilogue formula bit for bit."""
+    int4 = fmt == "int4"
+    assert rt.lib().ic_gemm_splitk_bytes(M, N, K, 1, int(int4)) > 0
+    a = _int8((M, K), 51, -127, 128)
+    s_a = torch.rand(M, generator=_gen(52)) * 0.05 + 1e-3
+    s_w = (torch.rand(N, generator=_gen(53)) * 2e-3 + 1e-4).to(torch.float16).float()
+    bias = torch.randn(N, generator=_gen(54)).to(torch.bfloat16)
+    if int4:
+        w = torch.randint(0, 256, (N, K // 2), generator=_gen(55), dtype=torch.uint8)
+        out = rt.gemm_w4a8(a.to(dev), w.to(dev), s_w.to(dev), s_a.to(dev), bias=bias.to(dev), out_dtype=torch.bfloat16)
+        wq = oracle.unpack_int4(w.numpy(), K)
+    else:
+        w = _int8((N, K), 55, -127, 128)
+        out = rt.fused_int8_gemm_dequant(a.to(dev), w.to(dev), s_w.to(dev), s_a.to(dev), bias=bias.to(dev),
+                                         out_dtype=torch.bfloat16)
+        wq = w.numpy()
+    ref = oracle.epilogue(oracle.gemm_acc(a.numpy(), wq), s_a.numpy(), s_w.numpy(), bias.float().numpy(),
+                          DT[torch.bfloat16])
+    assert np.array_equal(out.float().cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("M,N,K", SPLITK_SHAPES)
+def test_splitk_grouped_w4a8(rt, oracle, dev, M, N, K):
+    """Grouped scales with split K: each slice folds its groups in order and
+    the slices' fp32 partials are added in slice order, so outputs may differ
+    from the single fold chain by fp32 rounding only.  Both sums are within
+    G * 2^-24 * T of the exact value (T = sum of the absolute group terms), so
+    they differ by at most G * 2^-23 * T, plus one fp16 ulp where the final
+    rounding falls differently; and both sit within the fp32 dequant ->
+    F.linear tolerance."""
+    G = K // 128
+    assert rt.lib().ic_gemm_splitk_bytes(M, N, K, G, 1) > 0
+    a = _int8((M, K), 56, -127, 128)
+    w = torch.randint(0, 256, (N, K // 2), generator=_gen(57), dtype=torch.uint8)
+    s_a = torch.rand(M, generator=_gen(58)) * 0.05 + 1e-3
+    s_w = (torch.rand(N, G, generator=_gen(59)) * 2e-2 + 1e-3).to(torch.float16).float()
+    out = rt.gemm_w4a8(a.to(dev), w.to(dev), s_w.to(dev), s_a.to(dev), out_dtype=torch.float16).float().cpu()
+    wq = oracle.unpack_int4(w.numpy(), K)
+    acc = oracle.gemm_acc(a.numpy(), wq, G)  # [G, M, N]
+    ref = torch.from_numpy(oracle.epilogue(acc, s_a.numpy(), s_w.numpy(), None, DT[torch.float16]))
+    terms = (np.abs(acc).astype(np.float64) * s_w.numpy().T.astype(np.float64)[:, None, :]).sum(0)
+    T = torch.from_numpy(terms * s_a.numpy().astype(np.float64)[:, None])
+    big = torch.maximum(out.abs(), ref.abs()).clamp_min(2.0 ** -14)
+    ulp = torch.pow(2.0, torch.floor(torch.log2(big))) * 2.0 ** -10
+    assert ((out - ref).abs().double() <= G * 2.0 ** -23 * T + ulp.double()).all()
+    exact = (a.double() @ (torch.from_numpy(wq).double().reshape(N, G, 128)
+                           * s_w.double().reshape(N, G, 1)).reshape(N, K).T) * s_a.double().reshape(M, 1)
+    assert torch.allclose(out.double(), exact, rtol=1e-2, atol=1e-2 * exact.abs().max().item() * 1e-2)
+    assert _cos(out, exact.float()) >= 0.9999
+
+
 C5_ROWS = [0, 1, 255, 256, 12345, 32511, 32512, 32759]  # tile edges and the last, partial tile
 
 
