@@ -12,6 +12,24 @@ fallback (fp32 dequant -> F.linear) that the fp16/bf16 outputs are judged
 against.
 
 Reference citations are file:line in ThunderFun/ComfyUI-INT-Crush.
+
+How each function is pinned (tests/test_oracle.py, tests/test_numerics_proofs.py);
+none is left unpinned:
+  unpack_int4 / pack_int4   the reference's known answers (tests/test_quant_utils.py:65-99
+                            of the reference), all 256 byte values, round trips
+  prepare (Hadamard)        orthogonality and involution of H, closed-form entries
+                            against a Kronecker-product matmul, exact rational
+                            recomputation for wide-range blocks
+  prepare (divide/pad/perm) torch fp16/bf16 division, perm followed by its inverse,
+                            zero pads
+  quantize                  the reference CPU quantizer's vectors at its test shapes,
+                            hand-built ties and the 0.49999997 quirk, zero rows
+  gemm_acc                  int64 matmul; group sums add to the ungrouped sum
+  epilogue                  against linear_fallback_fp32 on the same integers
+  dequant_w4a16             single correctly rounded fp16 product (numpy fp16)
+  reference_fallback_forward against the integer chain (prepare -> quantize ->
+                            gemm_acc -> epilogue) within quantization error; a
+                            reversed perm or transposed group scales fail it
 """
 from __future__ import annotations
 

@@ -208,3 +208,35 @@ def test_dequant_w4a16_exact(oracle):
     w = oracle.dequant_w4a16(oracle.pack_int4(q), s, 256, 0)
     exact = q.astype(np.float64) * np.repeat(s.astype(np.float64), 128, axis=1)
     assert np.array_equal(w, exact.astype(np.float16).astype(np.float32))
+
+
+@pytest.mark.parametrize("int4", [True, False])
+def test_reference_fallback_forward_matches_integer_chain(oracle, int4):
+    """The fp32 fallback forward (SmoothRot divide, Hadamard by matmul, pad,
+    perm, fp32 dequant, F.linear) and the integer chain (prepare -> per-token
+    INT8 quantization -> exact accumulators -> epilogue) are independent
+    codings of the same layer; they agree within the activation-quantization
+    error.  A transposed operand, a wrong group layout or a misapplied perm
+    in either one breaks the agreement."""
+    g = torch.Generator().manual_seed(7)
+    M, K_in, K_w, N, R = 12, 1000, 1280, 40, 256  # rotation pad 1000 -> 1024, then w_in pad to 1280
+    x = torch.randn(M, K_in, generator=g).to(torch.float16)
+    sr = torch.exp(torch.randn(K_in, generator=g) * 0.5)
+    perm = torch.randperm(K_w, generator=g)
+    if int4:
+        q = torch.randint(-8, 8, (N, K_w), generator=g, dtype=torch.int8).numpy()
+        w = oracle.pack_int4(q)
+        s_w = (torch.rand(N, K_w // 128, generator=g) * 2e-2 + 1e-3).numpy().astype(np.float32)
+    else:
+        q = torch.randint(-127, 128, (N, K_w), generator=g, dtype=torch.int8).numpy()
+        w = q
+        s_w = (torch.rand(N, 1, generator=g) * 2e-3 + 1e-4).numpy().astype(np.float32)
+    fb = oracle.reference_fallback_forward(x, w, s_w, K_w, int4=int4, smoothrot=sr, rot_size=R, perm=perm).numpy()
+    y = oracle.prepare(x, oracle.DT_F16, smoothrot=sr, rot_size=R, w_in=K_w, perm=perm)
+    qa, s_a = oracle.quantize(y)
+    G = s_w.shape[1]
+    acc = oracle.gemm_acc(qa, q, G)
+    chain = oracle.epilogue(acc, s_a, s_w, None, out_dtype=oracle.DT_F32)
+    cos = float((fb * chain).sum() / np.sqrt((fb * fb).sum() * (chain * chain).sum()))
+    assert cos > 0.9999
+    assert np.abs(fb - chain).max() < 0.02 * np.abs(fb).max()
