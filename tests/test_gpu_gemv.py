@@ -76,8 +76,11 @@ def test_gemv_w4a8_bit_exact(rt, oracle, dev, M, N, K, grouped, via):
 
 
 def test_gemv_matches_tiled_gemm_rows(rt, dev):
-    """The same rows computed at M = 16 (GEMV) and inside an M = 300 GEMM agree bit for bit."""
-    K, N = 3072, 384
+    """The same rows computed at M = 16 (GEMV) and inside an M = 300 GEMM agree
+    bit for bit.  N = 6144 gives the GEMM enough tiles that it does not split
+    K (a grouped split-K sums its slices in another fp32 order)."""
+    K, N = 3072, 6144
+    assert rt.lib().ic_gemm_splitk_bytes(300, N, K, K // 128, 1) == 0
     a = _int8((300, K), 21).to(dev)
     packed = torch.randint(0, 256, (N, K // 2), generator=_gen(22), dtype=torch.uint8).to(dev)
     s_a = (torch.rand(300, generator=_gen(23)) * 0.05 + 1e-3).to(dev)
