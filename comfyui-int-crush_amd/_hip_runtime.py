@@ -65,6 +65,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "ic_rotate_quantize": ([_P, _I, _L, _L, _L, _P, _P, _I, _L, _P, _P, _P, _P, _L, _P, _P], _I),
     "ic_prepare_activation": ([_P, _I, _L, _L, _L, _P, _P, _I, _L, _P, _P, _P, _P, _L, _P], _I),
     "ic_dynamic_quantize": ([_P, _I, _L, _L, _L, _P, _L, _P, _P], _I),
+    "ic_norm_quantize": ([_P, _I, _L, _L, _L, _I, _P, _P, ctypes.c_float, _P, _L, _P, _P], _I),
     "ic_gemm_w8a8": ([_P, _L, _L, _L, _P, _L, _L, _P, _P, _P, _I, _P, _I, _L, _P], _I),
     "ic_gemm_w4a8": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _P, _I, _P, _I, _L, _P], _I),
     "ic_gemm_splitk_bytes": ([_L, _L, _L, _L, _I], _L),
@@ -320,6 +321,80 @@ def dynamic_quantize_activation(x: torch.Tensor, s_a_out: torch.Tensor | None = 
         q = q.reshape(orig_shape)
         s = s.reshape(*orig_shape[:-1])
     return q, s
+
+
+# ── normalisation fused with quantization (kernels/triton_quantize.py:201-567) ──
+IC_NORM_LAYER, IC_NORM_RMS, IC_SOFTMAX = 1, 2, 3
+
+
+def _f32_vec(t: torch.Tensor | None, K: int, who: str, device) -> torch.Tensor | None:
+    if t is None:
+        return None
+    v = t.detach().reshape(-1)
+    if v.numel() != K:
+        raise ValueError(f"{who} has {v.numel()} entries, expected {K}")
+    return v.to(device=device, dtype=torch.float32).contiguous()
+
+
+def _norm_quantize(x: torch.Tensor, kind: int, gamma, beta, eps: float, s_a_out, x_int8_out, who: str):
+    orig_shape = x.shape
+    x2 = _rows(x)
+    M, K = x2.shape
+    s = _alloc_or_reuse((M,), torch.float32, x2.device, s_a_out)
+    q = _alloc_or_reuse((M, K), torch.int8, x2.device, x_int8_out)
+    g = _f32_vec(gamma, K, "gamma", x2.device)
+    b = _f32_vec(beta, K, "beta", x2.device)
+    with torch.cuda.device(x2.device):
+        _call("ic_norm_quantize", _ptr(x2), _dt(x2.dtype, who), M, K, x2.stride(0), kind, _ptr(g), _ptr(b),
+              float(eps), _ptr(q), q.stride(0), _ptr(s), _stream(x2))
+    if orig_shape != x2.shape:
+        q = q.reshape(orig_shape)
+        s = s.reshape(*orig_shape[:-1])
+    return q, s
+
+
+def _cpu_quant_reshaped(y: torch.Tensor, orig_shape):
+    q, s = _cpu_per_row_int8_quant(y.reshape(-1, y.shape[-1]).float())
+    return q.reshape(orig_shape), s.reshape(*orig_shape[:-1])
+
+
+def fused_layernorm_quantize(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor | None = None,
+                             eps: float = 1e-5, s_a_out: torch.Tensor | None = None,
+                             x_int8_out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """LayerNorm over the last dim fused with per-row INT8 quantization
+    (kernels/triton_quantize.py:277-345).  Device tensors run ic_norm_quantize
+    (statistics in fp64, y in f32, quantized without rounding y to x's dtype,
+    as the reference GPU kernel does); CPU tensors follow the reference CPU
+    branch (F.layer_norm in f32, rounded to x's dtype, then torch.round)."""
+    if not x.is_cuda:
+        K = x.shape[-1]
+        y = torch.nn.functional.layer_norm(x.to(torch.float32), (K,), gamma.to(torch.float32),
+                                           beta.to(torch.float32) if beta is not None else None, eps)
+        return _cpu_quant_reshaped(y.to(x.dtype), x.shape)
+    return _norm_quantize(x, IC_NORM_LAYER, gamma, beta, eps, s_a_out, x_int8_out, "fused_layernorm_quantize")
+
+
+def fused_rmsnorm_quantize(x: torch.Tensor, gamma: torch.Tensor, eps: float = 1e-6,
+                           s_a_out: torch.Tensor | None = None,
+                           x_int8_out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """RMSNorm x / sqrt(mean(x^2) + eps) * gamma fused with per-row INT8
+    quantization (kernels/triton_quantize.py:397-459); CPU tensors follow the
+    reference CPU branch."""
+    if not x.is_cuda:
+        xf = x.to(torch.float32)
+        rms = torch.sqrt(torch.mean(xf * xf, dim=-1, keepdim=True) + eps)
+        return _cpu_quant_reshaped((xf / rms * gamma.to(torch.float32)).to(x.dtype), x.shape)
+    return _norm_quantize(x, IC_NORM_RMS, gamma, None, eps, s_a_out, x_int8_out, "fused_rmsnorm_quantize")
+
+
+def fused_softmax_quantize(x: torch.Tensor, s_a_out: torch.Tensor | None = None,
+                           x_int8_out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Softmax over the last dim fused with per-row INT8 quantization
+    (kernels/triton_quantize.py:518-567); CPU tensors follow the reference
+    CPU branch (f32 softmax, then torch.round)."""
+    if not x.is_cuda:
+        return _cpu_quant_reshaped(torch.softmax(x.to(torch.float32), dim=-1), x.shape)
+    return _norm_quantize(x, IC_SOFTMAX, None, None, 0.0, s_a_out, x_int8_out, "fused_softmax_quantize")
 
 
 # ── GEMMs ───────────────────────────────────────────────────────────────────

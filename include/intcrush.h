@@ -75,6 +75,25 @@ int ic_dynamic_quantize(const void* x, int dtype, int64_t M, int64_t K, int64_t 
                         int64_t ldq, float* s_out, void* stream);
 
 /*
+ * Row normalisation + per-token dynamic INT8 quantization, one kernel:
+ *   kind IC_NORM_LAYER  y = LayerNorm(x) * gamma (+ beta)   replaces fused_layernorm_quantize,
+ *                       kernels/triton_quantize.py:277-345 (kernel :209-274)
+ *   kind IC_NORM_RMS    y = x / sqrt(mean(x^2) + eps) * gamma   replaces fused_rmsnorm_quantize,
+ *                       kernels/triton_quantize.py:397-459 (kernel :348-394)
+ *   kind IC_SOFTMAX     y = softmax(x)   replaces fused_softmax_quantize,
+ *                       kernels/triton_quantize.py:518-567 (kernel :462-515)
+ * then s_out[m] = max(max|y|, 1e-8) / 127 and q_out = trunc(y / s +- 0.5) clamped
+ * to [-128, 127] (the reference GPU rule).  Row statistics are summed in fp64 and
+ * y is formed in f32; gamma / beta are f32 [K] (gamma required for LayerNorm and
+ * RMSNorm, beta only for LayerNorm and optional, both NULL for softmax).
+ *   x [M, K] (dtype), row stride ldx; q_out [M, K] int8, row stride ldq; s_out [M] f32
+ */
+enum { IC_NORM_LAYER = 1, IC_NORM_RMS = 2, IC_SOFTMAX = 3 };
+int ic_norm_quantize(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, int kind,
+                     const float* gamma, const float* beta, float eps, int8_t* q_out, int64_t ldq,
+                     float* s_out, void* stream);
+
+/*
  * W8A8: out[M,N] = f32(xq . w^T) * (s_a[m] * s_w[n]) + bias[n].
  * Replaces fused_int8_gemm_dequant, kernels/triton_int8_gemm.py:135-205.
  *   xq [M,K] int8, w [N,K] int8, s_a [M] f32, s_w [N] f32, bias [N] (bias_dtype) or NULL.

@@ -30,6 +30,10 @@ none is left unpinned:
   reference_fallback_forward against the integer chain (prepare -> quantize ->
                             gemm_acc -> epilogue) within quantization error; a
                             reversed perm or transposed group scales fail it
+  normalize_rows /          the reference tests' PyTorch formulas (codes within +-1,
+  norm_quantize             their own bar); closed forms (constant rows, uniform
+                            softmax, unit-variance LayerNorm); a LayerNorm without
+                            its mean subtraction fails them
 """
 from __future__ import annotations
 
@@ -235,6 +239,50 @@ def quantize(v, *, rule: str = "gpu"):
 def rotate_quantize(x, dtype: int, **kw):
     """prepare() followed by quantize(): the fused kernel's full contract."""
     return quantize(prepare(x, dtype, **kw))
+
+
+# ---------------------------------------------------------------- norm + quantize
+def normalize_rows(x, kind: str, gamma=None, beta=None, eps: float = 1e-5) -> np.ndarray:
+    """Row normalisation of the fused norm / softmax quantizers
+    (kernels/triton_quantize.py:209-274 LayerNorm, :348-394 RMSNorm, :462-515
+    softmax), as the canonical arithmetic of this build: row statistics in
+    fp64, eps taken as an f32 value, y formed in f32 with one rounding per
+    operation:
+      layer    mean = f32(S/K), rstd = f32(1/sqrt(sum (x - S/K)^2 / K + eps)),
+               y = f32(f32(x - mean) * rstd) * gamma (+ beta)
+      rms      rstd = f32(1/sqrt(sum x^2 / K + eps)), y = f32(x * rstd) * gamma
+      softmax  m = max x, e = f32(exp(f32(x - m))), inv = f32(1 / sum e), y = e * inv
+    The reference sums in f32 in Triton's order; its own tests bound the codes
+    to +-1 of an f32 PyTorch computation, which pins this restatement."""
+    xv = np.ascontiguousarray(x, dtype=np.float32)
+    M, K = xv.shape
+    e = float(np.float32(eps))
+    x64 = xv.astype(np.float64)
+    if kind == "layer":
+        mean64 = x64.sum(axis=1) / K
+        var = ((x64 - mean64[:, None]) ** 2).sum(axis=1) / K
+        mean = mean64.astype(np.float32)
+        rstd = (1.0 / np.sqrt(var + e)).astype(np.float32)
+        y = (xv - mean[:, None]) * rstd[:, None]
+        y = y * np.asarray(gamma, np.float32)[None, :]
+        if beta is not None:
+            y = y + np.asarray(beta, np.float32)[None, :]
+        return y.astype(np.float32)
+    if kind == "rms":
+        rstd = (1.0 / np.sqrt((x64 * x64).sum(axis=1) / K + e)).astype(np.float32)
+        return ((xv * rstd[:, None]) * np.asarray(gamma, np.float32)[None, :]).astype(np.float32)
+    if kind == "softmax":
+        m = xv.max(axis=1)
+        ex = np.exp((xv - m[:, None]).astype(np.float64)).astype(np.float32)
+        inv = (1.0 / ex.astype(np.float64).sum(axis=1)).astype(np.float32)
+        return (ex * inv[:, None]).astype(np.float32)
+    raise ValueError(f"unknown normalisation {kind!r}")
+
+
+def norm_quantize(x, kind: str, gamma=None, beta=None, eps: float = 1e-5):
+    """normalize_rows() then the GPU quantization rule: the full contract of
+    ic_norm_quantize.  Returns (int8 [M, K], float32 [M])."""
+    return quantize(normalize_rows(x, kind, gamma, beta, eps))
 
 
 # ---------------------------------------------------------------- weights
