@@ -170,32 +170,30 @@ class FluxStep:
         return torch.cat([torch.cos(args), torch.sin(args)], dim=-1)
 
     def _rope_tables(self):
-        """cos/sin [tokens, 64] of the three-axis rotary embedding."""
+        """Rotation matrices [tokens, 64, 2, 2] (fp32) of the three-axis rotary
+        embedding: [[cos, -sin], [sin, cos]] per frequency pair."""
         import torch
 
         angles = []
         for axis, dim in enumerate(ROPE_AXES):
             omega = 1.0 / ROPE_THETA ** (torch.arange(0, dim, 2, device=self.dev, dtype=torch.float64) / dim)
             angles.append(self.ids[:, axis].double()[:, None] * omega[None])
-        a = torch.cat(angles, dim=-1).float()
-        return torch.cos(a), torch.sin(a)
+        a = torch.cat(angles, dim=-1)
+        c, s = torch.cos(a), torch.sin(a)
+        return torch.stack((c, -s, s, c), dim=-1).reshape(*a.shape, 2, 2).float()
 
     @staticmethod
-    def _apply_rope(x, cos, sin):
+    def _apply_rope(x, freqs):
         """x [H, S, D]: rotate each (even, odd) pair by its angle, in fp32."""
-        import torch
-
-        xf = x.float().unflatten(-1, (-1, 2))
-        x0, x1 = xf[..., 0], xf[..., 1]
-        out = torch.stack((cos * x0 - sin * x1, sin * x0 + cos * x1), dim=-1)
-        return out.flatten(-2).to(x.dtype)
+        xf = x.float().reshape(*x.shape[:-1], -1, 1, 2)
+        out = freqs[..., 0] * xf[..., 0] + freqs[..., 1] * xf[..., 1]
+        return out.reshape(x.shape).to(x.dtype)
 
     @staticmethod
     def _rms_norm(x, scale):
-        import torch
+        import torch.nn.functional as F
 
-        xf = x.float()
-        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)).to(x.dtype) * scale
+        return F.rms_norm(x, (HEAD_DIM,), weight=scale, eps=1e-6)
 
     @staticmethod
     def _modulate(x, shift, scale):
@@ -205,18 +203,17 @@ class FluxStep:
         return torch.addcmul(shift, F.layer_norm(x, (HID,), eps=1e-6), 1 + scale)
 
     def _split_heads(self, qkv, scale):
-        """qkv [S, 9216] -> q, k (RMS-normed), v as [H, S, D] views/tensors."""
-        t = qkv.view(-1, 3, HEADS, HEAD_DIM)
-        q, k, v = (t[:, i].transpose(0, 1) for i in range(3))
+        """qkv [S, 9216] -> q, k (RMS-normed), v as [H, S, D]."""
+        q, k, v = qkv.view(-1, 3, HEADS, HEAD_DIM).permute(1, 2, 0, 3)
         return self._rms_norm(q, scale), self._rms_norm(k, scale), v
 
-    def attention(self, q, k, v, cos, sin):
+    def attention(self, q, k, v, freqs):
         """Joint attention over [H, S, D] inputs; returns [S, H*D]."""
         import torch.nn.functional as F
         from torch.nn.attention import SDPBackend, sdpa_kernel
 
-        q = self._apply_rope(q, cos, sin)
-        k = self._apply_rope(k, cos, sin)
+        q = self._apply_rope(q, freqs)
+        k = self._apply_rope(k, freqs)
         # the math backend is excluded: its batched products in bf16 are
         # not used on this GPU
         with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
@@ -227,7 +224,7 @@ class FluxStep:
         q, s_a = layer.quantize(self.rt, vec_silu)
         return layer.gemm(self.rt, q, s_a, self.act).chunk(6, dim=-1)
 
-    def _double_block(self, blk, img, txt, vec_silu, cos, sin):
+    def _double_block(self, blk, img, txt, vec_silu, freqs):
         import torch
         import torch.nn.functional as F
 
@@ -236,7 +233,7 @@ class FluxStep:
         tm = self._mod_w4a8(blk["txt_mod"], vec_silu)
         iq, ik, iv = self._split_heads(blk["img_qkv"](rt, self._modulate(img, im[0], im[1])), blk["qk_scale"])
         tq, tk, tv = self._split_heads(blk["txt_qkv"](rt, self._modulate(txt, tm[0], tm[1])), blk["qk_scale"])
-        attn = self.attention(torch.cat((tq, iq), 1), torch.cat((tk, ik), 1), torch.cat((tv, iv), 1), cos, sin)
+        attn = self.attention(torch.cat((tq, iq), 1), torch.cat((tk, ik), 1), torch.cat((tv, iv), 1), freqs)
         t_a, i_a = attn[:TXT_TOKENS], attn[TXT_TOKENS:]
         img = torch.addcmul(img, im[2], blk["img_proj"](rt, i_a))
         h = F.gelu(blk["img_mlp_up"](rt, self._modulate(img, im[3], im[4])), approximate="tanh")
@@ -246,7 +243,7 @@ class FluxStep:
         txt = torch.addcmul(txt, tm[5], blk["txt_mlp_down"](rt, h))
         return img, txt
 
-    def _single_block(self, blk, x, vec_silu, cos, sin):
+    def _single_block(self, blk, x, vec_silu, freqs):
         import torch
         import torch.nn.functional as F
 
@@ -255,7 +252,7 @@ class FluxStep:
         xn = self._modulate(x, shift, scale)
         q, k, v = self._split_heads(blk["qkv"](rt, xn), blk["qk_scale"])
         up = blk["mlp_up"](rt, xn)
-        out = blk["proj"](rt, self.attention(q, k, v, cos, sin))
+        out = blk["proj"](rt, self.attention(q, k, v, freqs))
         out = out + blk["mlp_down"](rt, F.gelu(up, approximate="tanh"))
         return torch.addcmul(x, gate, out)
 
@@ -273,12 +270,12 @@ class FluxStep:
                + mlp(self.guid_in, self._timestep_embedding(self.guidance, TIME_DIM).to(self.act))
                + mlp(self.vec_in, self.y))
         vec_silu = F.silu(vec)
-        cos, sin = self._rope_tables()
+        freqs = self._rope_tables()
         for blk in self.double:
-            img, txt = self._double_block(blk, img, txt, vec_silu, cos, sin)
+            img, txt = self._double_block(blk, img, txt, vec_silu, freqs)
         x = torch.cat((txt, img), 0)
         for blk in self.single:
-            x = self._single_block(blk, x, vec_silu, cos, sin)
+            x = self._single_block(blk, x, vec_silu, freqs)
         img = x[TXT_TOKENS:]
         shift, scale = self.final_mod(vec_silu).chunk(2, dim=-1)
         return self.final(self._modulate(img, shift, scale))
@@ -303,7 +300,7 @@ class FluxStep:
         vec_silu = torch.randn(1, HID, generator=g, device=dev).to(act)
         S = IMG_TOKENS + TXT_TOKENS
         qkv = [torch.randn(HEADS, S, HEAD_DIM, generator=g, device=dev).to(act) for _ in range(3)]
-        cos, sin = self._rope_tables()
+        freqs = self._rope_tables()
 
         def gemm():
             for M, l in lin:
@@ -322,7 +319,7 @@ class FluxStep:
 
         def attention():
             for _ in range(N_DOUBLE + N_SINGLE):
-                self.attention(*qkv, cos, sin)
+                self.attention(*qkv, freqs)
 
         def gemm_kind(name):
             sel = [(M, l) for M, l in lin if l in self._kind_layers(name)]
