@@ -66,6 +66,8 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "ic_prepare_activation": ([_P, _I, _L, _L, _L, _P, _P, _I, _L, _P, _P, _P, _P, _L, _P], _I),
     "ic_dynamic_quantize": ([_P, _I, _L, _L, _L, _P, _L, _P, _P], _I),
     "ic_norm_quantize": ([_P, _I, _L, _L, _L, _I, _P, _P, ctypes.c_float, _P, _L, _P, _P], _I),
+    "ic_norm_rotate_quantize": ([_P, _I, _L, _L, _L, _I, _P, _P, ctypes.c_float, _P, _P, _I, _L, _P, _P, _L,
+                                 _P, _P], _I),
     "ic_gemm_w8a8": ([_P, _L, _L, _L, _P, _L, _L, _P, _P, _P, _I, _P, _I, _L, _P], _I),
     "ic_gemm_w4a8": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _P, _I, _P, _I, _L, _P], _I),
     "ic_gemm_splitk_bytes": ([_L, _L, _L, _L, _I], _L),
@@ -351,6 +353,46 @@ def _norm_quantize(x: torch.Tensor, kind: int, gamma, beta, eps: float, s_a_out,
         q = q.reshape(orig_shape)
         s = s.reshape(*orig_shape[:-1])
     return q, s
+
+
+def norm_rotate_quantize(x: torch.Tensor, *, norm: str = "layer", weight: torch.Tensor | None = None,
+                         bias: torch.Tensor | None = None, eps: float = 1e-6, rot_size: int = 0,
+                         w_in: int | None = None, smoothrot: PreparedFactors | None = None,
+                         perm: torch.Tensor | None = None, s_a_out: torch.Tensor | None = None,
+                         x_int8_out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """LayerNorm ("layer") or RMSNorm ("rms") of each row, optional affine
+    (adaptive LayerNorm passes weight = 1 + scale, bias = shift), rounded once to
+    x.dtype, then rotate_quantize on the result -- one kernel, one HBM pass.
+
+    Equals rotate_quantize(RN_dtype(norm(x) * weight + bias), ...) with the row
+    statistics in fp64; the block-input fusion in front of the prep of
+    _ops.py:337-365 (no reference entry point fuses the two).  f16/bf16 rows,
+    K and w_in multiples of 16.  Returns (x_int8 [M, w_in], s_a [M] float32)."""
+    _need_cuda(x)
+    kind = {"layer": IC_NORM_LAYER, "rms": IC_NORM_RMS}.get(norm)
+    if kind is None:
+        raise ValueError(f"norm must be 'layer' or 'rms', got {norm!r}")
+    x2 = _rows(x)
+    M, K_in = x2.shape
+    R = int(rot_size)
+    if R not in VALID_ROT_SIZES:
+        raise ValueError(f"rot_size must be one of {VALID_ROT_SIZES}, got {R}")
+    K_r = ((K_in + R - 1) // R) * R if R else K_in
+    K_w = max(int(w_in) if w_in is not None else K_r, K_r)
+    dt = _dt(x2.dtype, "norm_rotate_quantize")
+    if smoothrot is not None and (smoothrot.dtype != x2.dtype or smoothrot.K != K_in):
+        raise ValueError("SmoothRot factors were prepared for another dtype or width")
+    if perm is not None and (perm.dtype != torch.int32 or perm.numel() != K_w or not perm.is_cuda):
+        raise ValueError("perm must be an int32 device tensor of length w_in (see prepare_perm)")
+    w = _f32_vec(weight, K_in, "weight", x2.device)
+    b = _f32_vec(bias, K_in, "bias", x2.device)
+    s_a = _alloc_or_reuse((M,), torch.float32, x2.device, s_a_out)
+    q = _alloc_or_reuse((M, K_w), torch.int8, x2.device, x_int8_out)
+    with torch.cuda.device(x2.device):
+        _call("ic_norm_rotate_quantize", _ptr(x2), dt, M, K_in, x2.stride(0), kind, _ptr(w), _ptr(b), float(eps),
+              _ptr(smoothrot.rcp) if smoothrot else None, _ptr(smoothrot.fdt) if smoothrot else None, R, K_w,
+              _ptr(perm), _ptr(q), q.stride(0), _ptr(s_a), _stream(x2))
+    return q, s_a
 
 
 def _cpu_quant_reshaped(y: torch.Tensor, orig_shape):

@@ -28,6 +28,9 @@ struct ic_rotq_args {
   const int32_t* perm; const float* sm_rcp; const float* sm_f;
   int8_t* q_out; int64_t ldq; float* s_out;
   void* y_out; int64_t ldy;
+  // row normalisation applied first (ic_norm_rotate_quantize): kind
+  // IC_NORM_LAYER / IC_NORM_RMS, optional f32 [K_in] scale and shift, eps
+  int norm = 0; const float* nw = nullptr; const float* nb = nullptr; float eps = 0.0f;
 };
 
 typedef uint16_t u16;

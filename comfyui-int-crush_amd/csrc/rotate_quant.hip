@@ -392,6 +392,30 @@ int ic_rotate_quantize(const void* x, int dtype, int64_t M, int64_t K_in, int64_
   return run_rotq(&a, true, stream);
 }
 
+int ic_norm_rotate_quantize(const void* x, int dtype, int64_t M, int64_t K_in, int64_t ldx, int norm_kind,
+                            const float* weight, const float* bias, float eps, const float* sr_rcp,
+                            const float* sr_f, int rot_size, int64_t K_w, const int32_t* perm, int8_t* q_out,
+                            int64_t ldq, float* s_out, void* stream) {
+  const char* who = "ic_norm_rotate_quantize";
+  ic_rotq_args a{x, dtype, M, K_in, ldx, sr_rcp, sr_f, rot_size, K_w, perm, nullptr, nullptr,
+                 q_out, ldq, s_out, nullptr, 0, norm_kind, weight, bias, eps};
+  if (norm_kind != IC_NORM_LAYER && norm_kind != IC_NORM_RMS)
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: norm_kind must be IC_NORM_LAYER or IC_NORM_RMS", who);
+  if (!(eps >= 0.0f)) return ic_set_error(IC_ERR_INVALID_ARG, "%s: eps must be >= 0", who);
+  int rc = check_rotq(&a, true, who);
+  if (rc) return rc;
+  if (a.M == 0) return IC_OK;
+  auto al16 = [](const void* p) { return (((uintptr_t)p) & 15) == 0; };
+  if (!fast_path_ok(a) || !al16(weight) || !al16(bias))
+    return ic_set_error(IC_ERR_UNSUPPORTED,
+                        "%s: needs f16/bf16 rows with K_in and K_w multiples of 16, K_w <= %d, 16-byte aligned "
+                        "rows, factors, perm, weight and bias", who, kTile * kMaxTiles);
+  hipStream_t st = (hipStream_t)stream;
+  const hipError_t e = dtype == IC_DTYPE_F16 ? ic_rq_norm_f16(a, st) : ic_rq_norm_bf16(a, st);
+  if (e != hipSuccess) return ic_set_error(IC_ERR_LAUNCH, "%s: %s", who, hipGetErrorString(e));
+  return IC_OK;
+}
+
 int ic_prepare_activation(const void* x, int dtype, int64_t M, int64_t K_in, int64_t ldx,
                           const float* sr_rcp, const float* sr_f, int rot_size, int64_t K_w,
                           const int32_t* perm, const float* sm_rcp, const float* sm_f,

@@ -1,7 +1,8 @@
 // Fast path of the fused prep + quantize (the general kernel and the
 // arithmetic it shares with this one are described in rotate_quant.hip).
 // Included by one translation unit per activation dtype and instantiation set
-// (rq_fast_{f16,bf16}{,_plain,_both}.hip) so the sets compile in parallel.
+// (rq_fast_{f16,bf16}{,_plain,_both}.hip, and rq_norm_{f16,bf16}.hip for the
+// normalising variants) so the sets compile in parallel.
 #pragma once
 #include "rq_common.h"
 
@@ -74,15 +75,38 @@ template <int TILE> constexpr int xbuf_doubles() { return TILE + 2 * (TILE / 16)
 IC_DEV int rbaddr(int p) { return p + 16 * (p >> 8); }
 template <int NT, int TILE> constexpr int rowbuf_len() { return NT * TILE + 16 * (NT * TILE / 256); }
 
+// Row sum over the workgroup in fp64 (TH/64 waves; red holds TH/64 doubles).
+template <int TH>
+IC_DEV double block_sum_f64(double v, double* red) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  __syncthreads();  // red is free again
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  double t = red[0];
+#pragma unroll
+  for (int w = 1; w < TH / 64; ++w) t += red[w];
+  return t;
+}
+
 // TH threads per workgroup (256, or 192 = three waves for rows of up to 3072
 // or 6144 values with R <= 256, whose Hadamard exchange stays inside a wave):
 // a tile is TH * 16 positions.
-template <int DT, int LOG4R, int NT, int VAR, int TH>
+//
+// NORM (IC_NORM_LAYER / IC_NORM_RMS, ic_norm_rotate_quantize): before the
+// prep, the row is normalised and rounded once to DT,
+//   y = RN_dt(f32(f32(f32(x - mean) * rstd) * nw[k]) + nb[k])     (LayerNorm)
+//   y = RN_dt(f32(f32(x * rstd) * nw[k]) + nb[k])                  (RMSNorm)
+// (nw / nb optional), mean = RN32(S1 / K_in) and rstd = RN32(1 / sqrt(V / K_in
+// + eps)) from fp64 sums over the row the registers already hold.  The prep
+// then treats y as its input: the same arithmetic as the chain normalise ->
+// activation tensor -> rotate_quantize, without the tensor.
+template <int DT, int LOG4R, int NT, int VAR, int TH, int NORM = 0>
 __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_fast_kernel(
     const u16* __restrict__ x, int64_t ldx, int M, int K_in, int K_r,
     const float* __restrict__ sr_rcp, const float* __restrict__ sr_f, int K_w,
     const int32_t* __restrict__ perm, int8_t* __restrict__ q_out, int64_t ldq,
-    float* __restrict__ s_out) {
+    float* __restrict__ s_out, const float* __restrict__ nw, const float* __restrict__ nb, float eps) {
   constexpr int RC = LOG4R <= 2 ? 0 : (LOG4R <= 4 ? 1 : 2);
   constexpr bool XCH = LOG4R >= 3;
   constexpr int kTile = TH * 16;  // positions per tile
@@ -90,6 +114,7 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
   __shared__ double xbuf[XCH ? xbuf_doubles<kTile>() : 2];
   __shared__ __attribute__((aligned(16))) u16 rowbuf[rowbuf_len<NT, kTile>()];
   __shared__ float red[TH / 64];
+  __shared__ double red_d[NORM != 0 ? TH / 64 : 1];
 
   constexpr bool PLAIN = VAR == kRqPlain;
   const int t = threadIdx.x;
@@ -150,6 +175,42 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
   for (; row < M; row += gridDim.x) {
     const int next = row + gridDim.x;
     __syncthreads();  // the previous row's gather is done with rowbuf and red
+    float n_mean = 0.0f, n_rstd = 1.0f;
+    if constexpr (NORM != 0) {
+      // row statistics from the registers (runs at or past K_in add nothing)
+      double s1 = 0.0;
+#pragma unroll
+      for (int c = 0; c < NT; ++c) {
+        if (c * kTile + 16 * t >= K_in) continue;
+        float xs[16];
+        unpack8<DT>(xr[c][0], xs);
+        unpack8<DT>(xr[c][1], xs + 8);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) s1 += NORM == IC_NORM_LAYER ? (double)xs[j] : (double)xs[j] * (double)xs[j];
+      }
+      s1 = block_sum_f64<TH>(s1, red_d);
+      if constexpr (NORM == IC_NORM_LAYER) {
+        const double mean = s1 / K_in;
+        double s2 = 0.0;
+#pragma unroll
+        for (int c = 0; c < NT; ++c) {
+          if (c * kTile + 16 * t >= K_in) continue;
+          float xs[16];
+          unpack8<DT>(xr[c][0], xs);
+          unpack8<DT>(xr[c][1], xs + 8);
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const double d = (double)xs[j] - mean;
+            s2 += d * d;
+          }
+        }
+        s2 = block_sum_f64<TH>(s2, red_d);
+        n_mean = (float)mean;
+        n_rstd = (float)(1.0 / __builtin_sqrt(s2 / K_in + (double)eps));
+      } else {
+        n_rstd = (float)(1.0 / __builtin_sqrt(s1 / K_in + (double)eps));
+      }
+    }
     float amax = 0.0f;
 #pragma unroll
     for (int c = 0; c < NT; ++c) {
@@ -164,6 +225,28 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
         float xs[16];
         unpack8<DT>(xa, xs);
         unpack8<DT>(xb, xs + 8);
+        float xn[NORM != 0 ? 16 : 1];  // normalised run, the divide's input
+        if constexpr (NORM != 0) {
+          if (p0 < K_in) {  // pad runs stay zero
+            float w[16], b[16];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const v4f wv = nw != nullptr ? ((const v4f*)(nw + p0))[i] : v4f{1.0f, 1.0f, 1.0f, 1.0f};
+              const v4f bv = nb != nullptr ? ((const v4f*)(nb + p0))[i] : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+              w[4 * i] = wv.x; w[4 * i + 1] = wv.y; w[4 * i + 2] = wv.z; w[4 * i + 3] = wv.w;
+              b[4 * i] = bv.x; b[4 * i + 1] = bv.y; b[4 * i + 2] = bv.z; b[4 * i + 3] = bv.w;
+            }
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+              float y = NORM == IC_NORM_LAYER ? (xs[j] - n_mean) * n_rstd : xs[j] * n_rstd;
+              if (nw != nullptr) y = y * w[j];
+              if (nb != nullptr) y = y + b[j];
+              xs[j] = round_to_dt<DT>(y);
+            }
+          }
+#pragma unroll
+          for (int j = 0; j < 16; ++j) xn[j] = xs[j];
+        }
         if (has_sr) {
           // fast path valid for products in DT's normal range; zeros and
           // pad runs take the exact path, which returns the same signed zero
@@ -179,8 +262,13 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
           if (__builtin_expect(!(pmin >= dt_min_normal<DT>()) || nonfinite, 0)) {
             if (p0 < K_in) {
               float xo[16];
-              unpack8<DT>(xa, xo);
-              unpack8<DT>(xb, xo + 8);
+              if constexpr (NORM != 0) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) xo[j] = xn[j];
+              } else {
+                unpack8<DT>(xa, xo);
+                unpack8<DT>(xb, xo + 8);
+              }
 #pragma unroll
               for (int j = 0; j < 16; ++j) xs[j] = div_round_dt<DT>(xo[j], rc[PLAIN ? 0 : c][j], sr_f, p0 + j);
             } else {
@@ -395,35 +483,35 @@ int persistent_grid(Kern kern, int threads, int64_t M) {
   return (int)(M < g ? M : g);
 }
 
-template <int DT, int LOG4R, int NT, int VAR, int TH = kThreads>
+template <int DT, int LOG4R, int NT, int VAR, int TH = kThreads, int NORM = 0>
 hipError_t launch_fast_t(const ic_rotq_args& a, hipStream_t st) {
-  auto kern = rq_fast_kernel<DT, LOG4R, NT, VAR, TH>;
+  auto kern = rq_fast_kernel<DT, LOG4R, NT, VAR, TH, NORM>;
   const int64_t K_r = LOG4R == 0 ? a.K_in : ((a.K_in + a.rot_size - 1) / a.rot_size) * a.rot_size;
   kern<<<dim3(persistent_grid(kern, TH, a.M)), dim3(TH), 0, st>>>(
       (const u16*)a.x, a.ldx, (int)a.M, (int)a.K_in, (int)K_r, a.sr_rcp, a.sr_f, (int)a.K_w, a.perm,
-      a.q_out, a.ldq, a.s_out);
+      a.q_out, a.ldq, a.s_out, a.nw, a.nb, a.eps);
   return hipGetLastError();
 }
 
-template <int DT, int LOG4R, int VAR>
+template <int DT, int LOG4R, int VAR, int NORM = 0>
 hipError_t launch_fast_nt(const ic_rotq_args& a, hipStream_t st) {
   if constexpr (LOG4R <= 4) {
     // three-wave workgroups where their tile fits the row more tightly
     // (3072: one full tile instead of 3/4 of one; 4097..6144: two)
     constexpr int T3 = 192 * 16;
-    if (a.K_w <= T3 && a.K_w > kTile / 2) return launch_fast_t<DT, LOG4R, 1, VAR, 192>(a, st);
-    if (a.K_w > kTile && a.K_w <= 2 * T3) return launch_fast_t<DT, LOG4R, 2, VAR, 192>(a, st);
+    if (a.K_w <= T3 && a.K_w > kTile / 2) return launch_fast_t<DT, LOG4R, 1, VAR, 192, NORM>(a, st);
+    if (a.K_w > kTile && a.K_w <= 2 * T3) return launch_fast_t<DT, LOG4R, 2, VAR, 192, NORM>(a, st);
   }
-  if (a.K_w <= kTile) return launch_fast_t<DT, LOG4R, 1, VAR>(a, st);
-  if (a.K_w <= 2 * kTile) return launch_fast_t<DT, LOG4R, 2, VAR>(a, st);
-  if (a.K_w <= 3 * kTile) return launch_fast_t<DT, LOG4R, 3, VAR>(a, st);
-  return launch_fast_t<DT, LOG4R, 4, VAR>(a, st);
+  if (a.K_w <= kTile) return launch_fast_t<DT, LOG4R, 1, VAR, kThreads, NORM>(a, st);
+  if (a.K_w <= 2 * kTile) return launch_fast_t<DT, LOG4R, 2, VAR, kThreads, NORM>(a, st);
+  if (a.K_w <= 3 * kTile) return launch_fast_t<DT, LOG4R, 3, VAR, kThreads, NORM>(a, st);
+  return launch_fast_t<DT, LOG4R, 4, VAR, kThreads, NORM>(a, st);
 }
 
 // VAR must match the arguments (the per-dtype dispatcher routes on them).
-template <int DT, int VAR>
+template <int DT, int VAR, int NORM = 0>
 hipError_t launch_fast(const ic_rotq_args& a, hipStream_t st) {
-  if (VAR == kRqPlain && a.rot_size == 0 && a.K_w == a.K_in && a.K_in <= 32 * 512) {
+  if (NORM == 0 && VAR == kRqPlain && a.rot_size == 0 && a.K_w == a.K_in && a.K_in <= 32 * 512) {
     const unsigned grid = (unsigned)((a.M + 3) / 4);
     if (a.K_in <= 8 * 512)
       quant_wave_kernel<DT, 8><<<grid, kThreads, 0, st>>>((const u16*)a.x, a.ldx, (int)a.M, (int)a.K_in, a.q_out, a.ldq, a.s_out);
@@ -434,12 +522,12 @@ hipError_t launch_fast(const ic_rotq_args& a, hipStream_t st) {
     return hipGetLastError();
   }
   switch (a.rot_size) {
-    case 0: return launch_fast_nt<DT, 0, VAR>(a, st);
-    case 16: return launch_fast_nt<DT, 2, VAR>(a, st);
-    case 64: return launch_fast_nt<DT, 3, VAR>(a, st);
-    case 256: return launch_fast_nt<DT, 4, VAR>(a, st);
-    case 1024: return launch_fast_nt<DT, 5, VAR>(a, st);
-    case 4096: return launch_fast_nt<DT, 6, VAR>(a, st);
+    case 0: return launch_fast_nt<DT, 0, VAR, NORM>(a, st);
+    case 16: return launch_fast_nt<DT, 2, VAR, NORM>(a, st);
+    case 64: return launch_fast_nt<DT, 3, VAR, NORM>(a, st);
+    case 256: return launch_fast_nt<DT, 4, VAR, NORM>(a, st);
+    case 1024: return launch_fast_nt<DT, 5, VAR, NORM>(a, st);
+    case 4096: return launch_fast_nt<DT, 6, VAR, NORM>(a, st);
   }
   return hipErrorInvalidValue;
 }

@@ -94,6 +94,28 @@ int ic_norm_quantize(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx
                      float* s_out, void* stream);
 
 /*
+ * LayerNorm / RMSNorm of each row fused in front of ic_rotate_quantize, for the
+ * pre-projection activations of a transformer block (the block-input fusion the
+ * reference's fused norm quantizers, kernels/triton_quantize.py:201-459, stop
+ * short of: they quantize without the SmoothRot / Hadamard / PermuQuant prep,
+ * so a rotated INT4 layer cannot use them).  No reference entry point fuses the
+ * two; callers that build y = norm(x) * (1 + scale) + shift and then call
+ * rotate_quantize (_ops.py:337-365 on y) use this instead:
+ *   y = RN_dtype(norm(x) * weight + bias)   weight / bias optional f32 [K_in]
+ *       (adaptive LayerNorm: weight = 1 + scale, bias = shift); statistics over
+ *       the K_in values in fp64, y formed in f32 and rounded once;
+ *   then exactly ic_rotate_quantize on y (SmoothRot divide, Hadamard, pad, perm,
+ *   per-token INT8).
+ * f16/bf16 rows only, with K_in and K_w multiples of 16, K_w <= ic_max_fused_row(),
+ * 16-byte aligned rows, factors, perm, weight and bias; other shapes return
+ * IC_ERR_UNSUPPORTED.
+ */
+int ic_norm_rotate_quantize(const void* x, int dtype, int64_t M, int64_t K_in, int64_t ldx, int norm_kind,
+                            const float* weight, const float* bias, float eps, const float* sr_rcp,
+                            const float* sr_f, int rot_size, int64_t K_w, const int32_t* perm, int8_t* q_out,
+                            int64_t ldq, float* s_out, void* stream);
+
+/*
  * W8A8: out[M,N] = f32(xq . w^T) * (s_a[m] * s_w[n]) + bias[n].
  * Replaces fused_int8_gemm_dequant, kernels/triton_int8_gemm.py:135-205.
  *   xq [M,K] int8, w [N,K] int8, s_a [M] f32, s_w [N] f32, bias [N] (bias_dtype) or NULL.

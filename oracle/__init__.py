@@ -264,13 +264,15 @@ def normalize_rows(x, kind: str, gamma=None, beta=None, eps: float = 1e-5) -> np
         mean = mean64.astype(np.float32)
         rstd = (1.0 / np.sqrt(var + e)).astype(np.float32)
         y = (xv - mean[:, None]) * rstd[:, None]
-        y = y * np.asarray(gamma, np.float32)[None, :]
+    elif kind == "rms":
+        rstd = (1.0 / np.sqrt((x64 * x64).sum(axis=1) / K + e)).astype(np.float32)
+        y = xv * rstd[:, None]
+    if kind in ("layer", "rms"):
+        if gamma is not None:
+            y = y * np.asarray(gamma, np.float32)[None, :]
         if beta is not None:
             y = y + np.asarray(beta, np.float32)[None, :]
         return y.astype(np.float32)
-    if kind == "rms":
-        rstd = (1.0 / np.sqrt((x64 * x64).sum(axis=1) / K + e)).astype(np.float32)
-        return ((xv * rstd[:, None]) * np.asarray(gamma, np.float32)[None, :]).astype(np.float32)
     if kind == "softmax":
         m = xv.max(axis=1)
         ex = np.exp((xv - m[:, None]).astype(np.float64)).astype(np.float32)
@@ -283,6 +285,13 @@ def norm_quantize(x, kind: str, gamma=None, beta=None, eps: float = 1e-5):
     """normalize_rows() then the GPU quantization rule: the full contract of
     ic_norm_quantize.  Returns (int8 [M, K], float32 [M])."""
     return quantize(normalize_rows(x, kind, gamma, beta, eps))
+
+
+def norm_rotate_quantize(x, dtype: int, kind: str, weight=None, bias=None, eps: float = 1e-6, **prep_kw):
+    """The contract of ic_norm_rotate_quantize: normalize_rows() (optional
+    affine), rounded once to the activation dtype, then rotate_quantize()."""
+    y = normalize_rows(to_dtype_values(x, dtype), kind, weight, bias, eps)
+    return rotate_quantize(round_dtype(y, dtype), dtype, **prep_kw)
 
 
 # ---------------------------------------------------------------- weights

@@ -6,7 +6,9 @@ against the reference tests' own PyTorch formulas at their own bar (codes within
 +-1, tests/test_w8a8_fused_kernels.py:31-57, :73-77 of the reference), against
 closed forms, and show a planted mistake fails; they also check the mirror's CPU
 branch is the reference CPU branch bit for bit.  GPU tests compare the
-ic_norm_quantize kernel with the oracle.
+ic_norm_quantize kernel with the oracle.  The block-input fusion
+ic_norm_rotate_quantize (normalise, round to the dtype, rotate_quantize) is
+checked against the oracle's composition of the same steps.
 """
 from __future__ import annotations
 
@@ -16,6 +18,7 @@ import torch
 import torch.nn.functional as F
 
 KINDS = ("layer", "rms", "softmax")
+DT = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 REF_SHAPES = [(1, 64), (4, 256), (16, 1024), (64, 4096)]  # the reference tests' shapes
 
 
@@ -225,3 +228,73 @@ def test_norm_quantize_buffers_shapes_and_edge_rows(rt, dev):
     q, s = rt.fused_softmax_quantize(torch.tensor([[1000.0, -1000.0, 0.0, 500.0]] * 8, device=dev))
     assert not torch.isnan(s).any().item() and (q >= 0).all().item()
     assert q[:, 0].eq(127).all().item()
+
+
+# ---------------------------------------------------------------- norm + rotate + quantize
+def test_oracle_norm_rotate_is_the_composition(oracle):
+    """The oracle contract of ic_norm_rotate_quantize is its definition:
+    normalise (fp64 statistics, f32 arithmetic), round once to the activation
+    dtype, then the pinned rotate_quantize.  Cross-check the first half against
+    F.layer_norm in f32 (rounded to bf16): the prepared codes agree within one
+    code, the reference tests' own bar for a fused norm quantizer."""
+    K = 3072
+    x, _, _ = _inputs(64, K, 41, dtype=torch.bfloat16)
+    g = torch.Generator().manual_seed(42)
+    scale = torch.randn(K, generator=g) * 0.1
+    shift = torch.randn(K, generator=g) * 0.1
+    sr = torch.exp(torch.randn(K, generator=g) * 0.5)
+    perm = torch.randperm(K, generator=g)
+    kw = dict(smoothrot=sr.numpy(), rot_size=256, perm=perm.numpy())
+    q, s = oracle.norm_rotate_quantize(x, oracle.DT_BF16, "layer", (1 + scale).numpy(), shift.numpy(), 1e-6, **kw)
+    y = (F.layer_norm(x.float(), (K,), eps=1e-6) * (1 + scale) + shift).to(torch.bfloat16)
+    rq, rs = oracle.rotate_quantize(y, oracle.DT_BF16, **kw)
+    assert np.abs(q.astype(np.int32) - rq.astype(np.int32)).max() <= 1
+    assert np.allclose(s, rs, rtol=1e-2)
+
+
+NRQ_CASES = [  # (M, K_in, w_in, rot_size, smoothrot+perm, affine)
+    (4608, 3072, 3072, 256, True, True),     # Flux pre-qkv / pre-MLP rows
+    (512, 3072, 3072, 256, True, False),
+    (300, 5120, 5120, 1024, True, True),     # Wan hidden rows, cross-wave rotation
+    (64, 13824, 14336, 1024, False, True),   # Wan FFN-down width, zero pad to the weight K
+    (40, 2048, 2048, 16, True, True),
+    (40, 4096, 4096, 0, True, True),         # no rotation: norm + divide + perm + quantize
+    (17, 1024, 1024, 64, False, False),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", NRQ_CASES)
+@pytest.mark.parametrize("norm", ["layer", "rms"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_norm_rotate_quantize_matches_oracle(rt, oracle, dev, case, norm, dtype):
+    """ic_norm_rotate_quantize against the oracle's composition, bit for bit:
+    the normalised values are rounded once to the dtype, after which every step
+    is the exactly defined rotate_quantize."""
+    M, K, K_w, R, with_prep, affine = case
+    g = torch.Generator().manual_seed(M + K + R)
+    x = (torch.randn(M, K, generator=g) * 3 + 0.5).to(dtype)
+    w = (1 + 0.2 * torch.randn(K, generator=g)) if affine else None
+    b = 0.1 * torch.randn(K, generator=g) if affine else None
+    sr = torch.exp(torch.randn(K, generator=g) * 0.5) if with_prep else None
+    perm = torch.randperm(K_w, generator=g) if with_prep else None
+    q, s = rt.norm_rotate_quantize(
+        x.to(dev), norm=norm, weight=w.to(dev) if w is not None else None,
+        bias=b.to(dev) if b is not None else None, eps=1e-6, rot_size=R, w_in=K_w,
+        smoothrot=rt.prepare_factors(sr.to(dev), dtype) if sr is not None else None,
+        perm=rt.prepare_perm(perm.to(dev), K_w) if perm is not None else None)
+    rq, rs = oracle.norm_rotate_quantize(
+        x, DT[dtype], norm, w.numpy() if w is not None else None, b.numpy() if b is not None else None, 1e-6,
+        smoothrot=sr.numpy() if sr is not None else None, rot_size=R, w_in=K_w,
+        perm=perm.numpy() if perm is not None else None)
+    assert np.array_equal(s.cpu().numpy(), rs)
+    assert np.array_equal(q.cpu().numpy(), rq)
+
+
+@pytest.mark.gpu
+def test_norm_rotate_quantize_rejects_unsupported(rt, dev):
+    x = torch.randn(4, 100, dtype=torch.float16, device=dev)  # K not a multiple of 16
+    with pytest.raises(RuntimeError, match="ic_norm_rotate_quantize"):
+        rt.norm_rotate_quantize(x, norm="layer", rot_size=0)
+    with pytest.raises(ValueError):
+        rt.norm_rotate_quantize(torch.randn(4, 64, dtype=torch.float16, device=dev), norm="batch")
