@@ -14,7 +14,10 @@ the GEMV kernels: double-block img_mod/txt_mod as rotated W4A8, single-block
 modulation as W4A16 (the naming rule of _ops.py:30-32 and :699-706 leaves
 a layer whose name contains "modulation" unrotated, and :843-851 sends an
 unrotated INT4 layer to W4A16).  Attention is torch's SDPA on its flash or
-memory-efficient backend; LayerNorm, modulation, QK RMSNorm, RoPE, GELU,
+memory-efficient backend.  The adaptive LayerNorm in front of qkv and MLP-up
+(LayerNorm without affine, then (1 + scale) * . + shift from the modulation)
+is fused into those linears' prep: one norm_rotate_quantize launch per linear
+reads the block input and writes its INT8 codes.  QK RMSNorm, RoPE, GELU,
 residual gates, the embedders and the final layer are torch ops in bf16 (the
 embedders and final layer are unquantized bf16 linears).
 
@@ -64,6 +67,16 @@ class QLinear:
     def quantize(self, rt, x, q_out=None, s_out=None):
         return rt.rotate_quantize(x, rot_size=ROT_SIZE, w_in=self.K, smoothrot=self.sr, perm=self.perm,
                                   s_a_out=s_out, x_int8_out=q_out)
+
+    def norm_quantize(self, rt, x, weight, bias, q_out=None, s_out=None):
+        """Adaptive LayerNorm (weight = 1 + scale, bias = shift) fused into the prep."""
+        return rt.norm_rotate_quantize(x, norm="layer", weight=weight, bias=bias, eps=1e-6, rot_size=ROT_SIZE,
+                                       w_in=self.K, smoothrot=self.sr, perm=self.perm, s_a_out=s_out,
+                                       x_int8_out=q_out)
+
+    def norm_call(self, rt, x, weight, bias):
+        q, s_a = self.norm_quantize(rt, x, weight, bias)
+        return self.gemm(rt, q, s_a, x.dtype)
 
     def gemm(self, rt, q, s_a, act, out=None):
         return rt.gemm_w4a8(q, self.w, self.s_w, s_a, bias=self.b, out_dtype=act, out=out)
@@ -224,6 +237,11 @@ class FluxStep:
         q, s_a = layer.quantize(self.rt, vec_silu)
         return layer.gemm(self.rt, q, s_a, self.act).chunk(6, dim=-1)
 
+    @staticmethod
+    def _ada(shift, scale):
+        """(weight, bias) of the fused adaptive LayerNorm: 1 + scale and shift, f32."""
+        return (1.0 + scale.float()).reshape(-1), shift.float().reshape(-1)
+
     def _double_block(self, blk, img, txt, vec_silu, freqs):
         import torch
         import torch.nn.functional as F
@@ -231,15 +249,15 @@ class FluxStep:
         rt = self.rt
         im = self._mod_w4a8(blk["img_mod"], vec_silu)
         tm = self._mod_w4a8(blk["txt_mod"], vec_silu)
-        iq, ik, iv = self._split_heads(blk["img_qkv"](rt, self._modulate(img, im[0], im[1])), blk["qk_scale"])
-        tq, tk, tv = self._split_heads(blk["txt_qkv"](rt, self._modulate(txt, tm[0], tm[1])), blk["qk_scale"])
+        iq, ik, iv = self._split_heads(blk["img_qkv"].norm_call(rt, img, *self._ada(im[0], im[1])), blk["qk_scale"])
+        tq, tk, tv = self._split_heads(blk["txt_qkv"].norm_call(rt, txt, *self._ada(tm[0], tm[1])), blk["qk_scale"])
         attn = self.attention(torch.cat((tq, iq), 1), torch.cat((tk, ik), 1), torch.cat((tv, iv), 1), freqs)
         t_a, i_a = attn[:TXT_TOKENS], attn[TXT_TOKENS:]
         img = torch.addcmul(img, im[2], blk["img_proj"](rt, i_a))
-        h = F.gelu(blk["img_mlp_up"](rt, self._modulate(img, im[3], im[4])), approximate="tanh")
+        h = F.gelu(blk["img_mlp_up"].norm_call(rt, img, *self._ada(im[3], im[4])), approximate="tanh")
         img = torch.addcmul(img, im[5], blk["img_mlp_down"](rt, h))
         txt = torch.addcmul(txt, tm[2], blk["txt_proj"](rt, t_a))
-        h = F.gelu(blk["txt_mlp_up"](rt, self._modulate(txt, tm[3], tm[4])), approximate="tanh")
+        h = F.gelu(blk["txt_mlp_up"].norm_call(rt, txt, *self._ada(tm[3], tm[4])), approximate="tanh")
         txt = torch.addcmul(txt, tm[5], blk["txt_mlp_down"](rt, h))
         return img, txt
 
@@ -249,9 +267,9 @@ class FluxStep:
 
         rt = self.rt
         shift, scale, gate = blk["mod"](rt, vec_silu).chunk(6, dim=-1)[:3]
-        xn = self._modulate(x, shift, scale)
-        q, k, v = self._split_heads(blk["qkv"](rt, xn), blk["qk_scale"])
-        up = blk["mlp_up"](rt, xn)
+        ada = self._ada(shift, scale)
+        q, k, v = self._split_heads(blk["qkv"].norm_call(rt, x, *ada), blk["qk_scale"])
+        up = blk["mlp_up"].norm_call(rt, x, *ada)
         out = blk["proj"](rt, self.attention(q, k, v, freqs))
         out = out + blk["mlp_down"](rt, F.gelu(up, approximate="tanh"))
         return torch.addcmul(x, gate, out)
@@ -297,6 +315,9 @@ class FluxStep:
         out = {(M, l.N): torch.empty(M, l.N, dtype=act, device=dev) for M, l in lin}
         for M, l in lin:  # valid codes and scales for the GEMM-only part
             l.quantize(rt, x[(M, l.K)], q[(M, l.K)], s_a[M])
+        ada_w = 1.0 + 0.1 * torch.randn(HID, generator=g, device=dev)
+        ada_b = 0.1 * torch.randn(HID, generator=g, device=dev)
+        normed = {id(l) for name in ("qkv", "mlp_up") for l in self._kind_layers(name)}
         vec_silu = torch.randn(1, HID, generator=g, device=dev).to(act)
         S = IMG_TOKENS + TXT_TOKENS
         qkv = [torch.randn(HEADS, S, HEAD_DIM, generator=g, device=dev).to(act) for _ in range(3)]
@@ -308,7 +329,10 @@ class FluxStep:
 
         def prep():
             for M, l in lin:
-                l.quantize(rt, x[(M, l.K)], q[(M, l.K)], s_a[M])
+                if id(l) in normed:
+                    l.norm_quantize(rt, x[(M, l.K)], ada_w, ada_b, q[(M, l.K)], s_a[M])
+                else:
+                    l.quantize(rt, x[(M, l.K)], q[(M, l.K)], s_a[M])
 
         def modulation():
             for blk in self.double:

@@ -5,8 +5,8 @@
 // fused_softmax_quantize (:462-567).
 //
 // Arithmetic (per row of K values x, read as f32):
-//   LayerNorm  mean = RN32(S1 / K), S1 = sum x in fp64;
-//              var = sum (x - S1/K)^2 / K in fp64; rstd = RN32(1 / sqrt(var + eps));
+//   LayerNorm  mean = RN32(S1 / K), var = max(S2 / K - (S1 / K)^2, 0) with
+//              S1 = sum x, S2 = sum x^2 in fp64; rstd = RN32(1 / sqrt(var + eps));
 //              y = RN32(RN32(x - mean) * rstd) * gamma (+ beta), each step RN32
 //   RMSNorm    rstd = RN32(1 / sqrt(sum x^2 / K + eps)) with the sum in fp64;
 //              y = RN32(x * rstd) * gamma
@@ -121,23 +121,16 @@ __global__ __launch_bounds__(kNQThreads) void norm_quant_kernel(
     }
     RowStats<KIND> st;
     if constexpr (KIND == IC_NORM_LAYER) {
-      double s1 = 0.0;
+      double s1 = 0.0, s2 = 0.0;
 #pragma unroll
       for (int i = 0; i < NC; ++i)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) s1 += (double)v[i][e];
-      const double mean = block_sum(s1, red_d) / K;
-      double s2 = 0.0;
-#pragma unroll
-      for (int i = 0; i < NC; ++i) {
-        if (tid + kNQThreads * i >= nchunks) break;
-#pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const double d = (double)v[i][e] - mean;
-          s2 += d * d;
+          s1 += (double)v[i][e];
+          s2 += (double)v[i][e] * (double)v[i][e];
         }
-      }
-      const double var = block_sum(s2, red_d) / K;
+      const double mean = block_sum(s1, red_d) / K;
+      const double var = __builtin_fmax(block_sum(s2, red_d) / K - mean * mean, 0.0);
       st.a = (float)mean;
       st.b = (float)(1.0 / __builtin_sqrt(var + (double)eps));
     } else if constexpr (KIND == IC_NORM_RMS) {
@@ -215,15 +208,14 @@ __global__ __launch_bounds__(kNQThreads) void norm_quant_generic_kernel(
     const void* xr = (const char*)x + (int64_t)row * ldx * (DT == IC_DTYPE_F32 ? 4 : 2);
     RowStats<KIND> st;
     if constexpr (KIND == IC_NORM_LAYER) {
-      double s1 = 0.0;
-      for (int k = tid; k < K; k += kNQThreads) s1 += (double)ld_as_f32<DT>(xr, k);
-      const double mean = block_sum(s1, red_d) / K;
-      double s2 = 0.0;
+      double s1 = 0.0, s2 = 0.0;
       for (int k = tid; k < K; k += kNQThreads) {
-        const double d = (double)ld_as_f32<DT>(xr, k) - mean;
+        const double d = (double)ld_as_f32<DT>(xr, k);
+        s1 += d;
         s2 += d * d;
       }
-      const double var = block_sum(s2, red_d) / K;
+      const double mean = block_sum(s1, red_d) / K;
+      const double var = __builtin_fmax(block_sum(s2, red_d) / K - mean * mean, 0.0);
       st.a = (float)mean;
       st.b = (float)(1.0 / __builtin_sqrt(var + (double)eps));
     } else if constexpr (KIND == IC_NORM_RMS) {

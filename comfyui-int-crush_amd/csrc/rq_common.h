@@ -69,3 +69,5 @@ hipError_t ic_rq_fast_bf16_both(const ic_rotq_args& a, hipStream_t st);
 // with the row normalisation of a.norm first (rq_norm_{f16,bf16}.hip)
 hipError_t ic_rq_norm_f16(const ic_rotq_args& a, hipStream_t st);
 hipError_t ic_rq_norm_bf16(const ic_rotq_args& a, hipStream_t st);
+hipError_t ic_rq_norm_f16_both(const ic_rotq_args& a, hipStream_t st);
+hipError_t ic_rq_norm_bf16_both(const ic_rotq_args& a, hipStream_t st);

@@ -1,8 +1,8 @@
 // Fast path of the fused prep + quantize (the general kernel and the
 // arithmetic it shares with this one are described in rotate_quant.hip).
 // Included by one translation unit per activation dtype and instantiation set
-// (rq_fast_{f16,bf16}{,_plain,_both}.hip, and rq_norm_{f16,bf16}.hip for the
-// normalising variants) so the sets compile in parallel.
+// (rq_fast_{f16,bf16}{,_plain,_both}.hip, and rq_norm_{f16,bf16}{,_both}.hip
+// for the normalising variants) so the sets compile in parallel.
 #pragma once
 #include "rq_common.h"
 
@@ -75,18 +75,28 @@ template <int TILE> constexpr int xbuf_doubles() { return TILE + 2 * (TILE / 16)
 IC_DEV int rbaddr(int p) { return p + 16 * (p >> 8); }
 template <int NT, int TILE> constexpr int rowbuf_len() { return NT * TILE + 16 * (NT * TILE / 256); }
 
-// Row sum over the workgroup in fp64 (TH/64 waves; red holds TH/64 doubles).
+// Workgroup sums of two fp64 values (TH/64 waves; red holds 2 * TH/64
+// doubles).  The caller's barrier at the top of the row guarantees red is no
+// longer being read, so one barrier suffices.
 template <int TH>
-IC_DEV double block_sum_f64(double v, double* red) {
+IC_DEV void block_sum2_f64(double& a, double& b, double* red) {
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  __syncthreads();  // red is free again
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  for (int o = 32; o >= 1; o >>= 1) {
+    a += __shfl_xor(a, o, 64);
+    b += __shfl_xor(b, o, 64);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    red[2 * (threadIdx.x >> 6)] = a;
+    red[2 * (threadIdx.x >> 6) + 1] = b;
+  }
   __syncthreads();
-  double t = red[0];
+  a = red[0];
+  b = red[1];
 #pragma unroll
-  for (int w = 1; w < TH / 64; ++w) t += red[w];
-  return t;
+  for (int w = 1; w < TH / 64; ++w) {
+    a += red[2 * w];
+    b += red[2 * w + 1];
+  }
 }
 
 // TH threads per workgroup (256, or 192 = three waves for rows of up to 3072
@@ -98,7 +108,9 @@ IC_DEV double block_sum_f64(double v, double* red) {
 //   y = RN_dt(f32(f32(f32(x - mean) * rstd) * nw[k]) + nb[k])     (LayerNorm)
 //   y = RN_dt(f32(f32(x * rstd) * nw[k]) + nb[k])                  (RMSNorm)
 // (nw / nb optional), mean = RN32(S1 / K_in) and rstd = RN32(1 / sqrt(V / K_in
-// + eps)) from fp64 sums over the row the registers already hold.  The prep
+// + eps)) from fp64 sums over the row the registers already hold: one pass,
+// V = S2 - S1^2 / K_in with S1 = sum x, S2 = sum x^2 (the sums of 16-bit
+// values are exact in fp64 for any realistic row).  The prep
 // then treats y as its input: the same arithmetic as the chain normalise ->
 // activation tensor -> rotate_quantize, without the tensor.
 template <int DT, int LOG4R, int NT, int VAR, int TH, int NORM = 0>
@@ -114,7 +126,7 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
   __shared__ double xbuf[XCH ? xbuf_doubles<kTile>() : 2];
   __shared__ __attribute__((aligned(16))) u16 rowbuf[rowbuf_len<NT, kTile>()];
   __shared__ float red[TH / 64];
-  __shared__ double red_d[NORM != 0 ? TH / 64 : 1];
+  __shared__ double red_d[NORM != 0 ? 2 * (TH / 64) : 1];
 
   constexpr bool PLAIN = VAR == kRqPlain;
   const int t = threadIdx.x;
@@ -178,7 +190,7 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
     float n_mean = 0.0f, n_rstd = 1.0f;
     if constexpr (NORM != 0) {
       // row statistics from the registers (runs at or past K_in add nothing)
-      double s1 = 0.0;
+      double s1 = 0.0, s2 = 0.0;
 #pragma unroll
       for (int c = 0; c < NT; ++c) {
         if (c * kTile + 16 * t >= K_in) continue;
@@ -186,29 +198,20 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
         unpack8<DT>(xr[c][0], xs);
         unpack8<DT>(xr[c][1], xs + 8);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) s1 += NORM == IC_NORM_LAYER ? (double)xs[j] : (double)xs[j] * (double)xs[j];
+        for (int j = 0; j < 16; ++j) {
+          const double d = (double)xs[j];
+          if constexpr (NORM == IC_NORM_LAYER) s1 += d;
+          s2 += d * d;
+        }
       }
-      s1 = block_sum_f64<TH>(s1, red_d);
+      block_sum2_f64<TH>(s1, s2, red_d);
       if constexpr (NORM == IC_NORM_LAYER) {
         const double mean = s1 / K_in;
-        double s2 = 0.0;
-#pragma unroll
-        for (int c = 0; c < NT; ++c) {
-          if (c * kTile + 16 * t >= K_in) continue;
-          float xs[16];
-          unpack8<DT>(xr[c][0], xs);
-          unpack8<DT>(xr[c][1], xs + 8);
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const double d = (double)xs[j] - mean;
-            s2 += d * d;
-          }
-        }
-        s2 = block_sum_f64<TH>(s2, red_d);
+        const double var = __builtin_fmax(s2 / K_in - mean * mean, 0.0);
         n_mean = (float)mean;
-        n_rstd = (float)(1.0 / __builtin_sqrt(s2 / K_in + (double)eps));
+        n_rstd = (float)(1.0 / __builtin_sqrt(var + (double)eps));
       } else {
-        n_rstd = (float)(1.0 / __builtin_sqrt(s1 / K_in + (double)eps));
+        n_rstd = (float)(1.0 / __builtin_sqrt(s2 / K_in + (double)eps));
       }
     }
     float amax = 0.0f;

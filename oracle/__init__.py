@@ -248,7 +248,8 @@ def normalize_rows(x, kind: str, gamma=None, beta=None, eps: float = 1e-5) -> np
     softmax), as the canonical arithmetic of this build: row statistics in
     fp64, eps taken as an f32 value, y formed in f32 with one rounding per
     operation:
-      layer    mean = f32(S/K), rstd = f32(1/sqrt(sum (x - S/K)^2 / K + eps)),
+      layer    mean = f32(S1/K), rstd = f32(1/sqrt(max(S2/K - (S1/K)^2, 0) + eps)),
+               S1 = sum x, S2 = sum x^2 (one pass; exact in fp64 for realistic rows),
                y = f32(f32(x - mean) * rstd) * gamma (+ beta)
       rms      rstd = f32(1/sqrt(sum x^2 / K + eps)), y = f32(x * rstd) * gamma
       softmax  m = max x, e = f32(exp(f32(x - m))), inv = f32(1 / sum e), y = e * inv
@@ -260,7 +261,7 @@ def normalize_rows(x, kind: str, gamma=None, beta=None, eps: float = 1e-5) -> np
     x64 = xv.astype(np.float64)
     if kind == "layer":
         mean64 = x64.sum(axis=1) / K
-        var = ((x64 - mean64[:, None]) ** 2).sum(axis=1) / K
+        var = np.maximum((x64 * x64).sum(axis=1) / K - mean64 * mean64, 0.0)
         mean = mean64.astype(np.float32)
         rstd = (1.0 / np.sqrt(var + e)).astype(np.float32)
         y = (xv - mean[:, None]) * rstd[:, None]
