@@ -73,6 +73,9 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "ic_gemm_splitk_bytes": ([_L, _L, _L, _L, _I], _L),
     "ic_gemm_w8a8_ws": ([_P, _L, _L, _L, _P, _L, _L, _P, _P, _P, _I, _P, _I, _L, _P, _L, _P], _I),
     "ic_gemm_w4a8_ws": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _P, _I, _P, _I, _L, _P, _L, _P], _I),
+    "ic_gemm_w8a8_ex": ([_P, _L, _L, _L, _P, _L, _L, _P, _P, _P, _I, _I, _P, _I, _L, _P, _I, _L, _P, _L, _P], _I),
+    "ic_gemm_w4a8_ex": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _P, _I, _I, _P, _I, _L, _P, _I, _L, _P, _L,
+                         _P], _I),
     "ic_gemm_w4a16": ([_P, _I, _L, _L, _L, _P, _L, _L, _P, _L, _P, _I, _P, _L, _P], _I),
     "ic_unpack_int4_to_int8": ([_P, _L, _L, _L, _P, _L, _P], _I),
     "ic_unpack_int4_to_float": ([_P, _P, _L, _L, _L, _L, _P, _I, _L, _P], _I),
@@ -468,22 +471,43 @@ def _splitk_workspace(M: int, N: int, K: int, G: int, int4: bool, device) -> tup
     return torch.empty(nb, dtype=torch.uint8, device=device), nb
 
 
+# Epilogue activation codes (kernels/triton_int8_gemm.py:24-27 for 0-2).
+ACT_NONE, ACT_SILU, ACT_GELU, ACT_GELU_TANH = 0, 1, 2, 3
+
+
+def _epilogue_args(activation: int, residual: torch.Tensor | None, M: int, N: int):
+    """Checked activation code and residual (pointer, dtype code, row stride,
+    tensor kept alive) for the ic_gemm_*_ex entry points."""
+    act = int(activation)
+    if act not in (ACT_NONE, ACT_SILU, ACT_GELU, ACT_GELU_TANH):
+        raise ValueError(f"activation must be 0 (none), 1 (SiLU), 2 (GELU) or 3 (GELU tanh), got {activation}")
+    if residual is None:
+        return act, None, 0, 0, None
+    r = residual.detach()
+    if r.dim() != 2:
+        r = r.reshape(-1, r.shape[-1])
+    if tuple(r.shape) != (M, N):
+        raise ValueError(f"residual shape {tuple(residual.shape)} does not match the output ({M}, {N})")
+    if r.stride(-1) != 1 or r.stride(0) < N:
+        r = r.contiguous()
+    return act, _ptr(r), _dt(r.dtype, "residual"), r.stride(0), r
+
+
 def fused_int8_gemm_dequant(x_int8: torch.Tensor, w_int8: torch.Tensor, s_w: torch.Tensor,
                             s_a: torch.Tensor, bias: torch.Tensor | None = None,
                             out_dtype: torch.dtype = torch.bfloat16, activation: int = 0,
                             residual: torch.Tensor | None = None,
                             out: torch.Tensor | None = None) -> torch.Tensor:
-    """W8A8: f32(x_int8 @ w_int8^T) * (s_a[m] * s_w[n]) + bias, cast to out_dtype.
+    """W8A8: f32(x_int8 @ w_int8^T) * (s_a[m] * s_w[n]) + bias, then the
+    optional activation and residual add in f32, cast to out_dtype.
 
-    Signature of kernels/triton_int8_gemm.py:135-205.  The optional SiLU/GELU
-    and residual epilogues of the reference (unused by its ops layer) are not
-    part of this path.
+    Signature of kernels/triton_int8_gemm.py:135-205, epilogue :119-130:
+    activation 0 none, 1 SiLU, 2 GELU (erf); 3 adds GELU with the tanh
+    approximation.  residual [M, N] f16/bf16/f32 is added after the activation.
     """
     assert x_int8.dtype == torch.int8, f"x_int8 must be int8, got {x_int8.dtype}"
     assert w_int8.dtype == torch.int8, f"w_int8 must be int8, got {w_int8.dtype}"
-    if activation != 0 or residual is not None:
-        raise NotImplementedError("activation/residual epilogues are not implemented on gfx950")
-    _need_cuda(x_int8, w_int8, s_w, s_a, bias)
+    _need_cuda(x_int8, w_int8, s_w, s_a, bias, residual)
     M, K = x_int8.shape
     N, K_w = w_int8.shape
     assert K == K_w, f"K mismatch: {K} vs {K_w}"
@@ -494,32 +518,38 @@ def fused_int8_gemm_dequant(x_int8: torch.Tensor, w_int8: torch.Tensor, s_w: tor
         raise ValueError(f"s_w must hold one scale per output channel ({N}), got {sw.numel()}")
     sa = s_a.detach().reshape(-1).to(torch.float32).contiguous()
     bp, bdt, _keep = _bias_args(bias, N)
+    act, rp, rdt, ldr, _rkeep = _epilogue_args(activation, residual, M, N)
     c = _out_buffer(out, M, N, out_dtype, x_int8.device)
     with torch.cuda.device(xq.device):
         ws, nb = _splitk_workspace(M, N, K, 1, False, xq.device)
-        _call("ic_gemm_w8a8_ws", _ptr(xq), M, K, xq.stride(0), _ptr(w), N, w.stride(0), _ptr(sa),
-              _ptr(sw), bp, bdt, _ptr(c), _dt(c.dtype, "out"), c.stride(0), _ptr(ws), nb, _stream(xq))
+        _call("ic_gemm_w8a8_ex", _ptr(xq), M, K, xq.stride(0), _ptr(w), N, w.stride(0), _ptr(sa),
+              _ptr(sw), bp, bdt, act, rp, rdt, ldr, _ptr(c), _dt(c.dtype, "out"), c.stride(0), _ptr(ws), nb,
+              _stream(xq))
     return c
 
 
-def fused_w4a8_gemm_dequant(x_int8, w_int8, s_w, s_a, bias=None, out_dtype=torch.bfloat16, out=None):
+def fused_w4a8_gemm_dequant(x_int8, w_int8, s_w, s_a, bias=None, out_dtype=torch.bfloat16, out=None,
+                            activation: int = 0, residual: torch.Tensor | None = None):
     """kernels/triton_w4a8_gemm.py:111-169: the INT8 GEMM on already unpacked
     INT4 weights ([N, K] int8, per-row s_w).  gemm_w4a8 is the fused path."""
-    return fused_int8_gemm_dequant(x_int8, w_int8, s_w, s_a, bias=bias, out_dtype=out_dtype, out=out)
+    return fused_int8_gemm_dequant(x_int8, w_int8, s_w, s_a, bias=bias, out_dtype=out_dtype,
+                                   activation=activation, residual=residual, out=out)
 
 
 def gemm_w4a8(x_int8: torch.Tensor, w_packed: torch.Tensor, s_w: torch.Tensor, s_a: torch.Tensor,
               bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16,
-              out: torch.Tensor | None = None) -> torch.Tensor:
+              out: torch.Tensor | None = None, activation: int = 0,
+              residual: torch.Tensor | None = None) -> torch.Tensor:
     """W4A8 with the INT4 unpack fused into the GEMM.
 
     w_packed [N, K/2] uint8; s_w [N, G] (or [N]) float scales, group size K/G.
     out = (sum_g f32(acc_g) * s_w[n,g]) * s_a[m] + bias  (G > 1)
     out = f32(acc) * (s_a[m] * s_w[n]) + bias           (G == 1)
+    then the activation and residual of fused_int8_gemm_dequant, in f32.
     """
     assert x_int8.dtype == torch.int8, f"x_int8 must be int8, got {x_int8.dtype}"
     assert w_packed.dtype == torch.uint8, f"w_packed must be uint8, got {w_packed.dtype}"
-    _need_cuda(x_int8, w_packed, s_w, s_a, bias)
+    _need_cuda(x_int8, w_packed, s_w, s_a, bias, residual)
     xq = _rows(x_int8)
     M, K = xq.shape
     N = w_packed.shape[0]
@@ -531,11 +561,13 @@ def gemm_w4a8(x_int8: torch.Tensor, w_packed: torch.Tensor, s_w: torch.Tensor, s
         raise ValueError(f"K={K} is not a multiple of the {G} scale groups")
     sa = s_a.detach().reshape(-1).to(torch.float32).contiguous()
     bp, bdt, _keep = _bias_args(bias, N)
+    act, rp, rdt, ldr, _rkeep = _epilogue_args(activation, residual, M, N)
     c = _out_buffer(out, M, N, out_dtype, xq.device)
     with torch.cuda.device(xq.device):
         ws, nb = _splitk_workspace(M, N, K, G, True, xq.device)
-        _call("ic_gemm_w4a8_ws", _ptr(xq), M, K, xq.stride(0), _ptr(w), N, w.stride(0), _ptr(sw), G,
-              _ptr(sa), bp, bdt, _ptr(c), _dt(c.dtype, "out"), c.stride(0), _ptr(ws), nb, _stream(xq))
+        _call("ic_gemm_w4a8_ex", _ptr(xq), M, K, xq.stride(0), _ptr(w), N, w.stride(0), _ptr(sw), G,
+              _ptr(sa), bp, bdt, act, rp, rdt, ldr, _ptr(c), _dt(c.dtype, "out"), c.stride(0), _ptr(ws), nb,
+              _stream(xq))
     return c
 
 

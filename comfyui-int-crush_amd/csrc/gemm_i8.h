@@ -1,0 +1,749 @@
+// INT8 x INT8 -> INT32 MFMA GEMM with fused dequant epilogue (gfx950).
+//
+//   out[m, n] = f32(acc[m, n]) * (s_a[m] * s_w[n]) + bias[n]                (per-row weight scale)
+//   out[m, n] = (sum_g f32(acc_g[m, n]) * s_w[n, g]) * s_a[m] + bias[n]     (per-group weight scale)
+//
+// A = activation codes [M, K] int8, K-major.  B = weights [N, K], K-major, as
+// int8 (W8A8, triton_int8_gemm.py:46-132) or as packed INT4 nibbles (W4A8,
+// triton_w4a8_gemm.py:40-108 plus the unpack of triton_int4_to_int8_unpack.py:26-52,
+// here fused into the weight staging so the unpacked weight never reaches HBM).
+//
+// Work decomposition (one 512-thread workgroup per CU, two waves per SIMD):
+//   * a BM x BN output tile per workgroup, 8 waves in a WGM x (8/WGM) grid, each
+//     wave owning (BM/WGM) x (BN*WGM/8) built from v_mfma_i32_32x32x32_i8 tiles
+//     whose int32 accumulators stay in architectural VGPRs;
+//   * K advances 128 bytes per stage (one 128-wide scale group) through an
+//     NS-deep LDS ring.  Every global read of the main loop -- activation
+//     rows, int8 or packed INT4 weight rows, per-group scales -- is a direct
+//     global->LDS DMA (global_load_lds) issued from inline assembly, so no
+//     VGPR holds staged data and the only memory waits are the explicit,
+//     static vmcnt waits of the pipeline (the compiler cannot see these DMAs
+//     and so does not serialise LDS accesses behind them).  A stage's DMAs
+//     are issued in slices between the MFMA K-steps of the stage before, so
+//     no wave stalls at a burst of DMA issues before its MFMAs;
+//   * activation and int8 weight chunks land XOR-swizzled by row (the issuing
+//     lane picks the global chunk), so the ds_read_b128 fragment loads are
+//     bank-conflict free;
+//   * packed INT4 weights are expanded once per workgroup and stage from the
+//     ring into an LDS tile as 16*q (int8): two masks and a byte permute per
+//     8 nibbles; the factor 16 is removed exactly in the epilogue;
+//   * per-group scales (group 128 = one stage) fold the int32 partials into an
+//     fp32 accumulator with one convert + FMA per element and group; two int32
+//     accumulator sets alternate between groups so the fold of group g runs
+//     while the MFMAs of group g+1 execute.
+#pragma once
+#include <type_traits>
+
+#include "gemm_common.h"
+
+namespace ic_gemm {
+struct GemmArgs {
+  const int8_t* A; int64_t lda; const uint8_t* B; int64_t ldb;
+  const float* s_a; const float* s_w; int G;
+  const void* bias; int bias_dt; void* C; int out_dt; int64_t ldc; int M, N, K;
+  int32_t* acc_out; bool int4;
+  void* ws = nullptr; int64_t ws_bytes = 0;  // split-K workspace (optional)
+  ic_epi epi{};                              // activation / residual epilogue
+};
+}  // namespace ic_gemm
+
+// GEMM launches with the activation / residual epilogue compiled in
+// (gemm_i8_epi.hip).
+int ic_gemm_run_epi(const ic_gemm::GemmArgs& g, hipStream_t st, const char* who, bool force_generic);
+
+namespace {
+using ic_gemm::GemmArgs;
+
+// Tile configuration: BM x BN output tile, WGM wave rows, NS-deep LDS ring.
+template <int BM_, int BN_, int WGM_, int NS_, bool INT4_, int GS_>
+struct Tile {
+  static constexpr int BM = BM_, BN = BN_, WGM = WGM_, NS = NS_;
+  static constexpr bool INT4 = INT4_;
+  static constexpr int GS = GS_;
+  static constexpr int A_BYTES = BM * kBK;
+  static constexpr int B_BYTES = INT4 ? BN * kBK / 2 : BN * kBK;  // packed for INT4
+  static constexpr int S_BYTES = GS ? BN * 4 : 0;
+  static constexpr int SLOT = A_BYTES + B_BYTES + S_BYTES;
+  static constexpr int BU_BYTES = INT4 ? BN * kBK : 0;  // one unpacked INT4 tile
+  static constexpr int EPI_RS = BN + 8;  // 16-bit output staging row stride (elements)
+  static constexpr size_t epi_bytes() { return (size_t)BM * EPI_RS * 2 + (size_t)(BM + 2 * BN) * 4; }
+  static constexpr size_t ring_bytes() { return (size_t)NS * SLOT + (size_t)BU_BYTES; }
+  static constexpr size_t lds_bytes() { return ring_bytes() > epi_bytes() ? ring_bytes() : epi_bytes(); }
+};
+
+// PART (split-K): workgroup (x, y) computes tile x over the K stages of
+// slice y of gridDim.y and writes its 4-byte partials -- the int32 sum
+// (per-row scales) or the fp32 group fold (grouped) -- to
+// acc_out[(y * M + m) * N + n]; splitk_reduce_kernel finishes them.
+template <class TL, int OUT_DT, bool ACC_OUT, bool PART = false, bool EPI = false>
+__global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
+    const int8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
+    const float* __restrict__ s_a, const float* __restrict__ s_w, int G,
+    const void* __restrict__ bias, int bias_dt, void* __restrict__ C, int64_t ldc, int M, int N,
+    int K, int32_t* __restrict__ acc_out, ic_epi epi) {
+  constexpr int BM = TL::BM, BN = TL::BN, WGM = TL::WGM, NS = TL::NS, GS = TL::GS;
+  constexpr bool INT4 = TL::INT4;
+  constexpr int WGN = 8 / WGM;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int A_DMA = BM / 64;                  // 1 KB DMA blocks of A per wave per stage
+  constexpr int B_DMA = INT4 ? BN / 128 : BN / 64;  // same for (packed) weights
+  constexpr int S_WAVES = GS ? BN / 64 : 0;       // waves issuing one scale DMA per stage
+  constexpr int D = A_DMA + B_DMA;
+  constexpr int PK = INT4 ? BN * (kBK / 2) / kNT : 0;  // packed weight bytes unpacked per thread
+  static_assert(TM >= 1 && TN >= 1 && A_DMA >= 1 && B_DMA >= 1, "tile too small");
+  static_assert(!INT4 || PK == 16 || PK == 32, "INT4 unpack split");
+  static_assert(GS == 0 || GS == 128, "group size");
+  static_assert(NS >= 2 && S_WAVES <= 8, "ring depth");
+
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_char*)smem;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = wave / WGN, wc = wave % WGN;
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  int tm, tn;
+  tile_coords(blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int KT_all = K / kBK;
+  const int kt0 = PART ? (int)((int64_t)blockIdx.y * KT_all / gridDim.y) : 0;
+  const int KT = PART ? (int)((int64_t)(blockIdx.y + 1) * KT_all / gridDim.y) - kt0 : KT_all;
+  const bool s_wave = wave < S_WAVES;
+
+  // ---- DMA addressing.  A / int8 B: lane L of a 1 KB block covers LDS row
+  // 8*blk + L/8, chunk slot L%8, and loads global chunk (L%8) ^ swz(row).
+  // Packed B: 16 rows of 64 bytes per block, unswizzled.  Scales: one dword
+  // per lane, column n0 + 64*wave + lane of group kt.
+  const int dma_row = lane >> 3;
+  uint32_t a_off[A_DMA];
+#pragma unroll
+  for (int c = 0; c < A_DMA; ++c) {
+    const int row = 8 * (wave + 8 * c) + dma_row;
+    a_off[c] = (uint32_t)(min(row, M - 1 - m0) * lda + (((lane & 7) ^ swz(row)) << 4));
+  }
+  uint32_t b_off[B_DMA];
+#pragma unroll
+  for (int c = 0; c < B_DMA; ++c) {
+    if constexpr (INT4) {
+      const int row = 16 * (wave + 8 * c) + (lane >> 2);
+      b_off[c] = (uint32_t)(min(row, N - 1 - n0) * ldb + ((lane & 3) << 4));
+    } else {
+      const int row = 8 * (wave + 8 * c) + dma_row;
+      b_off[c] = (uint32_t)(min(row, N - 1 - n0) * ldb + (((lane & 7) ^ swz(row)) << 4));
+    }
+  }
+  const uint32_t s_off = GS ? (uint32_t)(min(64 * wave + lane, N - 1 - n0) * G * 4) : 0u;
+  const int8_t* a_base = A + (int64_t)m0 * lda + (int64_t)kt0 * kBK;
+  const uint8_t* b_base = B + (int64_t)n0 * ldb + (int64_t)kt0 * (INT4 ? kBK / 2 : kBK);
+  const float* s_base = GS ? s_w + (int64_t)n0 * G + kt0 : nullptr;
+
+  // The D DMA instructions of one stage are issued in kParts slices, one per
+  // K-step of the MFMA loop: a wave that issued a whole stage at once stalled
+  // at issue instead of starting its MFMAs.  Slice p holds the blocks d with
+  // d % kParts == p (A blocks first, then B); the scale DMA goes last.
+  constexpr int kParts = kBK / 32;
+  auto issue_dma_part = [&](int kt, int part) {
+    const uint32_t slot = lds0 + (uint32_t)((kt % NS) * TL::SLOT);
+    const int8_t* ab = a_base + (int64_t)kt * kBK;
+#pragma unroll
+    for (int c = 0; c < A_DMA; ++c)
+      if (c % kParts == part) dma16(a_off[c], ab, slot + (uint32_t)((wave + 8 * c) * 1024));
+    const uint8_t* bb = b_base + (int64_t)kt * (INT4 ? kBK / 2 : kBK);
+#pragma unroll
+    for (int c = 0; c < B_DMA; ++c)
+      if ((A_DMA + c) % kParts == part) dma16(b_off[c], bb, slot + (uint32_t)(TL::A_BYTES + (wave + 8 * c) * 1024));
+    if constexpr (GS != 0) {
+      if (part == kParts - 1 && s_wave) dma4(s_off, s_base + kt, slot + (uint32_t)(TL::A_BYTES + TL::B_BYTES + wave * 256));
+    }
+  };
+  auto issue_dma = [&](int kt) {
+#pragma unroll
+    for (int p = 0; p < kParts; ++p) issue_dma_part(kt, p);
+  };
+  // Top of step s: stages s+1 .. s+NS-2 may stay in flight (D DMA
+  // instructions each, one more on the waves that also fetch scales); near the
+  // end of K, wait for everything.
+  auto wait_stage = [&](int s) {
+    if constexpr (NS > 2) {
+      if (s + NS - 2 < KT) {
+        if (s_wave) wait_vm<(D + 1) * (NS - 2)>();
+        else wait_vm<D * (NS - 2)>();
+        return;
+      }
+    }
+    wait_vm<0>();
+  };
+
+  // ---- packed INT4 -> 16*q int8 tile in LDS.  One buffer suffices: the
+  // barrier at the top of each step orders the MFMA reads of step s-1 before
+  // the unpack of step s.
+  auto unpack = [&](int kt) {
+    if constexpr (INT4) {
+      const char* bp = smem + (kt % NS) * TL::SLOT + TL::A_BYTES;
+      char* bu = smem + NS * TL::SLOT;
+#pragma unroll
+      for (int h = 0; h < PK / 16; ++h) {
+        const int idx = tid + kNT * h;      // 16-byte packed chunk index
+        const int row = idx >> 2, part = idx & 3;
+        const v4u p = *(const v4u*)(bp + idx * 16);
+        uint32_t w[8];
+        unpack8_x16(p.x, w[0], w[1]);
+        unpack8_x16(p.y, w[2], w[3]);
+        unpack8_x16(p.z, w[4], w[5]);
+        unpack8_x16(p.w, w[6], w[7]);
+        *(v4u*)(bu + lds_off(row, 2 * part)) = v4u{w[0], w[1], w[2], w[3]};
+        *(v4u*)(bu + lds_off(row, 2 * part + 1)) = v4u{w[4], w[5], w[6], w[7]};
+      }
+    }
+  };
+
+  typedef int v4i_t __attribute__((ext_vector_type(4)));
+  constexpr bool kPingPong = GS == 128 && TM * TN <= 2 * 2;
+  constexpr int NSET = kPingPong ? 2 : 1;
+  v16i acc[NSET][TM][TN];
+  v16f facc[GS == 128 ? TM : 1][GS == 128 ? TN : 1];
+#pragma unroll
+  for (int s = 0; s < NSET; ++s)
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[s][i][j] = v16i{};
+  if constexpr (GS == 128) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) facc[i][j] = v16f{};
+  }
+
+  auto out_row = [&](int i, int r) { return m0 + wr * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); };
+  auto out_col = [&](int j) { return n0 + wc * WN + j * 32 + (lane & 31); };
+
+  // Scales of group kt for this lane's columns, from the stage's LDS slot.
+  auto read_scales = [&](int kt, float* sw) {
+    if constexpr (GS == 128) {
+      const float* sS = (const float*)(smem + (kt % NS) * TL::SLOT + TL::A_BYTES + TL::B_BYTES);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        sw[j] = sS[wc * WN + j * 32 + (lane & 31)];
+        if constexpr (INT4) sw[j] *= 0.0625f;  // acc holds 16 * the true sum
+      }
+    }
+  };
+
+  // Fold of one 32x32 tile t of accumulator set FS (group g) into facc:
+  // facc += f32(acc_g) * s_w[n, g] (16 converts + 16 FMAs per lane).
+  auto fold_tile = [&](int g, auto fs_c, int t, const float* sw) {
+    constexpr int FS = decltype(fs_c)::value;
+    const int i = t / TN, j = t % TN;
+    // Anchors: empty volatile asm statements on the tile before and on its
+    // fp32 accumulator after the fold keep the register-only fold between the
+    // stage's barriers (volatile asm stays ordered), so it can neither be
+    // hoisted nor sunk out of the MFMA region it is interleaved with.
+    asm volatile("" : "+v"(acc[FS][i][j]));
+    if constexpr (ACC_OUT) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = out_row(i, r), nn = out_col(j);
+        if (m < M && nn < N)
+          acc_out[((int64_t)g * M + m) * N + nn] = INT4 ? (acc[FS][i][j][r] >> 4) : acc[FS][i][j][r];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) facc[i][j][r] = __builtin_fmaf((float)acc[FS][i][j][r], sw[j], facc[i][j][r]);
+    asm volatile("" : "+v"(facc[i][j]));  // nor sunk past the next barrier
+  };
+  auto fold = [&](int g, auto fs_c, const float* sw) {
+#pragma unroll
+    for (int t = 0; t < TM * TN; ++t) fold_tile(g, fs_c, t, sw);
+  };
+
+  // One stage (4 K-steps of 32) into accumulator set SET; ZF starts the set
+  // afresh (MFMA with a zero addend) on the first K-step.  With FOLD, the fold
+  // of the previous group (set FS, scales sw_f) is spread over the stage, one
+  // 32x32 tile per K-step, between the MFMAs of the other accumulator set.
+  auto mfma_stage = [&](int kt, int dma_kt, auto set_c, auto zero_c, auto fold_c, auto fs_c, int g_f,
+                        const float* sw_f) {
+    constexpr int SET = decltype(set_c)::value;
+    constexpr bool ZF = decltype(zero_c)::value;
+    constexpr bool FOLD = decltype(fold_c)::value;
+    const char* sA = smem + (kt % NS) * TL::SLOT;
+    const char* sB = INT4 ? smem + NS * TL::SLOT : sA + TL::A_BYTES;
+#pragma unroll
+    for (int ks = 0; ks < kBK / 32; ++ks) {
+      v4i_t a[TM], b[TN];
+      const int ch = 2 * ks + (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) a[i] = *(const v4i_t*)(sA + lds_off(wr * WM + i * 32 + (lane & 31), ch));
+#pragma unroll
+      for (int j = 0; j < TN; ++j) b[j] = *(const v4i_t*)(sB + lds_off(wc * WN + j * 32 + (lane & 31), ch));
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          if (ZF && ks == 0) acc[SET][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], v16i{}, 0, 0, 0);
+          else acc[SET][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[SET][i][j], 0, 0, 0);
+        }
+      if (dma_kt < KT) issue_dma_part(dma_kt, ks);
+      // The fold's instructions are placed among this K-step's MFMAs by the
+      // compiler; fixed MFMA:VALU interleave patterns measured 3-5 % slower.
+      if constexpr (FOLD) {
+        if (ks < TM * TN) fold_tile(g_f, fs_c, ks, sw_f);
+      }
+    }
+    if constexpr (FOLD && TM * TN > kBK / 32) {
+#pragma unroll
+      for (int t = kBK / 32; t < TM * TN; ++t) fold_tile(g_f, fs_c, t, sw_f);
+    }
+  };
+
+  // ---- prologue: NS-1 stages in flight
+#pragma unroll
+  for (int t = 0; t < NS - 1; ++t)
+    if (t < KT) issue_dma(t);
+
+  // One pipeline step: make stage s resident (this wave's DMAs, then the
+  // barrier for everyone's), expand packed weights (second barrier), then run
+  // the MFMAs of stage s while refilling the ring slot freed by step s-1.
+  using T0 = std::integral_constant<int, 0>;
+  using T1 = std::integral_constant<int, 1>;
+  using ZF = std::true_type;
+  using NZ = std::false_type;
+  float sw_a[TN], sw_b[TN];
+  auto step = [&](int s, auto set_c, auto zero_c, float* sw_read, auto fold_c, auto fs_c, int g_f,
+                  const float* sw_f) {
+    wait_stage(s);
+    lds_barrier();
+    if constexpr (INT4) {
+      unpack(s);
+      lds_barrier();
+    }
+    read_scales(s, sw_read);
+    // keep the (register-only) fold inside the MFMA region instead of letting
+    // it be hoisted above the barriers
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_stage(s, s + NS - 1, set_c, zero_c, fold_c, fs_c, g_f, sw_f);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  if constexpr (GS == 0) {
+    for (int s = 0; s < KT; ++s) step(s, T0{}, NZ{}, sw_a, NZ{}, T0{}, 0, sw_a);
+  } else if constexpr (kPingPong) {
+    // set g&1 accumulates group g while set (g-1)&1 (group g-1) is folded
+    step(0, T0{}, ZF{}, sw_a, NZ{}, T1{}, 0, sw_b);
+    int g = 1;
+    for (; g + 1 < KT; g += 2) {
+      step(g, T1{}, ZF{}, sw_b, ZF{}, T0{}, g - 1, sw_a);
+      step(g + 1, T0{}, ZF{}, sw_a, ZF{}, T1{}, g, sw_b);
+    }
+    if (g < KT) {
+      step(g, T1{}, ZF{}, sw_b, ZF{}, T0{}, g - 1, sw_a);
+      fold(g, T1{}, sw_b);
+    } else {
+      fold(g - 1, T0{}, sw_a);
+    }
+  } else {
+    for (int g = 0; g < KT; ++g) {
+      step(g, T0{}, ZF{}, sw_a, NZ{}, T0{}, 0, sw_a);
+      fold(g, T0{}, sw_a);
+    }
+  }
+
+  // ---- epilogue
+  if constexpr (PART) {
+    // partials of this K slice: 32 lanes of one accumulator row write 32
+    // consecutive columns (128 bytes)
+    int32_t* ws = acc_out + (int64_t)blockIdx.y * M * N;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = out_row(i, r), n = out_col(j);
+          if (m < M && n < N) {
+            if constexpr (GS == 0) ws[(int64_t)m * N + n] = acc[0][i][j][r];
+            else ((float*)ws)[(int64_t)m * N + n] = facc[i][j][r];
+          }
+        }
+    return;
+  }
+  if constexpr (ACC_OUT && GS == 0) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = out_row(i, r), n = out_col(j);
+          if (m < M && n < N) acc_out[(int64_t)m * N + n] = INT4 ? (acc[0][i][j][r] >> 4) : acc[0][i][j][r];
+        }
+  }
+  if (C == nullptr) return;
+  if constexpr (OUT_DT != IC_DTYPE_F32) {
+    // 16-bit outputs: finish each value in registers, stage the tile through
+    // LDS row-major, then write whole rows with 16-byte stores.  s_a, bias and
+    // the per-row weight scales are staged once per tile.  A 16-bit residual
+    // is read into the same staging tile first, with 16-byte loads; each lane
+    // then adds the residual of the slot it overwrites.
+    bool staged = (((uintptr_t)C) & 15) == 0 && (ldc & 7) == 0 && (N & 7) == 0;
+    bool res_lds = false;
+    if constexpr (EPI) {
+      res_lds = epi.res != nullptr;
+      if (res_lds && (epi.res_dt == IC_DTYPE_F32 || (((uintptr_t)epi.res) & 15) != 0 || (epi.ldr & 7) != 0))
+        staged = false;
+    }
+    if (staged) {
+      constexpr int RS = TL::EPI_RS;
+      constexpr int CPR = BN / 8;  // 16-byte chunks per tile row
+      lds_barrier();  // every wave is done with the last stage
+      u16* ot = (u16*)smem;
+      float* sa_l = (float*)(smem + BM * RS * 2);
+      float* b_l = sa_l + BM;
+      float* sw_l = b_l + BN;
+      if (res_lds) {
+        for (int c = tid; c < BM * CPR; c += kNT) {
+          const int row = c / CPR, col = (c % CPR) * 8;
+          const int m = m0 + row, n = n0 + col;
+          if (m < M && n < N)
+            *(v4u*)(ot + row * RS + col) = *(const v4u*)((const u16*)epi.res + (int64_t)m * epi.ldr + n);
+        }
+      }
+      for (int t = tid; t < BM; t += kNT) sa_l[t] = s_a[min(m0 + t, M - 1)];
+      for (int t = tid; t < BN; t += kNT) {
+        const int n = min(n0 + t, N - 1);
+        b_l[t] = bias != nullptr ? ld_any_f32(bias, bias_dt, n) : 0.0f;
+        if constexpr (GS == 0) sw_l[t] = s_w[n];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int nl = wc * WN + j * 32 + (lane & 31);
+        const float b = b_l[nl];
+        const float sw = GS == 0 ? sw_l[nl] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int ml = wr * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            float v;
+            if constexpr (GS == 0) {
+              float a = (float)acc[0][i][j][r];
+              if constexpr (INT4) a *= 0.0625f;
+              v = a * (sa_l[ml] * sw);
+            } else {
+              v = facc[i][j][r] * sa_l[ml];
+            }
+            if (bias != nullptr) v = v + b;
+            if constexpr (EPI) {
+              v = epi_act(v, epi.act);
+              if (res_lds) {
+                const u16 r = ot[ml * RS + nl];
+                v = v + (epi.res_dt == IC_DTYPE_F16 ? f16_to_f32(r) : bf16_to_f32(r));
+              }
+            }
+            u16 h;
+            if constexpr (OUT_DT == IC_DTYPE_F16) h = f32_to_f16(v);
+            else h = f32_to_bf16(v);
+            ot[ml * RS + nl] = h;
+          }
+          // with the epilogue options, keep the residual loads and activation
+          // code of one 32x32 tile from being hoisted over all tiles
+          if constexpr (EPI) __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      __syncthreads();
+#pragma unroll 4
+      for (int c = tid; c < BM * CPR; c += kNT) {
+        const int row = c / CPR, col = (c % CPR) * 8;
+        const int m = m0 + row, n = n0 + col;
+        if (m < M && n < N) *(v4u*)((u16*)C + (int64_t)m * ldc + n) = *(const v4u*)(ot + row * RS + col);
+      }
+      return;
+    }
+  }
+  // Each lane stores 16 rows of one column per 32x32 tile; row offsets within
+  // a tile stay in 32-bit arithmetic (the host bounds ldc).
+  constexpr int ESZ = OUT_DT == IC_DTYPE_F32 ? 4 : 2;
+  const bool full = m0 + BM <= M && n0 + BN <= N;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int n = out_col(j);
+    const int nc = min(n, N - 1);
+    const float b = bias != nullptr ? ld_any_f32(bias, bias_dt, nc) : 0.0f;
+    const float sw = GS == 0 ? s_w[nc] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int mr0 = m0 + wr * WM + i * 32 + 4 * (lane >> 5);
+      char* cb = (char*)C + ((int64_t)mr0 * ldc + n) * ESZ;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int dr = 8 * (r >> 2) + (r & 3);
+        const int m = mr0 + dr;
+        if (!full && (m >= M || n >= N)) continue;
+        float v;
+        if constexpr (GS == 0) {
+          float a = (float)acc[0][i][j][r];
+          if constexpr (INT4) a *= 0.0625f;
+          v = a * (s_a[m] * sw);
+        } else {
+          v = facc[i][j][r] * s_a[m];
+        }
+        if (bias != nullptr) v = v + b;
+        if constexpr (EPI) v = epi_apply(v, epi, m, n);
+        st_from_f32<OUT_DT>(cb + dr * (int)ldc * ESZ, 0, v);
+      }
+      // keep the scale loads of one 32x32 tile from being hoisted over all tiles
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
+// Shape-generic fallback (any K, any alignment): one thread per output, exact
+// int32 accumulation; same epilogue arithmetic as the MFMA kernel.
+template <bool INT4, int OUT_DT>
+__global__ __launch_bounds__(256) void gemm_i8_generic_kernel(
+    const int8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
+    const float* __restrict__ s_a, const float* __restrict__ s_w, int G, int gsize,
+    const void* __restrict__ bias, int bias_dt, void* __restrict__ C, int64_t ldc, int M, int N,
+    int K, int32_t* __restrict__ acc_out, ic_epi epi) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  const int m = blockIdx.y;
+  if (n >= N || m >= M) return;
+  const int8_t* a = A + (int64_t)m * lda;
+  const uint8_t* b = B + (int64_t)n * ldb;
+  float facc = 0.0f;
+  int acc = 0;
+  for (int k = 0; k < K; ++k) {
+    int w;
+    if constexpr (INT4) {
+      const int nib = (b[k >> 1] >> (4 * (k & 1))) & 0xf;
+      w = nib >= 8 ? nib - 16 : nib;
+    } else {
+      w = (int8_t)b[k];
+    }
+    acc += (int)a[k] * w;
+    if (G > 1 && ((k + 1) % gsize == 0 || k + 1 == K)) {
+      const int g = k / gsize;
+      if (acc_out) acc_out[((int64_t)g * M + m) * N + n] = acc;
+      facc = __builtin_fmaf((float)acc, s_w[(int64_t)n * G + g], facc);
+      acc = 0;
+    }
+  }
+  if (G <= 1 && acc_out) acc_out[(int64_t)m * N + n] = acc;
+  if (C == nullptr) return;
+  float v = G > 1 ? facc * s_a[m] : (float)acc * (s_a[m] * s_w[n]);
+  if (bias != nullptr) v = v + ld_any_f32(bias, bias_dt, n);
+  v = epi_apply(v, epi, m, n);
+  st_from_f32<OUT_DT>(C, (int64_t)m * ldc + n, v);
+}
+
+// Sum of the K-slice partials in slice order, then the operations of the
+// unsplit epilogue; per-row-scale outputs are therefore bit-identical to an
+// unsplit launch (exact int32 sums), grouped ones differ only in the order of
+// the fp32 group-fold additions.
+template <bool INT4, int GS, int OUT_DT>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(
+    const int32_t* __restrict__ ws, int S, const float* __restrict__ s_a, const float* __restrict__ s_w,
+    const void* __restrict__ bias, int bias_dt, void* __restrict__ C, int64_t ldc, int M, int N, ic_epi epi) {
+  const int64_t MN = (int64_t)M * N;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= MN) return;
+  const int m = (int)(i / N), n = (int)(i - (int64_t)m * N);
+  float v;
+  if constexpr (GS == 0) {
+    int t = 0;
+    for (int s = 0; s < S; ++s) t += ws[s * MN + i];
+    float a = (float)t;
+    if constexpr (INT4) a *= 0.0625f;
+    v = a * (s_a[m] * s_w[n]);
+  } else {
+    const float* f = (const float*)ws;
+    float t = f[i];
+    for (int s = 1; s < S; ++s) t = t + f[s * MN + i];
+    v = t * s_a[m];
+  }
+  if (bias != nullptr) v = v + ld_any_f32(bias, bias_dt, n);
+  v = epi_apply(v, epi, m, n);
+  st_from_f32<OUT_DT>(C, (int64_t)m * ldc + n, v);
+}
+
+
+// Workgroup rounds of a BM x BN tiling on the device's CUs times the tile
+// area, times the tile's relative cost per output (percent): proportional to
+// the run time of an MFMA-bound launch.
+int64_t tiling_cost(const GemmArgs& g, int bm, int bn, int pct = 100) {
+  const int64_t tiles = (int64_t)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn);
+  const int64_t cus = ic_num_cus();
+  return (tiles + cus - 1) / cus * bm * bn * pct;
+}
+
+// Tile choice by tile-area rounds (tiling_cost).  Per-row W8A8 takes
+// 256 x 192 where that fills the CUs in fewer rounds than 256 x 256
+// (4096 x 3072: 256 tiles instead of 192 on 256 CUs).  INT4 / grouped:
+// 256 x 128 unless 128 x 128 is cheaper; a 128 x 128 tile costs 1.44x more
+// per output (measured on the Flux shapes), so it wins only when it fills CUs
+// that 256 x 128 leaves idle (512 x 3072: 48 tiles of 256 x 128, 96 of
+// 128 x 128 on 256 CUs).
+struct TileShape { int bm, bn; };
+TileShape tile_choice(const GemmArgs& g, bool grouped) {
+  if (!g.int4 && !grouped) {
+    if (g.M > 128 && g.N > 128)
+      return tiling_cost(g, 256, 192) < tiling_cost(g, 256, 256) ? TileShape{256, 192} : TileShape{256, 256};
+    return {128, 128};
+  }
+  if (g.M > 128 && tiling_cost(g, 256, 128) <= tiling_cost(g, 128, 128, 144)) return {256, 128};
+  return {128, 128};
+}
+
+// K slices for `tiles` workgroups over KT stages: minimise rounds of
+// workgroups times stages per slice plus the partials' round trip through
+// HBM (8 bytes per output and slice; ~3.6 MB per stage time).  Only when the
+// unsplit launch would leave more than half the CUs idle; 1 = no split.
+int choose_splits(int64_t tiles, int KT, int64_t M, int64_t N) {
+  const int64_t cus = ic_num_cus();
+  if (tiles * 2 > cus || KT < 8) return 1;
+  double best = (double)((tiles + cus - 1) / cus) * KT;
+  int bs = 1;
+  for (int S = 2; S <= 16 && KT / S >= 4; ++S) {
+    const double c = (double)((tiles * S + cus - 1) / cus) * ((KT + S - 1) / S) + (double)S * M * N * 8.0 / 3.6e6;
+    if (c < best) { best = c; bs = S; }
+  }
+  return bs;
+}
+
+int splitk_plan(const GemmArgs& g, bool grouped) {
+  const TileShape t = tile_choice(g, grouped);
+  const int64_t tiles = (int64_t)((g.M + t.bm - 1) / t.bm) * ((g.N + t.bn - 1) / t.bn);
+  return choose_splits(tiles, g.K / kBK, g.M, g.N);
+}
+
+template <class TL, int OUT_DT, bool ACC, bool PART, bool EPI>
+hipError_t launch_kernel(const GemmArgs& g, int S, hipStream_t st) {
+  const int tiles = ((g.M + TL::BM - 1) / TL::BM) * ((g.N + TL::BN - 1) / TL::BN);
+  const size_t shm = TL::lds_bytes();
+  static_assert(TL::lds_bytes() <= 160 * 1024, "LDS budget");
+  auto kern = gemm_i8_kernel<TL, OUT_DT, ACC, PART, EPI>;
+  static bool attr_set = false;  // idempotent attribute; benign if raced
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  kern<<<dim3(tiles, S), dim3(kNT), shm, st>>>(g.A, g.lda, g.B, g.ldb, g.s_a, g.s_w, g.G, g.bias, g.bias_dt,
+                                               g.C, g.ldc, g.M, g.N, g.K, PART ? (int32_t*)g.ws : g.acc_out, g.epi);
+  return hipGetLastError();
+}
+
+template <class TL, int OUT_DT, bool ACC, bool EPI>
+hipError_t launch_mfma(const GemmArgs& g, hipStream_t st) {
+  if constexpr (!ACC) {
+    const int S = g.ws != nullptr ? splitk_plan(g, TL::GS != 0) : 1;
+    if (S > 1 && g.C != nullptr && g.ws_bytes >= (int64_t)S * g.M * g.N * 4) {
+      hipError_t e = launch_kernel<TL, OUT_DT, false, true, EPI>(g, S, st);
+      if (e != hipSuccess) return e;
+      const int64_t MN = (int64_t)g.M * g.N;
+      splitk_reduce_kernel<TL::INT4, TL::GS, OUT_DT><<<dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, st>>>(
+          (const int32_t*)g.ws, S, g.s_a, g.s_w, g.bias, g.bias_dt, g.C, g.ldc, g.M, g.N, g.epi);
+      return hipGetLastError();
+    }
+  }
+  return launch_kernel<TL, OUT_DT, ACC, false, EPI>(g, 1, st);
+}
+
+template <bool INT4, int GS, int OUT_DT, bool ACC, bool EPI>
+hipError_t pick_tile(const GemmArgs& g, hipStream_t st) {
+  const TileShape t = tile_choice(g, GS != 0);
+  if constexpr (!INT4 && GS == 0) {
+    if (t.bm == 256 && t.bn == 192) return launch_mfma<Tile<256, 192, 4, 2, false, 0>, OUT_DT, ACC, EPI>(g, st);
+    if (t.bm == 256) return launch_mfma<Tile<256, 256, 2, 2, false, 0>, OUT_DT, ACC, EPI>(g, st);
+    return launch_mfma<Tile<128, 128, 2, 4, false, 0>, OUT_DT, ACC, EPI>(g, st);
+  } else {
+    if (t.bm == 256) return launch_mfma<Tile<256, 128, 4, 3, INT4, GS>, OUT_DT, ACC, EPI>(g, st);
+    return launch_mfma<Tile<128, 128, 2, 4, INT4, GS>, OUT_DT, ACC, EPI>(g, st);
+  }
+}
+
+template <bool INT4, int GS, bool ACC, bool EPI>
+hipError_t pick_out(const GemmArgs& g, hipStream_t st) {
+  switch (g.out_dt) {
+    case IC_DTYPE_F16: return pick_tile<INT4, GS, IC_DTYPE_F16, ACC, EPI>(g, st);
+    case IC_DTYPE_BF16: return pick_tile<INT4, GS, IC_DTYPE_BF16, ACC, EPI>(g, st);
+    default: return pick_tile<INT4, GS, IC_DTYPE_F32, ACC, EPI>(g, st);
+  }
+}
+
+template <bool INT4, int OUT_DT>
+hipError_t launch_generic_t(const GemmArgs& g, int gsize, hipStream_t st) {
+  dim3 grid((unsigned)((g.N + 255) / 256), (unsigned)g.M);
+  gemm_i8_generic_kernel<INT4, OUT_DT><<<grid, dim3(256), 0, st>>>(
+      g.A, g.lda, g.B, g.ldb, g.s_a, g.s_w, g.G, gsize, g.bias, g.bias_dt, g.C, g.ldc, g.M, g.N, g.K,
+      g.acc_out, g.epi);
+  return hipGetLastError();
+}
+template <bool INT4>
+hipError_t launch_generic(const GemmArgs& g, int gsize, hipStream_t st) {
+  switch (g.out_dt) {
+    case IC_DTYPE_F16: return launch_generic_t<INT4, IC_DTYPE_F16>(g, gsize, st);
+    case IC_DTYPE_BF16: return launch_generic_t<INT4, IC_DTYPE_BF16>(g, gsize, st);
+    default: return launch_generic_t<INT4, IC_DTYPE_F32>(g, gsize, st);
+  }
+}
+
+bool mfma_shape_ok(const GemmArgs& g, int gsize) {
+  if (g.K % kBK != 0) return false;
+  if (g.G > 1 && gsize != 128) return false;
+  // 16-byte DMA / vector loads need aligned bases and strides; packed INT4
+  // rows are read 8 or 16 bytes at a time
+  if (((uintptr_t)g.A & 15) || ((uintptr_t)g.B & 15) || (g.lda & 15) || (g.ldb & 15)) return false;
+  return true;
+}
+
+// EPI: the activation / residual epilogue is compiled in (gemm_i8_epi.hip
+// instantiates that set; gemm_i8.hip the plain one).
+template <bool EPI>
+int run_gemm_t(GemmArgs g, hipStream_t st, const char* who, bool force_generic) {
+  if (g.M < 0 || g.N <= 0 || g.K <= 0 || g.lda < g.K || g.ldc < g.N)
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: bad shape M=%d N=%d K=%d lda=%lld ldc=%lld", who, g.M,
+                        g.N, g.K, (long long)g.lda, (long long)g.ldc);
+  if (g.int4 ? (g.ldb * 2 < g.K) : (g.ldb < g.K))
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: weight row stride %lld too small for K=%d", who,
+                        (long long)g.ldb, g.K);
+  if (g.ldc >= (1LL << 24))
+    return ic_set_error(IC_ERR_UNSUPPORTED, "%s: output row stride %lld too large", who, (long long)g.ldc);
+  if (g.G < 1) return ic_set_error(IC_ERR_INVALID_ARG, "%s: num_groups must be >= 1", who);
+  if (g.G > 1 && (g.K % g.G != 0))
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: K=%d not divisible by num_groups=%d", who, g.K, g.G);
+  if (g.out_dt != IC_DTYPE_F16 && g.out_dt != IC_DTYPE_BF16 && g.out_dt != IC_DTYPE_F32)
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: out dtype must be f16/bf16/f32", who);
+  if (g.bias && g.bias_dt != IC_DTYPE_F16 && g.bias_dt != IC_DTYPE_BF16 && g.bias_dt != IC_DTYPE_F32)
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: bias dtype must be f16/bf16/f32", who);
+  if (g.M == 0) return IC_OK;
+  if (!g.A || !g.B || !g.s_a || !g.s_w || (!g.C && !g.acc_out))
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: null pointer argument", who);
+  const int gsize = g.K / g.G;
+  hipError_t e;
+  if (!force_generic && mfma_shape_ok(g, gsize)) {
+    if constexpr (EPI) {
+      // the epilogue options never come with the debug accumulator output
+      if (g.int4) e = g.G > 1 ? pick_out<true, 128, false, true>(g, st) : pick_out<true, 0, false, true>(g, st);
+      else e = g.G > 1 ? pick_out<false, 128, false, true>(g, st) : pick_out<false, 0, false, true>(g, st);
+    } else {
+      const bool acc = g.acc_out != nullptr;
+      if (g.int4) {
+        if (g.G > 1) e = acc ? pick_out<true, 128, true, false>(g, st) : pick_out<true, 128, false, false>(g, st);
+        else e = acc ? pick_out<true, 0, true, false>(g, st) : pick_out<true, 0, false, false>(g, st);
+      } else {
+        if (g.G > 1) e = acc ? pick_out<false, 128, true, false>(g, st) : pick_out<false, 128, false, false>(g, st);
+        else e = acc ? pick_out<false, 0, true, false>(g, st) : pick_out<false, 0, false, false>(g, st);
+      }
+    }
+  } else {
+    e = g.int4 ? launch_generic<true>(g, gsize, st) : launch_generic<false>(g, gsize, st);
+  }
+  if (e != hipSuccess) return ic_set_error(IC_ERR_LAUNCH, "%s: %s", who, hipGetErrorString(e));
+  return IC_OK;
+}
+
+}  // namespace

@@ -43,7 +43,8 @@ template <bool INT4, int GS, int OUT_DT>
 __global__ __launch_bounds__(kGT) void gemv_i8_kernel(
     const int8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
     const float* __restrict__ s_a, const float* __restrict__ s_w, int G,
-    const void* __restrict__ bias, int bias_dt, void* __restrict__ C, int64_t ldc, int M, int N, int K) {
+    const void* __restrict__ bias, int bias_dt, void* __restrict__ C, int64_t ldc, int M, int N, int K,
+    ic_epi epi) {
   // GS == 128: block sums [KB][M][16]; otherwise per-wave totals [4][M][16]
   extern __shared__ int32_t sacc[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -138,6 +139,7 @@ __global__ __launch_bounds__(kGT) void gemv_i8_kernel(
     v = a * (s_a[m] * s_w[no]);
   }
   if (bias != nullptr) v = v + ld_any_f32(bias, bias_dt, no);
+  v = epi_apply(v, epi, m, no);
   st_from_f32<OUT_DT>(C, (int64_t)m * ldc + no, v);
 }
 
@@ -206,7 +208,7 @@ __global__ __launch_bounds__(kGT) void gemv_w4a16_kernel(
 template <bool INT4, int GS, int OUT_DT>
 hipError_t launch_gemv_i8(const int8_t* A, int64_t lda, const uint8_t* B, int64_t ldb, const float* s_a,
                           const float* s_w, int G, const void* bias, int bias_dt, void* C, int64_t ldc,
-                          int M, int N, int K, hipStream_t st) {
+                          int M, int N, int K, const ic_epi& epi, hipStream_t st) {
   auto kern = gemv_i8_kernel<INT4, GS, OUT_DT>;
   const size_t shm = (size_t)(GS == 128 ? K / kGBK : 4) * M * 16 * 4;
   static bool attr_set = false;  // idempotent attribute; benign if raced
@@ -216,21 +218,21 @@ hipError_t launch_gemv_i8(const int8_t* A, int64_t lda, const uint8_t* B, int64_
     attr_set = true;
   }
   kern<<<dim3((unsigned)((N + 15) / 16)), dim3(kGT), shm, st>>>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C,
-                                                                ldc, M, N, K);
+                                                                ldc, M, N, K, epi);
   return hipGetLastError();
 }
 
 template <bool INT4, int GS>
 hipError_t pick_gemv_out(int out_dt, const int8_t* A, int64_t lda, const uint8_t* B, int64_t ldb,
                          const float* s_a, const float* s_w, int G, const void* bias, int bias_dt, void* C,
-                         int64_t ldc, int M, int N, int K, hipStream_t st) {
+                         int64_t ldc, int M, int N, int K, const ic_epi& epi, hipStream_t st) {
   switch (out_dt) {
     case IC_DTYPE_F16:
-      return launch_gemv_i8<INT4, GS, IC_DTYPE_F16>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
+      return launch_gemv_i8<INT4, GS, IC_DTYPE_F16>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, epi, st);
     case IC_DTYPE_BF16:
-      return launch_gemv_i8<INT4, GS, IC_DTYPE_BF16>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
+      return launch_gemv_i8<INT4, GS, IC_DTYPE_BF16>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, epi, st);
     default:
-      return launch_gemv_i8<INT4, GS, IC_DTYPE_F32>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
+      return launch_gemv_i8<INT4, GS, IC_DTYPE_F32>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, epi, st);
   }
 }
 
@@ -256,11 +258,11 @@ bool ic_gemv_applicable(int64_t M, int64_t K, const void* x, int64_t ldx_bytes, 
          ((uintptr_t)w & 15) == 0 && (ldx_bytes & 15) == 0 && (ldw_bytes & 15) == 0;
 }
 
-extern "C" {
-
-int ic_gemv_w8a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8_t* w, int64_t N, int64_t ldw,
-                 const float* s_a, const float* s_w, const void* bias, int bias_dtype, void* out, int out_dtype,
-                 int64_t ldo, void* stream) {
+// GEMV bodies with the activation / residual epilogue (the GEMM entry points
+// route M <= 16 here with theirs; the C entry points below pass none).
+int ic_gemv_w8a8_epi(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8_t* w, int64_t N, int64_t ldw,
+                     const float* s_a, const float* s_w, const void* bias, int bias_dtype, void* out, int out_dtype,
+                     int64_t ldo, const ic_epi& epi, void* stream) {
   const char* who = "ic_gemv_w8a8";
   int rc = check_gemv_common(who, M, K, N, ldx, ldo, bias, bias_dtype);
   if (rc) return rc;
@@ -271,14 +273,14 @@ int ic_gemv_w8a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8
   if (out_dtype != IC_DTYPE_F16 && out_dtype != IC_DTYPE_BF16 && out_dtype != IC_DTYPE_F32)
     return ic_set_error(IC_ERR_INVALID_ARG, "%s: out dtype must be f16/bf16/f32", who);
   hipError_t e = pick_gemv_out<false, 0>(out_dtype, xq, ldx, (const uint8_t*)w, ldw, s_a, s_w, 1, bias, bias_dtype,
-                                         out, ldo, (int)M, (int)N, (int)K, (hipStream_t)stream);
+                                         out, ldo, (int)M, (int)N, (int)K, epi, (hipStream_t)stream);
   if (e != hipSuccess) return ic_set_error(IC_ERR_LAUNCH, "%s: %s", who, hipGetErrorString(e));
   return IC_OK;
 }
 
-int ic_gemv_w4a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed, int64_t N,
-                 int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a, const void* bias,
-                 int bias_dtype, void* out, int out_dtype, int64_t ldo, void* stream) {
+int ic_gemv_w4a8_epi(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed, int64_t N,
+                     int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a, const void* bias,
+                     int bias_dtype, void* out, int out_dtype, int64_t ldo, const ic_epi& epi, void* stream) {
   const char* who = "ic_gemv_w4a8";
   int rc = check_gemv_common(who, M, K, N, ldx, ldo, bias, bias_dtype);
   if (rc) return rc;
@@ -293,11 +295,26 @@ int ic_gemv_w4a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint
   hipStream_t st = (hipStream_t)stream;
   hipError_t e = num_groups > 1
                      ? pick_gemv_out<true, 128>(out_dtype, xq, ldx, w_packed, ldw, s_a, s_w, (int)num_groups, bias,
-                                                bias_dtype, out, ldo, (int)M, (int)N, (int)K, st)
+                                                bias_dtype, out, ldo, (int)M, (int)N, (int)K, epi, st)
                      : pick_gemv_out<true, 0>(out_dtype, xq, ldx, w_packed, ldw, s_a, s_w, 1, bias, bias_dtype, out,
-                                              ldo, (int)M, (int)N, (int)K, st);
+                                              ldo, (int)M, (int)N, (int)K, epi, st);
   if (e != hipSuccess) return ic_set_error(IC_ERR_LAUNCH, "%s: %s", who, hipGetErrorString(e));
   return IC_OK;
+}
+
+extern "C" {
+
+int ic_gemv_w8a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8_t* w, int64_t N, int64_t ldw,
+                 const float* s_a, const float* s_w, const void* bias, int bias_dtype, void* out, int out_dtype,
+                 int64_t ldo, void* stream) {
+  return ic_gemv_w8a8_epi(xq, M, K, ldx, w, N, ldw, s_a, s_w, bias, bias_dtype, out, out_dtype, ldo, ic_epi{}, stream);
+}
+
+int ic_gemv_w4a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed, int64_t N,
+                 int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a, const void* bias,
+                 int bias_dtype, void* out, int out_dtype, int64_t ldo, void* stream) {
+  return ic_gemv_w4a8_epi(xq, M, K, ldx, w_packed, N, ldw, s_w, num_groups, s_a, bias, bias_dtype, out, out_dtype,
+                          ldo, ic_epi{}, stream);
 }
 
 int ic_gemv_w4a16(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed, int64_t N,

@@ -159,3 +159,43 @@ IC_DEV float wave_max(float v) {
   for (int o = 32; o >= 1; o >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, o, 64));
   return v;
 }
+
+// ------------------------------------------------------------ GEMM epilogue options
+// After the dequant and bias of the INT8 GEMMs (kernels/triton_int8_gemm.py:119-130):
+// an activation on the f32 value, then a residual [M, N] (f16/bf16/f32, row
+// stride ldr) added, then the rounding to the output dtype.
+//   act 0: none; 1: SiLU v * sigmoid(v); 2: GELU 0.5 v (1 + erf(v / sqrt 2));
+//   3: GELU with the tanh approximation (not in the reference; the MLPs of
+//   DiT models such as Flux use it).
+struct ic_epi {
+  int act = 0;
+  const void* res = nullptr;
+  int res_dt = 0;
+  int64_t ldr = 0;
+};
+
+IC_DEV float epi_act(float v, int act) {
+  if (act == 1) {
+    v = v * (1.0f / (1.0f + expf(-v)));
+  } else if (act == 2) {
+    v = (v * 0.5f) * (1.0f + erff(v * 0.70710678118654752f));
+  } else if (act == 3) {
+    const float u = 0.79788456080286536f * (v + 0.044715f * (v * v * v));
+    v = (0.5f * v) * (1.0f + tanhf(u));
+  }
+  return v;
+}
+
+IC_DEV float epi_apply(float v, const ic_epi& e, int m, int n) {
+  v = epi_act(v, e.act);
+  if (e.res != nullptr) v = v + ld_any_f32(e.res, e.res_dt, (int64_t)m * e.ldr + n);
+  return v;
+}
+
+// GEMV bodies with an epilogue (gemv.hip), used by the GEMM entry points for M <= 16.
+int ic_gemv_w8a8_epi(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8_t* w, int64_t N, int64_t ldw,
+                     const float* s_a, const float* s_w, const void* bias, int bias_dtype, void* out, int out_dtype,
+                     int64_t ldo, const ic_epi& epi, void* stream);
+int ic_gemv_w4a8_epi(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed, int64_t N,
+                     int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a, const void* bias,
+                     int bias_dtype, void* out, int out_dtype, int64_t ldo, const ic_epi& epi, void* stream);

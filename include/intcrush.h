@@ -163,6 +163,30 @@ int ic_gemm_w4a8_ws(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const u
                     void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * The same GEMMs with the epilogue options of fused_int8_gemm_dequant
+ * (kernels/triton_int8_gemm.py:119-130, arguments :142-143): after dequant and
+ * bias, in f32,
+ *   activation 0: none; IC_ACT_SILU: v * sigmoid(v); IC_ACT_GELU:
+ *   0.5 v (1 + erf(v / sqrt 2)); IC_ACT_GELU_TANH: 0.5 v (1 + tanh(sqrt(2/pi)
+ *   (v + 0.044715 v^3))) (no counterpart in the reference; the MLPs of DiT
+ *   models such as Flux use it),
+ * then + residual[m, n] (f16/bf16/f32, row stride ldr; NULL for none), then
+ * the rounding to out_dtype.  Every M routes as ic_gemm_*_ws does (GEMV for
+ * M <= IC_GEMV_MAX_M, split-K with a workspace).  With activation 0 and no
+ * residual these are ic_gemm_w8a8_ws / ic_gemm_w4a8_ws.
+ */
+enum { IC_ACT_NONE = 0, IC_ACT_SILU = 1, IC_ACT_GELU = 2, IC_ACT_GELU_TANH = 3 };
+int ic_gemm_w8a8_ex(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8_t* w, int64_t N,
+                    int64_t ldw, const float* s_a, const float* s_w, const void* bias, int bias_dtype,
+                    int activation, const void* residual, int residual_dtype, int64_t ldr, void* out,
+                    int out_dtype, int64_t ldo, void* workspace, int64_t workspace_bytes, void* stream);
+int ic_gemm_w4a8_ex(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed,
+                    int64_t N, int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a,
+                    const void* bias, int bias_dtype, int activation, const void* residual,
+                    int residual_dtype, int64_t ldr, void* out, int out_dtype, int64_t ldo, void* workspace,
+                    int64_t workspace_bytes, void* stream);
+
+/*
  * W4A16: out = x . RN_dt(q * RN_dt(s))^T (+ bias), fp32 accumulation, dtype f16/bf16.
  * Replaces unpack_int4_to_float16 (kernels/triton_int4_unpack.py:62-88) + F.linear
  * of _ops.py:466-481.

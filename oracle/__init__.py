@@ -360,6 +360,39 @@ def epilogue(acc, s_a, s_w, bias=None, out_dtype: int = DT_F16) -> np.ndarray:
     return out
 
 
+def activate(v, act: int) -> np.ndarray:
+    """Epilogue activations of triton_int8_gemm.py:119-124 in float64:
+    1 SiLU v * sigmoid(v), 2 GELU 0.5 v (1 + erf(v / sqrt 2)); 3 is GELU with
+    the tanh approximation 0.5 v (1 + tanh(sqrt(2/pi) (v + 0.044715 v^3))),
+    which the reference kernel does not have (its Flux-style MLPs use it)."""
+    from scipy.special import erf
+
+    v = np.asarray(v, np.float64)
+    if act == 0:
+        return v.copy()
+    if act == 1:
+        with np.errstate(over="ignore"):
+            return v / (1.0 + np.exp(-v))
+    if act == 2:
+        return 0.5 * v * (1.0 + erf(v / np.sqrt(2.0)))
+    if act == 3:
+        return 0.5 * v * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (v + 0.044715 * v ** 3)))
+    raise ValueError(f"unknown activation {act}")
+
+
+def epilogue_ex(acc, s_a, s_w, bias=None, out_dtype: int = DT_F16, activation: int = 0, residual=None):
+    """The GEMM epilogue with the options of triton_int8_gemm.py:119-130: the
+    f32 dequant (+ bias) value of epilogue(), the activation in float64, plus
+    the residual, then one rounding to out_dtype.  The GPU evaluates the
+    activation and the add in f32, so it matches to a few f32 ulp before the
+    final rounding (within one ulp of out_dtype after it)."""
+    v = epilogue(acc, s_a, s_w, bias, DT_F32).astype(np.float64)
+    v = activate(v, activation)
+    if residual is not None:
+        v = v + np.asarray(residual, np.float64)
+    return round_dtype(v, out_dtype)
+
+
 # ---------------------------------------------------------------- fp32 fallback
 def dequant_weight_fp32(w, s_w, K: int, int4: bool):
     """IntCrushInt{4,8}Layout.dequantize (quant_layout.py:80-87, :163-168) with

@@ -1,0 +1,243 @@
+"""The activation / residual epilogue of the INT8 and W4A8 GEMMs
+(kernels/triton_int8_gemm.py:119-130 and its arguments :142-143).
+
+CPU: the oracle's activations against torch's own SiLU / GELU / GELU-tanh in
+float64, the reduction of the extended epilogue to the plain one, and the
+host-side argument checks.  GPU: every routing of the GEMM (GEMV at M <= 16,
+split K at small M, the MFMA tiles with the LDS-staged 16-bit epilogue, the
+direct epilogue for ragged N or an odd residual stride, the shape-generic
+kernel) for each activation and residual dtype.  With activation 0 the
+residual add is one f32 addition, so those outputs are bit-exact; with an
+activation the GPU's f32 expf / erff / tanhf may differ from the float64
+oracle by a few f32 ulp before the final rounding, so outputs are held to
+2^-20 (|v| + |act(v)| + |residual|) plus one ulp of the output dtype.  The
+f32 outputs are the ones that tell GELU from GELU-tanh (their difference is
+far above that bound and may hide under a bf16 ulp).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+DT = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+MANT = {torch.float16: 10, torch.bfloat16: 7}
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+# ------------------------------------------------------------------ CPU
+def _grid():
+    v = np.linspace(-30.0, 30.0, 6001)
+    return np.concatenate([v, [0.0, -0.0, 1e-30, -1e-30, 1e-3, -1e-3, 88.0, -88.0, 200.0, -200.0]])
+
+
+def test_oracle_silu_is_torch_silu(oracle):
+    v = _grid()
+    ref = F.silu(torch.from_numpy(v)).numpy()
+    assert np.allclose(oracle.activate(v, 1), ref, rtol=1e-13, atol=1e-300)
+
+
+@pytest.mark.parametrize("act,approx", [(2, "none"), (3, "tanh")])
+def test_oracle_gelu_is_torch_gelu(oracle, act, approx):
+    v = _grid()
+    ref = F.gelu(torch.from_numpy(v), approximate=approx).numpy()
+    assert np.allclose(oracle.activate(v, act), ref, rtol=1e-12, atol=1e-15)
+
+
+def test_oracle_activation_special_values(oracle):
+    for act in (1, 2, 3):
+        assert oracle.activate(np.array([0.0]), act)[0] == 0.0
+        big = oracle.activate(np.array([50.0, -50.0]), act)
+        assert big[0] == 50.0 and abs(big[1]) < 1e-15
+    # the two GELUs differ by far more than the f32 tolerance of the GPU tests
+    v = np.linspace(-4, 4, 801)
+    assert np.abs(oracle.activate(v, 2) - oracle.activate(v, 3)).max() > 1e-4
+    with pytest.raises(ValueError):
+        oracle.activate(v, 4)
+
+
+def test_epilogue_ex_reduces_to_epilogue(oracle):
+    g = np.random.default_rng(3)
+    acc = g.integers(-2 ** 20, 2 ** 20, (7, 9)).astype(np.int32)
+    s_a = (g.random(7) * 1e-3).astype(np.float32)
+    s_w = (g.random(9) * 1e-2).astype(np.float32)
+    b = g.standard_normal(9).astype(np.float32)
+    for dt in (0, 1, 2):
+        assert np.array_equal(oracle.epilogue_ex(acc, s_a, s_w, b, dt), oracle.epilogue(acc, s_a, s_w, b, dt))
+    # residual on unit scales: the integers themselves plus the residual
+    acc = np.arange(-6, 6, dtype=np.int32).reshape(3, 4)
+    r = np.full((3, 4), 0.5, np.float32)
+    out = oracle.epilogue_ex(acc, np.ones(3, np.float32), np.ones(4, np.float32), None, 2, 0, r)
+    assert np.array_equal(out, acc.astype(np.float32) + 0.5)
+    silu = oracle.epilogue_ex(acc, np.ones(3, np.float32), np.ones(4, np.float32), None, 2, 1, None)
+    assert silu[1, 2] == 0.0 and silu[0, 0] < 0 and silu[2, 3] > 4.9
+
+
+def test_epilogue_args_checks(rt):
+    with pytest.raises(ValueError, match="activation"):
+        rt._epilogue_args(4, None, 2, 2)
+    with pytest.raises(ValueError, match="activation"):
+        rt._epilogue_args(-1, None, 2, 2)
+    with pytest.raises(ValueError, match="residual shape"):
+        rt._epilogue_args(0, torch.zeros(3, 4), 3, 5)
+    wide = torch.zeros(3, 12, dtype=torch.float16)
+    act, ptr, dt, ldr, keep = rt._epilogue_args(1, wide[:, :5], 3, 5)
+    assert (act, dt, ldr) == (1, 0, 12) and ptr.value == wide.data_ptr()
+    # a transposed view is made contiguous; a 3-D residual is flattened to rows
+    _, _, _, ldr, keep = rt._epilogue_args(0, torch.zeros(5, 3).t(), 3, 5)
+    assert ldr == 5 and keep.is_contiguous()
+    _, _, dt, ldr, _ = rt._epilogue_args(0, torch.zeros(1, 3, 5, dtype=torch.bfloat16), 3, 5)
+    assert (dt, ldr) == (1, 5)
+    with pytest.raises(TypeError):
+        rt._epilogue_args(0, torch.zeros(3, 5, dtype=torch.float64), 3, 5)
+
+
+# ------------------------------------------------------------------ GPU
+# (M, N, K, route); the route is asserted where the library exposes it
+SHAPES = [
+    (5, 384, 512, "gemv"),
+    (100, 1000, 3072, "splitk"),
+    (384, 512, 512, "tiles"),
+    (260, 250, 384, "ragged"),
+]
+FMTS = ["int8", "int4", "int4g"]
+
+
+def _ulp(ref: np.ndarray, dtype) -> np.ndarray:
+    if dtype == torch.float32:
+        return np.zeros_like(ref, dtype=np.float64)
+    mant = MANT[dtype]
+    emin = -14 if dtype == torch.float16 else -126
+    e = np.floor(np.log2(np.maximum(np.abs(ref).astype(np.float64), 2.0 ** emin)))
+    return 2.0 ** (e - mant)
+
+
+def _problem(M, N, K, fmt, seed, oracle):
+    a = torch.randint(-127, 128, (M, K), generator=_gen(seed), dtype=torch.int8)
+    s_a = torch.rand(M, generator=_gen(seed + 1)) * 0.02 + 1e-3
+    G = K // 128 if fmt == "int4g" else 1
+    if fmt == "int8":
+        w = torch.randint(-127, 128, (N, K), generator=_gen(seed + 2), dtype=torch.int8)
+        wq = w.numpy()
+        s_w = (torch.rand(N, generator=_gen(seed + 3)) * 2e-3 + 1e-4).to(torch.float16).float()
+    else:
+        w = torch.randint(0, 256, (N, K // 2), generator=_gen(seed + 2), dtype=torch.uint8)
+        wq = oracle.unpack_int4(w.numpy(), K)
+        s_w = (torch.rand(N, G, generator=_gen(seed + 3)) * 3e-2 + 1e-3).to(torch.float16).float()
+    bias = torch.randn(N, generator=_gen(seed + 4)).to(torch.bfloat16)
+    acc = oracle.gemm_acc(a.numpy(), wq, G)
+    return a, w, s_a, s_w, bias, acc
+
+
+def _run(rt, fmt, a, w, s_a, s_w, bias, out_dtype, act, res, dev):
+    kw = dict(bias=bias.to(dev), out_dtype=out_dtype, activation=act, residual=res)
+    if fmt == "int8":
+        return rt.fused_int8_gemm_dequant(a.to(dev), w.to(dev), s_w.to(dev), s_a.to(dev), **kw)
+    return rt.gemm_w4a8(a.to(dev), w.to(dev), s_w.to(dev), s_a.to(dev), **kw)
+
+
+def _residuals(M, N, out_dtype, seed, dev):
+    """None, a contiguous one in the output's 16-bit dtype (bf16 for f32
+    outputs), an f32 one, and an f16 view with an odd row stride."""
+    g = _gen(seed)
+    r16 = torch.randn(M, N, generator=g).to(out_dtype if out_dtype != torch.float32 else torch.bfloat16)
+    r32 = torch.randn(M, N, generator=g) * 3.0
+    odd = torch.randn(M, N + 3, generator=g).to(torch.float16)
+    return [("none", None), ("r16", r16.to(dev)), ("r32", r32.to(dev)), ("odd", odd.to(dev)[:, :N])]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("M,N,K,route", SHAPES)
+def test_gemm_epilogue_matches_oracle(rt, oracle, dev, M, N, K, route, fmt, out_dtype):
+    if fmt == "int4g" and K % 128:
+        pytest.skip("grouped scales need K % 128 == 0")
+    G = K // 128 if fmt == "int4g" else 1
+    if route == "splitk":
+        assert rt.lib().ic_gemm_splitk_bytes(M, N, K, G, int(fmt != "int8")) > 0
+    elif route != "gemv":
+        assert rt.lib().ic_gemm_splitk_bytes(M, N, K, G, int(fmt != "int8")) == 0
+    a, w, s_a, s_w, bias, acc = _problem(M, N, K, fmt, 900 + M, oracle)
+    v32 = _run(rt, fmt, a, w, s_a, s_w, bias, torch.float32, 0, None, dev).cpu().numpy()
+    if not (route == "splitk" and fmt == "int4g"):
+        # (grouped split-K sums its slices in another order: test_gpu_kernels
+        # bounds that; the options below act on whatever value the GEMM made)
+        assert np.array_equal(v32, oracle.epilogue(acc, s_a.numpy(), s_w.numpy(), bias.float().numpy(), 2))
+    v = v32.astype(np.float64)
+    for rname, res in _residuals(M, N, out_dtype, 77, dev):
+        r = None if res is None else res.float().cpu().numpy()
+        for act in (0, 1, 2, 3):
+            out = _run(rt, fmt, a, w, s_a, s_w, bias, out_dtype, act, res, dev).float().cpu().numpy()
+            tag = f"{route} {fmt} {out_dtype} act={act} res={rname}"
+            if act == 0:
+                # one f32 addition, then the rounding: bit-exact
+                s = v32 if r is None else (v32 + r.astype(np.float32))
+                ref = oracle.round_dtype(s.astype(np.float64), DT[out_dtype])
+                assert np.array_equal(out, ref), tag
+                continue
+            act_v = oracle.activate(v, act)
+            ref = oracle.round_dtype(act_v if r is None else act_v + r, DT[out_dtype])
+            av = np.abs(act_v)
+            bound = 2.0 ** -20 * (np.abs(v) + av + (0 if r is None else np.abs(r))) + _ulp(ref, out_dtype)
+            err = np.abs(out.astype(np.float64) - ref)
+            bad = err > bound
+            assert not bad.any(), f"{tag}: {bad.sum()} outside, worst {err.max():.3g}"
+            # the outputs are not trivially equal to the unactivated ones
+            assert np.abs(ref - oracle.round_dtype(v if r is None else v + r, DT[out_dtype])).max() > 1e-2
+
+
+@pytest.mark.gpu
+def test_gemm_epilogue_generic_kernel(rt, oracle, dev):
+    """K not a multiple of the MFMA step: the shape-generic kernel applies the
+    same epilogue."""
+    M, N, K = 70, 96, 200
+    a, w, s_a, s_w, bias, acc = _problem(M, N, K, "int8", 31, oracle)
+    r = torch.randn(M, N, generator=_gen(32)).to(torch.float16)
+    v32 = oracle.epilogue(acc, s_a.numpy(), s_w.numpy(), bias.float().numpy(), DT[torch.float32])
+    out = _run(rt, "int8", a, w, s_a, s_w, bias, torch.float32, 0, r.to(dev), dev).cpu().numpy()
+    assert np.array_equal(out, v32 + r.float().numpy())
+    out = _run(rt, "int8", a, w, s_a, s_w, bias, torch.float32, 1, r.to(dev), dev).cpu().numpy()
+    ref = oracle.epilogue_ex(acc, s_a.numpy(), s_w.numpy(), bias.float().numpy(), 2, 1, r.float().numpy())
+    assert np.allclose(out, ref, rtol=2e-6, atol=1e-6)
+
+
+@pytest.mark.gpu
+def test_gemm_epilogue_rejects_bad_arguments(rt, dev):
+    a = torch.zeros(32, 128, dtype=torch.int8, device=dev)
+    w = torch.zeros(64, 128, dtype=torch.int8, device=dev)
+    s = torch.ones(64, device=dev)
+    sa = torch.ones(32, device=dev)
+    with pytest.raises(ValueError, match="activation"):
+        rt.fused_int8_gemm_dequant(a, w, s, sa, activation=5)
+    with pytest.raises(ValueError, match="residual shape"):
+        rt.fused_int8_gemm_dequant(a, w, s, sa, residual=torch.zeros(32, 63, device=dev))
+    with pytest.raises(ValueError):
+        rt.fused_int8_gemm_dequant(a, w, s, sa, residual=torch.zeros(32, 64))  # host residual
+    # the C entry point checks its own arguments too
+    P = rt._ptr
+    out = torch.empty(32, 64, dtype=torch.bfloat16, device=dev)
+    rc = rt.lib().ic_gemm_w8a8_ex(P(a), 32, 128, 128, P(w), 64, 128, P(sa), P(s), None, 0, 7, None, 0, 0,
+                                  P(out), 1, 64, None, 0, None)
+    assert rc != 0 and b"activation" in rt.lib().ic_last_error()
+    r = torch.zeros(32, 64, device=dev)
+    rc = rt.lib().ic_gemm_w8a8_ex(P(a), 32, 128, 128, P(w), 64, 128, P(sa), P(s), None, 0, 1, P(r), 2, 10,
+                                  P(out), 1, 64, None, 0, None)
+    assert rc != 0 and b"stride" in rt.lib().ic_last_error()
+
+
+@pytest.mark.gpu
+def test_gemm_epilogue_default_is_plain_gemm(rt, dev):
+    """activation 0 and no residual run the plain kernels: identical bits."""
+    g = _gen(5)
+    a = torch.randint(-127, 128, (512, 1024), generator=g, dtype=torch.int8).to(dev)
+    w = torch.randint(0, 256, (768, 512), generator=g, dtype=torch.uint8).to(dev)
+    s_w = (torch.rand(768, 8, generator=g) * 1e-2 + 1e-3).to(dev)
+    s_a = (torch.rand(512, generator=g) * 1e-2).to(dev)
+    x = rt.gemm_w4a8(a, w, s_w, s_a, out_dtype=torch.bfloat16)
+    y = rt.gemm_w4a8(a, w, s_w, s_a, out_dtype=torch.bfloat16, activation=0, residual=None)
+    assert torch.equal(x, y)
