@@ -17,9 +17,11 @@ unrotated INT4 layer to W4A16).  Attention is torch's SDPA on its flash or
 memory-efficient backend.  The adaptive LayerNorm in front of qkv and MLP-up
 (LayerNorm without affine, then (1 + scale) * . + shift from the modulation)
 is fused into those linears' prep: one norm_rotate_quantize launch per linear
-reads the block input and writes its INT8 codes.  QK RMSNorm, RoPE, GELU,
-residual gates, the embedders and the final layer are torch ops in bf16 (the
-embedders and final layer are unquantized bf16 linears).
+reads the block input and writes its INT8 codes.  The MLP's GELU (tanh form)
+is the MLP-up GEMM's epilogue activation, and the single block's
+proj(attn) + down(h) sum is the MLP-down GEMM's residual epilogue.  QK
+RMSNorm, RoPE, residual gates, the embedders and the final layer are torch
+ops in bf16 (the embedders and final layer are unquantized bf16 linears).
 
 The single-stream block's fused linear1/linear2 are the config's separate
 qkv + MLP-up and proj + MLP-down linears; proj(attn) + down(gelu(up)) equals
@@ -42,6 +44,7 @@ IMG_TOKENS, TXT_TOKENS = 4096, 512
 IN_CH, CTX_DIM, VEC_DIM, TIME_DIM = 64, 4096, 768, 256
 ROPE_AXES, ROPE_THETA = (16, 56, 56), 10000
 ROT_SIZE, GROUP = 256, 128
+GELU_TANH = 3  # GEMM epilogue activation code (GELU, tanh approximation)
 MOD_N = 6 * HID  # 18432
 # (name, K, N) of the quantized linears of one block and stream
 BLOCK_LINEARS = (("qkv", HID, 3 * HID), ("proj", HID, HID), ("mlp_up", HID, MLP), ("mlp_down", MLP, HID))
@@ -74,16 +77,17 @@ class QLinear:
                                        w_in=self.K, smoothrot=self.sr, perm=self.perm, s_a_out=s_out,
                                        x_int8_out=q_out)
 
-    def norm_call(self, rt, x, weight, bias):
+    def norm_call(self, rt, x, weight, bias, activation=0):
         q, s_a = self.norm_quantize(rt, x, weight, bias)
-        return self.gemm(rt, q, s_a, x.dtype)
+        return self.gemm(rt, q, s_a, x.dtype, activation=activation)
 
-    def gemm(self, rt, q, s_a, act, out=None):
-        return rt.gemm_w4a8(q, self.w, self.s_w, s_a, bias=self.b, out_dtype=act, out=out)
+    def gemm(self, rt, q, s_a, act, out=None, activation=0, residual=None):
+        return rt.gemm_w4a8(q, self.w, self.s_w, s_a, bias=self.b, out_dtype=act, out=out,
+                            activation=activation, residual=residual)
 
-    def __call__(self, rt, x):
+    def __call__(self, rt, x, residual=None):
         q, s_a = self.quantize(rt, x)
-        return self.gemm(rt, q, s_a, x.dtype)
+        return self.gemm(rt, q, s_a, x.dtype, residual=residual)
 
 
 class W4A16Linear(QLinear):
@@ -244,7 +248,6 @@ class FluxStep:
 
     def _double_block(self, blk, img, txt, vec_silu, freqs):
         import torch
-        import torch.nn.functional as F
 
         rt = self.rt
         im = self._mod_w4a8(blk["img_mod"], vec_silu)
@@ -254,24 +257,23 @@ class FluxStep:
         attn = self.attention(torch.cat((tq, iq), 1), torch.cat((tk, ik), 1), torch.cat((tv, iv), 1), freqs)
         t_a, i_a = attn[:TXT_TOKENS], attn[TXT_TOKENS:]
         img = torch.addcmul(img, im[2], blk["img_proj"](rt, i_a))
-        h = F.gelu(blk["img_mlp_up"].norm_call(rt, img, *self._ada(im[3], im[4])), approximate="tanh")
+        h = blk["img_mlp_up"].norm_call(rt, img, *self._ada(im[3], im[4]), activation=GELU_TANH)
         img = torch.addcmul(img, im[5], blk["img_mlp_down"](rt, h))
         txt = torch.addcmul(txt, tm[2], blk["txt_proj"](rt, t_a))
-        h = F.gelu(blk["txt_mlp_up"].norm_call(rt, txt, *self._ada(tm[3], tm[4])), approximate="tanh")
+        h = blk["txt_mlp_up"].norm_call(rt, txt, *self._ada(tm[3], tm[4]), activation=GELU_TANH)
         txt = torch.addcmul(txt, tm[5], blk["txt_mlp_down"](rt, h))
         return img, txt
 
     def _single_block(self, blk, x, vec_silu, freqs):
         import torch
-        import torch.nn.functional as F
 
         rt = self.rt
         shift, scale, gate = blk["mod"](rt, vec_silu).chunk(6, dim=-1)[:3]
         ada = self._ada(shift, scale)
         q, k, v = self._split_heads(blk["qkv"].norm_call(rt, x, *ada), blk["qk_scale"])
-        up = blk["mlp_up"].norm_call(rt, x, *ada)
+        h = blk["mlp_up"].norm_call(rt, x, *ada, activation=GELU_TANH)
         out = blk["proj"](rt, self.attention(q, k, v, freqs))
-        out = out + blk["mlp_down"](rt, F.gelu(up, approximate="tanh"))
+        out = blk["mlp_down"](rt, h, residual=out)  # proj(attn) + down(h) in the epilogue
         return torch.addcmul(x, gate, out)
 
     def forward(self):
@@ -323,9 +325,12 @@ class FluxStep:
         qkv = [torch.randn(HEADS, S, HEAD_DIM, generator=g, device=dev).to(act) for _ in range(3)]
         freqs = self._rope_tables()
 
+        gelu = {id(l) for l in self._kind_layers("mlp_up")}
+
         def gemm():
             for M, l in lin:
-                l.gemm(rt, q[(M, l.K)], s_a[M], act, out=out[(M, l.N)])
+                l.gemm(rt, q[(M, l.K)], s_a[M], act, out=out[(M, l.N)],
+                       activation=GELU_TANH if id(l) in gelu else 0)
 
         def prep():
             for M, l in lin:
@@ -350,7 +355,8 @@ class FluxStep:
 
             def fn():
                 for M, l in sel:
-                    l.gemm(rt, q[(M, l.K)], s_a[M], act, out=out[(M, l.N)])
+                    l.gemm(rt, q[(M, l.K)], s_a[M], act, out=out[(M, l.N)],
+                           activation=GELU_TANH if id(l) in gelu else 0)
             return fn
 
         return {"gemm_w4a8": gemm, "rotate_quantize": prep, "modulation_gemvs": modulation,

@@ -60,6 +60,37 @@ def test_oracle_activation_special_values(oracle):
         oracle.activate(v, 4)
 
 
+def _f32_gelu_as(v, rcp_ulp=0, exp_ulp=0):
+    """The kernel's f32 GELU (Abramowitz & Stegun 7.1.26 erf) in numpy f32,
+    with its reciprocal and exp2 results moved by rcp_ulp / exp_ulp ulp (the
+    hardware instructions are within 1 ulp)."""
+    f = np.float32
+    a = np.abs(v) * f(0.70710678118654752)
+    t = f(1) / (f(1) + f(0.3275911) * a)
+    if rcp_ulp:
+        t = np.nextafter(t, f(rcp_ulp * np.inf))
+    p = t * (f(0.254829592) + t * (f(-0.284496736) + t * (f(1.421413741) + t * (f(-1.453152027)
+                                                                                + t * f(1.061405429)))))
+    e = np.exp2(((a * a) * f(-1.44269504088896341)).astype(np.float64)).astype(np.float32)
+    if exp_ulp:
+        e = np.nextafter(e, f(exp_ulp * np.inf))
+    q = p * e
+    return (v * f(0.5)) * np.where(v >= 0, f(2) - q, q)
+
+
+def test_gelu_erf_approximation_bound(oracle):
+    """The published 1.5e-7 bound of the erf approximation plus f32 rounding
+    keeps the kernel's GELU within 2^-21 (|v| + |GELU(v)|) of float64 GELU:
+    inside the 2^-20 the GPU tests allow, on both sides of every branch."""
+    v = np.concatenate([np.linspace(-12, 12, 240001), np.geomspace(1e-6, 12, 20001),
+                        -np.geomspace(1e-6, 12, 20001), [0.0]]).astype(np.float32)
+    ref = oracle.activate(v.astype(np.float64), 2)
+    for ru in (-1, 0, 1):
+        for eu in (-1, 0, 1):
+            err = np.abs(_f32_gelu_as(v, ru, eu).astype(np.float64) - ref)
+            assert (err <= 2.0 ** -21 * (np.abs(v) + np.abs(ref))).all(), (ru, eu)
+
+
 def test_epilogue_ex_reduces_to_epilogue(oracle):
     g = np.random.default_rng(3)
     acc = g.integers(-2 ** 20, 2 ** 20, (7, 9)).astype(np.int32)
