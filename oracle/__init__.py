@@ -26,6 +26,8 @@ none is left unpinned:
                             hand-built ties and the 0.49999997 quirk, zero rows
   gemm_acc                  int64 matmul; group sums add to the ungrouped sum
   epilogue                  against linear_fallback_fp32 on the same integers
+  activate / epilogue_ex    torch's F.silu / F.gelu (erf and tanh forms) in float64 over a dense
+                            grid and saturation values; reduces to epilogue without options
   dequant_w4a16             single correctly rounded fp16 product (numpy fp16)
   reference_fallback_forward against the integer chain (prepare -> quantize ->
                             gemm_acc -> epilogue) within quantization error; a
