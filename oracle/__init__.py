@@ -13,8 +13,8 @@ against.
 
 Reference citations are file:line in ThunderFun/ComfyUI-INT-Crush.
 
-How each function is pinned (tests/test_oracle.py, tests/test_numerics_proofs.py);
-none is left unpinned:
+How each function is pinned (tests/test_oracle.py, tests/test_numerics_proofs.py,
+tests/test_norm_quant.py, tests/test_gemm_epilogue.py); none is left unpinned:
   unpack_int4 / pack_int4   the reference's known answers (tests/test_quant_utils.py:65-99
                             of the reference), all 256 byte values, round trips
   prepare (Hadamard)        orthogonality and involution of H, closed-form entries
