@@ -223,20 +223,77 @@ def make_intcrush_ops(quant_format: str, rot_size: int, use_pytorch: bool = Fals
                 out.add_(adapter.h(x_raw, out).to(out.dtype))
                 return adapter.g(out)
 
-            def _apply_residuals(self, x: torch.Tensor, out: torch.Tensor,
-                                 x_prep: torch.Tensor | None = None) -> torch.Tensor:
-                """SVD low-rank residual, then the adapter (_ops.py:367-387)."""
+            def _svd_factors(self, x: torch.Tensor):
+                """L1 [N, r] and L2 [r, K] on x's device and dtype, cached on the
+                module (_ops.py:372-381); (None, None) without an SVD branch."""
                 L1, L2 = self._intcrush_L1, self._intcrush_L2
-                if L1 is not None and L2 is not None:
-                    if L1.device != x.device or L1.dtype != x.dtype:
-                        L1 = self._intcrush_L1 = L1.to(device=x.device, dtype=x.dtype)
-                    if L2.device != x.device or L2.dtype != x.dtype:
-                        L2 = self._intcrush_L2 = L2.to(device=x.device, dtype=x.dtype)
+                if L1 is None or L2 is None:
+                    return None, None
+                if L1.device != x.device or L1.dtype != x.dtype:
+                    L1 = self._intcrush_L1 = L1.to(device=x.device, dtype=x.dtype)
+                if L2.device != x.device or L2.dtype != x.dtype:
+                    L2 = self._intcrush_L2 = L2.to(device=x.device, dtype=x.dtype)
+                return L1, L2
+
+            def _apply_residuals(self, x: torch.Tensor, out: torch.Tensor,
+                                 x_prep: torch.Tensor | None = None, folded: bool = False,
+                                 lora_folded: bool = False) -> torch.Tensor:
+                """SVD low-rank residual, then the adapter (_ops.py:367-387).
+                folded / lora_folded: the SVD branch / standard LoRA were already
+                added by the GEMM's residual epilogue (_fold_linear_residuals)."""
+                L1, L2 = self._svd_factors(x)
+                if L1 is not None and not folded:
                     src = x_prep if x_prep is not None else x.reshape(-1, x.shape[-1])
                     mid = src.to(L1.dtype) @ L2.t()
                     out.addmm_(mid.to(out.dtype), L1.t().to(out.dtype), beta=1, alpha=1)
-                self._apply_adapter(x.reshape(-1, x.shape[-1]), out)
+                if not lora_folded:
+                    self._apply_adapter(x.reshape(-1, x.shape[-1]), out)  # in place, as :386
                 return out
+
+            def _fold_linear_residuals(self, x: torch.Tensor, x_prep: torch.Tensor | None, params,
+                                       out_dtype: torch.dtype, svd_src: torch.Tensor | None):
+                """The corrections the reference adds to the GEMM output one
+                addmm_ at a time -- the zero-point term (_ops.py:459-461, here
+                group-aware), the SVD low-rank branch (:370-384) and a standard
+                LoRA (:236-244) -- as one [M, N] tensor in the output dtype, for
+                the GEMM's residual epilogue: one small GEMM over the
+                concatenated factors [sum_g x_prep | svd_src L2^T | c x down^T]
+                times [-(s zp) | L1 | up]^T, each factor in the dtype the
+                reference multiplies it in.  svd_src is what the path's SVD
+                branch reads (the prepared activation on the INT4 paths, the raw
+                input on the INT8 path).  Returns (residual or None, standard
+                LoRA folded)."""
+                x2 = x.reshape(-1, x.shape[-1])
+                M = x2.shape[0]
+                A, B = [], []
+                if params.zp is not None:
+                    N = params.zp.numel()
+                    s = params.scale.reshape(N, -1).float()
+                    G = s.shape[1]
+                    A.append(x_prep.float().reshape(M, G, -1).sum(-1))
+                    B.append(-(s * params.zp.reshape(-1, 1).float()))
+                L1, L2 = self._svd_factors(x)
+                if L1 is not None:
+                    A.append(svd_src.to(L1.dtype) @ L2.t())
+                    B.append(L1)
+                lora = False
+                adapter = self._intcrush_adapter
+                if adapter is not None and adapter.name == "lora":
+                    if not self._intcrush_adapter_ready or self._intcrush_adapter_device != x2.device:
+                        _move_adapter_weights(adapter, x2.device, x2.dtype)
+                        self._intcrush_adapter_ready = True
+                        self._intcrush_adapter_device = x2.device
+                    up, down, alpha = adapter.weights[0], adapter.weights[1], adapter.weights[2]
+                    rank = down.shape[0]
+                    c = (float(alpha) / rank if alpha else 1.0) * self._intcrush_lora_strength
+                    A.append(F.linear(x2, down) * c)
+                    B.append(up)
+                    lora = True
+                if not A:
+                    return None, False
+                a = torch.cat([t.to(out_dtype) for t in A], 1)
+                b = torch.cat([t.to(out_dtype) for t in B], 1)
+                return a @ b.t(), lora
 
             def _finish_forward(self, out: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
                 return out.to(x.dtype).reshape(*x.shape[:-1], -1)
@@ -331,10 +388,9 @@ def make_intcrush_ops(quant_format: str, rot_size: int, use_pytorch: bool = Fals
                                                  perm=st.perm) if need_prep else None)
                 q, s_a = _rt.rotate_quantize(x2, rot_size=R, w_in=self._intcrush_w_in, smoothrot=st.smoothrot,
                                              perm=st.perm)
-                out = _rt.gemm_w4a8(q, qdata, params.scale, s_a, bias=bias, out_dtype=x.dtype)
-                if params.zp is not None:
-                    self._zp_correction(out, x_prep, params.scale, params.zp)
-                out = self._apply_residuals(x, out, x_prep=x_prep)
+                res, lora = self._fold_linear_residuals(x, x_prep, params, x.dtype, x_prep)
+                out = _rt.gemm_w4a8(q, qdata, params.scale, s_a, bias=bias, out_dtype=x.dtype, residual=res)
+                out = self._apply_residuals(x, out, x_prep=x_prep, folded=True, lora_folded=lora)
                 return self._finish_forward(out, x)
 
             def _forward_int4_w4a16(self, qdata, weight, bias, x):
@@ -392,13 +448,17 @@ def make_intcrush_ops(quant_format: str, rot_size: int, use_pytorch: bool = Fals
                 if fused:
                     out = _rt.fused_quant_int8_gemm_dequant(x_prep, qdata, params.scale, bias=bias,
                                                             out_dtype=compute_dtype)
-                else:
-                    q, s_a = _rt.rotate_quantize(x2, rot_size=R, w_in=self._intcrush_w_in, smoothrot=st.smoothrot,
-                                                 perm=st.perm, smooth=st.smooth)
-                    out = _rt.fused_int8_gemm_dequant(q, qdata, params.scale, s_a, bias=bias, out_dtype=compute_dtype)
-                if zp is not None:
-                    self._zp_correction(out, x_prep, params.scale, zp)
-                out = self._apply_residuals(x, out)
+                    if zp is not None:
+                        self._zp_correction(out, x_prep, params.scale, zp)
+                    out = self._apply_residuals(x, out)
+                    return self._finish_forward(out, x)
+                q, s_a = _rt.rotate_quantize(x2, rot_size=R, w_in=self._intcrush_w_in, smoothrot=st.smoothrot,
+                                             perm=st.perm, smooth=st.smooth)
+                # the INT8 path's SVD branch reads the raw input (_ops.py:578)
+                res, lora = self._fold_linear_residuals(x, x_prep, params, compute_dtype, x2)
+                out = _rt.fused_int8_gemm_dequant(q, qdata, params.scale, s_a, bias=bias, out_dtype=compute_dtype,
+                                                  residual=res)
+                out = self._apply_residuals(x, out, folded=True, lora_folded=lora)
                 return self._finish_forward(out, x)
 
             # ── state-dict loading (_ops.py:583-761) ─────────────────

@@ -157,6 +157,98 @@ def test_svd_residual_and_zero_point_w4a8(dev):
     assert _cos(out, ref) >= 0.9999
 
 
+def _lora(N, K, rank, seed):
+    """A standard LoRA adapter as ComfyUI hands it over (name, weights
+    (up [N, r], down [r, K], alpha))."""
+    import types
+
+    g = torch.Generator().manual_seed(seed)
+    up = torch.randn(N, rank, generator=g) * 0.05
+    down = torch.randn(rank, K, generator=g) * 0.05
+    return types.SimpleNamespace(name="lora", weights=(up, down, float(rank) / 2))
+
+
+def _attach(lin, adapter, strength):
+    lin._intcrush_adapter = adapter
+    lin._intcrush_lora_strength = strength
+    lin._intcrush_adapter_ready = False
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_folded_residuals_w4a8(dev, dtype):
+    """Zero point, SVD branch and a standard LoRA reach the W4A8 GEMM as one
+    residual: the output is round(f32 GEMM + residual) bit for bit, stays
+    within two output ulps of the reference's one-addmm_-per-term order, and
+    matches the fp32 fallback with the same corrections."""
+    rt = __graft_entry__._submodule("_hip_runtime")
+    M, K, N, R = 40, 512, 96, 64
+    ops = ops_mod.make_intcrush_ops("int4_crush", R)
+    sd = int4_layer(N, K, G=4, seed=21, zp=True, svd_rank=8)
+    lin_cpu = load_linear(ops, "blk.fc", sd, K, N)
+    lin = _to_dev(load_linear(ops, "blk.fc", sd, K, N), dev)
+    _attach(lin, _lora(N, K, 16, 22), 0.8)
+    _attach(lin_cpu, _lora(N, K, 16, 22), 0.8)
+    x = _x(M, K, dtype, 23).to(dev)
+    out = lin(x)
+    # the same pieces by hand: GEMM in f32, the folded residual, one rounding
+    params = lin.weight._params
+    st = lin._intcrush_state(x)
+    kw = dict(rot_size=R, w_in=lin._intcrush_w_in, smoothrot=st.smoothrot, perm=st.perm)
+    x_prep = rt.prepare_activation(x, **kw)
+    q, s_a = rt.rotate_quantize(x, **kw)
+    res, lora = lin._fold_linear_residuals(x, x_prep, params, dtype, x_prep)
+    assert lora and res.dtype == dtype and tuple(res.shape) == (M, N)
+    v = rt.gemm_w4a8(q, lin.weight._qdata, params.scale, s_a, bias=lin.bias, out_dtype=torch.float32)
+    assert torch.equal(out, (v + res.float()).to(dtype))
+    # the reference's order: GEMM rounded, then each correction by its own addmm_
+    # (four roundings to the dtype where the fold has two): against the exact
+    # float64 sum the fold is no less accurate
+    plain = rt.gemm_w4a8(q, lin.weight._qdata, params.scale, s_a, bias=lin.bias, out_dtype=dtype)
+    lin._zp_correction(plain, x_prep, params.scale, params.zp)
+    plain = lin._apply_residuals(x, plain, x_prep=x_prep)
+    xd, xpd = x.double(), x_prep.double()
+    G = params.scale.reshape(N, -1).shape[1]
+    zt = xpd.reshape(M, G, -1).sum(-1) @ (params.scale.reshape(N, G).double() * params.zp.double().reshape(-1, 1)).t()
+    L1, L2 = lin._intcrush_L1.double(), lin._intcrush_L2.double()
+    up, down, alpha = (t.double() if torch.is_tensor(t) else t for t in lin._intcrush_adapter.weights)
+    exact = v.double() - zt + (xpd @ L2.t()) @ L1.t() + (alpha / 16 * 0.8) * ((xd @ down.t()) @ up.t())
+    e_fold = (out.double() - exact).abs()
+    e_plain = (plain.double() - exact).abs()
+    assert e_fold.mean() <= 1.05 * e_plain.mean(), (e_fold.mean().item(), e_plain.mean().item())
+    ref = lin_cpu(x.float().cpu()) + sd["bias"].float()  # fp32 fallback (it drops the bias)
+    assert _cos(out.float().cpu(), ref) >= 0.9999
+
+
+def test_folded_residuals_int8_eager(dev):
+    """INT8 with a zero point runs eagerly; the zero-point term and a LoRA
+    go through the GEMM's residual epilogue, the SVD branch on the raw input
+    as the reference's INT8 path has it."""
+    rt = __graft_entry__._submodule("_hip_runtime")
+    M, K, N = 33, 256, 64
+    ops = ops_mod.make_intcrush_ops("int8_crush", 0)
+    sd = int8_layer(N, K, seed=24, zp=True)
+    lin = _to_dev(load_linear(ops, "blk.fc", sd, K, N), dev)
+    _attach(lin, _lora(N, K, 8, 25), 1.0)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(26)).to(torch.float16)
+    out = lin(x.to(dev))
+    assert lin._graph_runner is None
+    params = lin.weight._params
+    st = lin._intcrush_state(x.to(dev))
+    x2 = x.to(dev)
+    x_prep = rt.prepare_activation(x2, rot_size=0, w_in=lin._intcrush_w_in, smoothrot=st.smoothrot, perm=st.perm,
+                                   smooth=st.smooth)
+    q, s_a = rt.rotate_quantize(x2, rot_size=0, w_in=lin._intcrush_w_in, smoothrot=st.smoothrot, perm=st.perm,
+                                smooth=st.smooth)
+    res, lora = lin._fold_linear_residuals(x2, x_prep, params, torch.float16, x2)
+    assert lora
+    v = rt.fused_int8_gemm_dequant(q, lin.weight._qdata, params.scale, s_a, bias=lin.bias, out_dtype=torch.float32)
+    assert torch.equal(out, (v + res.float()).to(torch.float16))
+    up, down, alpha = _lora(N, K, 8, 25).weights
+    W = (sd["weight"].float() - sd["weight_zp"].reshape(-1, 1)) * sd["weight_scale"].float().reshape(-1, 1)
+    ref = x.float() @ W.t() + sd["bias"].float() + (alpha / 8) * ((x.float() @ down.t()) @ up.t())
+    assert _cos(out.float().cpu(), ref) >= 0.9999
+
+
 def test_gpu_forward_refuses_silent_fallback(dev, monkeypatch):
     ops = ops_mod.make_intcrush_ops("int4_crush", 64)
     lin = _to_dev(load_linear(ops, "blk.fc", int4_layer(16, 256, seed=11), 256, 16), dev)
