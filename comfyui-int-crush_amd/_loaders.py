@@ -17,6 +17,7 @@ import logging
 
 import torch
 
+from ._checkpoint import parse_padded_layers
 from ._lora import attach_lora_as_buffers, clear_intcrush_lora
 from ._ops import make_intcrush_ops
 from ._quant_utils import VALID_ROT_SIZES
@@ -133,15 +134,6 @@ class SimpleINT8UNetLoader:
         return (model,)
 
 
-def _parse_padded(padded_str: str) -> dict[str, int]:
-    out = {}
-    for entry in padded_str.split(";"):
-        if "=" in entry:
-            k, v = entry.split("=", 1)
-            out[k.strip()] = int(v.strip())
-    return out
-
-
 def _apply_padded_layer_fixes(model, padded_str: str) -> None:
     """Trim weight columns of layers whose in_features were padded by the
     converter and fix the patch-embedding channel count (_loaders.py:164-226).
@@ -149,7 +141,7 @@ def _apply_padded_layer_fixes(model, padded_str: str) -> None:
     import comfy.utils
 
     m = model.model
-    for layer_key, orig_in in _parse_padded(padded_str).items():
+    for layer_key, orig_in in parse_padded_layers(padded_str).items():
         module_path = layer_key.rsplit(".weight", 1)[0]
         try:
             module = comfy.utils.get_attr(m, module_path)

@@ -6,6 +6,8 @@ The PyTorch paths are the reference fallback (_ops.py:483-491, :538-545),
 so their outputs are checked against the oracle's restatement of it."""
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -252,3 +254,88 @@ def test_casting_hooks_are_used_and_released():
     co.CAST_CALLS.clear()
     lin(torch.randn(2, 128))
     assert [c[0] for c in co.CAST_CALLS] == ["cast", "uncast"]
+
+
+# ------------------------------------------------------------------ checkpoint round trip
+ckpt = __graft_entry__._submodule("_checkpoint")
+
+
+def test_padded_layers_format_round_trip():
+    d = {"img_in.weight": 64, "blocks.3.ffn.2.weight": 13824}
+    s = ckpt.format_padded_layers(d)
+    assert s == "img_in.weight=64;blocks.3.ffn.2.weight=13824"
+    assert ckpt.parse_padded_layers(s) == d
+    assert ckpt.parse_padded_layers("a.weight=5;junk; b.weight = 7 ") == {"a.weight": 5, "b.weight": 7}
+    for bad in ({"img_in": 64}, {"a;b.weight": 3}, {"a.weight": 0}):
+        with pytest.raises(ValueError):
+            ckpt.format_padded_layers(bad)
+
+
+def test_checkpoint_round_trip_int4(tmp_path):
+    """Every tensor of an INT4 checkpoint (packed weights, group scales,
+    perm, SmoothRot factors, zero point, SVD factors) and its metadata come
+    back bit for bit, and the INT4 loader node reads the saved rot size."""
+    import folder_paths
+
+    folder_paths.ROOTS["diffusion_models"] = str(tmp_path / "dm")
+    K, N = 256, 32
+    layers = {"double_blocks.0.img_attn.qkv": (int4_layer(N, K, G=2, seed=30, zp=True, svd_rank=4), K),
+              "single_blocks.0.modulation.lin": (int4_layer(N, K, seed=31, perm=False, smoothrot=False), K)}
+    sd = {}
+    for name, (lsd, in_f) in layers.items():
+        sd.update({f"{name}.{k}": v for k, v in lsd.items()})
+        sd[f"__in__.{name}.weight"] = torch.tensor([in_f])  # the stand-in loader's in_features
+    path = str(tmp_path / "dm" / "rt4.safetensors")
+    meta = ckpt.save_checkpoint(path, sd, rot_size=64, extra_metadata={"note": "test"})
+    assert meta == {"int_crush.format_version": "3", "int_crush.rot_size": "64", "note": "test"}
+    back, info = ckpt.load_checkpoint(path)
+    assert set(back) == set(sd) and all(torch.equal(back[k], sd[k]) and back[k].dtype == sd[k].dtype for k in sd)
+    assert (info.fmt, info.format_version, info.rot_size, info.padded_layers) == ("int4_crush", "3", 64, {})
+    (model,) = loaders.SimpleINT4UNetLoader().load("rt4.safetensors", 256)
+    qkv = model.model.double_blocks._modules["0"].img_attn.qkv
+    assert qkv._intcrush_rot_size == 64 and qkv.weight._params.zp is not None
+    x = torch.randn(3, K)
+    lsd = layers["double_blocks.0.img_attn.qkv"][0]
+    assert torch.equal(qkv.weight._qdata, lsd["weight"])
+    assert torch.isfinite(qkv(x)).all()
+
+
+def test_checkpoint_round_trip_int8_padded(tmp_path):
+    """An INT8 checkpoint with a padded layer: the metadata round-trips and
+    the INT8 loader trims the layer back to its original width."""
+    import folder_paths
+
+    folder_paths.ROOTS["diffusion_models"] = str(tmp_path / "dm")
+    K, N = 256, 32
+    sd = {f"double_blocks.0.img_mlp.0.{k}": v for k, v in int8_layer(N, K, seed=32).items()}
+    sd.update({f"img_in.{k}": v for k, v in int8_layer(N, K + 64, seed=33).items()})
+    path = str(tmp_path / "dm" / "rt8.safetensors")
+    ckpt.save_checkpoint(path, sd, rot_size=0, padded_layers={"img_in.weight": K})
+    back, info = ckpt.load_checkpoint(path)
+    assert all(torch.equal(back[k], sd[k]) for k in sd)
+    assert (info.fmt, info.rot_size, info.padded_layers) == ("int8_crush", 0, {"img_in.weight": K})
+    (model,) = loaders.SimpleINT8UNetLoader().load("rt8.safetensors", 256)
+    assert tuple(model.model.img_in.weight._qdata.shape) == (N, K)
+    assert torch.equal(model.model.img_in.weight._qdata, sd["img_in.weight"][:, :K])
+
+
+def test_checkpoint_save_rejects_bad_input(tmp_path):
+    sd = {f"fc.{k}": v for k, v in int8_layer(8, 64, seed=34).items()}
+    p = str(tmp_path / "x.safetensors")
+    with pytest.raises(ValueError, match="rot_size"):
+        ckpt.save_checkpoint(p, sd, rot_size=128)
+    with pytest.raises(KeyError):
+        ckpt.save_checkpoint(p, sd, rot_size=0, padded_layers={"other.weight": 32})
+    with pytest.raises(ValueError, match="below the stored"):
+        ckpt.save_checkpoint(p, sd, rot_size=0, padded_layers={"fc.weight": 64})
+    with pytest.raises(ValueError, match="weight format"):
+        ckpt.save_checkpoint(p, {"a": torch.zeros(2)}, rot_size=0)
+    with pytest.raises(ValueError, match="unknown weight format"):
+        ckpt.save_checkpoint(p, sd, rot_size=0, fmt="int2")
+    assert not os.path.exists(p)
+    # a file without INT-Crush metadata reads as such
+    from safetensors.torch import save_file
+
+    save_file({"a": torch.zeros(2)}, p)
+    _, info = ckpt.load_checkpoint(p)
+    assert (info.fmt, info.rot_size, info.padded_layers) == (None, None, {})
