@@ -72,6 +72,8 @@ def _parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (PMC calibration)")
+    ap.add_argument("--no-vendor", action="store_true",
+                    help="skip the hipBLASLt reference GEMM on the same shape")
     ap.add_argument("--eager", action="store_true",
                     help="launch eagerly instead of replaying a captured graph (for counter collection)")
     return ap.parse_args()
@@ -422,6 +424,41 @@ def measure_peaks():
                       "HBM: 1 GiB device copy, read + write bytes"}
 
 
+def vendor_reference(cfg, reps=20):
+    """The vendor library on the same GEMM shape, as a reference point for
+    the roofline fraction: hipBLASLt through torch._int_mm (int8 x int8 ->
+    int32, no dequant epilogue, no INT4 unpack, no group fold) for the INT8
+    MFMA configs, torch.matmul in the activation dtype on a dense
+    pre-dequantized weight for W4A16.  Synthetic operands of the config's
+    shape; not part of the timed step."""
+    import torch
+
+    M, K, N = cfg["M"], cfg["K"], cfg["N"]
+    g = torch.Generator(device="cuda:0").manual_seed(7)
+    if cfg["fmt"] == "w4a16":
+        act = torch.float16 if cfg["act"] == "fp16" else torch.bfloat16
+        a = torch.randn(M, K, generator=g, device="cuda:0").to(act)
+        b = (torch.randn(K, N, generator=g, device="cuda:0") * 0.02).to(act)
+        fn, kernel, ops_unit = (lambda: torch.matmul(a, b)), f"torch.matmul {cfg['act']} (hipBLASLt)", "TFLOP/s"
+    else:
+        a = torch.randint(-127, 128, (M, K), generator=g, device="cuda:0", dtype=torch.int8)
+        b = torch.randint(-127, 128, (K, N), generator=g, device="cuda:0", dtype=torch.int8)
+        fn, kernel, ops_unit = (lambda: torch._int_mm(a, b)), "torch._int_mm int8->int32 (hipBLASLt)", "TOPS"
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    e.synchronize()
+    ms = s.elapsed_time(e) / reps
+    return {"kernel": kernel, "kernel_ms": round(ms, 5), "achieved": round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 1),
+            "unit": ops_unit, "note": "same M, K, N; plain GEMM without this path's fused work"}
+
+
 def traffic_for(workload_key):
     """HBM bytes per launch of the dominant kernel from committed rocprofv3 counters."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
@@ -497,6 +534,8 @@ def main():
         line["prep_quant"] = {"kernel": "rotate_quantize", "bound": "hbm", "kernel_ms": round(p_ms, 5),
                               "algorithmic_bytes": prep_bytes, "achieved": round(pach, 1),
                               "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(pach / PEAK_HBM_GBPS, 4)}
+    if M > rt.GEMV_MAX_M and not args.no_vendor:
+        line["vendor_gemm"] = vendor_reference(cfg)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(cfg, inp)
     print(json.dumps(line), flush=True)
