@@ -61,6 +61,18 @@ CONFIGS = {
                         fmt="int8", M=32760, K_in=13824, K=14336, N=5120, rot=1024, smoothrot=False,
                         perm=False, G=1, act="fp16", dist="student_t", cpu_rows=2048),
 }
+# The rest of the Wan2.1-14B block's linears, for the C5 set
+for _fmt, _tag in (("int4", "w4a8"), ("int8", "w8a8")):
+    for _lin, _K, _N in (("qkv", 5120, 15360), ("proj", 5120, 5120), ("up", 5120, 13824)):
+        CONFIGS[f"c5{_lin}_{_tag}"] = dict(
+            name=f"C5 Wan {_lin} {_tag.upper()} {_K}->{_N}, M=32760, R=1024", fmt=_fmt, M=32760, K=_K, N=_N,
+            rot=1024, smoothrot=False, perm=False, G=_K // 128 if _fmt == "int4" else 1, act="fp16",
+            dist="student_t", cpu_rows=2048)
+# C5 set: the four linears of one Wan2.1-14B block, timed one after another
+SETS = {f"c5set_{t}": dict(name=f"C5 Wan2.1-14B block linear set {t.upper()} (qkv, proj, FFN-up, FFN-down), "
+                                f"M=32760, R=1024" + (", g128" if t == "w4a8" else ""),
+                           members=[f"c5{m}_{t}" for m in ("qkv", "proj", "up", "down")])
+        for t in ("w4a8", "w8a8")}
 
 
 def _parse():
@@ -68,7 +80,7 @@ def _parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS) + [STEP_CONFIG])
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS) + sorted(SETS) + [STEP_CONFIG])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (PMC calibration)")
@@ -459,6 +471,63 @@ def vendor_reference(cfg, reps=20):
             "unit": ops_unit, "note": "same M, K, N; plain GEMM without this path's fused work"}
 
 
+def set_main(args, rt):
+    """A set of linears (the C5 Wan block): each member's prep + GEMM step timed
+    as in a single-linear config, one after another; the line reports the
+    set's ops over the summed step times, the GEMMs' roofline over their
+    summed kernel times, and the CPU fallback on each member's bounded
+    token slice."""
+    import torch
+
+    st = SETS[args.config]
+    tot_ops = step_ms = gemm_ms = prep_ms = 0.0
+    cpu_s = cpu_ops = 0.0
+    members = []
+    cores = None
+    for key in st["members"]:
+        cfg = CONFIGS[key]
+        inp = make_inputs(cfg)
+        s_ms, _wall, g_ms, p_ms, copies = gpu_bench(cfg, inp, args.steps, args.warmup, rt)
+        ops, _gb, _pb = algorithmic(cfg)
+        tot_ops += ops
+        step_ms += s_ms
+        gemm_ms += g_ms
+        prep_ms += p_ms or 0.0
+        members.append({"linear": cfg["name"], "ms_per_step": round(s_ms, 5), "gemm_ms": round(g_ms, 5),
+                        "prep_ms": round(p_ms, 5) if p_ms is not None else None,
+                        "gemm_tops": round(ops / (g_ms * 1e-3) / 1e12, 1)})
+        if not args.no_cpu:
+            cb = cpu_baseline(cfg, inp)
+            cpu_s += cb["seconds_per_call"]
+            rows = min(cfg["M"], cfg.get("cpu_rows", cfg["M"]))
+            cpu_ops += 2.0 * rows * cfg["N"] * cfg["K"]
+            cores = cb["cores"]
+        del inp
+        torch.cuda.empty_cache()
+    first = CONFIGS[st["members"][0]]
+    fmt = first["fmt"]
+    achieved = tot_ops / (gemm_ms * 1e-3) / 1e12
+    line = {
+        "metric": METRIC, "value": round(tot_ops / (step_ms * 1e-3) / 1e12, 3), "unit": "TOPS",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(step_ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": st["name"], "M": first["M"], "members": members, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "kernel": "gemm_w4a8" if fmt == "int4" else "gemm_w8a8",
+                     "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TOPS",
+                     "frac": round(achieved / PEAK_INT8_TOPS, 4), "kernel_ms": round(gemm_ms, 5),
+                     "algorithmic_ops_per_step": tot_ops, "traffic": None},
+        "prep_quant_ms": round(prep_ms, 5),
+    }
+    line["peak_measured"] = measure_peaks()
+    line["roofline"]["frac_of_measured_peak"] = round(achieved / line["peak_measured"]["int8_tops"], 4)
+    if not args.no_cpu:
+        line["cpu_baseline"] = {"value": round(cpu_ops / cpu_s / 1e12, 5), "unit": "TOPS", "cores": cores,
+                                "kind": "port", "seconds": round(cpu_s, 3),
+                                "sample": "each member's first 2048 of 32760 tokens, fp32 dequant + prep + "
+                                          "F.linear per call, median of 3 after 1 warm-up, summed"}
+    print(json.dumps(line), flush=True)
+
+
 def traffic_for(workload_key):
     """HBM bytes per launch of the dominant kernel from committed rocprofv3 counters."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
@@ -486,6 +555,9 @@ def main():
     EAGER = args.eager
     if args.config == STEP_CONFIG:
         flux_step_main(args, rt)
+        return
+    if args.config in SETS:
+        set_main(args, rt)
         return
     cfg = CONFIGS[args.config]
     inp = make_inputs(cfg)
