@@ -720,6 +720,7 @@ __all__ = [
     "fused_quant_int8_gemm_dequant", "fused_w4a8_gemm_dequant", "unpack_int4_to_int8",
     "unpack_int4_to_float16", "rotate_quantize", "prepare_activation", "gemm_w4a8", "gemm_w4a16",
     "unpack_int4_to_float", "prepare_factors", "prepare_perm", "PreparedFactors", "gemm_acc_i32",
-    "gemv", "GEMV_MAX_M",
+    "gemv", "GEMV_MAX_M", "fused_layernorm_quantize", "fused_rmsnorm_quantize", "fused_softmax_quantize",
+    "norm_rotate_quantize", "ACT_NONE", "ACT_SILU", "ACT_GELU", "ACT_GELU_TANH",
     "load_library",
 ]

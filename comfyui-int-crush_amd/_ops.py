@@ -292,8 +292,8 @@ def make_intcrush_ops(quant_format: str, rot_size: int, use_pytorch: bool = Fals
                 if not A:
                     return None, False
                 a = torch.cat([t.to(out_dtype) for t in A], 1)
-                b = torch.cat([t.to(out_dtype) for t in B], 1)
-                return a @ b.t(), lora
+                bt = torch.cat([t.to(out_dtype) for t in B], 1).t().contiguous()  # [k, N], no transposed view
+                return a @ bt, lora
 
             def _finish_forward(self, out: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
                 return out.to(x.dtype).reshape(*x.shape[:-1], -1)
