@@ -528,6 +528,35 @@ def fused_int8_gemm_dequant(x_int8: torch.Tensor, w_int8: torch.Tensor, s_w: tor
     return c
 
 
+def int8_gemm_int8out(x_int8: torch.Tensor, w_int8: torch.Tensor, s_w: torch.Tensor, s_a: torch.Tensor,
+                      c_out: torch.Tensor | None = None,
+                      s_c_out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """W8A8 GEMM re-quantized to INT8 with a per-row scale, for chained GEMMs
+    (kernels/triton_int8_gemm.py:392-536; the returned s_c is the next GEMM's s_a).
+
+    The reference documents it as fused_int8_gemm_dequant followed by
+    dynamic_quantize_activation; its kernel computes the row abs-max inside
+    each N-tile and every tile writes s_c, so the last tile's scale wins and
+    the other tiles' codes use their own.  Here the scale is the abs-max of
+    the whole row, exactly that documented equivalence: the W8A8 GEMM writes
+    the f32 dequantized values (no bias) into a temporary, then the per-token
+    quantizer (q = trunc(v / s +- 0.5), s = max(|v|, 1e-8) / 127) runs on it.
+    """
+    assert x_int8.dtype == torch.int8, f"x_int8 must be int8, got {x_int8.dtype}"
+    assert w_int8.dtype == torch.int8, f"w_int8 must be int8, got {w_int8.dtype}"
+    M, K = x_int8.shape
+    N, K_w = w_int8.shape
+    assert K == K_w, f"K mismatch: {K} vs {K_w}"
+    if c_out is not None:
+        assert tuple(c_out.shape) == (M, N), f"c_out shape mismatch: {tuple(c_out.shape)} vs ({M}, {N})"
+        assert c_out.dtype == torch.int8, f"c_out must be int8, got {c_out.dtype}"
+    if s_c_out is not None:
+        assert tuple(s_c_out.shape) == (M,), f"s_c_out shape mismatch: {tuple(s_c_out.shape)} vs ({M},)"
+        assert s_c_out.dtype == torch.float32, f"s_c_out must be float32, got {s_c_out.dtype}"
+    v = fused_int8_gemm_dequant(x_int8, w_int8, s_w, s_a, out_dtype=torch.float32)
+    return dynamic_quantize_activation(v, s_a_out=s_c_out, x_int8_out=c_out)
+
+
 def fused_w4a8_gemm_dequant(x_int8, w_int8, s_w, s_a, bias=None, out_dtype=torch.bfloat16, out=None,
                             activation: int = 0, residual: torch.Tensor | None = None):
     """kernels/triton_w4a8_gemm.py:111-169: the INT8 GEMM on already unpacked
@@ -721,6 +750,6 @@ __all__ = [
     "unpack_int4_to_float16", "rotate_quantize", "prepare_activation", "gemm_w4a8", "gemm_w4a16",
     "unpack_int4_to_float", "prepare_factors", "prepare_perm", "PreparedFactors", "gemm_acc_i32",
     "gemv", "GEMV_MAX_M", "fused_layernorm_quantize", "fused_rmsnorm_quantize", "fused_softmax_quantize",
-    "norm_rotate_quantize", "ACT_NONE", "ACT_SILU", "ACT_GELU", "ACT_GELU_TANH",
+    "norm_rotate_quantize", "ACT_NONE", "ACT_SILU", "ACT_GELU", "ACT_GELU_TANH", "int8_gemm_int8out",
     "load_library",
 ]

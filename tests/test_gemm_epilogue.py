@@ -8,11 +8,13 @@ split K at small M, the MFMA tiles with the LDS-staged 16-bit epilogue, the
 direct epilogue for ragged N or an odd residual stride, the shape-generic
 kernel) for each activation and residual dtype.  With activation 0 the
 residual add is one f32 addition, so those outputs are bit-exact; with an
-activation the GPU's f32 expf / erff / tanhf may differ from the float64
-oracle by a few f32 ulp before the final rounding, so outputs are held to
-2^-20 (|v| + |act(v)| + |residual|) plus one ulp of the output dtype.  The
-f32 outputs are the ones that tell GELU from GELU-tanh (their difference is
-far above that bound and may hide under a bf16 ulp).
+activation the GPU's f32 evaluation (hardware exp2 and reciprocal, the
+Abramowitz & Stegun erf) may differ from the float64 oracle by a few f32 ulp
+before the final rounding, so outputs are held to 2^-20 (|v| + |act(v)| +
+|residual|) plus one ulp of the output dtype.  The f32 outputs are the ones
+that tell GELU from GELU-tanh (their difference is far above that bound and
+may hide under a bf16 ulp).  Also int8_gemm_int8out (the GEMM re-quantized to
+INT8 with whole-row scales), bit-exact against the oracle.
 """
 from __future__ import annotations
 
@@ -272,3 +274,33 @@ def test_gemm_epilogue_default_is_plain_gemm(rt, dev):
     x = rt.gemm_w4a8(a, w, s_w, s_a, out_dtype=torch.bfloat16)
     y = rt.gemm_w4a8(a, w, s_w, s_a, out_dtype=torch.bfloat16, activation=0, residual=None)
     assert torch.equal(x, y)
+
+
+# ------------------------------------------------------------------ int8_gemm_int8out
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K", [(300, 1000, 512), (5, 384, 256), (512, 3072, 1024)])
+def test_int8_gemm_int8out_matches_oracle(rt, oracle, dev, M, N, K):
+    """INT8 codes and per-row scales of the re-quantized GEMM output equal the
+    oracle's quantizer applied to the oracle's f32 dequant, bit for bit; the
+    scale is the whole row's: a row whose abs-max sits in its last N-tile
+    scales every tile by it (the reference kernel's per-tile scale would not)."""
+    a, w, s_a, s_w, _bias, acc = _problem(M, N, K, "int8", 41, oracle)
+    # plant the row abs-max of row 0 in its last column
+    w[-1, :] = 127
+    a[0, :] = 127
+    s_w[-1] = s_w.max()
+    acc = oracle.gemm_acc(a.numpy(), w.numpy())
+    c, s_c = rt.int8_gemm_int8out(a.to(dev), w.to(dev), s_w.to(dev), s_a.to(dev))
+    v = oracle.epilogue(acc, s_a.numpy(), s_w.numpy(), None, 2)
+    q_ref, s_ref = oracle.quantize(v)
+    assert np.array_equal(s_c.cpu().numpy(), s_ref)
+    assert np.array_equal(c.cpu().numpy(), q_ref)
+    assert abs(v[0]).argmax() == N - 1 and c[0, -1].item() == 127
+    # pre-allocated outputs are filled in place
+    c2 = torch.empty(M, N, dtype=torch.int8, device=dev)
+    s2 = torch.empty(M, dtype=torch.float32, device=dev)
+    r = rt.int8_gemm_int8out(a.to(dev), w.to(dev), s_w.to(dev), s_a.to(dev), c_out=c2, s_c_out=s2)
+    assert r[0].data_ptr() == c2.data_ptr() and r[1].data_ptr() == s2.data_ptr()
+    assert torch.equal(c2.cpu(), c.cpu()) and torch.equal(s2.cpu(), s_c.cpu())
+    with pytest.raises(AssertionError):
+        rt.int8_gemm_int8out(a.to(dev), w.to(dev), s_w.to(dev), s_a.to(dev), c_out=c2[:, :-1])
