@@ -21,15 +21,18 @@ IC_DEV int lds_off(int row, int chunk) { return row * kBK + ((chunk ^ swz(row)) 
 // wave-uniform 64-bit base and a per-lane 32-bit byte offset) to M0 + 16*lane
 // (4*lane).  Issued from inline assembly so that the compiler neither tracks
 // it nor orders LDS accesses behind it; completion is waited for explicitly
-// with wait_vm before the workgroup barrier that publishes the stage.  M0 holds
-// no compiler value in these kernels (gfx950 LDS instructions do not use it).
+// with wait_vm before the workgroup barrier that publishes the stage.  No
+// memory clobber: the slot a DMA fills is read only after a wait_vm and a
+// barrier (both compiler barriers), so LDS reads of other slots may be
+// scheduled across the issue.  M0 holds no compiler value in these kernels
+// (gfx950 LDS instructions do not use it).
 IC_DEV void dma16(uint32_t voff, const void* sbase, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(sbase)
-               : "memory", "m0");
+               : "m0");
 }
 IC_DEV void dma4(uint32_t voff, const void* sbase, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(voff), "s"(sbase)
-               : "memory", "m0");
+               : "m0");
 }
 
 // Block until at most N vector-memory operations of this wave are outstanding

@@ -162,10 +162,23 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
 #pragma unroll
     for (int p = 0; p < kParts; ++p) issue_dma_part(kt, p);
   };
+  // Per-row-scale kernels issue a full stage on every step: past the end of K
+  // a redundant reload of the last stage into the slot the step frees, which
+  // nothing reads.  The step then has no branch around its DMA issue, so the
+  // compiler schedules the next K-step's LDS reads among this one's MFMAs
+  // (4-6 % faster W8A8; the grouped kernels, VALU-bound, gained nothing and
+  // keep the exact issue).  The trailing reloads are drained before the
+  // epilogue reuses LDS.
+  constexpr bool kFullSteps = GS == 0;
   // Top of step s: stages s+1 .. s+NS-2 may stay in flight (D DMA
   // instructions each, one more on the waves that also fetch scales); near the
-  // end of K, wait for everything.
+  // end of K (exact issue), wait for everything.
   auto wait_stage = [&](int s) {
+    if constexpr (kFullSteps) {
+      if (s_wave) wait_vm<(D + 1) * (NS - 2)>();
+      else wait_vm<D * (NS - 2)>();
+      return;
+    }
     if constexpr (NS > 2) {
       if (s + NS - 2 < KT) {
         if (s_wave) wait_vm<(D + 1) * (NS - 2)>();
@@ -285,7 +298,8 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
           if (ZF && ks == 0) acc[SET][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], v16i{}, 0, 0, 0);
           else acc[SET][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[SET][i][j], 0, 0, 0);
         }
-      if (dma_kt < KT) issue_dma_part(dma_kt, ks);
+      if constexpr (kFullSteps) issue_dma_part(min(dma_kt, KT - 1), ks);
+      else if (dma_kt < KT) issue_dma_part(dma_kt, ks);
       // The fold's instructions are placed among this K-step's MFMAs by the
       // compiler; fixed MFMA:VALU interleave patterns measured 3-5 % slower.
       if constexpr (FOLD) {
@@ -301,7 +315,8 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
   // ---- prologue: NS-1 stages in flight
 #pragma unroll
   for (int t = 0; t < NS - 1; ++t)
-    if (t < KT) issue_dma(t);
+    if constexpr (kFullSteps) issue_dma(min(t, KT - 1));
+    else if (t < KT) issue_dma(t);
 
   // One pipeline step: make stage s resident (this wave's DMAs, then the
   // barrier for everyone's), expand packed weights (second barrier), then run
@@ -351,6 +366,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
   }
 
   // ---- epilogue
+  if constexpr (kFullSteps) wait_vm<0>();  // trailing redundant reloads land before LDS is reused
   if constexpr (PART) {
     // partials of this K slice: 32 lanes of one accumulator row write 32
     // consecutive columns (128 bytes)
