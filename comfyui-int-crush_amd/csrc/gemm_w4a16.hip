@@ -130,15 +130,13 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4a16_kernel(
 #pragma unroll
     for (int p = 0; p < kParts; ++p) issue_dma_part(kt, p);
   };
+  // Every step issues a full stage (past the end of K a redundant reload of
+  // the last stage into the slot the step frees, which nothing reads; drained
+  // before the epilogue), so the stages after s always hold NS-2 steps of DMAs
+  // and the DMA issue needs no branch between the MFMA K-steps.
   auto wait_stage = [&](int s) {
-    if constexpr (NS > 2) {
-      if (s + NS - 2 < KT) {
-        if (s_wave) wait_vm<(D + 1) * (NS - 2)>();
-        else wait_vm<D * (NS - 2)>();
-        return;
-      }
-    }
-    wait_vm<0>();
+    if (s_wave) wait_vm<(D + 1) * (NS - 2)>();
+    else wait_vm<D * (NS - 2)>();
   };
 
   // ---- packed INT4 -> 16-bit weights in LDS, 32 values per thread (one
@@ -187,7 +185,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4a16_kernel(
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a[i]),
                                                                 __builtin_bit_cast(v8bf, b[j]), acc[i][j], 0, 0, 0);
         }
-      if (dma_kt < KT) issue_dma_part(dma_kt, ks);
+      issue_dma_part(min(dma_kt, KT - 1), ks);
     }
   };
 
@@ -196,7 +194,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4a16_kernel(
   // freed by the previous step
 #pragma unroll
   for (int t = 0; t < NS - 1; ++t)
-    if (t < KT) issue_dma(t);
+    issue_dma(min(t, KT - 1));
   for (int s = 0; s < KT; ++s) {
     wait_stage(s);
     lds_barrier();
@@ -207,6 +205,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4a16_kernel(
     __builtin_amdgcn_sched_barrier(0);
   }
 
+  wait_vm<0>();  // the trailing redundant reloads land before LDS is reused
   // ---- epilogue: v = acc (+ bias), rounded once to DT
   if ((((uintptr_t)C) & 15) == 0 && (ldc & 7) == 0 && (N & 7) == 0) {
     // stage the tile through LDS row-major, then write whole rows with 16-byte stores
