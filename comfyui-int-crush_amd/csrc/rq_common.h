@@ -40,11 +40,13 @@ template <int DT> IC_DEV float bits16_f32(u16 b) {
 }
 
 // Layout of register element j of thread t after the rotation phases for rot
-// size class RC (0: none/16, 1: 64/256, 2: 1024/4096), tile-local position.
+// size class RC (0: none/16, 1: 64/256, 2: 1024/4096, 3: 1024 rotated inside
+// each wave's own 1024 positions), tile-local position.
 template <int RC> IC_DEV int tile_pos(int t, int j) {
   if constexpr (RC == 0) return 16 * t + j;
   else if constexpr (RC == 1) return 256 * (t >> 4) + 16 * j + (t & 15);
-  else return 256 * j + t;
+  else if constexpr (RC == 2) return 256 * j + t;
+  else return 1024 * (t >> 6) + 256 * (j & 3) + 4 * (t & 63) + (j >> 2);
 }
 
 constexpr int kFastMaxTiles = 4;  // fast path: K_w <= 16384

@@ -99,9 +99,12 @@ IC_DEV void block_sum2_f64(double& a, double& b, double* red) {
   }
 }
 
-// TH threads per workgroup (256, or 192 = three waves for rows of up to 3072
-// or 6144 values with R <= 256, whose Hadamard exchange stays inside a wave):
-// a tile is TH * 16 positions.
+// TH threads per workgroup (256; 192 = three waves for rows of up to 3072 or
+// 6144 values and 320 = five waves for rows of 4097..5120 values, both with
+// R <= 1024, whose Hadamard exchange stays inside a wave): a tile is TH * 16
+// positions.  For R = 1024 a wave's 64 x 16 positions are exactly one block,
+// so its last digit is exchanged through the wave's own slice of the LDS
+// buffer, without a workgroup barrier.
 //
 // NORM (IC_NORM_LAYER / IC_NORM_RMS, ic_norm_rotate_quantize): before the
 // prep, the row is normalised and rounded once to DT,
@@ -119,10 +122,10 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
     const float* __restrict__ sr_rcp, const float* __restrict__ sr_f, int K_w,
     const int32_t* __restrict__ perm, int8_t* __restrict__ q_out, int64_t ldq,
     float* __restrict__ s_out, const float* __restrict__ nw, const float* __restrict__ nb, float eps) {
-  constexpr int RC = LOG4R <= 2 ? 0 : (LOG4R <= 4 ? 1 : 2);
+  constexpr int RC = LOG4R <= 2 ? 0 : (LOG4R <= 4 ? 1 : (LOG4R == 5 ? 3 : 2));
   constexpr bool XCH = LOG4R >= 3;
   constexpr int kTile = TH * 16;  // positions per tile
-  static_assert(TH == 256 || (TH % 64 == 0 && LOG4R <= 4), "cross-wave rotation needs four waves");
+  static_assert(TH == 256 || (TH % 64 == 0 && LOG4R <= 5), "cross-wave rotation needs four waves");
   __shared__ double xbuf[XCH ? xbuf_doubles<kTile>() : 2];
   __shared__ __attribute__((aligned(16))) u16 rowbuf[rowbuf_len<NT, kTile>()];
   __shared__ float red[TH / 64];
@@ -300,7 +303,24 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
         for (int h = 0; h < 16; ++h) v[h] = xbuf[xslot(256 * g + 16 * h + l)];
         stage_lo(v);
         if constexpr (LOG4R >= 4) stage_hi(v);
-        if constexpr (LOG4R >= 5) {
+        if constexpr (LOG4R == 5) {
+          // digit 4 spans the wave's four 256-groups: element 4i+b of lane ln
+          // takes position 1024w + 256b + 4ln + i (tile_pos<3>)
+#pragma unroll
+          for (int h = 0; h < 16; ++h) xbuf[xslot(256 * g + 16 * h + l)] = v[h];
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+          const int wb = 1024 * (t >> 6) + 4 * (t & 63);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int b = 0; b < 4; ++b) v[4 * i + b] = xbuf[xslot(wb + 256 * b + i)];
+          stage_lo(v);
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        } else if constexpr (LOG4R >= 6) {
           // digits 4-5 span all four waves
 #pragma unroll
           for (int h = 0; h < 16; ++h) xbuf[xslot(256 * g + 16 * h + l)] = v[h];
@@ -308,7 +328,7 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
 #pragma unroll
           for (int gg = 0; gg < 16; ++gg) v[gg] = xbuf[xslot(256 * gg + t)];
           stage_lo(v);
-          if constexpr (LOG4R >= 6) stage_hi(v);
+          stage_hi(v);
           __syncthreads();  // every wave has read xbuf before the next tile rewrites it
         } else {
           __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -351,6 +371,14 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
         v4u* dst = (v4u*)(rowbuf + rbaddr(base + 16 * t));
         dst[0] = v4u{w[0], w[1], w[2], w[3]};
         dst[1] = v4u{w[4], w[5], w[6], w[7]};
+      } else if constexpr (RC == 3) {
+        // elements b, 4+b, 8+b, 12+b are four consecutive positions: one 8-byte store
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const uint32_t lo = (uint32_t)f32_bits16<DT>(z[b]) | ((uint32_t)f32_bits16<DT>(z[4 + b]) << 16);
+          const uint32_t hi = (uint32_t)f32_bits16<DT>(z[8 + b]) | ((uint32_t)f32_bits16<DT>(z[12 + b]) << 16);
+          *(v2u*)(rowbuf + rbaddr(base + tile_pos<3>(t, b))) = v2u{lo, hi};
+        }
       } else {
 #pragma unroll
         for (int j = 0; j < 16; ++j) rowbuf[rbaddr(base + tile_pos<RC>(t, j))] = f32_bits16<DT>(z[j]);
@@ -498,7 +526,12 @@ hipError_t launch_fast_t(const ic_rotq_args& a, hipStream_t st) {
 
 template <int DT, int LOG4R, int VAR, int NORM = 0>
 hipError_t launch_fast_nt(const ic_rotq_args& a, hipStream_t st) {
-  if constexpr (LOG4R <= 4) {
+  if constexpr (LOG4R == 5) {
+    // five one-block waves cover 4097..5120 values in one tile (Wan's 5120
+    // would otherwise take two 4096-tiles, 37.5 % of them padding)
+    if (a.K_w > kTile && a.K_w <= 320 * 16) return launch_fast_t<DT, LOG4R, 1, VAR, 320, NORM>(a, st);
+  }
+  if constexpr (LOG4R <= 5) {
     // three-wave workgroups where their tile fits the row more tightly
     // (3072: one full tile instead of 3/4 of one; 4097..6144: two)
     constexpr int T3 = 192 * 16;

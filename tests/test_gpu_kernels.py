@@ -120,6 +120,10 @@ ROT_CASES = [
     (5120, 64, None, True, True, False),
     (6144, 256, None, False, True, False),
     (3072, 16, None, True, False, False),       # three-wave workgroups, one full tile
+    (5120, 1024, None, True, True, False),      # five one-block waves, one tile (Wan qkv/proj/FFN-up prep)
+    (4200, 1024, None, False, True, False),     # the same, rotation pad 4200 -> 5120
+    (2500, 1024, None, True, False, False),     # three one-block waves, pad 2500 -> 3072
+    (6000, 1024, 6400, True, True, False),      # three-wave workgroups, two tiles, then w_in pad
 ]
 
 

@@ -255,7 +255,7 @@ def test_oracle_norm_rotate_is_the_composition(oracle):
 NRQ_CASES = [  # (M, K_in, w_in, rot_size, smoothrot+perm, affine)
     (4608, 3072, 3072, 256, True, True),     # Flux pre-qkv / pre-MLP rows
     (512, 3072, 3072, 256, True, False),
-    (300, 5120, 5120, 1024, True, True),     # Wan hidden rows, cross-wave rotation
+    (300, 5120, 5120, 1024, True, True),     # Wan hidden rows, five one-block waves
     (64, 13824, 14336, 1024, False, True),   # Wan FFN-down width, zero pad to the weight K
     (40, 2048, 2048, 16, True, True),
     (40, 4096, 4096, 0, True, True),         # no rotation: norm + divide + perm + quantize
