@@ -100,9 +100,9 @@ IC_DEV void block_sum2_f64(double& a, double& b, double* red) {
 }
 
 // TH threads per workgroup (256; 192 = three waves for rows of up to 3072 or
-// 6144 values and 320 = five waves for rows of 4097..5120 values, both with
-// R <= 1024, whose Hadamard exchange stays inside a wave): a tile is TH * 16
-// positions.  For R = 1024 a wave's 64 x 16 positions are exactly one block,
+// 6144 values, 320 = five waves for rows of 4097..5120 values and 448 = seven
+// for 12289..14336, all with R <= 1024, whose Hadamard exchange stays inside a
+// wave): a tile is TH * 16 positions.  For R = 1024 a wave's 64 x 16 positions are exactly one block,
 // so its last digit is exchanged through the wave's own slice of the LDS
 // buffer, without a workgroup barrier.
 //
@@ -530,6 +530,9 @@ hipError_t launch_fast_nt(const ic_rotq_args& a, hipStream_t st) {
     // five one-block waves cover 4097..5120 values in one tile (Wan's 5120
     // would otherwise take two 4096-tiles, 37.5 % of them padding)
     if (a.K_w > kTile && a.K_w <= 320 * 16) return launch_fast_t<DT, LOG4R, 1, VAR, 320, NORM>(a, st);
+    // seven one-block waves, two tiles: 12289..14336 values (Wan's FFN-down
+    // 14336 instead of four 4096-tiles; ~99 KB of LDS, one workgroup per CU)
+    if (a.K_w > 3 * kTile && a.K_w <= 2 * 448 * 16) return launch_fast_t<DT, LOG4R, 2, VAR, 448, NORM>(a, st);
   }
   if constexpr (LOG4R <= 5) {
     // three-wave workgroups where their tile fits the row more tightly
