@@ -534,6 +534,11 @@ hipError_t launch_fast_nt(const ic_rotq_args& a, hipStream_t st) {
     // 14336 instead of four 4096-tiles; ~99 KB of LDS, one workgroup per CU)
     if (a.K_w > 3 * kTile && a.K_w <= 2 * 448 * 16) return launch_fast_t<DT, LOG4R, 2, VAR, 448, NORM>(a, st);
   }
+  if constexpr (LOG4R >= 3 && LOG4R <= 5) {
+    // one tile of twelve waves for 8193..12288 values (Flux's 12288): the
+    // per-thread constants of one tile instead of three
+    if (a.K_w > 2 * kTile && a.K_w <= 768 * 16) return launch_fast_t<DT, LOG4R, 1, VAR, 768, NORM>(a, st);
+  }
   if constexpr (LOG4R <= 5) {
     // three-wave workgroups where their tile fits the row more tightly
     // (3072: one full tile instead of 3/4 of one; 4097..6144: two)
