@@ -538,6 +538,8 @@ hipError_t launch_fast_nt(const ic_rotq_args& a, hipStream_t st) {
     // one tile of twelve waves for 8193..12288 values (Flux's 12288): the
     // per-thread constants of one tile instead of three
     if (a.K_w > 2 * kTile && a.K_w <= 768 * 16) return launch_fast_t<DT, LOG4R, 1, VAR, 768, NORM>(a, st);
+    // two tiles of eight waves for 12289..16384 (Flux's single-block 15360)
+    if (a.K_w > 3 * kTile) return launch_fast_t<DT, LOG4R, 2, VAR, 512, NORM>(a, st);
   }
   if constexpr (LOG4R <= 5) {
     // three-wave workgroups where their tile fits the row more tightly

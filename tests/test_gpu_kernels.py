@@ -126,6 +126,7 @@ ROT_CASES = [
     (6000, 1024, 6400, True, True, False),      # three-wave workgroups, two tiles, then w_in pad
     (9216, 256, None, True, True, False),       # one twelve-wave tile, 3072 positions of it padding
     (10000, 1024, 11008, False, True, False),   # the same tile with one-block waves, pads to 10240 and 11008
+    (15360, 256, None, True, True, False),      # two eight-wave tiles (Flux single-block output projection)
 ]
 
 

@@ -259,6 +259,7 @@ NRQ_CASES = [  # (M, K_in, w_in, rot_size, smoothrot+perm, affine)
     (64, 13824, 14336, 1024, False, True),   # Wan FFN-down width, seven one-block waves, zero pad
     (48, 12288, 12288, 256, True, True),     # one twelve-wave tile
     (33, 9008, 9216, 64, True, False),       # the same tile, rotation pad 9008 -> 9024, then w_in pad
+    (24, 15360, 16384, 16, True, True),      # two eight-wave tiles, w_in pad
     (40, 2048, 2048, 16, True, True),
     (40, 4096, 4096, 0, True, True),         # no rotation: norm + divide + perm + quantize
     (17, 1024, 1024, 64, False, False),
