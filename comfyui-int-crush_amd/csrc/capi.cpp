@@ -33,6 +33,18 @@ int ic_num_cus() {
   return n;
 }
 
+// Dynamic-LDS limit of a kernel, set once per device: done[] holds one flag
+// per device id (hipFuncSetAttribute applies to the current device).
+hipError_t ic_set_lds_limit(const void* kern, int bytes, unsigned char* done) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev >= 0 && dev < 64 && done[dev]) return hipSuccess;
+  e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess && dev >= 0 && dev < 64) done[dev] = 1;  // idempotent; a race only repeats the call
+  return e;
+}
+
 extern "C" {
 const char* ic_version(void) { return "intcrush-gfx950 0.1.0"; }
 const char* ic_last_error(void) { return g_err; }

@@ -143,9 +143,17 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
   // K-step of the MFMA loop: a wave that issued a whole stage at once stalled
   // at issue instead of starting its MFMAs.  Slice p holds the blocks d with
   // d % kParts == p (A blocks first, then B); the scale DMA goes last.
+  //
+  // kt may run past the end of K (per-row-scale kernels, below): the slot is
+  // still kt % NS, the one the current step frees, and only the source is
+  // clamped to the last stage, so a redundant reload never lands in a slot
+  // that a later step reads.
   constexpr int kParts = kBK / 32;
-  auto issue_dma_part = [&](int kt, int part) {
-    const uint32_t slot = lds0 + (uint32_t)((kt % NS) * TL::SLOT);
+  constexpr bool kFullSteps = GS == 0;  // see below
+  auto issue_dma_part = [&](int kt_slot, int part) {
+    const uint32_t slot = lds0 + (uint32_t)((kt_slot % NS) * TL::SLOT);
+    // (the exact-issue kernels never pass kt_slot >= KT)
+    const int kt = kFullSteps ? __builtin_amdgcn_readfirstlane(min(kt_slot, KT - 1)) : kt_slot;
     const int8_t* ab = a_base + (int64_t)kt * kBK;
 #pragma unroll
     for (int c = 0; c < A_DMA; ++c)
@@ -163,13 +171,12 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
     for (int p = 0; p < kParts; ++p) issue_dma_part(kt, p);
   };
   // Per-row-scale kernels issue a full stage on every step: past the end of K
-  // a redundant reload of the last stage into the slot the step frees, which
-  // nothing reads.  The step then has no branch around its DMA issue, so the
+  // a redundant reload of the last stage's bytes into the slot the step frees,
+  // which nothing reads.  The step then has no branch around its DMA issue, so the
   // compiler schedules the next K-step's LDS reads among this one's MFMAs
   // (4-6 % faster W8A8; the grouped kernels, VALU-bound, gained nothing and
   // keep the exact issue).  The trailing reloads are drained before the
   // epilogue reuses LDS.
-  constexpr bool kFullSteps = GS == 0;
   // Top of step s: stages s+1 .. s+NS-2 may stay in flight (D DMA
   // instructions each, one more on the waves that also fetch scales); near the
   // end of K (exact issue), wait for everything.
@@ -298,7 +305,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
           if (ZF && ks == 0) acc[SET][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], v16i{}, 0, 0, 0);
           else acc[SET][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[SET][i][j], 0, 0, 0);
         }
-      if constexpr (kFullSteps) issue_dma_part(min(dma_kt, KT - 1), ks);
+      if constexpr (kFullSteps) issue_dma_part(dma_kt, ks);
       else if (dma_kt < KT) issue_dma_part(dma_kt, ks);
       // The fold's instructions are placed among this K-step's MFMAs by the
       // compiler; fixed MFMA:VALU interleave patterns measured 3-5 % slower.
@@ -315,7 +322,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
   // ---- prologue: NS-1 stages in flight
 #pragma unroll
   for (int t = 0; t < NS - 1; ++t)
-    if constexpr (kFullSteps) issue_dma(min(t, KT - 1));
+    if constexpr (kFullSteps) issue_dma(t);
     else if (t < KT) issue_dma(t);
 
   // One pipeline step: make stage s resident (this wave's DMAs, then the
@@ -641,12 +648,8 @@ hipError_t launch_kernel(const GemmArgs& g, int S, hipStream_t st) {
   const size_t shm = TL::lds_bytes();
   static_assert(TL::lds_bytes() <= 160 * 1024, "LDS budget");
   auto kern = gemm_i8_kernel<TL, OUT_DT, ACC, PART, EPI>;
-  static bool attr_set = false;  // idempotent attribute; benign if raced
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static unsigned char lds_set[64];  // per device
+  if (hipError_t e = ic_set_lds_limit((const void*)kern, (int)shm, lds_set)) return e;
   kern<<<dim3(tiles, S), dim3(kNT), shm, st>>>(g.A, g.lda, g.B, g.ldb, g.s_a, g.s_w, g.G, g.bias, g.bias_dt,
                                                g.C, g.ldc, g.M, g.N, g.K, PART ? (int32_t*)g.ws : g.acc_out, g.epi);
   return hipGetLastError();

@@ -111,8 +111,11 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4a16_kernel(
   const uint8_t* b_base = B + (int64_t)n0 * ldb;
   const float* s_base = s_w + (int64_t)n0 * G;
 
-  auto issue_dma_part = [&](int kt, int part) {
-    const uint32_t slot = lds0 + (uint32_t)((kt % NS) * TL::SLOT);
+  // kt_slot may run past the end of K: the slot stays kt_slot % NS (the one
+  // the current step frees) and only the source is clamped to the last stage.
+  auto issue_dma_part = [&](int kt_slot, int part) {
+    const uint32_t slot = lds0 + (uint32_t)((kt_slot % NS) * TL::SLOT);
+    const int kt = __builtin_amdgcn_readfirstlane(min(kt_slot, KT - 1));  // wave-uniform
     const char* ab = a_base + (int64_t)kt * kBK;
 #pragma unroll
     for (int c = 0; c < A_DMA; ++c)
@@ -131,7 +134,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4a16_kernel(
     for (int p = 0; p < kParts; ++p) issue_dma_part(kt, p);
   };
   // Every step issues a full stage (past the end of K a redundant reload of
-  // the last stage into the slot the step frees, which nothing reads; drained
+  // the last stage's bytes into the slot the step frees, which nothing reads; drained
   // before the epilogue), so the stages after s always hold NS-2 steps of DMAs
   // and the DMA issue needs no branch between the MFMA K-steps.
   auto wait_stage = [&](int s) {
@@ -185,7 +188,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4a16_kernel(
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a[i]),
                                                                 __builtin_bit_cast(v8bf, b[j]), acc[i][j], 0, 0, 0);
         }
-      issue_dma_part(min(dma_kt, KT - 1), ks);
+      issue_dma_part(dma_kt, ks);
     }
   };
 
@@ -194,7 +197,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4a16_kernel(
   // freed by the previous step
 #pragma unroll
   for (int t = 0; t < NS - 1; ++t)
-    issue_dma(min(t, KT - 1));
+    issue_dma(t);
   for (int s = 0; s < KT; ++s) {
     wait_stage(s);
     lds_barrier();
@@ -283,12 +286,8 @@ hipError_t launch_w4a16(const u16* A, int64_t lda, const uint8_t* B, int64_t ldb
   const size_t shm = TL::lds_bytes();
   static_assert(TL::lds_bytes() <= 160 * 1024, "LDS budget");
   auto kern = gemm_w4a16_kernel<TL, DT>;
-  static bool attr_set = false;  // idempotent attribute; benign if raced
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static unsigned char lds_set[64];  // per device
+  if (hipError_t e = ic_set_lds_limit((const void*)kern, (int)shm, lds_set)) return e;
   kern<<<dim3(tiles), dim3(kNT), shm, st>>>(A, lda, B, ldb, s_w, G, gsize, bias, bias_dt, C, ldc, M, N, K);
   return hipGetLastError();
 }

@@ -211,12 +211,8 @@ hipError_t launch_gemv_i8(const int8_t* A, int64_t lda, const uint8_t* B, int64_
                           int M, int N, int K, const ic_epi& epi, hipStream_t st) {
   auto kern = gemv_i8_kernel<INT4, GS, OUT_DT>;
   const size_t shm = (size_t)(GS == 128 ? K / kGBK : 4) * M * 16 * 4;
-  static bool attr_set = false;  // idempotent attribute; benign if raced
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static unsigned char lds_set[64];  // per device
+  if (hipError_t e = ic_set_lds_limit((const void*)kern, 160 * 1024, lds_set)) return e;
   kern<<<dim3((unsigned)((N + 15) / 16)), dim3(kGT), shm, st>>>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C,
                                                                 ldc, M, N, K, epi);
   return hipGetLastError();

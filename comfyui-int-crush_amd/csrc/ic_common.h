@@ -18,6 +18,9 @@
 int ic_set_error(int code, const char* fmt, ...);
 int ic_check_launch(const char* who);
 int ic_num_cus();  // compute units of the current device
+// hipFuncSetAttribute(MaxDynamicSharedMemorySize) once per kernel and device;
+// done points at the caller's 64 per-device flags.
+hipError_t ic_set_lds_limit(const void* kern, int bytes, unsigned char* done);
 // GEMV routing test shared by the GEMM entry points (gemv.hip); strides in bytes.
 bool ic_gemv_applicable(int64_t M, int64_t K, const void* x, int64_t ldx_bytes, const void* w, int64_t ldw_bytes);
 

@@ -502,12 +502,15 @@ __global__ __launch_bounds__(kThreads) void quant_wave_kernel(
   }
 }
 
-template <class Kern>
-int persistent_grid(Kern kern, int threads, int64_t M) {
-  static thread_local int per_cu = 0;  // resident workgroups per CU for this kernel
+// Persistent grid: resident workgroups per CU (queried once per kernel
+// instantiation -- KERN is a template argument, so each instantiation keeps
+// its own cached occupancy) times the CUs of the current device.
+template <auto KERN>
+int persistent_grid(int threads, int64_t M) {
+  static thread_local int per_cu = 0;
   if (per_cu == 0) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, 0) != hipSuccess || n <= 0) n = 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, KERN, threads, 0) != hipSuccess || n <= 0) n = 1;
     per_cu = n;
   }
   const int64_t g = (int64_t)per_cu * ic_num_cus();
@@ -516,9 +519,9 @@ int persistent_grid(Kern kern, int threads, int64_t M) {
 
 template <int DT, int LOG4R, int NT, int VAR, int TH = kThreads, int NORM = 0>
 hipError_t launch_fast_t(const ic_rotq_args& a, hipStream_t st) {
-  auto kern = rq_fast_kernel<DT, LOG4R, NT, VAR, TH, NORM>;
+  constexpr auto kern = rq_fast_kernel<DT, LOG4R, NT, VAR, TH, NORM>;
   const int64_t K_r = LOG4R == 0 ? a.K_in : ((a.K_in + a.rot_size - 1) / a.rot_size) * a.rot_size;
-  kern<<<dim3(persistent_grid(kern, TH, a.M)), dim3(TH), 0, st>>>(
+  kern<<<dim3(persistent_grid<kern>(TH, a.M)), dim3(TH), 0, st>>>(
       (const u16*)a.x, a.ldx, (int)a.M, (int)a.K_in, (int)K_r, a.sr_rcp, a.sr_f, (int)a.K_w, a.perm,
       a.q_out, a.ldq, a.s_out, a.nw, a.nb, a.eps);
   return hipGetLastError();
