@@ -73,6 +73,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "ic_gemm_splitk_bytes": ([_L, _L, _L, _L, _I], _L),
     "ic_gemm_w8a8_ws": ([_P, _L, _L, _L, _P, _L, _L, _P, _P, _P, _I, _P, _I, _L, _P, _L, _P], _I),
     "ic_gemm_w4a8_ws": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _P, _I, _P, _I, _L, _P, _L, _P], _I),
+    "ic_gemm_w4a8_noalloc": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _P, _I, _P, _I, _L, _P], _I),
     "ic_gemm_w8a8_ex": ([_P, _L, _L, _L, _P, _L, _L, _P, _P, _P, _I, _I, _P, _I, _L, _P, _I, _L, _P, _L, _P], _I),
     "ic_gemm_w4a8_ex": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _P, _I, _I, _P, _I, _L, _P, _I, _L, _P, _L,
                          _P], _I),

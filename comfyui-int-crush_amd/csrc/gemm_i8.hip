@@ -1,8 +1,41 @@
 // INT8 / packed-INT4 MFMA GEMM entry points (kernels in gemm_i8.h; the
 // epilogue-option instantiations compile in gemm_i8_epi.hip).
+#include <mutex>
+
 #include "gemm_i8.h"
 
 namespace {
+
+// Split-K scratch of ic_gemm_w4a8_noalloc: one array per device, loaded with
+// the code object and held until the process ends.  Host code never passes
+// `scratch` itself to a kernel (on the host the name is only a stand-in for
+// the symbol); it uses the device address hipGetSymbolAddress returns, looked
+// up once per device with that device current and kept in scratch_ptr.
+constexpr int64_t kScratchBytes = IC_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+void* scratch_ptr[kMaxDevices];
+
+int scratch_for_current_device(void** out, const char* who) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return ic_set_error(IC_ERR_LAUNCH, "%s: hipGetDevice: %s", who, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return ic_set_error(IC_ERR_UNSUPPORTED, "%s: device %d beyond the %d supported", who, dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return ic_set_error(IC_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) on device %d: %s", who, dev,
+                          hipGetErrorString(e));
+    scratch_ptr[dev] = p;
+  }
+  *out = scratch_ptr[dev];
+  return IC_OK;
+}
 
 int run_gemm(GemmArgs g, hipStream_t st, const char* who, bool force_generic) {
   if (g.epi.act != 0 || g.epi.res != nullptr) return ic_gemm_run_epi(g, st, who, force_generic);
@@ -95,6 +128,24 @@ int ic_gemm_w4a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint
                  void* stream) {
   return ic_gemm_w4a8_ws(xq, M, K, ldx, w_packed, N, ldw, s_w, num_groups, s_a, bias, bias_dtype, out, out_dtype,
                          ldo, nullptr, 0, stream);
+}
+
+int ic_gemm_w4a8_noalloc(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed, int64_t N,
+                         int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a, const void* bias,
+                         int bias_dtype, void* out, int out_dtype, int64_t ldo, void* stream) {
+  const char* who = "ic_gemm_w4a8_noalloc";
+  const int64_t need = ic_gemm_splitk_bytes(M, N, K, num_groups, 1);
+  if (need > kScratchBytes)
+    return ic_set_error(IC_ERR_UNSUPPORTED,
+                        "%s: M=%lld N=%lld K=%lld splits K over %lld bytes of partials, above the %lld-byte static "
+                        "scratch; use ic_gemm_w4a8_ws with a workspace",
+                        who, (long long)M, (long long)N, (long long)K, (long long)need, (long long)kScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    if (int rc = scratch_for_current_device(&ws, who)) return rc;
+  }
+  return ic_gemm_w4a8_ex(xq, M, K, ldx, w_packed, N, ldw, s_w, num_groups, s_a, bias, bias_dtype, 0, nullptr, 0, 0,
+                         out, out_dtype, ldo, ws, need, stream);
 }
 
 int ic_gemm_w8a8_acc_i32(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8_t* w,

@@ -163,6 +163,25 @@ int ic_gemm_w4a8_ws(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const u
                     void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * ic_gemm_w4a8_ws without the workspace argument: the split-K partials go to a
+ * static scratch array of IC_NOALLOC_SCRATCH_BYTES per device, inside the
+ * library's code object, so the call allocates nothing (no hipMalloc, no
+ * workspace from the caller).  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under hipGraph capture,
+ * tight serving loops, harnesses that forbid allocation).  Shapes whose
+ * split-K plan needs more partials than the scratch holds return
+ * IC_ERR_UNSUPPORTED (ic_gemm_splitk_bytes tells in advance).  The scratch is
+ * shared by every call on a device: calls that overlap in time on one device
+ * (different streams, different threads) race; calls on one stream do not.
+ * Nothing in it needs clearing: every partial is written before it is read.
+ */
+#define IC_NOALLOC_SCRATCH_BYTES (32LL << 20)
+int ic_gemm_w4a8_noalloc(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed,
+                         int64_t N, int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a,
+                         const void* bias, int bias_dtype, void* out, int out_dtype, int64_t ldo,
+                         void* stream);
+
+/*
  * The same GEMMs with the epilogue options of fused_int8_gemm_dequant
  * (kernels/triton_int8_gemm.py:119-130, arguments :142-143): after dequant and
  * bias, in f32,
