@@ -116,7 +116,10 @@ class DenseLinear:
 
 
 class FluxStep:
-    def __init__(self, rt, dev, seed=0):
+    """The step's model.  n_double / n_single shorten the block stacks (the
+    tests run one block of each kind at the step's full token counts)."""
+
+    def __init__(self, rt, dev, seed=0, n_double=N_DOUBLE, n_single=N_SINGLE):
         import torch
 
         self.rt, self.dev, self.act = rt, dev, torch.bfloat16
@@ -133,14 +136,14 @@ class FluxStep:
         self.vec_in = (DenseLinear(VEC_DIM, HID, g, dev, act), DenseLinear(HID, HID, g, dev, act))
         ones = torch.ones(HEAD_DIM, device=dev, dtype=act)
         self.double = []
-        for _ in range(N_DOUBLE):
+        for _ in range(n_double):
             blk = {"img_mod": q(HID, MOD_N), "txt_mod": q(HID, MOD_N), "qk_scale": ones}
             for stream in ("img", "txt"):
                 for name, K, N in BLOCK_LINEARS:
                     blk[f"{stream}_{name}"] = q(K, N)
             self.double.append(blk)
         self.single = []
-        for _ in range(N_SINGLE):
+        for _ in range(n_single):
             blk = {"mod": W4A16Linear(rt, HID, MOD_N, g, dev, act), "qk_scale": ones}
             for name, K, N in BLOCK_LINEARS:
                 blk[name] = q(K, N)
@@ -276,8 +279,10 @@ class FluxStep:
         out = blk["mlp_down"](rt, h, residual=out)  # proj(attn) + down(h) in the epilogue
         return torch.addcmul(x, gate, out)
 
-    def forward(self):
-        """One denoise step; returns the predicted latent tokens [4096, 64]."""
+    def forward(self, collect=None):
+        """One denoise step; returns the predicted latent tokens [4096, 64].
+        collect: optional list that receives each block's outputs ((img, txt)
+        after a double block, x after a single block)."""
         import torch
         import torch.nn.functional as F
 
@@ -293,9 +298,13 @@ class FluxStep:
         freqs = self._rope_tables()
         for blk in self.double:
             img, txt = self._double_block(blk, img, txt, vec_silu, freqs)
+            if collect is not None:
+                collect.append((img, txt))
         x = torch.cat((txt, img), 0)
         for blk in self.single:
             x = self._single_block(blk, x, vec_silu, freqs)
+            if collect is not None:
+                collect.append(x)
         img = x[TXT_TOKENS:]
         shift, scale = self.final_mod(vec_silu).chunk(2, dim=-1)
         return self.final(self._modulate(img, shift, scale))
@@ -347,7 +356,7 @@ class FluxStep:
                 blk["mod"](rt, vec_silu)
 
         def attention():
-            for _ in range(N_DOUBLE + N_SINGLE):
+            for _ in range(len(self.double) + len(self.single)):
                 self.attention(*qkv, freqs)
 
         def gemm_kind(name):
@@ -373,7 +382,7 @@ class FluxStep:
         lin_ops = sum(2.0 * M * l.K * l.N for M, l in self.quantized_linears())
         mod_ops = sum(2.0 * l.K * l.N for l in self.modulation_linears())
         S = IMG_TOKENS + TXT_TOKENS
-        attn_flops = (N_DOUBLE + N_SINGLE) * 4.0 * HEADS * S * S * HEAD_DIM
+        attn_flops = (len(self.double) + len(self.single)) * 4.0 * HEADS * S * S * HEAD_DIM
         wbytes = sum(l.w.numel() + 4 * l.s_w.numel() for _, l in self.quantized_linears())
         return dict(lin_ops=lin_ops, mod_ops=mod_ops, attn_flops=attn_flops, weight_bytes=wbytes,
                     n_layers=len(self.quantized_linears()), n_mods=len(self.modulation_linears()))

@@ -84,6 +84,7 @@ __global__ __launch_bounds__(kThreads) void rotate_quant_kernel(
 
   __shared__ double tbuf[kTile / 16 * kPadStride];  // 36 KB; reused as the row buffer
   __shared__ float red[kThreads / 64];
+  __shared__ uint32_t xred[DT == IC_DTYPE_BF16 && LOG4R == 6 ? 2 * (kThreads / 64) : 1];
 
   const int t = threadIdx.x;
   const int64_t row = blockIdx.x;
@@ -113,6 +114,7 @@ __global__ __launch_bounds__(kThreads) void rotate_quant_kernel(
       for (int j = 0; j < 16; ++j)
         if (p0 + j < K_in) xs[j] = div_round_dt<DT>(xs[j], rc[j], sr_f, p0 + j);
     }
+    if constexpr (DT == IC_DTYPE_BF16 && LOG4R >= 2) bf16_flush_small<LOG4R, kThreads>(xs, xred);
 #pragma unroll
     for (int j = 0; j < 16; ++j) v[j] = (double)xs[j];
     if constexpr (LOG4R >= 2) { stage_lo(v); stage_hi(v); }

@@ -51,6 +51,66 @@ template <int RC> IC_DEV int tile_pos(int t, int j) {
 
 constexpr int kFastMaxTiles = 4;  // fast path: K_w <= 16384
 
+// ---- bf16 flush of values far below their Hadamard block's maximum.
+// The fp64 butterflies are exact when the nonzero inputs of a block (8-bit
+// significands) span at most kFlushSpan(k) = 43 - 2k binades (R = 4^k): each
+// partial sum is then an integer multiple of the smallest input's quantum
+// below 2^53.  bf16 rows can span far more (GELU outputs reach 1e-37 next to
+// values of 100); values more than kFlushSpan(k) binades below the block's
+// largest magnitude, |x| < 2^(e_max - kFlushSpan(k)), are replaced by zero
+// before the rotation, which then stays exact.  Such a value moves an output
+// by at most 2^-(kFlushSpan(k) - k) of the block's largest input, below what
+// the reference's own fp32-accumulating matmul (_quant_utils.py:117-147)
+// resolves; the oracle applies the same rule.  fp16 rows (40 binades of
+// range) are always exact and never flushed.
+template <int LOG4R> constexpr int kFlushSpan() { return 43 - 2 * LOG4R; }
+
+// xs: the 16 consecutive input positions of this thread (after the SmoothRot
+// divide); a block of R positions is the R/16 consecutive threads of one
+// aligned group (R = 4096: the four waves of the workgroup, reduced through
+// xred, 2 * TH / 64 words of LDS, with one workgroup barrier).  e_max is the
+// f32 exponent field of the block's largest |x|; bf16 subnormals have field 0.
+template <int LOG4R, int TH>
+IC_DEV void bf16_flush_small(float* xs, uint32_t* xred) {
+  constexpr int G = (1 << (2 * LOG4R)) / 16;  // threads per block
+  uint32_t mx = 0u, mn = 0xffffffffu;         // max |x| bits, min nonzero |x| bits - 1
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const uint32_t a = __float_as_uint(xs[j]) & 0x7fffffffu;
+    mx = mx > a ? mx : a;
+    const uint32_t am1 = a - 1u;  // zero wraps to the maximum
+    mn = mn < am1 ? mn : am1;
+  }
+#pragma unroll
+  for (int o = 1; o < (G < 64 ? G : 64); o <<= 1) {
+    const uint32_t a = (uint32_t)__shfl_xor((int)mx, o, 64);
+    const uint32_t b = (uint32_t)__shfl_xor((int)mn, o, 64);
+    mx = mx > a ? mx : a;
+    mn = mn < b ? mn : b;
+  }
+  if constexpr (G > 64) {
+    static_assert(G == TH, "a block of more than one wave spans the whole workgroup");
+    if ((threadIdx.x & 63) == 0) {
+      xred[2 * (threadIdx.x >> 6)] = mx;
+      xred[2 * (threadIdx.x >> 6) + 1] = mn;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < TH / 64; ++w) {
+      mx = mx > xred[2 * w] ? mx : xred[2 * w];
+      mn = mn < xred[2 * w + 1] ? mn : xred[2 * w + 1];
+    }
+  }
+  const int emax = (int)(mx >> 23), emin = (int)((mn + 1u) >> 23);
+  const bool wide = mn != 0xffffffffu && emax - emin > kFlushSpan<LOG4R>();
+  if (__builtin_expect(__any(wide), 0)) {  // wave-uniform
+    const uint32_t thr = emax > kFlushSpan<LOG4R>() ? (uint32_t)(emax - kFlushSpan<LOG4R>()) << 23 : 0u;
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if ((__float_as_uint(xs[j]) & 0x7fffffffu) < thr) xs[j] = 0.0f;
+  }
+}
+
 // Instantiation sets of the fast-path kernels (see rq_fast.h).
 constexpr int kRqPlain = 0;    // no SmoothRot factors, no perm
 constexpr int kRqGeneral = 1;  // either one; flags read at run time

@@ -130,6 +130,7 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
   __shared__ __attribute__((aligned(16))) u16 rowbuf[rowbuf_len<NT, kTile>()];
   __shared__ float red[TH / 64];
   __shared__ double red_d[NORM != 0 ? 2 * (TH / 64) : 1];
+  __shared__ uint32_t xred[DT == IC_DTYPE_BF16 && LOG4R == 6 ? 2 * (TH / 64) : 1];
 
   constexpr bool PLAIN = VAR == kRqPlain;
   const int t = threadIdx.x;
@@ -283,6 +284,7 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
             }
           }
         }
+        if constexpr (DT == IC_DTYPE_BF16 && LOG4R >= 2) bf16_flush_small<LOG4R, TH>(xs, xred);
 #pragma unroll
         for (int j = 0; j < 16; ++j) v[j] = (double)xs[j];
       } else {

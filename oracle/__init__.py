@@ -189,6 +189,20 @@ def prepare(x, dtype: int, *, smoothrot=None, rot_size: int = 0, w_in: int | Non
     return out
 
 
+def flush_small_bf16(blk: np.ndarray, k: int) -> np.ndarray:
+    """bf16 rows only: inputs more than 43 - 2k binades below the largest
+    finite magnitude of their Hadamard block (R = 4^k) become zero before the
+    rotation (the rule intcrush_oracle.c's flush_small_bf16 applies)."""
+    blk = np.array(blk, dtype=np.float64)
+    fin = np.abs(blk[np.isfinite(blk)])
+    mx = fin.max() if fin.size else 0.0
+    if mx == 0.0:
+        return blk
+    thr = 2.0 ** (int(np.frexp(mx)[1]) - 1 - (43 - 2 * k))
+    blk[np.abs(blk) < thr] = 0.0
+    return blk
+
+
 def _prepare_exact_rows(xv, dtype, srf, R, K_w, pm, smf, out):
     """Recompute rows containing a block whose double sum is not provably exact."""
     L = lib()
@@ -205,6 +219,8 @@ def _prepare_exact_rows(xv, dtype, srf, R, K_w, pm, smf, out):
         redo = False
         for b0 in range(0, K_r, R):
             blk = a[b0:b0 + R]
+            if dtype == DT_BF16:
+                blk = flush_small_bf16(blk, k)
             nz = blk[blk != 0]
             if nz.size:
                 emax = int(np.max(np.frexp(np.abs(nz))[1])) - 1

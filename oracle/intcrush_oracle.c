@@ -115,6 +115,29 @@ static void had_fast(double* v, int R, int k) {
 }
 
 /*
+ * bf16 rows: inputs more than 43 - 2k binades below the largest magnitude of
+ * their Hadamard block (R = 4^k) are replaced by zero before the rotation,
+ * |x| < 2^(e_max - (43 - 2k)) with e_max = floor(log2 max|x|) over the
+ * block's finite values.  The remaining inputs span at most 43 - 2k binades,
+ * so every butterfly partial sum is exact in double (block_sum_exact holds);
+ * the flushed values change an output by less than 2^-(43 - 3k) of the
+ * block's largest input.  fp16 and f32 rows are not flushed.
+ */
+static void flush_small_bf16(double* v, int R, int k) {
+  double mx = 0.0;
+  for (int j = 0; j < R; ++j) {
+    const double a = fabs(v[j]);
+    if (isfinite(a) && a > mx) mx = a;
+  }
+  if (mx == 0.0) return;
+  int e;
+  frexp(mx, &e);
+  const double thr = ldexp(1.0, (e - 1) - (43 - 2 * k));
+  for (int j = 0; j < R; ++j)
+    if (fabs(v[j]) < thr) v[j] = 0.0;
+}
+
+/*
  * _prep_activation (_ops.py:337-365) + old SmoothQuant (_ops.py:529-533) for
  * one row block [M, K_in] -> [M, K_w]:
  *   x / RN_dt(f)  rounded to dt                       (_ops.py:349-350)
@@ -163,6 +186,7 @@ int oc_prepare(const float* x, int dtype, int64_t M, int64_t K_in, const float* 
       for (int64_t j = 0; j < K_r; ++j) y[j] = a[j];
     } else {
       for (int64_t b0 = 0; b0 < K_r; b0 += R) {
+        if (dtype == 1) flush_small_bf16(a + b0, R, k);
         if (!block_sum_exact(a + b0, R, p)) ++inexact;
         if (fast) {
           had_fast(a + b0, R, k);

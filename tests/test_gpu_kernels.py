@@ -127,6 +127,8 @@ ROT_CASES = [
     (9216, 256, None, True, True, False),       # one twelve-wave tile, 3072 positions of it padding
     (10000, 1024, 11008, False, True, False),   # the same tile with one-block waves, pads to 10240 and 11008
     (15360, 256, None, True, True, False),      # two eight-wave tiles (Flux single-block output projection)
+    (16384, 1024, None, True, True, False),     # two eight-wave tiles, one-block waves (RC = 3 layout)
+    (15360, 64, None, False, True, False),      # two eight-wave tiles, 64-blocks
 ]
 
 
@@ -157,6 +159,55 @@ def test_rotate_quantize_bit_exact(rt, oracle, dev, dtype, case):
     assert np.array_equal(y.float().cpu().numpy(), y_ref)
     assert np.array_equal(s.cpu().numpy(), s_ref)
     assert np.array_equal(q.cpu().numpy(), q_ref)
+
+
+def _bf16_wide_rows(M, K, R, seed):
+    """bf16 rows whose Hadamard blocks span far beyond double's exact range:
+    GELU-tanh of N(0, 16) (tails down to ~1e-37 next to values of ~20), and a
+    first row of crafted blocks [1, 2^-8, t, 0, ...]: their outputs
+    2^-k (1 +- 2^-8) sit on bf16 rounding midpoints, and the tiny term t is
+    either inside the exact span (2^-30, breaks the tie upwards) or beyond it
+    (2^-100, flushed, tie to even)."""
+    g = _gen(seed)
+    x = torch.nn.functional.gelu(torch.randn(M, K, generator=g) * 4.0, approximate="tanh")
+    x[0] = 0.0
+    for b, b0 in enumerate(range(0, K, R)):
+        x[0, b0] = 1.0
+        x[0, b0 + 1] = 2.0 ** -8
+        x[0, b0 + 2] = 2.0 ** -30 if b % 2 else 2.0 ** -100
+    return x.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("R", [16, 64, 256, 1024, 4096])
+@pytest.mark.parametrize("path", ["fast", "general"])
+def test_bf16_wide_span_rows_match_oracle(rt, oracle, dev, R, path):
+    """Rows with ~1e-37 tails (post-GELU activations): the kernels flush
+    inputs beyond each block's exact span exactly as the oracle does and
+    rotate the rest exactly -- prepared values, codes and scales bit-exact.
+    "fast" runs the single-pass kernel (SmoothRot + perm, aligned rows);
+    "general" the one-workgroup-per-row kernel (an odd row stride)."""
+    M, K = 6, 8192
+    x = _bf16_wide_rows(M, K, R, seed=R)
+    K_w, sr, perm, _ = _prep_inputs(K, R, None, True, True, False, seed=R + 1)
+    srp = rt.prepare_factors(sr.to(dev), torch.bfloat16)
+    pp = rt.prepare_perm(perm.to(dev), K_w)
+    xd = x.to(dev)
+    if path == "general":
+        xd = torch.zeros(M, K + 3, dtype=torch.bfloat16, device=dev)[:, :K]
+        xd.copy_(x.to(dev))
+    q, s = rt.rotate_quantize(xd, rot_size=R, w_in=K_w, smoothrot=srp, perm=pp)
+    y = rt.prepare_activation(xd, rot_size=R, w_in=K_w, smoothrot=srp, perm=pp)
+    y_ref = oracle.prepare(x, 1, smoothrot=sr, rot_size=R, w_in=K_w, perm=perm)
+    q_ref, s_ref = oracle.quantize(y_ref)
+    assert np.array_equal(y.float().cpu().numpy(), y_ref)
+    assert np.array_equal(s.cpu().numpy(), s_ref)
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+    # the crafted row: no SmoothRot / perm, outputs of block 0 / 1 on known values
+    y0 = rt.prepare_activation(x[:1].to(dev), rot_size=R).float().cpu()
+    k = {16: 2, 64: 3, 256: 4, 1024: 5, 4096: 6}[R]
+    u = 2.0 ** -k
+    assert float(y0[0, 0]) == u  # block 0: 2^-100 flushed, 2^-k (1 + 2^-8) ties to even
+    assert float(y0[0, R]) == u * (1 + 2.0 ** -7)  # block 1: 2^-30 kept, the tie breaks upwards
 
 
 def test_rotate_quantize_f32(rt, oracle, dev):
@@ -339,14 +390,42 @@ def test_c5_full_size_prep_sampled_rows(rt, oracle, dev, dtype):
     """Wan FFN-down activation prep at full size: 32760 rows of 13824 (1% of
     channels x20), rotated in 1024-blocks and padded to 14336.  Rows are
     independent, so sampled rows (first, last, tile edges) must equal the
-    oracle's prep and quantization bit for bit.  (Student-t rows are covered
-    at small M; sampling 4.5e8 of them on the CPU would dominate the test.)"""
+    oracle's prep and quantization bit for bit.  (Heavy-tailed Student-t rows
+    are the accuracy gate's input, test_c5_accuracy_gate_student_t.)"""
     M, K_in, K_w = 32760, 13824, 14336
     x = _acts(M, K_in, dtype, seed=41, outliers=0.01)
     q, s = rt.rotate_quantize(x.to(dev), rot_size=1024, w_in=K_w)
     rows = torch.tensor(C5_ROWS)
     y_ref = oracle.prepare(x[rows], DT[dtype], smoothrot=None, rot_size=1024, w_in=K_w, perm=None, smooth=None)
     q_ref, s_ref = oracle.quantize(y_ref)
+    assert np.array_equal(s[rows.to(dev)].cpu().numpy(), s_ref)
+    assert np.array_equal(q[rows.to(dev)].cpu().numpy(), q_ref)
+
+
+# (M, K_in, R, w_in, SmoothRot + perm): the persistent row loop of the wide
+# prep tiles (each workgroup walks rows r, r + grid, ...; the next row's
+# activations are loaded while the current one is rotated).  Sampled rows: the
+# first ones (first row of a workgroup), the first rows of a workgroup's second
+# and later iterations, and the last rows.
+FULL_PREP = [
+    (4608, 12288, 256, None, True),    # C3: one twelve-wave tile
+    (4608, 15360, 256, None, True),    # Flux single-block projection: two eight-wave tiles
+    (2048, 16384, 1024, None, True),   # two eight-wave tiles, one-block waves
+    (2048, 15360, 64, None, False),
+]
+FULL_PREP_ROWS = [0, 1, 255, 256, 257, 511, 512, 1023, 1024, 1500, 2047]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,K_in,R,w_in,srp", FULL_PREP)
+def test_wide_prep_persistent_rows(rt, oracle, dev, dtype, M, K_in, R, w_in, srp):
+    K_w, sr, perm, _ = _prep_inputs(K_in, R, w_in, srp, srp, False, seed=K_in + 3)
+    x = _acts(M, K_in, dtype, seed=K_in + 5, outliers=0.01)
+    srf = rt.prepare_factors(sr.to(dev), dtype) if sr is not None else None
+    pp = rt.prepare_perm(perm.to(dev), K_w) if perm is not None else None
+    q, s = rt.rotate_quantize(x.to(dev), rot_size=R, w_in=K_w, smoothrot=srf, perm=pp)
+    rows = torch.tensor([r for r in FULL_PREP_ROWS if r < M] + [M - 2, M - 1])
+    q_ref, s_ref = oracle.rotate_quantize(x[rows], DT[dtype], smoothrot=sr, rot_size=R, w_in=K_w, perm=perm)
     assert np.array_equal(s[rows.to(dev)].cpu().numpy(), s_ref)
     assert np.array_equal(q[rows.to(dev)].cpu().numpy(), q_ref)
 
@@ -475,6 +554,40 @@ def test_w4a8_linear_vs_fp32_fallback(rt, oracle, dev, dtype):
                                                         bias.float().numpy()))
     rel = (out - ref).norm() / ref.norm()
     assert _cos(out, ref) >= 0.9999, f"cosine {_cos(out, ref)} rel {rel}"
+
+
+@pytest.mark.parametrize("fmt", ["w4a8_g128", "w8a8"])
+def test_c5_accuracy_gate_student_t(rt, oracle, dev, fmt):
+    """The C5 accuracy gate on its heavy-tailed input: Wan FFN-down
+    (13824 -> 14336 with the R=1024 pad, N=5120) at full K and N on 256
+    Student-t (nu = 4) fp16 rows.  Weights are a random layer of the padded
+    space quantized by the converter's rule (_quant_utils.py:237-270: INT4
+    with fp16 scales per 128-group, or INT8 per output row).  The fused prep +
+    GEMM output must reach cosine >= 0.9999 against the reference fp32
+    fallback (fp32 prep, W = q * s, F.linear), the north-star bar."""
+    M, K_in, K, N, R = 256, 13824, 14336, 5120, 1024
+    x = _acts(M, K_in, torch.float16, seed=61, student_t=True)
+    W = torch.randn(N, K, generator=_gen(62)) * 0.02
+    if fmt == "w8a8":
+        s_w = (W.abs().amax(1) / 127.0).clamp(min=1e-8).to(torch.float16).float()
+        wq = (W / s_w[:, None]).round().clamp(-128, 127).to(torch.int8)
+        wt = wq
+    else:
+        Wg = W.reshape(N, K // 128, 128)
+        s_w = (Wg.abs().amax(-1) / 7.0).clamp(min=1e-8).to(torch.float16).float()
+        wq = (Wg / s_w[..., None]).round().clamp(-8, 7).to(torch.int8).reshape(N, K)
+        wt = torch.from_numpy(oracle.pack_int4(wq.numpy()))
+    q, s = rt.rotate_quantize(x.to(dev), rot_size=R, w_in=K)
+    if fmt == "w8a8":
+        out = rt.fused_int8_gemm_dequant(q, wt.to(dev), s_w.to(dev), s, out_dtype=torch.float16)
+    else:
+        out = rt.gemm_w4a8(q, wt.to(dev), s_w.to(dev), s, out_dtype=torch.float16)
+    out = out.float().cpu()
+    ref = oracle.reference_fallback_forward(x, wt.numpy(), s_w.numpy(), K, int4=fmt != "w8a8", rot_size=R)
+    c = _cos(out, ref)
+    rel = float((out - ref).norm() / ref.norm())
+    assert torch.isfinite(out).all()
+    assert c >= 0.9999, f"cosine {c:.7f}, relative error {rel:.4g}"
 
 
 def test_w8a8_linear_vs_fp32_fallback(rt, oracle, dev):

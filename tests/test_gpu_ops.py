@@ -257,3 +257,51 @@ def test_gpu_forward_refuses_silent_fallback(dev, monkeypatch):
     monkeypatch.delenv("INTCRUSH_ALLOW_TORCH_FALLBACK", raising=False)
     with pytest.raises(RuntimeError, match="refusing a silent PyTorch"):
         lin(torch.randn(2, 256, device=dev, dtype=torch.float16))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fused_quant_int8_gemm_dequant(rt, oracle, dev, dtype):
+    """fused_quant_int8_gemm_dequant (kernels/triton_int8_gemm.py:331-389):
+    per-token quantization of x then the W8A8 GEMM; equals the oracle's
+    quantize -> accumulators -> epilogue bit for bit."""
+    M, K, N = 300, 1024, 384
+    g = torch.Generator().manual_seed(70)
+    x = (torch.randn(M, K, generator=g) * 3).to(dtype)
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    s_w = (torch.rand(N, generator=g) * 2e-3 + 1e-4).to(torch.float16).float()
+    bias = torch.randn(N, generator=g).to(dtype)
+    out = rt.fused_quant_int8_gemm_dequant(x.to(dev), w.to(dev), s_w.to(dev), bias=bias.to(dev), out_dtype=dtype)
+    q, s = oracle.quantize(oracle.to_dtype_values(x, DT[dtype]))
+    ref = oracle.epilogue(oracle.gemm_acc(q, w.numpy()), s, s_w.numpy(), bias.float().numpy(), DT[dtype])
+    assert np.array_equal(out.float().cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("zp", [False, True])
+def test_int8_layer_use_fused_w8a8(oracle, dev, monkeypatch, zp):
+    """The USE_FUSED_W8A8 branch of the INT8 forward (_ops.py:546-558): the
+    prepared activation goes through fused_quant_int8_gemm_dequant, then the
+    zero-point term when present.  Graphs are off so the eager branch runs."""
+    rt = __graft_entry__._submodule("_hip_runtime")
+    monkeypatch.setattr(rt, "USE_FUSED_W8A8", True)
+    monkeypatch.setattr(rt, "USE_CUDA_GRAPHS", False)
+    M, K, N, R = 48, 512, 160, 256
+    ops = ops_mod.make_intcrush_ops("int8_crush", R)
+    sd = int8_layer(N, K, seed=71, perm=True, smoothrot=True, zp=zp)
+    lin = _to_dev(load_linear(ops, "double_blocks.1.img_attn.qkv", sd, K, N), dev)
+    x = _x(M, K, torch.bfloat16, 72)
+    out = lin(x.to(dev)).float().cpu()
+    y = oracle.prepare(x, DT[torch.bfloat16], smoothrot=sd["weight_smoothrot_factors"], rot_size=R, w_in=K,
+                       perm=sd["weight_perm"])
+    q, s = oracle.quantize(y)
+    s_w = sd["weight_scale"].float().numpy()
+    ref = oracle.epilogue(oracle.gemm_acc(q, sd["weight"].numpy()), s, s_w, sd["bias"].float().numpy(),
+                          DT[torch.bfloat16])
+    if not zp:
+        assert lin._graph_runner is None
+        assert np.array_equal(out.numpy(), ref)
+        return
+    # zero point: out -= (sum_k x_prep) * (s * zp), one rounding of the bf16 output
+    corr = y.astype(np.float64).sum(1)[:, None] * (s_w.reshape(-1) * sd["weight_zp"].numpy())[None, :]
+    exact = ref.astype(np.float64) - corr
+    assert _cos(out, torch.from_numpy(exact)) >= 0.9999
+    assert np.allclose(out.numpy(), exact, rtol=2e-2, atol=2e-2 * np.abs(exact).max() * 1e-2)

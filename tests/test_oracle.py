@@ -120,17 +120,92 @@ def test_prepare_smoothrot_divide_exact(oracle):
             assert got[i, j] == oracle._round_fraction(q, 0), (i, j)
 
 
-def test_bf16_wide_block_uses_exact_path(oracle):
-    """A bf16 block spanning 2^-100..2^60 is not exact in double: the oracle
-    must fall back to rationals and agree with an exact direct sum."""
-    R = 16
-    vals = torch.tensor([[2.0 ** 60, 2.0 ** -100, -3.0, 2.0 ** -90] + [1.0] * 12], dtype=torch.bfloat16)
-    got = oracle.prepare(vals, 1, rot_size=R)
+def _exact_rot(vals, R):
+    """Exact rationals of H x for one block (no rounding)."""
     H = _kron_h(R)
-    xv = [Fraction(float(v)) for v in vals[0].float()]
-    for i in range(R):
-        exact = sum((Fraction(H[i, j]) * xv[j] for j in range(R)), Fraction(0))
-        assert got[0, i] == oracle._round_fraction(exact, 1)
+    xv = [Fraction(float(v)) for v in vals]
+    return [sum((Fraction(H[i, j]) * xv[j] for j in range(R)), Fraction(0)) for i in range(R)]
+
+
+def _flush_rational(vals, R):
+    """The bf16 flush restated independently: zero every input below
+    2^(floor(log2 max|x|) - (43 - 2k)), R = 4^k."""
+    k = {16: 2, 64: 3, 256: 4, 1024: 5, 4096: 6}[R]
+    mx = max(abs(Fraction(float(v))) for v in vals)
+    e = mx.numerator.bit_length() - mx.denominator.bit_length()
+    if Fraction(2) ** e > mx:
+        e -= 1
+    thr = Fraction(2) ** (e - (43 - 2 * k))
+    return [v if abs(Fraction(float(v))) >= thr else 0.0 for v in vals]
+
+
+def test_bf16_wide_block_flush_then_exact(oracle):
+    """A bf16 block spanning 2^-100..2^10: inputs below 2^(10 - 39) are
+    flushed (R = 16, k = 2) and the rest rotated exactly; equal to the exact
+    rational Hadamard of the kept inputs, rounded once."""
+    R = 16
+    vals = torch.tensor([[2.0 ** 10, 2.0 ** -100, -3.0, 2.0 ** -90] + [1.0] * 11 + [2.0 ** -29]],
+                        dtype=torch.bfloat16)
+    got = oracle.prepare(vals, 1, rot_size=R)
+    kept = _flush_rational(vals[0].float().tolist(), R)
+    assert kept[1] == 0.0 and kept[3] == 0.0 and kept[2] == -3.0 and kept[15] == 2.0 ** -29
+    for i, q in enumerate(_exact_rot(kept, R)):
+        assert got[0, i] == oracle._round_fraction(q, 1)
+
+
+def test_bf16_midpoint_plus_tiny_term(oracle):
+    """(1 + 2^-8) / 4 is a bf16 rounding midpoint.  A tiny term inside the
+    exact span breaks the tie upwards exactly; one beyond the span is flushed
+    and the tie goes to even (0.25), as the reference's fp32-accumulating
+    matmul would also lose it."""
+    R = 16
+    for tiny, up in ((2.0 ** -30, True), (2.0 ** -100, False)):
+        vals = torch.tensor([[1.0, 2.0 ** -8, tiny] + [0.0] * 13], dtype=torch.bfloat16)
+        got = oracle.prepare(vals, 1, rot_size=R)
+        assert got[0, 0] == (0.25 + 2.0 ** -9 if up else 0.25), tiny
+
+
+@pytest.mark.parametrize("R", [16, 64, 256, 1024])
+def test_bf16_flush_only_moves_ties_and_near_ties(oracle, R):
+    """Random wide-span bf16 blocks (GELU-like tails down to 1e-37): the
+    flushed result equals the kept inputs' exact rotation (rounded once), is
+    within one bf16 ulp of the exact unflushed rotation, and differs from it
+    only where a rounding boundary lies between the two exact values."""
+    g = torch.Generator().manual_seed(R)
+    x = torch.randn(2, R, generator=g) * 3
+    tiny = torch.rand(2, R, generator=g) < 0.1
+    x[tiny] = torch.randn(int(tiny.sum()), generator=g) * torch.pow(10.0, -torch.randint(10, 37, (int(tiny.sum()),), generator=g).float())
+    xb = x.to(torch.bfloat16)
+    got = oracle.prepare(xb, 1, rot_size=R)
+    for m in range(2):
+        full = _exact_rot(xb[m].float().tolist(), R)
+        kept = _exact_rot(_flush_rational(xb[m].float().tolist(), R), R)
+        for i in range(R):
+            z = got[m, i]
+            assert z == oracle._round_fraction(kept[i], 1)
+            zf = oracle._round_fraction(full[i], 1)
+            if z != zf:
+                lo, hi = sorted((kept[i], full[i]))
+                assert abs(z - zf) <= 2.0 ** (np.floor(np.log2(max(abs(z), abs(zf)))) - 7)
+                # a midpoint between the two candidates lies in [lo, hi]
+                mid = Fraction(float(z) + float(zf)) / 2
+                assert lo <= mid <= hi
+
+
+def test_bf16_flushed_blocks_are_exact_in_double(oracle):
+    """After the flush, the C oracle's double butterflies never report an
+    inexact block on bf16 rows, whatever the input range."""
+    import ctypes
+
+    L = oracle.lib()
+    g = torch.Generator().manual_seed(9)
+    for R in (16, 64, 256, 1024, 4096):
+        x = torch.randn(3, 4096, generator=g) * torch.pow(2.0, torch.randint(-120, 100, (3, 4096), generator=g).float())
+        xv = np.ascontiguousarray(x.to(torch.bfloat16).float().numpy())
+        out = np.zeros((3, 4096), np.float32)
+        n = ctypes.c_int64(-1)
+        rc = L.oc_prepare(oracle._p(xv), 1, 3, 4096, None, R, 4096, None, None, oracle._p(out), ctypes.byref(n), 1)
+        assert rc == 0 and n.value == 0, (R, n.value)
 
 
 # ---------------------------------------------------------------- quantization
