@@ -64,6 +64,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "ic_smoothrot_prepare": ([_P, _L, _I, _P, _P, _P], _I),
     "ic_rotate_quantize": ([_P, _I, _L, _L, _L, _P, _P, _I, _L, _P, _P, _P, _P, _L, _P, _P], _I),
     "ic_prepare_activation": ([_P, _I, _L, _L, _L, _P, _P, _I, _L, _P, _P, _P, _P, _L, _P], _I),
+    "ic_permute_quantize": ([_P, _I, _L, _L, _L, _L, _P, _P, _P, _P, _L, _P, _P, _L, _P], _I),
     "ic_dynamic_quantize": ([_P, _I, _L, _L, _L, _P, _L, _P, _P], _I),
     "ic_norm_quantize": ([_P, _I, _L, _L, _L, _I, _P, _P, ctypes.c_float, _P, _L, _P, _P], _I),
     "ic_norm_rotate_quantize": ([_P, _I, _L, _L, _L, _I, _P, _P, ctypes.c_float, _P, _P, _I, _L, _P, _P, _L,
@@ -256,17 +257,41 @@ def rotate_quantize(x: torch.Tensor, *, rot_size: int = 0, w_in: int | None = No
     s_a = _alloc_or_reuse((M,), torch.float32, x2.device, s_a_out)
     q = _alloc_or_reuse((M, K_w), torch.int8, x2.device, x_int8_out)
     with torch.cuda.device(x2.device):
-        if K_w <= lib().ic_max_fused_row() // (2 if dt == IC_DTYPE_F32 else 1):
+        if K_w <= _fused_limit(dt):
             _call("ic_rotate_quantize", _ptr(x2), dt, M, K_in, x2.stride(0),
                   _ptr(smoothrot.rcp) if smoothrot else None, _ptr(smoothrot.fdt) if smoothrot else None,
                   R, K_w, _ptr(perm), _ptr(smooth.rcp) if smooth else None,
                   _ptr(smooth.fdt) if smooth else None, _ptr(q), q.stride(0), _ptr(s_a), _stream(x2))
         else:
-            # rows wider than one workgroup holds: prepare, then quantize (two passes)
-            y = prepare_activation(x2, rot_size=R, w_in=K_w, smoothrot=smoothrot, perm=perm, smooth=smooth)
-            _call("ic_dynamic_quantize", _ptr(y), dt, M, K_w, y.stride(0), _ptr(q), q.stride(0),
-                  _ptr(s_a), _stream(y))
+            y = _rotate_wide(x2, R, smoothrot, dt)
+            _call("ic_permute_quantize", _ptr(y), dt, M, y.shape[1], y.stride(0), K_w, _ptr(perm),
+                  _ptr(smooth.rcp) if smooth else None, _ptr(smooth.fdt) if smooth else None,
+                  _ptr(q), q.stride(0), _ptr(s_a), None, 0, _stream(y))
     return q, s_a
+
+
+def _fused_limit(dt: int) -> int:
+    """Widest row the single-pass prep kernels hold."""
+    return lib().ic_max_fused_row() // (2 if dt == IC_DTYPE_F32 else 1)
+
+
+def _rotate_wide(x2: torch.Tensor, R: int, smoothrot: PreparedFactors | None, dt: int) -> torch.Tensor:
+    """SmoothRot divide + block Hadamard of rows wider than the single-pass
+    kernels hold, into [M, K_r] in x's dtype: the rotation is block-diagonal,
+    so ic_prepare_activation runs on column chunks of whole blocks.  The pad,
+    perm gather and old-SmoothQuant divide follow in ic_permute_quantize."""
+    M, K_in = x2.shape
+    K_r = ((K_in + R - 1) // R) * R if R else K_in
+    lim = _fused_limit(dt)
+    step = (lim // R) * R if R else lim
+    y = torch.empty(M, K_r, dtype=x2.dtype, device=x2.device)
+    for c0 in range(0, K_r, step):
+        kin = min(step, K_in - c0)
+        kw = min(step, K_r - c0)
+        _call("ic_prepare_activation", _ptr(x2[:, c0:]), dt, M, kin, x2.stride(0),
+              _ptr(smoothrot.rcp[c0:]) if smoothrot else None, _ptr(smoothrot.fdt[c0:]) if smoothrot else None,
+              R, kw, None, None, None, _ptr(y[:, c0:]), y.stride(0), _stream(x2))
+    return y
 
 
 def prepare_activation(x: torch.Tensor, *, rot_size: int = 0, w_in: int | None = None,
@@ -283,17 +308,20 @@ def prepare_activation(x: torch.Tensor, *, rot_size: int = 0, w_in: int | None =
     K_r = ((K_in + R - 1) // R) * R if R else K_in
     K_w = max(int(w_in) if w_in is not None else K_r, K_r)
     dt = _dt(x2.dtype, "prepare_activation")
-    lim = lib().ic_max_fused_row() // (2 if dt == IC_DTYPE_F32 else 1)
-    if K_w > lim:
-        raise ValueError(f"prepare_activation: rows wider than {lim} are not supported")
     if perm is not None and (perm.dtype != torch.int32 or perm.numel() != K_w):
         raise ValueError("perm must be an int32 device tensor of length w_in (see prepare_perm)")
     y = _alloc_or_reuse((M, K_w), x2.dtype, x2.device, out)
     with torch.cuda.device(x2.device):
-        _call("ic_prepare_activation", _ptr(x2), dt, M, K_in, x2.stride(0),
-              _ptr(smoothrot.rcp) if smoothrot else None, _ptr(smoothrot.fdt) if smoothrot else None,
-              R, K_w, _ptr(perm), _ptr(smooth.rcp) if smooth else None,
-              _ptr(smooth.fdt) if smooth else None, _ptr(y), y.stride(0), _stream(x2))
+        if K_w <= _fused_limit(dt):
+            _call("ic_prepare_activation", _ptr(x2), dt, M, K_in, x2.stride(0),
+                  _ptr(smoothrot.rcp) if smoothrot else None, _ptr(smoothrot.fdt) if smoothrot else None,
+                  R, K_w, _ptr(perm), _ptr(smooth.rcp) if smooth else None,
+                  _ptr(smooth.fdt) if smooth else None, _ptr(y), y.stride(0), _stream(x2))
+        else:
+            yr = _rotate_wide(x2, R, smoothrot, dt)
+            _call("ic_permute_quantize", _ptr(yr), dt, M, yr.shape[1], yr.stride(0), K_w, _ptr(perm),
+                  _ptr(smooth.rcp) if smooth else None, _ptr(smooth.fdt) if smooth else None,
+                  None, 0, None, _ptr(y), y.stride(0), _stream(yr))
     return y
 
 
@@ -521,6 +549,7 @@ def fused_int8_gemm_dequant(x_int8: torch.Tensor, w_int8: torch.Tensor, s_w: tor
     bp, bdt, _keep = _bias_args(bias, N)
     act, rp, rdt, ldr, _rkeep = _epilogue_args(activation, residual, M, N)
     c = _out_buffer(out, M, N, out_dtype, x_int8.device)
+    _warn_if_scalar_gemm("fused_int8_gemm_dequant", K, 1, xq, w)
     with torch.cuda.device(xq.device):
         ws, nb = _splitk_workspace(M, N, K, 1, False, xq.device)
         _call("ic_gemm_w8a8_ex", _ptr(xq), M, K, xq.stride(0), _ptr(w), N, w.stride(0), _ptr(sa),
@@ -566,6 +595,25 @@ def fused_w4a8_gemm_dequant(x_int8, w_int8, s_w, s_a, bias=None, out_dtype=torch
                                    activation=activation, residual=residual, out=out)
 
 
+_SCALAR_WARNED: set = set()
+
+
+def _warn_if_scalar_gemm(who: str, K: int, G: int, *tensors: torch.Tensor) -> None:
+    """The INT8 / W4A8 GEMMs run MFMA tiles only for K a multiple of 128,
+    group sizes that are multiples of 128 and 16-byte aligned operands and
+    row strides; anything else takes the scalar kernel (one thread per output,
+    ~100x slower).  Log that once per shape instead of running it silently."""
+    gs = K // G
+    ok = K % 128 == 0 and (G == 1 or gs % 128 == 0)
+    for t in tensors:
+        ok = ok and t.data_ptr() % 16 == 0 and (t.dim() < 2 or (t.stride(0) * t.element_size()) % 16 == 0)
+    key = (who, K, G)
+    if not ok and key not in _SCALAR_WARNED:
+        _SCALAR_WARNED.add(key)
+        log.warning("[INT-Crush] %s: K=%d, group size %d or operand alignment has no MFMA tiling; "
+                    "running the scalar fallback kernel (about 100x slower)", who, K, gs)
+
+
 def gemm_w4a8(x_int8: torch.Tensor, w_packed: torch.Tensor, s_w: torch.Tensor, s_a: torch.Tensor,
               bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16,
               out: torch.Tensor | None = None, activation: int = 0,
@@ -593,6 +641,7 @@ def gemm_w4a8(x_int8: torch.Tensor, w_packed: torch.Tensor, s_w: torch.Tensor, s
     bp, bdt, _keep = _bias_args(bias, N)
     act, rp, rdt, ldr, _rkeep = _epilogue_args(activation, residual, M, N)
     c = _out_buffer(out, M, N, out_dtype, xq.device)
+    _warn_if_scalar_gemm("gemm_w4a8", K, G, xq, w)
     with torch.cuda.device(xq.device):
         ws, nb = _splitk_workspace(M, N, K, G, True, xq.device)
         _call("ic_gemm_w4a8_ex", _ptr(xq), M, K, xq.stride(0), _ptr(w), N, w.stride(0), _ptr(sw), G,

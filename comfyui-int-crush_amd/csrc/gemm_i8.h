@@ -137,7 +137,9 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
   const uint32_t s_off = GS ? (uint32_t)(min(64 * wave + lane, N - 1 - n0) * G * 4) : 0u;
   const int8_t* a_base = A + (int64_t)m0 * lda + (int64_t)kt0 * kBK;
   const uint8_t* b_base = B + (int64_t)n0 * ldb + (int64_t)kt0 * (INT4 ? kBK / 2 : kBK);
-  const float* s_base = GS ? s_w + (int64_t)n0 * G + kt0 : nullptr;
+  const float* s_base = GS ? s_w + (int64_t)n0 * G : nullptr;
+  // scale groups of 128 * spg columns: stage kt0 + kt folds with group (kt0 + kt) / spg
+  const int spg = GS ? (K / G) / kBK : 1;
 
   // The D DMA instructions of one stage are issued in kParts slices, one per
   // K-step of the MFMA loop: a wave that issued a whole stage at once stalled
@@ -163,7 +165,8 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
     for (int c = 0; c < B_DMA; ++c)
       if ((A_DMA + c) % kParts == part) dma16(b_off[c], bb, slot + (uint32_t)(TL::A_BYTES + (wave + 8 * c) * 1024));
     if constexpr (GS != 0) {
-      if (part == kParts - 1 && s_wave) dma4(s_off, s_base + kt, slot + (uint32_t)(TL::A_BYTES + TL::B_BYTES + wave * 256));
+      if (part == kParts - 1 && s_wave)
+        dma4(s_off, s_base + (kt0 + kt) / spg, slot + (uint32_t)(TL::A_BYTES + TL::B_BYTES + wave * 256));
     }
   };
   auto issue_dma = [&](int kt) {
@@ -710,9 +713,13 @@ hipError_t launch_generic(const GemmArgs& g, int gsize, hipStream_t st) {
   }
 }
 
+// Grouped scales take the MFMA kernels for group sizes that are multiples of
+// 128: the fold runs once per 128-column stage with that stage's group scale
+// (for 256, 384, ... each group's two or more stages fold separately).  The
+// debug accumulator output writes one slab per group and needs 128.
 bool mfma_shape_ok(const GemmArgs& g, int gsize) {
   if (g.K % kBK != 0) return false;
-  if (g.G > 1 && gsize != 128) return false;
+  if (g.G > 1 && (gsize % kBK != 0 || (g.acc_out != nullptr && gsize != kBK))) return false;
   // 16-byte DMA / vector loads need aligned bases and strides; packed INT4
   // rows are read 8 or 16 bytes at a time
   if (((uintptr_t)g.A & 15) || ((uintptr_t)g.B & 15) || (g.lda & 15) || (g.ldb & 15)) return false;

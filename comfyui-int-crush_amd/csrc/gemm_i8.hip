@@ -48,7 +48,7 @@ extern "C" {
 
 int64_t ic_gemm_splitk_bytes(int64_t M, int64_t N, int64_t K, int64_t num_groups, int int4) {
   if (M <= IC_GEMV_MAX_M || N <= 0 || K <= 0 || K % kBK != 0 || num_groups < 1) return 0;
-  if (num_groups > 1 && K / num_groups != 128) return 0;
+  if (num_groups > 1 && (K % num_groups != 0 || (K / num_groups) % 128 != 0)) return 0;
   if (M * N > (1LL << 31)) return 0;
   GemmArgs g{nullptr, K, nullptr, K, nullptr, nullptr, (int)num_groups, nullptr, 0, nullptr, IC_DTYPE_F32,
              N, (int)M, (int)N, (int)K, nullptr, int4 != 0};

@@ -264,6 +264,60 @@ __global__ __launch_bounds__(kThreads) void quant_rows_kernel(
   for (int k = t; k < K; k += kThreads) q_out[row * ldq + k] = (int8_t)quant_code(ld_as_f32<DT>(xrow, k), rs);
 }
 
+// Second pass of the preparation for rows wider than the fused kernels hold:
+// the rotated rows y [M, K_y] (SmoothRot divide and block Hadamard already
+// applied, in column chunks) are padded with zeros to K_w, gathered by the
+// PermuQuant indices, divided by the old SmoothQuant factors, then quantized
+// per token (QUANT) or written in the activation type.  One workgroup per
+// row; the quantizing form reads the row twice (abs-max, then codes), the
+// second time from L2.
+template <int DT, bool QUANT>
+__global__ __launch_bounds__(kThreads) void permute_rows_kernel(
+    const void* __restrict__ y, int64_t ldy, int K_y, int K_w, const int32_t* __restrict__ perm,
+    const float* __restrict__ sm_rcp, const float* __restrict__ sm_f, int8_t* __restrict__ q_out, int64_t ldq,
+    float* __restrict__ s_out, void* __restrict__ out, int64_t ldo) {
+  constexpr int ESZ = DT == IC_DTYPE_F32 ? 4 : 2;
+  __shared__ float red[kThreads / 64];
+  const int t = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const char* yrow = (const char*)y + row * ldy * ESZ;
+  auto value = [&](int o) {
+    int src = o;
+    if (perm != nullptr) src = (unsigned)perm[o] < (unsigned)K_w ? perm[o] : 0;  // malformed -> position 0
+    float v = src < K_y ? ld_as_f32<DT>(yrow, src) : 0.0f;
+    if (sm_rcp != nullptr) v = div_round_dt<DT>(v, sm_rcp[o], sm_f, o);
+    return v;
+  };
+  if constexpr (!QUANT) {
+    for (int o = t; o < K_w; o += kThreads) st_from_f32<DT>((char*)out + row * ldo * ESZ, o, value(o));
+  } else {
+    float m = 0.0f;
+    for (int o = t; o < K_w; o += kThreads) m = __builtin_fmaxf(m, __builtin_fabsf(value(o)));
+    m = wave_max(m);
+    if ((t & 63) == 0) red[t >> 6] = m;
+    __syncthreads();
+    m = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+    const float s = quant_scale(m);
+    const double rs = 1.0 / (double)s;
+    if (t == 0) s_out[row] = s;
+    for (int o = t; o < K_w; o += kThreads) q_out[row * ldq + o] = (int8_t)quant_code(value(o), rs);
+  }
+}
+
+template <int DT>
+hipError_t launch_permute_rows(const void* y, int64_t ldy, int64_t M, int64_t K_y, int64_t K_w, const int32_t* perm,
+                               const float* sm_rcp, const float* sm_f, int8_t* q_out, int64_t ldq, float* s_out,
+                               void* out, int64_t ldo, hipStream_t st) {
+  const dim3 grid((unsigned)M), block(kThreads);
+  if (q_out != nullptr)
+    permute_rows_kernel<DT, true><<<grid, block, 0, st>>>(y, ldy, (int)K_y, (int)K_w, perm, sm_rcp, sm_f, q_out, ldq,
+                                                          s_out, nullptr, 0);
+  else
+    permute_rows_kernel<DT, false><<<grid, block, 0, st>>>(y, ldy, (int)K_y, (int)K_w, perm, sm_rcp, sm_f, nullptr,
+                                                           0, nullptr, out, ldo);
+  return hipGetLastError();
+}
+
 // SmoothRot / SmoothQuant factor preparation: fdt[k] = RN_dt(f[k]) as f32 and
 // rcp[k] = RN32(1 / fdt[k]) (IEEE divide).
 template <int DT>
@@ -428,6 +482,40 @@ int ic_prepare_activation(const void* x, int dtype, int64_t M, int64_t K_in, int
 }
 
 int64_t ic_max_fused_row(void) { return (int64_t)kTile * kMaxTiles; }
+
+int ic_permute_quantize(const void* y, int dtype, int64_t M, int64_t K_y, int64_t ldy, int64_t K_w,
+                        const int32_t* perm, const float* sm_rcp, const float* sm_f, int8_t* q_out, int64_t ldq,
+                        float* s_out, void* out, int64_t ldo, void* stream) {
+  const char* who = "ic_permute_quantize";
+  if (dtype != IC_DTYPE_F16 && dtype != IC_DTYPE_BF16 && dtype != IC_DTYPE_F32)
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: dtype must be f16/bf16/f32", who);
+  if (M < 0 || K_y <= 0 || K_w < K_y || ldy < K_y || K_w > 0x7fffffffLL || M > 0x7fffffffLL)
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: bad shape M=%lld K_y=%lld K_w=%lld ldy=%lld", who, (long long)M,
+                        (long long)K_y, (long long)K_w, (long long)ldy);
+  if ((sm_rcp == nullptr) != (sm_f == nullptr))
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: factor arrays come in (rcp, f) pairs", who);
+  const bool quant = q_out != nullptr || s_out != nullptr;
+  if (quant == (out != nullptr))
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: give either q_out and s_out or out", who);
+  if (M == 0) return IC_OK;
+  if (!y || (quant && (!q_out || !s_out || ldq < K_w)) || (!quant && ldo < K_w))
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: bad pointers or output stride", who);
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e;
+  switch (dtype) {
+    case IC_DTYPE_F16:
+      e = launch_permute_rows<IC_DTYPE_F16>(y, ldy, M, K_y, K_w, perm, sm_rcp, sm_f, q_out, ldq, s_out, out, ldo, st);
+      break;
+    case IC_DTYPE_BF16:
+      e = launch_permute_rows<IC_DTYPE_BF16>(y, ldy, M, K_y, K_w, perm, sm_rcp, sm_f, q_out, ldq, s_out, out, ldo, st);
+      break;
+    default:
+      e = launch_permute_rows<IC_DTYPE_F32>(y, ldy, M, K_y, K_w, perm, sm_rcp, sm_f, q_out, ldq, s_out, out, ldo, st);
+      break;
+  }
+  if (e != hipSuccess) return ic_set_error(IC_ERR_LAUNCH, "%s: %s", who, hipGetErrorString(e));
+  return IC_OK;
+}
 
 int ic_dynamic_quantize(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, int8_t* q_out,
                         int64_t ldq, float* s_out, void* stream) {

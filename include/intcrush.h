@@ -69,6 +69,22 @@ int ic_prepare_activation(const void* x, int dtype, int64_t M, int64_t K_in, int
                           const int32_t* perm, const float* sm_rcp, const float* sm_f,
                           void* y_out, int64_t ldy, void* stream);
 
+/*
+ * Second pass of the preparation for rows wider than ic_max_fused_row() (or
+ * half of it for f32): the caller first runs ic_prepare_activation without
+ * perm / old-SmoothQuant factors over column chunks of the row that are whole
+ * Hadamard blocks (the rotation is block-diagonal), into y [M, K_y] (K_y the
+ * rotated width); this pass pads with zeros to K_w, gathers by perm, divides
+ * by the old-SmoothQuant factors, and either quantizes per token (q_out
+ * [M, K_w] int8, s_out [M] f32) or writes out [M, K_w] in dtype (pass q_out =
+ * s_out = NULL).  Together they replace _prep_activation (_ops.py:337-365),
+ * the old SmoothQuant divide (_ops.py:529-533) and dynamic_quantize_activation
+ * (kernels/triton_quantize.py:151-198) for any row width.
+ */
+int ic_permute_quantize(const void* y, int dtype, int64_t M, int64_t K_y, int64_t ldy, int64_t K_w,
+                        const int32_t* perm, const float* sm_rcp, const float* sm_f, int8_t* q_out, int64_t ldq,
+                        float* s_out, void* out, int64_t ldo, void* stream);
+
 /* Per-token dynamic INT8 quantization of any width.
  * Replaces dynamic_quantize_activation, kernels/triton_quantize.py:151-198. */
 int ic_dynamic_quantize(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, int8_t* q_out,
@@ -133,6 +149,11 @@ int ic_gemm_w8a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8
  *   num_groups == 1: out = f32(acc) * (s_a[m] * s_w[n]) + bias[n]
  *   num_groups  > 1: out = (sum_g f32(acc_g) * s_w[n,g]) * s_a[m] + bias[n],
  *                    the sum an fma chain in g order, groups of K/num_groups.
+ *                    Group sizes that are multiples of 128 fold once per 128
+ *                    columns (acc_g of each 128-column part with its group's
+ *                    scale) on the MFMA kernels; other group sizes, K not a
+ *                    multiple of 128 and unaligned operands run a scalar
+ *                    kernel (one thread per output, about 100x slower).
  */
 int ic_gemm_w4a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed,
                  int64_t N, int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a,

@@ -601,3 +601,88 @@ def test_w8a8_linear_vs_fp32_fallback(rt, oracle, dev):
     out = rt.fused_int8_gemm_dequant(q, w.to(dev), s_w.to(dev), s, out_dtype=torch.float16).float().cpu()
     ref = torch.from_numpy(oracle.linear_fallback_fp32(x.float().numpy(), w.numpy(), s_w.numpy(), K, False))
     assert _cos(out, ref) >= 0.9999
+
+
+# ------------------------------------------------------------------ rows wider than one workgroup
+@pytest.mark.parametrize("dtype,K_in,R,w_in", [
+    (torch.bfloat16, 20480, 256, None),
+    (torch.float16, 24576, 1024, 25600),      # rotation and w_in pads on top of the chunking
+    (torch.bfloat16, 17000, 64, None),        # pad 17000 -> 17024 inside the last chunk
+])
+def test_wide_rows_prep_bit_exact(rt, oracle, dev, dtype, K_in, R, w_in):
+    """Rows wider than the single-pass kernels hold (16384 16-bit values): the
+    rotation runs on column chunks of whole Hadamard blocks, then the pad,
+    perm gather and quantization in a second pass -- the same values, codes
+    and scales as the oracle's one-shot prep."""
+    M = 5
+    K_w, sr, perm, _ = _prep_inputs(K_in, R, w_in, True, True, False, seed=K_in)
+    x = _acts(M, K_in, dtype, seed=K_in + 1, outliers=0.01)
+    srp = rt.prepare_factors(sr.to(dev), dtype)
+    pp = rt.prepare_perm(perm.to(dev), K_w)
+    q, s = rt.rotate_quantize(x.to(dev), rot_size=R, w_in=K_w, smoothrot=srp, perm=pp)
+    y = rt.prepare_activation(x.to(dev), rot_size=R, w_in=K_w, smoothrot=srp, perm=pp)
+    y_ref = oracle.prepare(x, DT[dtype], smoothrot=sr, rot_size=R, w_in=K_w, perm=perm)
+    q_ref, s_ref = oracle.quantize(y_ref)
+    assert np.array_equal(y.float().cpu().numpy(), y_ref)
+    assert np.array_equal(s.cpu().numpy(), s_ref)
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+
+
+def test_wide_rows_prep_f32_and_old_smooth(rt, oracle, dev):
+    """f32 rows wider than 8192 (the f32 single-pass limit) with the
+    old-SmoothQuant divide after the gather: values within the documented
+    f32 bound (blocks whose double sums are inexact: +-1 code)."""
+    M, K = 4, 12288
+    K_w, _, perm, sm = _prep_inputs(K, 256, None, False, True, True, seed=5)
+    x = _acts(M, K, torch.float32, seed=6)
+    smp = rt.prepare_factors(sm.to(dev), torch.float32)
+    q, s = rt.rotate_quantize(x.to(dev), rot_size=256, w_in=K_w, perm=rt.prepare_perm(perm.to(dev), K_w), smooth=smp)
+    q_ref, s_ref = oracle.rotate_quantize(x, 2, rot_size=256, w_in=K_w, perm=perm, smooth=sm)
+    assert np.allclose(s.cpu().numpy(), s_ref, rtol=1e-6)
+    assert np.abs(q.cpu().numpy().astype(int) - q_ref.astype(int)).max() <= 1
+
+
+# ------------------------------------------------------------------ group sizes other than 128
+@pytest.mark.parametrize("gs", [256, 512, 64])
+@pytest.mark.parametrize("M,N,K", [(300, 384, 2048), (64, 3072, 4096), (4608, 3072, 1024)])
+def test_w4a8_group_sizes(rt, oracle, dev, gs, M, N, K):
+    """Group sizes 256 / 512 run the MFMA kernels (tiled and split-K), folding
+    each 128-column part with its group's scale: bit-exact against the
+    oracle's epilogue over 128-column accumulators with the scales repeated.
+    Group size 64 runs the scalar kernel: bit-exact against the 64-group fold."""
+    G = K // gs
+    a = _int8((M, K), 81, -127, 128)
+    w = torch.randint(0, 256, (N, K // 2), generator=_gen(82), dtype=torch.uint8)
+    s_a = torch.rand(M, generator=_gen(83)) * 0.05 + 1e-3
+    s_w = (torch.rand(N, G, generator=_gen(84)) * 2e-2 + 1e-3).to(torch.float16).float()
+    bias = torch.randn(N, generator=_gen(85)).to(torch.bfloat16)
+    out = rt.gemm_w4a8(a.to(dev), w.to(dev), s_w.to(dev), s_a.to(dev), bias=bias.to(dev), out_dtype=torch.bfloat16)
+    out = out.float().cpu()
+    wq = oracle.unpack_int4(w.numpy(), K)
+    rows = torch.tensor(sorted({0, 1, M // 2, M - 1}))
+    if gs >= 128:
+        acc = oracle.gemm_acc(a[rows].numpy(), wq, K // 128)
+        sw = np.repeat(s_w.numpy(), gs // 128, axis=1)
+    else:
+        acc = oracle.gemm_acc(a[rows].numpy(), wq, G)
+        sw = s_w.numpy()
+    ref = torch.from_numpy(oracle.epilogue(acc, s_a[rows].numpy(), sw, bias.float().numpy(), 1))
+    split = rt.lib().ic_gemm_splitk_bytes(M, N, K, G, 1) > 0
+    if not split:
+        assert torch.equal(out[rows], ref)
+    else:  # slices of the fold added in slice order (bounded in test_splitk_grouped_w4a8)
+        assert _cos(out[rows], ref) >= 0.99999
+        assert torch.allclose(out[rows], ref, rtol=1e-2, atol=1e-2 * ref.abs().max().item())
+
+
+@pytest.mark.parametrize("G", [48, 12])  # group sizes 64 and 256 at K = 3072
+def test_w4a16_group_sizes(rt, oracle, dev, G):
+    M, N, K = 200, 256, 3072
+    x = _acts(M, K, torch.bfloat16, seed=86)
+    packed = torch.randint(0, 256, (N, K // 2), generator=_gen(87), dtype=torch.uint8)
+    s_w = (torch.rand(N, G, generator=_gen(88)) * 2e-2 + 1e-3).to(torch.float16).float()
+    out = rt.gemm_w4a16(x.to(dev), packed.to(dev), s_w.to(dev)).float().cpu()
+    w = torch.from_numpy(oracle.dequant_w4a16(packed.numpy(), s_w.numpy(), K, 1))
+    ref = x.float() @ w.t()
+    assert torch.allclose(out, ref, rtol=2e-2, atol=2e-2 * ref.abs().max().item() * 1e-2)
+    assert _cos(out, ref) >= 0.9999

@@ -305,3 +305,26 @@ def test_int8_layer_use_fused_w8a8(oracle, dev, monkeypatch, zp):
     exact = ref.astype(np.float64) - corr
     assert _cos(out, torch.from_numpy(exact)) >= 0.9999
     assert np.allclose(out.numpy(), exact, rtol=2e-2, atol=2e-2 * np.abs(exact).max() * 1e-2)
+
+
+@pytest.mark.parametrize("dtype,K", [(torch.bfloat16, 20480), (torch.float32, 12288)])
+def test_w4a8_layer_wider_than_one_workgroup(oracle, dev, dtype, K):
+    """Rotated INT4 layers whose rows are wider than the single-pass prep
+    holds (20480 bf16 values, 12288 f32 values) through the ops Linear:
+    the chunked rotation + second pass, then the W4A8 GEMM.  bf16: bit-exact
+    against the oracle chain; f32: within the fp32 fallback's tolerance."""
+    M, N, R = 24, 256, 256
+    ops = ops_mod.make_intcrush_ops("int4_crush", R)
+    sd = int4_layer(N, K, seed=90)
+    lin = _to_dev(load_linear(ops, "single_blocks.0.linear2", sd, K, N), dev)
+    x = _x(M, K, dtype, 91)
+    out = lin(x.to(dev)).float().cpu()
+    y = oracle.prepare(x, DT[dtype], smoothrot=sd["weight_smoothrot_factors"], rot_size=R, w_in=K,
+                       perm=sd["weight_perm"])
+    q, s = oracle.quantize(y)
+    ref = oracle.epilogue(oracle.gemm_acc(q, oracle.unpack_int4(sd["weight"].numpy(), K), K // 128), s,
+                          sd["weight_scale"].float().numpy(), sd["bias"].float().numpy(), DT[dtype])
+    if dtype == torch.bfloat16:
+        assert np.array_equal(out.numpy(), ref)
+    else:
+        assert _cos(out, torch.from_numpy(ref)) >= 0.9999
