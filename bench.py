@@ -303,6 +303,19 @@ def flux_step_bench(args, rt):
     per_kind = {name: round(_time_graph(fn, reps)[0], 4) for name, fn in kinds.items()}
     r = dict(step_ms=step_ms, part_ms=part_ms, per_kind=per_kind, replay_equal=replay_equal, finite=finite)
     r.update(model.op_counts())
+    # the same step through the drop-in ops layer (IntCrushOps.Linear per linear)
+    del parts, kinds
+    dropin = bench_flux.DropInFluxStep(rt, torch.device("cuda:0"))
+    for _ in range(max(1, args.warmup)):
+        dropin.forward()
+    torch.cuda.synchronize()
+    d_eager = dropin.forward().clone()
+    torch.cuda.synchronize()
+    d_ms, d_out = _time_graph(dropin.forward, reps)
+    torch.cuda.synchronize()
+    a, b = d_out.double().reshape(-1), eager.double().reshape(-1)
+    r.update(dropin_step_ms=d_ms, dropin_replay_equal=bool(torch.equal(d_out, d_eager)),
+             dropin_cos_vs_fused=float((a @ b) / (a.norm() * b.norm())))
     return r
 
 
@@ -366,6 +379,13 @@ def flux_step_main(args, rt):
                           "other_torch_ops = step minus the timed parts (norms, modulation, RoPE, GELU, "
                           "residuals, embedders, final layer, concatenations)",
         "graph_replay_equals_eager": r["replay_equal"], "output_finite": r["finite"],
+        "dropin_step": {"ms": round(r["dropin_step_ms"], 4),
+                        "graph_replay_equals_eager": r["dropin_replay_equal"],
+                        "output_cosine_vs_fused_step": round(r["dropin_cos_vs_fused"], 7),
+                        "note": "the same model with every quantized linear an IntCrushOps.Linear "
+                                "(make_intcrush_ops('int4_crush', 256), ComfyUI stand-in from tests/fake_comfy): "
+                                "per linear prep + W4A8 GEMM, adaLN / GELU-tanh / residuals as torch ops, "
+                                "whole step in one hipGraph"},
     }
     peaks = measure_peaks()
     line["peak_measured"] = peaks

@@ -386,3 +386,105 @@ class FluxStep:
         wbytes = sum(l.w.numel() + 4 * l.s_w.numel() for _, l in self.quantized_linears())
         return dict(lin_ops=lin_ops, mod_ops=mod_ops, attn_flops=attn_flops, weight_bytes=wbytes,
                     n_layers=len(self.quantized_linears()), n_mods=len(self.modulation_linears()))
+
+
+# ── the same step through the drop-in ops layer ─────────────────────────────
+def _ensure_comfy():
+    """ComfyUI is not installed in this image: put the minimal stand-in of
+    the modules the ops layer imports (tests/fake_comfy) on the path."""
+    import importlib.util
+    import os
+    import sys
+
+    if importlib.util.find_spec("comfy") is None:
+        sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests", "fake_comfy"))
+
+
+class DropInFluxStep(FluxStep):
+    """FluxStep with every quantized linear an IntCrushOps.Linear from
+    make_intcrush_ops("int4_crush", 256), loaded through
+    _load_from_state_dict with the same packed weights, fp16 group scales,
+    SmoothRot factors, PermuQuant indices and biases: the path a ComfyUI user
+    of the drop-in gets (reference _ops.py:817-862).  Each linear runs its own
+    prep + GEMM; the adaptive LayerNorm, GELU-tanh and residual sums are torch
+    ops between them, as in a DiT's own forward, so none of the hand fusions
+    of FluxStep apply.  Names follow ComfyUI's Flux so the rotation rule
+    (_ops.py:30-32) sends img_mod / txt_mod to rotated W4A8 GEMVs and the
+    single block's modulation to W4A16.  The W4A16 bias is kept
+    (INTCRUSH_W4A16_BIAS=1) so the two steps compute the same function."""
+
+    def __init__(self, rt, dev, seed=0, n_double=N_DOUBLE, n_single=N_SINGLE):
+        import os
+
+        super().__init__(rt, dev, seed, n_double, n_single)
+        _ensure_comfy()
+        import __graft_entry__
+
+        # registers the INT-Crush layouts with comfy.quant_ops (a no-op if the
+        # package was imported after comfy and already did)
+        __graft_entry__._submodule("quant_layout").register_intcrush_layouts()
+        os.environ["INTCRUSH_W4A16_BIAS"] = "1"
+        ops = __graft_entry__._submodule("_ops").make_intcrush_ops("int4_crush", ROT_SIZE)
+        self.lin = {}
+        for i, blk in enumerate(self.double):
+            for s in ("img", "txt"):
+                self._wrap(ops, blk[f"{s}_mod"], f"double_blocks.{i}.{s}_mod.lin")
+                for name, path in (("qkv", "attn.qkv"), ("proj", "attn.proj"), ("mlp_up", "mlp.0"),
+                                   ("mlp_down", "mlp.2")):
+                    self._wrap(ops, blk[f"{s}_{name}"], f"double_blocks.{i}.{s}_{path}")
+        for i, blk in enumerate(self.single):
+            self._wrap(ops, blk["mod"], f"single_blocks.{i}.modulation.lin")
+            for name in ("qkv", "proj", "mlp_up", "mlp_down"):
+                self._wrap(ops, blk[name], f"single_blocks.{i}.{name}")
+
+    def _wrap(self, ops, layer, prefix):
+        import torch
+
+        sd = {"weight": layer.w, "weight_scale": layer.s_w.to(torch.float16), "bias": layer.b}
+        if layer.rotated:
+            sd["weight_smoothrot_factors"] = layer.sr.fdt
+            sd["weight_perm"] = layer.perm.long()
+        lin = ops.Linear(layer.K, layer.N, bias=True, device=layer.w.device, dtype=torch.bfloat16)
+        full = {f"{prefix}.{k}": v for k, v in sd.items()}
+        missing, unexpected, errors = [], [], []
+        lin._load_from_state_dict(full, prefix + ".", {}, True, missing, unexpected, errors)
+        if errors:
+            raise RuntimeError(f"loading {prefix}: {errors}")
+        if lin._intcrush_rot_need != layer.rotated:
+            raise RuntimeError(f"{prefix}: rotation rule gave {lin._intcrush_rot_need}")
+        self.lin[id(layer)] = lin
+
+    def _call(self, layer, x):
+        return self.lin[id(layer)](x)
+
+    def _mod_w4a8(self, layer, vec_silu):
+        return self._call(layer, vec_silu).chunk(6, dim=-1)
+
+    def _double_block(self, blk, img, txt, vec_silu, freqs):
+        import torch
+        import torch.nn.functional as F
+
+        im = self._mod_w4a8(blk["img_mod"], vec_silu)
+        tm = self._mod_w4a8(blk["txt_mod"], vec_silu)
+        iq, ik, iv = self._split_heads(self._call(blk["img_qkv"], self._modulate(img, im[0], im[1])), blk["qk_scale"])
+        tq, tk, tv = self._split_heads(self._call(blk["txt_qkv"], self._modulate(txt, tm[0], tm[1])), blk["qk_scale"])
+        attn = self.attention(torch.cat((tq, iq), 1), torch.cat((tk, ik), 1), torch.cat((tv, iv), 1), freqs)
+        t_a, i_a = attn[:TXT_TOKENS], attn[TXT_TOKENS:]
+        img = torch.addcmul(img, im[2], self._call(blk["img_proj"], i_a))
+        h = F.gelu(self._call(blk["img_mlp_up"], self._modulate(img, im[3], im[4])), approximate="tanh")
+        img = torch.addcmul(img, im[5], self._call(blk["img_mlp_down"], h))
+        txt = torch.addcmul(txt, tm[2], self._call(blk["txt_proj"], t_a))
+        h = F.gelu(self._call(blk["txt_mlp_up"], self._modulate(txt, tm[3], tm[4])), approximate="tanh")
+        txt = torch.addcmul(txt, tm[5], self._call(blk["txt_mlp_down"], h))
+        return img, txt
+
+    def _single_block(self, blk, x, vec_silu, freqs):
+        import torch
+        import torch.nn.functional as F
+
+        shift, scale, gate = self._call(blk["mod"], vec_silu).chunk(6, dim=-1)[:3]
+        xm = self._modulate(x, shift, scale)
+        q, k, v = self._split_heads(self._call(blk["qkv"], xm), blk["qk_scale"])
+        h = F.gelu(self._call(blk["mlp_up"], xm), approximate="tanh")
+        out = self._call(blk["proj"], self.attention(q, k, v, freqs)) + self._call(blk["mlp_down"], h)
+        return torch.addcmul(x, gate, out)

@@ -238,3 +238,30 @@ def test_flux_step_graph_replay_equals_eager(flux):
             flux.forward()  # eager work between replays
             torch.cuda.synchronize()
         assert torch.isfinite(eager).all()
+
+
+def test_dropin_ops_step_matches_fused_step(rt, flux):
+    """The C4 step through the drop-in ops layer (IntCrushOps.Linear for every
+    quantized linear, torch adaLN / GELU / residuals between them) computes
+    the same function as the fused step: each block's output within cosine
+    0.9999 (the fused prep rounds the normalised activations once, the
+    unfused path twice; the fused GELU is evaluated in f32, torch's in bf16),
+    and its hipGraph replays equal its eager output."""
+    dropin = bf.DropInFluxStep(rt, flux.dev, seed=0, n_double=1, n_single=1)
+    with torch.no_grad():
+        got, ref = [], []
+        out = dropin.forward(collect=got)
+        ref_out = flux.forward(collect=ref)
+        torch.cuda.synchronize()
+        for name, a, b in (("double img", got[0][0], ref[0][0]), ("double txt", got[0][1], ref[0][1]),
+                           ("single", got[1], ref[1]), ("final", out, ref_out)):
+            assert torch.isfinite(a).all(), name
+            assert _cos(a, b) >= 0.9999, f"{name}: cosine {_cos(a, b):.6f}"
+        eager = dropin.forward().clone()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            o = dropin.forward()
+        for _ in range(2):
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(o, eager)
