@@ -38,6 +38,19 @@ METRIC = "W4A8 linear TOPS & % INT8-MFMA peak at Flux shapes; denoise step ms"
 PEAK_INT8_TOPS = 5000.0       # MI355X dense INT8 MFMA, published
 PEAK_FP16_TFLOPS = 2500.0     # MI355X dense FP16/BF16 MFMA, published
 PEAK_HBM_GBPS = 8000.0        # MI355X HBM3E, published
+PEAK_SCLK_MHZ = 2400.0        # MI355X peak engine clock the published MFMA peaks assume
+
+
+def cpu_model():
+    """The host CPU's model name, from /proc/cpuinfo (None where absent)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 CONFIGS = {
     "c1": dict(name="C1 W8A8 linear 3072->3072, M=4096, rot 0", fmt="int8", M=4096, K=3072, N=3072,
@@ -237,7 +250,7 @@ def cpu_baseline(cfg, inp):
     t = statistics.median(ts)
     shape = "full shape" if rows == M else f"first {rows} of {M} tokens (throughput of the slice)"
     return {"value": round(2.0 * rows * N * K / t / 1e12, 5), "unit": "TOPS", "cores": cores,
-            "kind": "port", "seconds_per_call": round(t, 5),
+            "cpu": cpu_model(), "kind": "port", "seconds_per_call": round(t, 5),
             "sample": f"{rows}x{cfg.get('K_in', K)} -> {N}, {shape}, fp32 dequant + prep + F.linear per call "
                       f"(the reference fallback re-dequantizes every forward), median of 3 after 1 warm-up"}
 
@@ -392,7 +405,8 @@ def flux_step_main(args, rt):
     line["roofline"]["frac_of_measured_peak"] = round(gemm_tops / peaks["int8_tops"], 4)
     if not args.no_cpu:
         tops, cores = flux_step_cpu_baseline()
-        line["cpu_baseline"] = {"value": round(tops / 1e12, 5), "unit": "TOPS", "cores": cores, "kind": "port",
+        line["cpu_baseline"] = {"value": round(tops / 1e12, 5), "unit": "TOPS", "cores": cores, "cpu": cpu_model(),
+                                "kind": "port",
                                 "extrapolated_linears_s": round(total_ops / tops, 2),
                                 "sample": "one layer of each Flux linear shape (qkv, proj, mlp_up, mlp_down) at "
                                           "512 tokens, fp32 dequant + prep + F.linear per call, median of 3; "
@@ -418,25 +432,31 @@ def measure_peaks():
     lib.bp_grid.restype = ctypes.c_int
     lib.bp_ops_per_launch.restype = ctypes.c_double
     lib.bp_ops_per_launch.argtypes = [ctypes.c_int, ctypes.c_int]
-    for f in (lib.bp_mfma_i8, lib.bp_mfma_f16):
-        f.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
-        f.restype = ctypes.c_int
+    lib.bp_mfma_i8.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    lib.bp_mfma_f16.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.bp_mfma_i8.restype = lib.bp_mfma_f16.restype = lib.bp_wall_clock_khz.restype = ctypes.c_int
     out = torch.empty(lib.bp_grid() * 256, dtype=torch.int32, device="cuda:0")
+    clk = torch.zeros(4, dtype=torch.int64, device="cuda:0")
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     iters = 4000
+    launch = {0: lambda c=None: lib.bp_mfma_i8(iters, ctypes.c_void_p(out.data_ptr()), c, stream),
+              1: lambda c=None: lib.bp_mfma_f16(iters, ctypes.c_void_p(out.data_ptr()), stream)}
     rates = {}
-    for kind, fn in ((0, lib.bp_mfma_i8), (1, lib.bp_mfma_f16)):
+    for kind in (0, 1):
         for _ in range(2):  # warm-up: clocks settle under load
-            if fn(iters, ctypes.c_void_p(out.data_ptr()), stream) != 0:
+            if launch[kind]() != 0:
                 raise RuntimeError("peak probe launch failed")
         s = torch.cuda.Event(enable_timing=True)
         e = torch.cuda.Event(enable_timing=True)
         s.record()
-        for _ in range(5):
-            fn(iters, ctypes.c_void_p(out.data_ptr()), stream)
+        for i in range(5):
+            launch[kind](ctypes.c_void_p(clk.data_ptr()) if kind == 0 and i == 4 else None)
         e.record()
         e.synchronize()
         rates[kind] = 5 * lib.bp_ops_per_launch(kind, iters) / (s.elapsed_time(e) * 1e-3) / 1e12
+    c0, c1, w0, w1 = clk.tolist()
+    wall_khz = lib.bp_wall_clock_khz()
+    sclk_mhz = (c1 - c0) / (w1 - w0) * wall_khz / 1e3 if w1 > w0 and wall_khz > 0 else None
     a = torch.empty(1 << 30, dtype=torch.uint8, device="cuda:0")
     b = torch.empty_like(a)
     b.copy_(a)
@@ -451,8 +471,12 @@ def measure_peaks():
     hbm = 5 * 2 * a.numel() / (s.elapsed_time(e) * 1e-3) / 1e9
     del a, b
     return {"int8_tops": round(rates[0], 1), "fp16_tflops": round(rates[1], 1), "hbm_copy_gbps": round(hbm, 1),
+            "sclk_mhz": round(sclk_mhz) if sclk_mhz else None,
+            "int8_peak_at_sclk_tops": round(PEAK_INT8_TOPS * sclk_mhz / PEAK_SCLK_MHZ, 1) if sclk_mhz else None,
             "method": "register-only MFMA loops (v_mfma_i32_32x32x32_i8, v_mfma_f32_32x32x16_f16), "
                       "2 workgroups of 4 waves per CU, 4 independent accumulator chains per wave; "
+                      "sclk: shader-clock ticks over wall-clock ticks across one wave's INT8 loop; "
+                      f"int8_peak_at_sclk: the published peak scaled by sclk / {PEAK_SCLK_MHZ} MHz; "
                       "HBM: 1 GiB device copy, read + write bytes"}
 
 
@@ -542,7 +566,7 @@ def set_main(args, rt):
     line["roofline"]["frac_of_measured_peak"] = round(achieved / line["peak_measured"]["int8_tops"], 4)
     if not args.no_cpu:
         line["cpu_baseline"] = {"value": round(cpu_ops / cpu_s / 1e12, 5), "unit": "TOPS", "cores": cores,
-                                "kind": "port", "seconds": round(cpu_s, 3),
+                                "cpu": cpu_model(), "kind": "port", "seconds": round(cpu_s, 3),
                                 "sample": "each member's first 2048 of 32760 tokens, fp32 dequant + prep + "
                                           "F.linear per call, median of 3 after 1 warm-up, summed"}
     print(json.dumps(line), flush=True)

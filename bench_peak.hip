@@ -11,6 +11,12 @@
 // at the end so the loop cannot be removed.  The grid is bp_grid() = two
 // 256-thread workgroups per CU (two waves per SIMD); `out` must hold
 // bp_grid() * 256 ints.  The launchers return the hipError_t of the launch.
+//
+// bp_mfma_i8 also samples the shader clock: when `clk` is not null, the first
+// lane of workgroup 0 stores the shader-clock counter (clock64) and the
+// constant-rate wall clock (wall_clock64, bp_wall_clock_khz() ticks per ms)
+// before and after its loop into clk[0..3], so the host can compute the
+// engine clock the MFMA loop actually ran at.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -24,8 +30,15 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
-__global__ __launch_bounds__(kThreads) void mfma_i8_loop(int iters, int* __restrict__ out) {
+__global__ __launch_bounds__(kThreads) void mfma_i8_loop(int iters, int* __restrict__ out,
+                                                         long long* __restrict__ clk) {
   const int lane = threadIdx.x & 63;
+  const bool sample = clk != nullptr && blockIdx.x == 0 && threadIdx.x == 0;
+  long long c0 = 0, w0 = 0;
+  if (sample) {
+    c0 = clock64();
+    w0 = wall_clock64();
+  }
   v4i a = {lane, lane + 1, lane + 2, lane + 3};
   v4i b = {lane ^ 5, lane ^ 7, lane ^ 9, lane ^ 11};
   v16i acc[kChains];
@@ -36,6 +49,16 @@ __global__ __launch_bounds__(kThreads) void mfma_i8_loop(int iters, int* __restr
     for (int c = 0; c < kChains; ++c) acc[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc[c], 0, 0, 0);
   }
   int s = 0;
+#pragma unroll
+  for (int c = 0; c < kChains; ++c) s += acc[c][0];
+  if (sample) {  // after a use of every chain, so the loop is inside the window
+    const long long c1 = clock64(), w1 = wall_clock64();
+    clk[0] = c0;
+    clk[1] = c1;
+    clk[2] = w0;
+    clk[3] = w1;
+  }
+  s = 0;
 #pragma unroll
   for (int c = 0; c < kChains; ++c)
 #pragma unroll
@@ -85,10 +108,19 @@ double bp_ops_per_launch(int kind, int iters) {
   return (double)bp_grid() * (kThreads / 64) * iters * kChains * (kind == 0 ? 65536.0 : 32768.0);
 }
 
-int bp_mfma_i8(int iters, int* out, void* stream) {
+// Ticks per millisecond of the wall clock that wall_clock64() reads.
+int bp_wall_clock_khz(void) {
+  int dev = 0, khz = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess)
+    return 0;
+  return khz;
+}
+
+int bp_mfma_i8(int iters, int* out, long long* clk, void* stream) {
   const int grid = bp_grid();
   if (grid <= 0 || iters <= 0 || out == nullptr) return (int)hipErrorInvalidValue;
-  mfma_i8_loop<<<dim3(grid), dim3(kThreads), 0, (hipStream_t)stream>>>(iters, out);
+  mfma_i8_loop<<<dim3(grid), dim3(kThreads), 0, (hipStream_t)stream>>>(iters, out, clk);
   return (int)hipGetLastError();
 }
 
