@@ -411,11 +411,10 @@ class DropInFluxStep(FluxStep):
     of FluxStep apply.  Names follow ComfyUI's Flux so the rotation rule
     (_ops.py:30-32) sends img_mod / txt_mod to rotated W4A8 GEMVs and the
     single block's modulation to W4A16.  The W4A16 bias is kept
-    (INTCRUSH_W4A16_BIAS=1) so the two steps compute the same function."""
+    (INTCRUSH_W4A16_BIAS=1, set only while forward runs) so the two steps
+    compute the same function."""
 
     def __init__(self, rt, dev, seed=0, n_double=N_DOUBLE, n_single=N_SINGLE):
-        import os
-
         super().__init__(rt, dev, seed, n_double, n_single)
         _ensure_comfy()
         import __graft_entry__
@@ -423,7 +422,6 @@ class DropInFluxStep(FluxStep):
         # registers the INT-Crush layouts with comfy.quant_ops (a no-op if the
         # package was imported after comfy and already did)
         __graft_entry__._submodule("quant_layout").register_intcrush_layouts()
-        os.environ["INTCRUSH_W4A16_BIAS"] = "1"
         ops = __graft_entry__._submodule("_ops").make_intcrush_ops("int4_crush", ROT_SIZE)
         self.lin = {}
         for i, blk in enumerate(self.double):
@@ -436,6 +434,19 @@ class DropInFluxStep(FluxStep):
             self._wrap(ops, blk["mod"], f"single_blocks.{i}.modulation.lin")
             for name in ("qkv", "proj", "mlp_up", "mlp_down"):
                 self._wrap(ops, blk[name], f"single_blocks.{i}.{name}")
+
+    def forward(self, *args, **kwargs):
+        import os
+
+        prev = os.environ.get("INTCRUSH_W4A16_BIAS")
+        os.environ["INTCRUSH_W4A16_BIAS"] = "1"
+        try:
+            return super().forward(*args, **kwargs)
+        finally:
+            if prev is None:
+                del os.environ["INTCRUSH_W4A16_BIAS"]
+            else:
+                os.environ["INTCRUSH_W4A16_BIAS"] = prev
 
     def _wrap(self, ops, layer, prefix):
         import torch

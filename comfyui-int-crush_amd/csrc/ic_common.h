@@ -139,13 +139,22 @@ IC_DEV int quant_code(float v, double rs) {
   return c;
 }
 
-// Same code without the clamp, for values v with |v| <= m (the row abs-max the
-// scale was built from): then |RN32(v/s)| <= RN32(127 * (1 + 2^-24)) < 127.5,
-// so trunc(q +- 0.5) already lies in [-127, 127]; infinite or NaN quotients
-// only arise with m = inf or v = NaN, where v_cvt_i32_f32 returns 0 and the
-// clamped form returns 0 as well.
-IC_DEV int quant_code_nc(float v, double rs) {
-  const float q = (float)((double)v * rs);
+// The same code for 16-bit activations v with |v| <= m (the row abs-max the
+// scale was built from), without the clamp and in f32 arithmetic.  No clamp:
+// |RN32(v/s)| <= RN32(127 * (1 + 2^-24)) < 127.5, so trunc(q +- 0.5) already
+// lies in [-127, 127]; infinite or NaN quotients only arise with m = inf or
+// v = NaN, where v_cvt_i32_f32 returns 0 and the clamped form returns 0 too.
+// The quotient: with r = RN32(1/s), it is corrected once (Markstein):
+//   q0 = RN32(v r),  e = RN32(v - s q0) (exact),  q = RN32(q0 + e r)
+// and q = RN32(v/s) for every fp16 / bf16 value v with |v| <= m, m itself a
+// value of that type (the row abs-max after rounding): checked exhaustively
+// over all such pairs (v, m) of both types and both signs, every code equal
+// to the reference rule (tests/numerics_quant_check.c); a single rounding of
+// v r (+- 0.5) is not (thousands of pairs per type differ).  v = +-inf or NaN gives 0 as the fp64 form does.
+IC_DEV int quant_code_mk(float v, float s, float r) {
+  const float q0 = v * r;
+  const float e = __builtin_fmaf(-q0, s, v);
+  const float q = __builtin_fmaf(e, r, q0);
   return (int)(q + __builtin_copysignf(0.5f, q));
 }
 
@@ -161,6 +170,21 @@ IC_DEV float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, o, 64));
   return v;
+}
+
+// Maximum over the wave of a value that is >= +0 and never NaN (an abs-max
+// built with fmaxf), returned in every lane.  Such floats order as their bit
+// patterns, so the reduction runs on integers through DPP lane moves within
+// each row of 16 lanes, then the four row results are read as scalars.
+IC_DEV float wave_max_nonneg(float v) {
+  int x = __float_as_int(v);
+  x = max(x, __builtin_amdgcn_mov_dpp(x, 0xB1, 0xf, 0xf, false));   // quad_perm [1,0,3,2]
+  x = max(x, __builtin_amdgcn_mov_dpp(x, 0x4E, 0xf, 0xf, false));   // quad_perm [2,3,0,1]
+  x = max(x, __builtin_amdgcn_mov_dpp(x, 0x141, 0xf, 0xf, false));  // row_half_mirror
+  x = max(x, __builtin_amdgcn_mov_dpp(x, 0x140, 0xf, 0xf, false));  // row_mirror
+  const int r01 = max(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16));
+  const int r23 = max(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48));
+  return __int_as_float(max(r01, r23));
 }
 
 // ------------------------------------------------------------ GEMM epilogue options

@@ -34,13 +34,14 @@ template <int DT> IC_DEV void unpack8(v4u a, float* o) {
   }
 }
 
-// quantize 16 values (|v| <= row abs-max) and pack the codes little-endian
-IC_DEV v4u quant16(const float* v, double rs) {
+// quantize 16 values of the activation type (|v| <= row abs-max) with scale
+// s and r = RN32(1/s), and pack the codes little-endian
+IC_DEV v4u quant16(const float* v, float s, float r) {
   uint32_t w[4];
 #pragma unroll
   for (int d = 0; d < 4; ++d)
-    w[d] = pack4_lo_bytes(quant_code_nc(v[4 * d], rs), quant_code_nc(v[4 * d + 1], rs),
-                          quant_code_nc(v[4 * d + 2], rs), quant_code_nc(v[4 * d + 3], rs));
+    w[d] = pack4_lo_bytes(quant_code_mk(v[4 * d], s, r), quant_code_mk(v[4 * d + 1], s, r),
+                          quant_code_mk(v[4 * d + 2], s, r), quant_code_mk(v[4 * d + 3], s, r));
   return v4u{w[0], w[1], w[2], w[3]};
 }
 
@@ -48,10 +49,10 @@ IC_DEV v4u quant16(const float* v, double rs) {
 // rounding boundary of DT (a midpoint between neighbours, including the
 // overflow threshold) or lies below DT's normal range.  Boundary test on the
 // f32 bits: the bits below DT's precision are exactly 100...0.
-template <int DT> IC_DEV bool rn32_is_dt_boundary(float z) {
+template <int DT> IC_DEV uint32_t rn32_boundary_key(float z) {
   const uint32_t w = __float_as_uint(z);
-  if constexpr (DT == IC_DTYPE_F16) return (w & 0x1fffu) == 0x1000u;
-  else return (w & 0xffffu) == 0x8000u;
+  if constexpr (DT == IC_DTYPE_F16) return (w ^ 0x1000u) & 0x1fffu;  // zero iff (w & 0x1fff) == 0x1000
+  else return (w ^ 0x8000u) & 0xffffu;
 }
 
 // Three instantiation sets (VAR): kRqPlain (no SmoothRot factors, no perm),
@@ -172,14 +173,18 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
     }
   }
 
-  // Activation runs are loaded from a clamped, always valid address; runs past
-  // K_in are zeroed after the load (only in the last, partial tiles).
+  // Activation runs are loaded into registers one row ahead; runs past K_in
+  // (only in the last, partial tiles) are zero instead.
   v4u xr[NT][2];
   auto load_x = [&](int r, int c) {
-    const int p0 = min(c * kTile + 16 * t, K_in - 16);
-    const v4u* src = (const v4u*)(x + (int64_t)r * ldx + p0);
-    xr[c][0] = src[0];
-    xr[c][1] = src[1];
+    const int p0 = c * kTile + 16 * t;
+    if (p0 < K_in) {
+      const v4u* src = (const v4u*)(x + (int64_t)r * ldx + p0);
+      xr[c][0] = src[0];
+      xr[c][1] = src[1];
+    } else {
+      xr[c][0] = xr[c][1] = v4u{0, 0, 0, 0};
+    }
   };
   int row = blockIdx.x;
   if (row < M) {
@@ -226,9 +231,8 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
       const int p0 = base + 16 * t;
       double v[16];
       if (base < K_in) {  // uniform: the tile holds input values
-        v4u xa = xr[c][0], xb = xr[c][1];
+        const v4u xa = xr[c][0], xb = xr[c][1];
         if (next < M) load_x(next, c);
-        if (base + kTile > K_in && p0 >= K_in) xa = xb = v4u{0, 0, 0, 0};
         float xs[16];
         unpack8<DT>(xa, xs);
         unpack8<DT>(xb, xs + 8);
@@ -255,18 +259,19 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
           for (int j = 0; j < 16; ++j) xn[j] = xs[j];
         }
         if (has_sr) {
-          // fast path valid for products in DT's normal range; zeros and
-          // pad runs take the exact path, which returns the same signed zero
-          float pmin = __builtin_huge_valf();
+          // fast path valid for products p = RN32(x * rcp) in DT's normal
+          // range, which |RN_dt(p)| > min normal guarantees (RN_dt moves p by
+          // at most half a DT ulp); zeros, pad runs and non-finite values
+          // take the exact path, which returns the same signed zero
+          float hmin = __builtin_huge_valf();
           bool nonfinite = false;
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
-            const float p = xs[j] * rc[PLAIN ? 0 : c][j];
-            pmin = __builtin_fminf(pmin, __builtin_fabsf(p));
-            if constexpr (DT == IC_DTYPE_BF16) nonfinite |= !__builtin_isfinite(p);
-            xs[j] = round_to_dt<DT>(p);
+            xs[j] = round_to_dt<DT>(xs[j] * rc[PLAIN ? 0 : c][j]);
+            hmin = __builtin_fminf(hmin, __builtin_fabsf(xs[j]));
+            if constexpr (DT == IC_DTYPE_BF16) nonfinite |= !__builtin_isfinite(xs[j]);
           }
-          if (__builtin_expect(!(pmin >= dt_min_normal<DT>()) || nonfinite, 0)) {
+          if (__builtin_expect(!(hmin > dt_min_normal<DT>()) || nonfinite, 0)) {
             if (p0 < K_in) {
               float xo[16];
               if constexpr (NORM != 0) {
@@ -338,31 +343,28 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
           __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
       }
-      // ---- round once to DT: RN32 first, exact round-to-odd for the rare runs
-      // holding a DT rounding boundary, a tiny value or a zero
+      // ---- round once to DT: RN32 first; exact round-to-odd for the rare runs
+      // holding a DT rounding boundary, a tiny value or a zero, and for the
+      // runs of a tile that reaches into the pad to K_w (zeroed there)
       float z[16];
       float zmin = __builtin_huge_valf(), zmax = 0.0f;
-      bool boundary = false;
+      uint32_t bmin = 0xffffffffu;  // zero iff some z[j] is a DT boundary
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         z[j] = (float)v[j];
         zmin = __builtin_fminf(zmin, __builtin_fabsf(z[j]));
         zmax = __builtin_fmaxf(zmax, __builtin_fabsf(z[j]));
-        boundary |= rn32_is_dt_boundary<DT>(z[j]);
+        const uint32_t key = rn32_boundary_key<DT>(z[j]);
+        bmin = bmin < key ? bmin : key;
       }
-      if (__builtin_expect(boundary || !(zmin >= dt_min_normal<DT>()), 0)) {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) z[j] = rto24(v[j]);
-      }
-      if (base + kTile > K_r) {  // uniform: the tile reaches into the pad to K_w
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-          if (base + tile_pos<(LOG4R == 0 ? 0 : RC)>(t, j) >= K_r) z[j] = 0.0f;
-      }
-      if (__builtin_expect(boundary || !(zmin >= dt_min_normal<DT>()) || base + kTile > K_r, 0)) {
+      if (__builtin_expect(bmin == 0u || !(zmin >= dt_min_normal<DT>()) || base + kTile > K_r, 0)) {
         zmax = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) zmax = __builtin_fmaxf(zmax, __builtin_fabsf(z[j]));
+        for (int j = 0; j < 16; ++j) {
+          z[j] = rto24(v[j]);
+          if (base + kTile > K_r && base + tile_pos<(LOG4R == 0 ? 0 : RC)>(t, j) >= K_r) z[j] = 0.0f;
+          zmax = __builtin_fmaxf(zmax, __builtin_fabsf(z[j]));
+        }
       }
       amax = __builtin_fmaxf(amax, zmax);
       if constexpr (LOG4R == 0 || RC == 0) {
@@ -388,7 +390,7 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
     }
 
     // ---- row scale: RN_dt is monotone, so max |RN_dt(z)| = RN_dt(max |z|)
-    amax = wave_max(amax);
+    amax = wave_max_nonneg(amax);
     if ((t & 63) == 0) red[t >> 6] = amax;
     __syncthreads();
     float mr = red[0];
@@ -396,7 +398,7 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
     for (int w = 1; w < TH / 64; ++w) mr = __builtin_fmaxf(mr, red[w]);
     const float m = round_to_dt<DT>(mr);
     const float s = quant_scale(m);
-    const double rs = 1.0 / (double)s;
+    const float rcp_s = 1.0f / s;
     if (t == 0) s_out[row] = s;
 
     // ---- gather + quantize + store 16 codes per run
@@ -417,7 +419,7 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
         unpack8<DT>(*(const v4u*)(rowbuf + rbaddr(o0)), vv);
         unpack8<DT>(*(const v4u*)(rowbuf + rbaddr(o0) + 8), vv + 8);
       }
-      const v4u codes = quant16(vv, rs);
+      const v4u codes = quant16(vv, s, rcp_s);
       if (o0 < K_w) *(v4u*)(qrow + o0) = codes;
       __builtin_amdgcn_sched_barrier(0);  // one run at a time keeps the register footprint small
     }
@@ -476,19 +478,19 @@ __global__ __launch_bounds__(kThreads) void quant_wave_kernel(
       }
     }
   }
-  m = wave_max(m);
+  m = wave_max_nonneg(m);
   const float s = quant_scale(m);
-  const double rs = 1.0 / (double)s;
+  const float rcp_s = 1.0f / s;
   if (lane == 0) s_out[row] = s;
   int8_t* qrow = q_out + (int64_t)row * ldq;
   auto quant_chunk = [&](int i) {
     const int e = (i * 64 + lane) * 8;
     float v[8];
     unpack8<DT>(a[i], v);
-    const uint32_t w0 = pack4_lo_bytes(quant_code_nc(v[0], rs), quant_code_nc(v[1], rs),
-                                       quant_code_nc(v[2], rs), quant_code_nc(v[3], rs));
-    const uint32_t w1 = pack4_lo_bytes(quant_code_nc(v[4], rs), quant_code_nc(v[5], rs),
-                                       quant_code_nc(v[6], rs), quant_code_nc(v[7], rs));
+    const uint32_t w0 = pack4_lo_bytes(quant_code_mk(v[0], s, rcp_s), quant_code_mk(v[1], s, rcp_s),
+                                       quant_code_mk(v[2], s, rcp_s), quant_code_mk(v[3], s, rcp_s));
+    const uint32_t w1 = pack4_lo_bytes(quant_code_mk(v[4], s, rcp_s), quant_code_mk(v[5], s, rcp_s),
+                                       quant_code_mk(v[6], s, rcp_s), quant_code_mk(v[7], s, rcp_s));
     if (e < K) *(v2u*)(qrow + e) = v2u{w0, w1};
   };
   if constexpr (MAXCH <= 8) {

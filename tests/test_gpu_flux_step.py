@@ -21,6 +21,8 @@ _quant_utils.py:237-270.
 """
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -265,3 +267,5 @@ def test_dropin_ops_step_matches_fused_step(rt, flux):
             g.replay()
             torch.cuda.synchronize()
             assert torch.equal(o, eager)
+    # the W4A16-bias switch the drop-in step needs is scoped to its forward
+    assert "INTCRUSH_W4A16_BIAS" not in os.environ

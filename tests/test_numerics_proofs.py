@@ -7,6 +7,8 @@ rational rounding.  INTCRUSH_EXHAUSTIVE=1 widens the samples to every pair.
 from __future__ import annotations
 
 import os
+import shutil
+import subprocess
 from fractions import Fraction
 
 import numpy as np
@@ -51,6 +53,12 @@ def test_smoothrot_divide_fast_path(oracle, dt):
         want = _round_dt(xs.astype(np.float64) / np.float64(f), dt, oracle)
         ok = (got == want) | (np.isnan(got) & np.isnan(want))
         assert ok.all(), (f, xs[~ok][:4])
+        # the fast path as compiled for fp16: one rounding of the exact
+        # product (v_fma_mix), taken when |RN_dt(x * rcp)| > min normal
+        with np.errstate(all="ignore"):
+            h = _round_dt(xs.astype(np.float64) * np.float64(rcp), dt, oracle)
+        fast = (np.abs(h) > tiny) & np.isfinite(h)
+        assert np.array_equal(h[fast], want[fast]), (f, xs[fast][h[fast] != want[fast]][:4])
 
 
 def test_double_rounding_of_quotients_is_exact(oracle):
@@ -98,3 +106,20 @@ def test_quant_divide_via_fp64_reciprocal():
     got = (v.astype(np.float64) * (1.0 / s.astype(np.float64))).astype(np.float32)
     want = v / s
     assert np.array_equal(got, want)
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="needs gcc")
+@pytest.mark.parametrize("dt", [0, 1])
+def test_quant_markstein_exhaustive(tmp_path, dt):
+    """quant_code_mk: q0 = RN32(v r), e = fma(-q0, s, v), q = fma(e, r, q0),
+    code = trunc(RN32(q +- 0.5)), r = RN32(1/s), equals the reference code for
+    every (v, m) of the 16-bit type with |v| <= m (both signs), while the
+    single-rounding shortcut does not (so the checker detects a wrong formula)."""
+    src = os.path.join(os.path.dirname(os.path.abspath(__file__)), "numerics_quant_check.c")
+    exe = str(tmp_path / "qcheck")
+    subprocess.check_call(["gcc", "-O2", "-fopenmp", "-ffp-contract=off", src, "-o", exe, "-lm"])
+    out = subprocess.run([exe, str(dt)], capture_output=True, text=True, timeout=300, check=True).stdout.split()
+    fields = dict(zip(out[0::2], (int(v) for v in out[1::2])))
+    assert fields["pairs"] > 10**9
+    assert fields["mismatches"] == 0
+    assert fields["shortcut_mismatches"] > 0
