@@ -20,7 +20,10 @@
 //                 the four waves are added in wave order.
 //
 // Every lane of a wave reads 16 packed bytes (32 values) of one weight row per
-// block, so a wave-wide load covers 16 rows x 64 bytes.
+// block, so a wave-wide load covers 16 rows x 64 bytes.  When the M x K
+// activations fit 16 KB (M = 1 up to K = 8192 for 16-bit activations) they
+// are staged in LDS once per workgroup and read per block from there, so the
+// registers hold weights only and more waves keep loads in flight.
 #include "dequant4.h"
 
 namespace {
@@ -39,13 +42,19 @@ IC_DEV void unpack8_x16(uint32_t P, uint32_t& w0, uint32_t& w1) {
   w1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
 }
 
-template <bool INT4, int GS, int OUT_DT>
+// XL: as in the W4A16 GEMV below, the M x K activation codes (at most
+// kXlBytes) are staged in LDS once per workgroup, after the first batch of
+// weight loads is issued, and read per block when used: fewer VGPRs, more
+// waves per SIMD, more weight bytes in flight.
+constexpr int kXlBytes = 16384;
+template <bool INT4, int GS, int OUT_DT, bool XL>
 __global__ __launch_bounds__(kGT) void gemv_i8_kernel(
     const int8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
     const float* __restrict__ s_a, const float* __restrict__ s_w, int G,
     const void* __restrict__ bias, int bias_dt, void* __restrict__ C, int64_t ldc, int M, int N, int K,
     ic_epi epi) {
-  // GS == 128: block sums [KB][M][16]; otherwise per-wave totals [4][M][16]
+  // GS == 128: block sums [KB][M][16]; otherwise per-wave totals [4][M][16];
+  // with XL the activation codes [M][K] follow
   extern __shared__ int32_t sacc[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n0 = blockIdx.x * 16;
@@ -53,59 +62,101 @@ __global__ __launch_bounds__(kGT) void gemv_i8_kernel(
   const int n = min(n0 + col, N - 1);
   const int am = min(col, M - 1);  // token row fed by this lane (rows >= M repeat the last one)
   const int KB = K / kGBK;
-  const int8_t* arow = A + (int64_t)am * lda + 32 * c;
+  int8_t* xs = (int8_t*)(sacc + (GS == 128 ? KB : 4) * M * 16);
+  const int8_t* arow = XL ? xs + (int64_t)am * K + 32 * c : A + (int64_t)am * lda + 32 * c;
   const uint8_t* brow = B + (int64_t)n * ldb + (INT4 ? 16 * c : 32 * c);
 
   // Loads of up to kBatch blocks are issued before any of them is used, so a
   // wave keeps kBatch weight loads (plus activation loads) in flight.
   constexpr int kBatch = 8;
   v4i tot = {0, 0, 0, 0};
-  for (int b0 = wave; b0 < KB; b0 += 4 * kBatch) {
-    v4u pw[kBatch];
-    v4i a0[kBatch], a1[kBatch], w1[kBatch];
+  // One block: two MFMAs on this lane's 32 activation codes and 32 weights.
+  auto mma_block = [&](int b, const v4i& av0, const v4i& av1, const v4u& pwu, const v4i& w1u) {
+    v4i b0v, b1v;
+    if constexpr (INT4) {
+      uint32_t w[8];
+      unpack8_x16(pwu.x, w[0], w[1]);
+      unpack8_x16(pwu.y, w[2], w[3]);
+      unpack8_x16(pwu.z, w[4], w[5]);
+      unpack8_x16(pwu.w, w[6], w[7]);
+      b0v = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+      b1v = v4i{(int)w[4], (int)w[5], (int)w[6], (int)w[7]};
+    } else {
+      b0v = __builtin_bit_cast(v4i, pwu);
+      b1v = w1u;
+    }
+    if constexpr (GS == 128) {
+      v4i s = __builtin_amdgcn_mfma_i32_16x16x64_i8(av0, b0v, v4i{0, 0, 0, 0}, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_i32_16x16x64_i8(av1, b1v, s, 0, 0, 0);
+      // D layout: lane holds rows 4*(lane/16) + i of column lane%16
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const int b = b0 + 4 * u;
-      if (b < KB) {  // uniform across the wave
-        a0[u] = *(const v4i*)(arow + kGBK * b);
-        a1[u] = *(const v4i*)(arow + kGBK * b + 16);
-        if constexpr (INT4) {
-          pw[u] = *(const v4u*)(brow + (kGBK / 2) * b);
-        } else {
-          pw[u] = *(const v4u*)(brow + kGBK * b);
-          w1[u] = *(const v4i*)(brow + kGBK * b + 16);
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * c + i;
+        if (r < M) sacc[(b * M + r) * 16 + col] = s[i];
+      }
+    } else {
+      tot = __builtin_amdgcn_mfma_i32_16x16x64_i8(av0, b0v, tot, 0, 0, 0);
+      tot = __builtin_amdgcn_mfma_i32_16x16x64_i8(av1, b1v, tot, 0, 0, 0);
+    }
+  };
+  if constexpr (XL) {
+    v4u pw[kBatch];
+    v4i w1[INT4 ? 1 : kBatch];
+    auto load_batch = [&](int b0) {
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int b = b0 + 4 * u;
+        if (b < KB) {  // uniform across the wave
+          if constexpr (INT4) {
+            pw[u] = *(const v4u*)(brow + (kGBK / 2) * b);
+          } else {
+            pw[u] = *(const v4u*)(brow + kGBK * b);
+            w1[u] = *(const v4i*)(brow + kGBK * b + 16);
+          }
         }
+      }
+    };
+    // the first batch of weight loads is in flight while the codes are staged
+    load_batch(wave);
+    const int per_row = K / 16;  // 16-byte chunks
+    for (int i = tid; i < M * per_row; i += kGT) {
+      const int r = i / per_row, k16 = i - r * per_row;
+      *(v4i*)(xs + (int64_t)r * K + 16 * k16) = *(const v4i*)(A + (int64_t)r * lda + 16 * k16);
+    }
+    __syncthreads();
+    for (int b0 = wave; b0 < KB; b0 += 4 * kBatch) {
+      if (b0 != wave) load_batch(b0);
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int b = b0 + 4 * u;
+        if (b >= KB) break;
+        mma_block(b, *(const v4i*)(arow + kGBK * b), *(const v4i*)(arow + kGBK * b + 16), pw[u],
+                  w1[INT4 ? 0 : u]);
       }
     }
+  } else {
+    for (int b0 = wave; b0 < KB; b0 += 4 * kBatch) {
+      v4u pw[kBatch];
+      v4i a0[kBatch], a1[kBatch], w1[kBatch];
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const int b = b0 + 4 * u;
-      if (b >= KB) break;
-      v4i b0v, b1v;
-      if constexpr (INT4) {
-        uint32_t w[8];
-        unpack8_x16(pw[u].x, w[0], w[1]);
-        unpack8_x16(pw[u].y, w[2], w[3]);
-        unpack8_x16(pw[u].z, w[4], w[5]);
-        unpack8_x16(pw[u].w, w[6], w[7]);
-        b0v = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
-        b1v = v4i{(int)w[4], (int)w[5], (int)w[6], (int)w[7]};
-      } else {
-        b0v = __builtin_bit_cast(v4i, pw[u]);
-        b1v = w1[u];
-      }
-      if constexpr (GS == 128) {
-        v4i s = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[u], b0v, v4i{0, 0, 0, 0}, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[u], b1v, s, 0, 0, 0);
-        // D layout: lane holds rows 4*(lane/16) + i of column lane%16
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = 4 * c + i;
-          if (r < M) sacc[(b * M + r) * 16 + col] = s[i];
+      for (int u = 0; u < kBatch; ++u) {
+        const int b = b0 + 4 * u;
+        if (b < KB) {  // uniform across the wave
+          a0[u] = *(const v4i*)(arow + kGBK * b);
+          a1[u] = *(const v4i*)(arow + kGBK * b + 16);
+          if constexpr (INT4) {
+            pw[u] = *(const v4u*)(brow + (kGBK / 2) * b);
+          } else {
+            pw[u] = *(const v4u*)(brow + kGBK * b);
+            w1[u] = *(const v4i*)(brow + kGBK * b + 16);
+          }
         }
-      } else {
-        tot = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[u], b0v, tot, 0, 0, 0);
-        tot = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[u], b1v, tot, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int b = b0 + 4 * u;
+        if (b >= KB) break;
+        mma_block(b, a0[u], a1[u], pw[u], w1[u]);
       }
     }
   }
@@ -144,52 +195,93 @@ __global__ __launch_bounds__(kGT) void gemv_i8_kernel(
 }
 
 // W4A16 weight dequantization RN_dt(q * RN_dt(s)) of 8 nibbles.
-template <int DT>
+//
+// XL: the M x K activations (at most kXlBytes) are first copied into LDS and
+// each block's fragments read from there when used.  Held in registers for a
+// batch of 8 blocks, they were 4x the weight bytes per lane and 128 VGPRs,
+// which left two waves per SIMD and too few weight loads in flight (16.5 us,
+// 1.8 TB/s, at the Flux modulation shape; 12.7 us with the staging).
+template <int DT, bool XL>
 __global__ __launch_bounds__(kGT) void gemv_w4a16_kernel(
     const u16* __restrict__ X, int64_t ldx, const uint8_t* __restrict__ B, int64_t ldb,
     const float* __restrict__ s_w, int G, int gsize, const void* __restrict__ bias, int bias_dt,
     u16* __restrict__ C, int64_t ldc, int M, int N, int K) {
   __shared__ float sacc[4 * 16 * 16];
+  extern __shared__ __attribute__((aligned(16))) u16 xs[];  // XL: M rows of K values
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n0 = blockIdx.x * 16;
   const int c = lane >> 4, col = lane & 15;
   const int n = min(n0 + col, N - 1);
   const int am = min(col, M - 1);
   const int KB = K / kGBK;
-  const u16* xrow = X + (int64_t)am * ldx + 32 * c;
   const uint8_t* brow = B + (int64_t)n * ldb + 16 * c;
   const float* swrow = s_w + (int64_t)n * G;
+  const u16* xrow = XL ? xs + (int64_t)am * K + 32 * c : X + (int64_t)am * ldx + 32 * c;
 
   constexpr int kBatch = 8;
   v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int b0 = wave; b0 < KB; b0 += 4 * kBatch) {
-    v4u xv[kBatch][4], pw[kBatch];
-    float sv[kBatch];
+  // One block: four MFMAs on this lane's 32 activations and 32 dequantized weights.
+  auto mma_block = [&](int b, const v4u* xq, const v4u& pwu, float svu) {
+    const uint32_t p4[4] = {pwu.x, pwu.y, pwu.z, pwu.w};
+    const DeqScale d = deq_scale<DT>(svu);
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const int b = b0 + 4 * u;
-      if (b < KB) {  // uniform across the wave
+    for (int j = 0; j < 4; ++j) {
+      uint32_t o[4];
+      deq8<DT>(p4[j], d, o);
+      const v4u wv = {o[0], o[1], o[2], o[3]};
+      const v4u xa = XL ? *(const v4u*)(xrow + kGBK * b + 8 * j) : xq[j];
+      if constexpr (DT == IC_DTYPE_F16)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h_t, xa), __builtin_bit_cast(v8h_t, wv), acc, 0, 0, 0);
+      else
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf_t, xa), __builtin_bit_cast(v8bf_t, wv), acc, 0, 0, 0);
+    }
+  };
+  if constexpr (XL) {
+    // staged first: holding a batch of weights across the copy costs ~20
+    // VGPRs, and the lower occupancy measured slower than the overlap gained
+    const int per_row = K / 8;  // 16-byte chunks
+    for (int i = tid; i < M * per_row; i += kGT) {
+      const int r = i / per_row, k8 = i - r * per_row;
+      *(v4u*)(xs + (int64_t)r * K + 8 * k8) = *(const v4u*)(X + (int64_t)r * ldx + 8 * k8);
+    }
+    __syncthreads();
+    for (int b0 = wave; b0 < KB; b0 += 4 * kBatch) {
+      v4u pw[kBatch];
+      float sv[kBatch];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) xv[u][j] = *(const v4u*)(xrow + kGBK * b + 8 * j);
-        pw[u] = *(const v4u*)(brow + (kGBK / 2) * b);
-        sv[u] = swrow[G > 1 ? (kGBK * b + 32 * c) / gsize : 0];
+      for (int u = 0; u < kBatch; ++u) {
+        const int b = b0 + 4 * u;
+        if (b < KB) {  // uniform across the wave
+          pw[u] = *(const v4u*)(brow + (kGBK / 2) * b);
+          sv[u] = swrow[G > 1 ? (kGBK * b + 32 * c) / gsize : 0];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int b = b0 + 4 * u;
+        if (b >= KB) break;
+        mma_block(b, nullptr, pw[u], sv[u]);
       }
     }
+  } else {
+    for (int b0 = wave; b0 < KB; b0 += 4 * kBatch) {
+      v4u xv[kBatch][4], pw[kBatch];
+      float sv[kBatch];
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const int b = b0 + 4 * u;
-      if (b >= KB) break;
-      const uint32_t p4[4] = {pw[u].x, pw[u].y, pw[u].z, pw[u].w};
-      const DeqScale d = deq_scale<DT>(sv[u]);
+      for (int u = 0; u < kBatch; ++u) {
+        const int b = b0 + 4 * u;
+        if (b < KB) {  // uniform across the wave
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        uint32_t o[4];
-        deq8<DT>(p4[j], d, o);
-        const v4u wv = {o[0], o[1], o[2], o[3]};
-        if constexpr (DT == IC_DTYPE_F16)
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h_t, xv[u][j]), __builtin_bit_cast(v8h_t, wv), acc, 0, 0, 0);
-        else
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf_t, xv[u][j]), __builtin_bit_cast(v8bf_t, wv), acc, 0, 0, 0);
+          for (int j = 0; j < 4; ++j) xv[u][j] = *(const v4u*)(xrow + kGBK * b + 8 * j);
+          pw[u] = *(const v4u*)(brow + (kGBK / 2) * b);
+          sv[u] = swrow[G > 1 ? (kGBK * b + 32 * c) / gsize : 0];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int b = b0 + 4 * u;
+        if (b >= KB) break;
+        mma_block(b, xv[u], pw[u], sv[u]);
       }
     }
   }
@@ -205,17 +297,26 @@ __global__ __launch_bounds__(kGT) void gemv_w4a16_kernel(
   st_from_f32<DT>(C, (int64_t)m * ldc + no, v);
 }
 
-template <bool INT4, int GS, int OUT_DT>
-hipError_t launch_gemv_i8(const int8_t* A, int64_t lda, const uint8_t* B, int64_t ldb, const float* s_a,
-                          const float* s_w, int G, const void* bias, int bias_dt, void* C, int64_t ldc,
-                          int M, int N, int K, const ic_epi& epi, hipStream_t st) {
-  auto kern = gemv_i8_kernel<INT4, GS, OUT_DT>;
-  const size_t shm = (size_t)(GS == 128 ? K / kGBK : 4) * M * 16 * 4;
+template <bool INT4, int GS, int OUT_DT, bool XL>
+hipError_t launch_gemv_i8_t(const int8_t* A, int64_t lda, const uint8_t* B, int64_t ldb, const float* s_a,
+                            const float* s_w, int G, const void* bias, int bias_dt, void* C, int64_t ldc,
+                            int M, int N, int K, const ic_epi& epi, hipStream_t st) {
+  auto kern = gemv_i8_kernel<INT4, GS, OUT_DT, XL>;
+  const size_t shm = (size_t)(GS == 128 ? K / kGBK : 4) * M * 16 * 4 + (XL ? (size_t)M * K : 0);
   static unsigned char lds_set[64];  // per device
   if (hipError_t e = ic_set_lds_limit((const void*)kern, 160 * 1024, lds_set)) return e;
   kern<<<dim3((unsigned)((N + 15) / 16)), dim3(kGT), shm, st>>>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C,
                                                                 ldc, M, N, K, epi);
   return hipGetLastError();
+}
+
+template <bool INT4, int GS, int OUT_DT>
+hipError_t launch_gemv_i8(const int8_t* A, int64_t lda, const uint8_t* B, int64_t ldb, const float* s_a,
+                          const float* s_w, int G, const void* bias, int bias_dt, void* C, int64_t ldc,
+                          int M, int N, int K, const ic_epi& epi, hipStream_t st) {
+  if ((int64_t)M * K <= kXlBytes)
+    return launch_gemv_i8_t<INT4, GS, OUT_DT, true>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, epi, st);
+  return launch_gemv_i8_t<INT4, GS, OUT_DT, false>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, epi, st);
 }
 
 template <bool INT4, int GS>
@@ -330,12 +431,20 @@ int ic_gemv_w4a16(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, c
   const int G = (int)num_groups, gsize = (int)(K / num_groups);
   const dim3 grid((unsigned)((N + 15) / 16));
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == IC_DTYPE_F16)
-    gemv_w4a16_kernel<IC_DTYPE_F16><<<grid, kGT, 0, st>>>((const u16*)x, ldx, w_packed, ldw, s_w, G, gsize, bias,
-                                                         bias_dtype, (u16*)out, ldo, (int)M, (int)N, (int)K);
-  else
-    gemv_w4a16_kernel<IC_DTYPE_BF16><<<grid, kGT, 0, st>>>((const u16*)x, ldx, w_packed, ldw, s_w, G, gsize, bias,
-                                                          bias_dtype, (u16*)out, ldo, (int)M, (int)N, (int)K);
+  const int64_t xl_bytes = M * K * 2;
+  const bool xl = xl_bytes <= kXlBytes;
+  const size_t shm = xl ? (size_t)xl_bytes : 0;
+  auto args = [&](auto kern) {
+    kern<<<grid, kGT, shm, st>>>((const u16*)x, ldx, w_packed, ldw, s_w, G, gsize, bias, bias_dtype, (u16*)out, ldo,
+                                 (int)M, (int)N, (int)K);
+  };
+  if (dtype == IC_DTYPE_F16) {
+    if (xl) args(gemv_w4a16_kernel<IC_DTYPE_F16, true>);
+    else args(gemv_w4a16_kernel<IC_DTYPE_F16, false>);
+  } else {
+    if (xl) args(gemv_w4a16_kernel<IC_DTYPE_BF16, true>);
+    else args(gemv_w4a16_kernel<IC_DTYPE_BF16, false>);
+  }
   return ic_check_launch(who);
 }
 
