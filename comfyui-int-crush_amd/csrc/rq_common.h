@@ -111,6 +111,33 @@ IC_DEV void bf16_flush_small(float* xs, uint32_t* xred) {
   }
 }
 
+// Global -> LDS DMA of 16 bytes per lane (global_load_lds_dwordx4): lane i
+// reads base + voff and writes LDS address lds + 16 * i.  base and lds must
+// be wave-uniform (they are read into scalar registers here).  Issued from
+// inline assembly so that the compiler does not track it; its completion is
+// waited for explicitly with wait_vm_n.  The memory clobber keeps the
+// compiler's own memory accesses on their side of the issue.
+IC_DEV void dma16_lds(uint32_t voff, const void* base, uint32_t lds) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  const void* sb = (const void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(__builtin_amdgcn_readfirstlane(lds)),
+               "v"(voff), "s"(sb)
+               : "m0", "memory");
+}
+
+// Block until at most n vector-memory operations of this wave are in flight
+// (they retire in issue order); n is wave-uniform, 0..4.
+template <int N> IC_DEV void wait_vm_imm() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+IC_DEV void wait_vm_n(int n) {
+  if (n <= 0) wait_vm_imm<0>();
+  else if (n == 1) wait_vm_imm<1>();
+  else if (n == 2) wait_vm_imm<2>();
+  else if (n == 3) wait_vm_imm<3>();
+  else wait_vm_imm<4>();
+}
+
 // Instantiation sets of the fast-path kernels (see rq_fast.h).
 constexpr int kRqPlain = 0;    // no SmoothRot factors, no perm
 constexpr int kRqGeneral = 1;  // either one; flags read at run time

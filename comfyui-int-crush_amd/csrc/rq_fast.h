@@ -173,8 +173,16 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
     }
   }
 
-  // Activation runs are loaded into registers one row ahead; runs past K_in
-  // (only in the last, partial tiles) are zero instead.
+  // Activation runs of the next row are fetched while the current row is
+  // processed; runs past K_in (only in the last, partial tiles) are zero.
+  //   kDma (R = 64..1024, whose exchanges stay inside each wave's own 1024-
+  //   position slice of xbuf): global -> LDS DMA into that slice, issued once
+  //   the row's last exchange has been read, waited for with an explicit
+  //   vmcnt at the top of the next row and copied into registers there.  The
+  //   compiler otherwise moved register prefetches into fresh registers in
+  //   mid-row, which waited for the loads (and the previous row's stores) there.
+  //   Otherwise: register loads one row ahead.
+  constexpr bool kDma = XCH && LOG4R <= 5;
   v4u xr[NT][2];
   auto load_x = [&](int r, int c) {
     const int p0 = c * kTile + 16 * t;
@@ -186,12 +194,53 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
       xr[c][0] = xr[c][1] = v4u{0, 0, 0, 0};
     }
   };
+  // DMA staging: the NT tiles' 32 bytes per lane at slice + 2048 c + 16 lane
+  // (first 8 values) and + 1024 (last 8); NT * 2 KB fit the 8 KB slice.
+  const int wave_u = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int lane = t & 63;
+  char* const slice = (char*)(xbuf + (XCH ? xslot(1024 * wave_u) : 0));
+  const uint32_t slice_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)slice;
+  auto stage_row = [&](int r) {
+    const u16* rb = x + (int64_t)r * ldx;
+#pragma unroll
+    for (int c = 0; c < NT; ++c) {
+      if (c * kTile >= K_in) break;  // uniform
+      // pad runs read the row's last 16 values (a valid address) and are zeroed after
+      const uint32_t voff = 2u * (uint32_t)min(c * kTile + 16 * t, K_in - 16);
+      dma16_lds(voff, rb, slice_lds + (uint32_t)(c * 2048));
+      dma16_lds(voff + 16u, rb, slice_lds + (uint32_t)(c * 2048 + 1024));
+    }
+  };
+  // Vector-memory operations each wave issues after its DMA of a row: one
+  // 16-byte code store per tile that every lane of every wave stores (plus,
+  // on some waves, pad-tile stores and the scale store, which only add).
+  const int kStoresAfterDma = min(K_w / kTile, NT);
+  if constexpr (!PLAIN) {
+    if constexpr (kDma) {
+      // the constants' loads complete here (the compiler waits for them
+      // before these reads); an empty asm then is their last writer, so no
+      // wait for them is carried into the row loop, where it would also
+      // wait for the DMA and the previous row's stores
+#pragma unroll
+      for (int c = 0; c < NTC; ++c) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) asm volatile("" : "+v"(rc[c][j]));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(po[c][i]));
+      }
+    }
+  }
   int row = blockIdx.x;
   if (row < M) {
+    if constexpr (kDma) {
+      stage_row(row);
+    } else {
 #pragma unroll
-    for (int c = 0; c < NT; ++c)
-      if (c * kTile < K_in) load_x(row, c);
+      for (int c = 0; c < NT; ++c)
+        if (c * kTile < K_in) load_x(row, c);
+    }
   }
+  bool first_row = true;
 
   for (; row < M; row += gridDim.x) {
     const int next = row + gridDim.x;
@@ -203,6 +252,23 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
     // barrier; a wave that is ahead now yields to the ones behind it
     // (measured 7-12 % faster at C3, outputs unchanged).
     __builtin_amdgcn_s_setprio(3);
+    if constexpr (kDma) {
+      // this row's activations: DMA issued during the previous row (or above),
+      // followed since by at least kStoresAfterDma stores of this wave
+      if (first_row) wait_vm_imm<0>();
+      else wait_vm_n(kStoresAfterDma);
+      first_row = false;
+#pragma unroll
+      for (int c = 0; c < NT; ++c) {
+        if (c * kTile >= K_in) break;  // uniform
+        if (c * kTile + 16 * t < K_in) {
+          xr[c][0] = *(const v4u*)(slice + c * 2048 + lane * 16);
+          xr[c][1] = *(const v4u*)(slice + c * 2048 + 1024 + lane * 16);
+        } else {
+          xr[c][0] = xr[c][1] = v4u{0, 0, 0, 0};
+        }
+      }
+    }
     float n_mean = 0.0f, n_rstd = 1.0f;
     if constexpr (NORM != 0) {
       // row statistics from the registers (runs at or past K_in add nothing)
@@ -239,7 +305,7 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
       double v[16];
       if (base < K_in) {  // uniform: the tile holds input values
         const v4u xa = xr[c][0], xb = xr[c][1];
-        if (next < M) load_x(next, c);
+        if (!kDma && next < M) load_x(next, c);
         float xs[16];
         unpack8<DT>(xa, xs);
         unpack8<DT>(xb, xs + 8);
@@ -399,6 +465,9 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
     }
 
     __builtin_amdgcn_s_setprio(0);
+    if constexpr (kDma) {
+      if (next < M) stage_row(next);  // every exchange read of this row has returned
+    }
     // ---- row scale: RN_dt is monotone, so max |RN_dt(z)| = RN_dt(max |z|)
     amax = wave_max_nonneg(amax);
     if ((t & 63) == 0) red[t >> 6] = amax;
