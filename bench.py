@@ -93,7 +93,7 @@ def _parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS) + sorted(SETS) + [STEP_CONFIG])
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS) + sorted(SETS) + [STEP_CONFIG, MLP_CONFIG])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (PMC calibration)")
@@ -572,6 +572,88 @@ def set_main(args, rt):
     print(json.dumps(line), flush=True)
 
 
+# ------------------------------------------------ C4 MLP: chained epilogue
+# The Flux MLP between its two quantized linears, two ways: (a) the up-
+# projection GEMM with its GELU-tanh epilogue, then the down-projection's full
+# prep (SmoothRot divide, R = 256 Hadamard, perm, per-row INT8 quantization);
+# (b) the chained up-projection (ic_gemm_*_chain: GELU, divide and Hadamard
+# in the GEMM's epilogue), then the rest of the prep (perm and quantization).
+MLP_CONFIG = "c4mlp"
+MLP_SHAPES = ((4096, "double-block image stream"), (512, "double-block text stream"), (4608, "C3 rows"))
+
+
+def mlp_chain_main(args, rt):
+    import torch
+
+    dev = torch.device("cuda:0")
+    K, N, R = 3072, 12288, 256
+    dt = torch.bfloat16
+    rows = []
+    for kind in ("w4a8", "w8a8"):
+        for M, what in MLP_SHAPES:
+            g = torch.Generator().manual_seed(M)
+            xq = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8).to(dev)
+            s_a = (torch.rand(M, generator=g) * 0.02 + 0.005).to(dev)
+            bias = (torch.randn(N, generator=g) * 0.1).to(dev)
+            if kind == "w8a8":
+                w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(dev)
+                s_w = (torch.rand(N, generator=g) * 2e-3 + 1e-4).to(dev)
+            else:
+                w = torch.randint(0, 256, (N, K // 2), generator=g, dtype=torch.uint8).to(dev)
+                s_w = (torch.rand(N, K // 128, generator=g) * 0.02 + 1e-3).to(dev)
+            srf = rt.prepare_factors(torch.exp(torch.randn(N, generator=g) * 0.5).to(dev), dt)
+            perm = rt.prepare_perm(torch.randperm(N, generator=g).to(dev), N)
+            h = torch.empty(M, N, dtype=dt, device=dev)
+            y = torch.empty_like(h)
+            q = torch.empty(M, N, dtype=torch.int8, device=dev)
+            sq = torch.empty(M, dtype=torch.float32, device=dev)
+            q2 = torch.empty_like(q)
+            sq2 = torch.empty_like(sq)
+
+            def up():
+                if kind == "w8a8":
+                    rt.fused_int8_gemm_dequant(xq, w, s_w, s_a, bias=bias, out_dtype=dt, activation=rt.ACT_GELU_TANH,
+                                               out=h)
+                else:
+                    rt.gemm_w4a8(xq, w, s_w, s_a, bias=bias, out_dtype=dt, activation=rt.ACT_GELU_TANH, out=h)
+
+            def prep_full():
+                rt.rotate_quantize(h, rot_size=R, w_in=N, smoothrot=srf, perm=perm, s_a_out=sq, x_int8_out=q)
+
+            def chain():
+                rt.gemm_chain(xq, w, s_w, s_a, rot_size=R, smoothrot=srf, bias=bias, out_dtype=dt,
+                              activation=rt.ACT_GELU_TANH, out=y)
+
+            def prep_rest():
+                rt.rotate_quantize(y, rot_size=0, w_in=N, perm=perm, s_a_out=sq2, x_int8_out=q2)
+
+            t = {"up": [], "prep_full": [], "chain": [], "prep_rest": []}
+            for _ in range(3):  # interleaved repeats, averaged
+                for name, fn in (("up", up), ("prep_full", prep_full), ("chain", chain), ("prep_rest", prep_rest)):
+                    t[name].append(_time_graph(fn, args.steps)[0] * 1e3)
+            up(); prep_full(); chain(); prep_rest()
+            torch.cuda.synchronize()
+            same = bool(torch.equal(q, q2) and torch.equal(sq, sq2))
+            a = {k: sum(v) / len(v) for k, v in t.items()}
+            rows.append({"weights": kind, "M": M, "rows": what, "gemm_gelu_us": round(a["up"], 1),
+                         "prep_full_us": round(a["prep_full"], 1), "two_kernel_us": round(a["up"] + a["prep_full"], 1),
+                         "chain_gemm_us": round(a["chain"], 1), "prep_rest_us": round(a["prep_rest"], 1),
+                         "chained_us": round(a["chain"] + a["prep_rest"], 1), "codes_identical": same})
+            del xq, w, h, y, q, q2
+            torch.cuda.empty_cache()
+    head = rows[0]
+    line = {
+        "metric": "Flux MLP up-projection + down-projection prep, chained epilogue against two kernels",
+        "value": head["chained_us"], "unit": "us", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(head["chained_us"] / 1e3, 5), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": f"C4 MLP 3072->12288 (GELU-tanh) -> prep of 12288->3072 (R=256, SmoothRot, perm), "
+                               f"bf16; value: W4A8 g128 at M={head['M']}", "parallelism": "single GPU",
+                   "rows": rows},
+    }
+    print(json.dumps(line), flush=True)
+
+
 def traffic_for(workload_key):
     """HBM bytes per launch of the dominant kernel from committed rocprofv3 counters."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
@@ -602,6 +684,9 @@ def main():
         return
     if args.config in SETS:
         set_main(args, rt)
+        return
+    if args.config == MLP_CONFIG:
+        mlp_chain_main(args, rt)
         return
     cfg = CONFIGS[args.config]
     inp = make_inputs(cfg)

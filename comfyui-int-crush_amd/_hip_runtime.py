@@ -78,6 +78,8 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "ic_gemm_w8a8_ex": ([_P, _L, _L, _L, _P, _L, _L, _P, _P, _P, _I, _I, _P, _I, _L, _P, _I, _L, _P, _L, _P], _I),
     "ic_gemm_w4a8_ex": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _P, _I, _I, _P, _I, _L, _P, _I, _L, _P, _L,
                          _P], _I),
+    "ic_gemm_w8a8_chain": ([_P, _L, _L, _L, _P, _L, _L, _P, _P, _P, _I, _I, _P, _P, _I, _P, _I, _L, _P], _I),
+    "ic_gemm_w4a8_chain": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _P, _I, _I, _P, _P, _I, _P, _I, _L, _P], _I),
     "ic_gemm_w4a16": ([_P, _I, _L, _L, _L, _P, _L, _L, _P, _L, _P, _I, _P, _L, _P], _I),
     "ic_unpack_int4_to_int8": ([_P, _L, _L, _L, _P, _L, _P], _I),
     "ic_unpack_int4_to_float": ([_P, _P, _L, _L, _L, _L, _P, _I, _L, _P], _I),
@@ -650,6 +652,69 @@ def gemm_w4a8(x_int8: torch.Tensor, w_packed: torch.Tensor, s_w: torch.Tensor, s
     return c
 
 
+CHAIN_ROT_SIZES = (16, 64, 256)
+
+
+def gemm_chain(x_int8: torch.Tensor, w: torch.Tensor, s_w: torch.Tensor, s_a: torch.Tensor, *,
+               rot_size: int, smoothrot: PreparedFactors | None = None, bias: torch.Tensor | None = None,
+               out_dtype: torch.dtype = torch.bfloat16, activation: int = 0,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """Chained MLP epilogue (ic_gemm_w8a8_chain / ic_gemm_w4a8_chain): the
+    up-projection GEMM whose output rows leave already prepared as the next
+    linear's activation.
+
+    w int8 [N, K] (W8A8, s_w [N]) or packed uint8 [N, K/2] (W4A8, s_w [N, G]).
+    Each output h = RN_dt(act(dequant + bias)) as in fused_int8_gemm_dequant /
+    gemm_w4a8 with `activation`, then divided by the next linear's SmoothRot
+    factors (prepared for out_dtype; None: no divide) and rotated in blocks of
+    rot_size (16, 64 or 256) columns, each step rounded to out_dtype: the
+    first half of _prep_activation (_ops.py:337-365).  Returns y [M, N]; the
+    down-projection's codes are then rotate_quantize(y, rot_size=0,
+    w_in=K_w, perm=perm), which pads, gathers and takes the whole row's scale.
+    """
+    assert x_int8.dtype == torch.int8, f"x_int8 must be int8, got {x_int8.dtype}"
+    _need_cuda(x_int8, w, s_w, s_a, bias)
+    if out_dtype not in (torch.float16, torch.bfloat16):
+        raise TypeError("gemm_chain writes the next linear's activation: float16 or bfloat16")
+    R = int(rot_size)
+    if R not in CHAIN_ROT_SIZES:
+        raise ValueError(f"gemm_chain rotates blocks of {CHAIN_ROT_SIZES} columns, got rot_size={R}")
+    if smoothrot is not None and smoothrot.dtype != out_dtype:
+        raise ValueError("prepared SmoothRot factors were built for another activation dtype")
+    xq = _rows(x_int8)
+    M, K = xq.shape
+    wr = _rows(w)
+    N = wr.shape[0]
+    if smoothrot is not None and smoothrot.K != N:
+        raise ValueError(f"SmoothRot factors have {smoothrot.K} entries, expected N={N}")
+    sa = s_a.detach().reshape(-1).to(torch.float32).contiguous()
+    bp, bdt, _keep = _bias_args(bias, N)
+    c = _out_buffer(out, M, N, out_dtype, xq.device)
+    rp = _ptr(smoothrot.rcp) if smoothrot is not None else None
+    fp = _ptr(smoothrot.fdt) if smoothrot is not None else None
+    with torch.cuda.device(xq.device):
+        if wr.dtype == torch.int8:
+            assert wr.shape[1] == K, f"K mismatch: {K} vs {wr.shape[1]}"
+            sw = s_w.detach().reshape(-1).to(torch.float32).contiguous()
+            if sw.numel() != N:
+                raise ValueError(f"s_w must hold one scale per output channel ({N}), got {sw.numel()}")
+            _call("ic_gemm_w8a8_chain", _ptr(xq), M, K, xq.stride(0), _ptr(wr), N, wr.stride(0), _ptr(sa),
+                  _ptr(sw), bp, bdt, int(activation), rp, fp, R, _ptr(c), _dt(c.dtype, "out"), c.stride(0),
+                  _stream(xq))
+        elif wr.dtype == torch.uint8:
+            assert wr.shape[1] * 2 >= K, f"packed weight too narrow for K={K}"
+            sw = s_w.detach().reshape(N, -1).to(torch.float32).contiguous()
+            G = sw.shape[1]
+            if K % G:
+                raise ValueError(f"K={K} is not a multiple of the {G} scale groups")
+            _call("ic_gemm_w4a8_chain", _ptr(xq), M, K, xq.stride(0), _ptr(wr), N, wr.stride(0), _ptr(sw), G,
+                  _ptr(sa), bp, bdt, int(activation), rp, fp, R, _ptr(c), _dt(c.dtype, "out"), c.stride(0),
+                  _stream(xq))
+        else:
+            raise TypeError(f"gemm_chain weights must be int8 or packed uint8, got {wr.dtype}")
+    return c
+
+
 def gemm_w4a16(x: torch.Tensor, w_packed: torch.Tensor, s_w: torch.Tensor,
                bias: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """W4A16: x @ RN_dt(q * RN_dt(s))^T (+ bias) in x.dtype (fp16/bf16)."""
@@ -801,5 +866,6 @@ __all__ = [
     "unpack_int4_to_float", "prepare_factors", "prepare_perm", "PreparedFactors", "gemm_acc_i32",
     "gemv", "GEMV_MAX_M", "fused_layernorm_quantize", "fused_rmsnorm_quantize", "fused_softmax_quantize",
     "norm_rotate_quantize", "ACT_NONE", "ACT_SILU", "ACT_GELU", "ACT_GELU_TANH", "int8_gemm_int8out",
+    "gemm_chain", "CHAIN_ROT_SIZES",
     "load_library",
 ]

@@ -35,6 +35,7 @@
 #include <type_traits>
 
 #include "gemm_common.h"
+#include "rq_common.h"
 
 namespace ic_gemm {
 struct GemmArgs {
@@ -69,13 +70,24 @@ struct Tile {
   static constexpr size_t epi_bytes() { return (size_t)BM * EPI_RS * 2 + (size_t)(BM + 2 * BN) * 4; }
   static constexpr size_t ring_bytes() { return (size_t)NS * SLOT + (size_t)BU_BYTES; }
   static constexpr size_t lds_bytes() { return ring_bytes() > epi_bytes() ? ring_bytes() : epi_bytes(); }
+  // chained epilogue (ROT): the staging tile and its scale rows, the SmoothRot
+  // reciprocals of the tile's columns, then every wave's fp64 exchange slice
+  static constexpr size_t chain_xoff() { return (epi_bytes() + (size_t)BN * 4 + 15) / 16 * 16; }
+  static constexpr size_t chain_bytes() { return chain_xoff() + (size_t)rq::xbuf_doubles<kNT * 16>() * 8; }
+  static constexpr size_t chain_lds_bytes() { return ring_bytes() > chain_bytes() ? ring_bytes() : chain_bytes(); }
 };
 
 // PART (split-K): workgroup (x, y) computes tile x over the K stages of
 // slice y of gridDim.y and writes its 4-byte partials -- the int32 sum
 // (per-row scales) or the fp32 group fold (grouped) -- to
 // acc_out[(y * M + m) * N + n]; splitk_reduce_kernel finishes them.
-template <class TL, int OUT_DT, bool ACC_OUT, bool PART = false, bool EPI = false>
+//
+// ROT (2, 3, 4; with EPI and a 16-bit output): the chained MLP epilogue of
+// ic_gemm_*_chain.  Each finished tile of h = RN_dt(epilogue value) is
+// prepared, in LDS, as the next linear's activation -- SmoothRot divide and
+// R = 4^ROT block Hadamard, the first half of _prep_activation -- before it
+// is stored.
+template <class TL, int OUT_DT, bool ACC_OUT, bool PART = false, bool EPI = false, int ROT = 0>
 __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
     const int8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
     const float* __restrict__ s_a, const float* __restrict__ s_w, int G,
@@ -242,6 +254,89 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
 
   auto out_row = [&](int i, int r) { return m0 + wr * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); };
   auto out_col = [&](int j) { return n0 + wc * WN + j * 32 + (lane & 31); };
+
+  // Chained prep of a staged tile (ROT): ot holds h = RN_dt(epilogue value)
+  // row-major with row stride BN + 8.  In passes of 8192 positions each lane
+  // takes 16 consecutive columns of one row and, exactly as the fast prep
+  // kernel does, divides them by the SmoothRot factors (RN_dt(RN32(h * rcp))
+  // where that product is a normal DT value, the IEEE quotient otherwise),
+  // applies the bf16 flush rule, runs the radix-4 digits in fp64 (digits 0-1
+  // in registers, 2-3 through this wave's exchange slice), rounds once to DT
+  // and writes the rotated values back in place.  A block of R columns never
+  // straddles tiles (R divides BN), so each block is whole in one lane group.
+  auto chain_rotate = [&](u16* ot, const float* rc_l, double* xb) {
+    if constexpr (ROT != 0) {
+      static_assert(EPI && !ACC_OUT && !PART && OUT_DT != IC_DTYPE_F32, "chained epilogue configuration");
+      static_assert(BN == 256 && ROT >= 2 && ROT <= 4, "chained rotation tiles");
+      constexpr int RS = TL::EPI_RS;
+      constexpr int RC = ROT <= 2 ? 0 : 1;
+      constexpr int kPass = BM * BN / (kNT * 16);
+      const bool has_sr = epi.sr_rcp != nullptr;
+      for (int ps = 0; ps < kPass; ++ps) {
+        const int p0 = ps * (kNT * 16) + 16 * tid;
+        const int row = p0 / BN, col = p0 % BN;
+        const v4u ha = *(const v4u*)(ot + row * RS + col);
+        const v4u hb = *(const v4u*)(ot + row * RS + col + 8);
+        const uint32_t hw[8] = {ha.x, ha.y, ha.z, ha.w, hb.x, hb.y, hb.z, hb.w};
+        float xs[16];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          xs[2 * i] = rq::bits16_f32<OUT_DT>((u16)(hw[i] & 0xffffu));
+          xs[2 * i + 1] = rq::bits16_f32<OUT_DT>((u16)(hw[i] >> 16));
+        }
+        if (has_sr) {
+          float rc[16], xo[16];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const v4f r = *(const v4f*)(rc_l + col + 4 * i);
+            rc[4 * i] = r.x; rc[4 * i + 1] = r.y; rc[4 * i + 2] = r.z; rc[4 * i + 3] = r.w;
+          }
+          float hmin = __builtin_huge_valf();
+          bool nonfinite = false;
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            xo[j] = xs[j];
+            xs[j] = round_to_dt<OUT_DT>(xs[j] * rc[j]);
+            hmin = __builtin_fminf(hmin, __builtin_fabsf(xs[j]));
+            if constexpr (OUT_DT == IC_DTYPE_BF16) nonfinite |= !__builtin_isfinite(xs[j]);
+          }
+          if (__builtin_expect(!(hmin > dt_min_normal<OUT_DT>()) || nonfinite, 0)) {
+            // columns of a partial last tile read a valid factor and are never stored
+            const int kc = min(n0 + col, N - 16);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) xs[j] = div_round_dt<OUT_DT>(xo[j], rc[j], epi.sr_f, kc + j);
+          }
+        }
+        if constexpr (OUT_DT == IC_DTYPE_BF16) rq::bf16_flush_small<ROT, kNT>(xs, nullptr);
+        double v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = (double)xs[j];
+        rq::stage_lo(v);
+        rq::stage_hi(v);
+        if constexpr (ROT >= 3) {
+#pragma unroll
+          for (int j = 0; j < 16; ++j) xb[rq::xslot(16 * tid + j)] = v[j];
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+          const int g = tid >> 4, l = tid & 15;
+#pragma unroll
+          for (int h = 0; h < 16; ++h) v[h] = xb[rq::xslot(256 * g + 16 * h + l)];
+          rq::stage_lo(v);
+          if constexpr (ROT >= 4) rq::stage_hi(v);
+          // every lane has read its slots before the next pass rewrites them
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int p = ps * (kNT * 16) + rq::tile_pos<RC>(tid, j);
+          ot[(p / BN) * RS + p % BN] = rq::f32_bits16<OUT_DT>(round_f64_to_dt<OUT_DT>(v[j]));
+        }
+      }
+    }
+  };
 
   // Scales of group kt for this lane's columns, from the stage's LDS slot.
   auto read_scales = [&](int kt, float* sw) {
@@ -428,6 +523,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
       float* sa_l = (float*)(smem + BM * RS * 2);
       float* b_l = sa_l + BM;
       float* sw_l = b_l + BN;
+      float* rc_l = sw_l + BN;  // ROT: SmoothRot reciprocals of the tile's columns
       if (res_lds) {
         for (int c = tid; c < BM * CPR; c += kNT) {
           const int row = c / CPR, col = (c % CPR) * 8;
@@ -441,6 +537,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
         const int n = min(n0 + t, N - 1);
         b_l[t] = bias != nullptr ? ld_any_f32(bias, bias_dt, n) : 0.0f;
         if constexpr (GS == 0) sw_l[t] = s_w[n];
+        if constexpr (ROT != 0) rc_l[t] = epi.sr_rcp != nullptr ? epi.sr_rcp[n] : 1.0f;
       }
       __syncthreads();
 #pragma unroll
@@ -480,6 +577,10 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
         }
       }
       __syncthreads();
+      if constexpr (ROT != 0) {
+        chain_rotate(ot, rc_l, (double*)(smem + TL::chain_xoff()));
+        __syncthreads();
+      }
 #pragma unroll 4
       for (int c = tid; c < BM * CPR; c += kNT) {
         const int row = c / CPR, col = (c % CPR) * 8;
@@ -724,6 +825,36 @@ bool mfma_shape_ok(const GemmArgs& g, int gsize) {
   // rows are read 8 or 16 bytes at a time
   if (((uintptr_t)g.A & 15) || ((uintptr_t)g.B & 15) || (g.lda & 15) || (g.ldb & 15)) return false;
   return true;
+}
+
+// Chained MLP epilogue launches (gemm_i8_chain.hip): 128 x 256 tiles, whose
+// 256 columns hold whole R-blocks for R <= 256 and whose staging tile and
+// fp64 exchange slices fit the LDS together.  The caller has checked the
+// shape, the alignment of the staged output path and R.
+template <class TL, int OUT_DT, int ROT>
+hipError_t launch_chain_t(const GemmArgs& g, hipStream_t st) {
+  const int tiles = ((g.M + TL::BM - 1) / TL::BM) * ((g.N + TL::BN - 1) / TL::BN);
+  constexpr size_t shm = TL::chain_lds_bytes();
+  static_assert(shm <= 160 * 1024, "LDS budget");
+  auto kern = gemm_i8_kernel<TL, OUT_DT, false, false, true, ROT>;
+  static unsigned char lds_set[64];  // per device
+  if (hipError_t e = ic_set_lds_limit((const void*)kern, (int)shm, lds_set)) return e;
+  kern<<<dim3(tiles), dim3(kNT), shm, st>>>(g.A, g.lda, g.B, g.ldb, g.s_a, g.s_w, g.G, g.bias, g.bias_dt, g.C,
+                                            g.ldc, g.M, g.N, g.K, nullptr, g.epi);
+  return hipGetLastError();
+}
+template <class TL, int OUT_DT>
+hipError_t launch_chain_r(const GemmArgs& g, int log4r, hipStream_t st) {
+  switch (log4r) {
+    case 2: return launch_chain_t<TL, OUT_DT, 2>(g, st);
+    case 3: return launch_chain_t<TL, OUT_DT, 3>(g, st);
+    default: return launch_chain_t<TL, OUT_DT, 4>(g, st);
+  }
+}
+template <class TL>
+hipError_t launch_chain(const GemmArgs& g, int log4r, hipStream_t st) {
+  if (g.out_dt == IC_DTYPE_F16) return launch_chain_r<TL, IC_DTYPE_F16>(g, log4r, st);
+  return launch_chain_r<TL, IC_DTYPE_BF16>(g, log4r, st);
 }
 
 // EPI: the activation / residual epilogue is compiled in (gemm_i8_epi.hip

@@ -199,6 +199,10 @@ struct ic_epi {
   const void* res = nullptr;
   int res_dt = 0;
   int64_t ldr = 0;
+  // chained MLP epilogue (ic_gemm_*_chain): the next linear's SmoothRot
+  // reciprocals RN32(1/f) and factors f, per output column (both NULL: none)
+  const float* sr_rcp = nullptr;
+  const float* sr_f = nullptr;
 };
 
 // v * sigmoid(t) = v / (1 + e^-t) from the hardware exp2 and reciprocal

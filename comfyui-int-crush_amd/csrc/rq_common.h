@@ -49,6 +49,29 @@ template <int RC> IC_DEV int tile_pos(int t, int j) {
   else return 1024 * (t >> 6) + 256 * (j & 3) + 4 * (t & 63) + (j >> 2);
 }
 
+// LDS layouts of the fast path and the chained GEMM epilogue (doubles in the
+// exchange buffer, 16-bit values in the row buffer).  Exchange slot of tile
+// position p: 2 doubles of padding per 16 positions and 16 per 256.  Then the
+// b128 row writes of 16 lanes hit 16 distinct 4-bank groups (row stride 36
+// dwords) and the transposed b64 reads of the four 16-lane groups of a wave
+// land on alternate halves of the 64 banks.  Row-buffer address of position
+// p: 16 values of padding per 256, so the strided writes of the four 16-lane
+// groups of a wave use distinct banks.
+IC_DEV int xslot(int p) { return p + 2 * (p >> 4) + 16 * (p >> 8); }
+template <int TILE> constexpr int xbuf_doubles() { return TILE + 2 * (TILE / 16) + 16 * (TILE / 256); }
+IC_DEV int rbaddr(int p) { return p + 16 * (p >> 8); }
+template <int NT, int TILE> constexpr int rowbuf_len() { return NT * TILE + 16 * (NT * TILE / 256); }
+
+// RN_dt(y) of an fp64 value through RN32: exact unless RN32(y) is itself a
+// rounding boundary of DT (a midpoint between neighbours, including the
+// overflow threshold) or lies below DT's normal range.  Boundary test on the
+// f32 bits: the bits below DT's precision are exactly 100...0.
+template <int DT> IC_DEV uint32_t rn32_boundary_key(float z) {
+  const uint32_t w = __float_as_uint(z);
+  if constexpr (DT == IC_DTYPE_F16) return (w ^ 0x1000u) & 0x1fffu;  // zero iff (w & 0x1fff) == 0x1000
+  else return (w ^ 0x8000u) & 0xffffu;
+}
+
 constexpr int kFastMaxTiles = 4;  // fast path: K_w <= 16384
 
 // ---- bf16 flush of values far below their Hadamard block's maximum.

@@ -45,16 +45,6 @@ IC_DEV v4u quant16(const float* v, float s, float r) {
   return v4u{w[0], w[1], w[2], w[3]};
 }
 
-// RN_dt(y) of an fp64 value through RN32: exact unless RN32(y) is itself a
-// rounding boundary of DT (a midpoint between neighbours, including the
-// overflow threshold) or lies below DT's normal range.  Boundary test on the
-// f32 bits: the bits below DT's precision are exactly 100...0.
-template <int DT> IC_DEV uint32_t rn32_boundary_key(float z) {
-  const uint32_t w = __float_as_uint(z);
-  if constexpr (DT == IC_DTYPE_F16) return (w ^ 0x1000u) & 0x1fffu;  // zero iff (w & 0x1fff) == 0x1000
-  else return (w ^ 0x8000u) & 0xffffu;
-}
-
 // Three instantiation sets (VAR): kRqPlain (no SmoothRot factors, no perm),
 // kRqBoth (both, known at compile time) and kRqGeneral (either one, read at
 // run time).  The plain kernels drop the per-run divide, its range checks,
@@ -64,18 +54,6 @@ template <int DT> IC_DEV uint32_t rn32_boundary_key(float z) {
 // per CU while the per-thread constants fit half the register file (K_w <=
 // 12288, or any width for plain rows); wider rows with factors or a perm keep
 // one.
-// LDS layouts (doubles in the exchange buffer, 16-bit values in the row
-// buffer).  Exchange slot of tile position p: 2 doubles of padding per 16
-// positions and 16 per 256.  Then the b128 row writes of 16 lanes hit 16
-// distinct 4-bank groups (row stride 36 dwords) and the transposed b64 reads
-// of the four 16-lane groups of a wave land on alternate halves of the 64
-// banks.  Row-buffer address of position p: 16 values of padding per 256, so
-// the strided writes of the four 16-lane groups of a wave use distinct banks.
-IC_DEV int xslot(int p) { return p + 2 * (p >> 4) + 16 * (p >> 8); }
-template <int TILE> constexpr int xbuf_doubles() { return TILE + 2 * (TILE / 16) + 16 * (TILE / 256); }
-IC_DEV int rbaddr(int p) { return p + 16 * (p >> 8); }
-template <int NT, int TILE> constexpr int rowbuf_len() { return NT * TILE + 16 * (NT * TILE / 256); }
-
 // Workgroup sums of two fp64 values (TH/64 waves; red holds 2 * TH/64
 // doubles).  The caller's barrier at the top of the row guarantees red is no
 // longer being read, so one barrier suffices.

@@ -227,6 +227,38 @@ int ic_gemm_w4a8_ex(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const u
                     int64_t workspace_bytes, void* stream);
 
 /*
+ * Chained MLP epilogue: the up-projection GEMM of an MLP, finished as the
+ * next linear's prepared activation.  Each output is first what
+ * ic_gemm_*_ex computes with this activation and no residual,
+ *   h = RN_dt(act(dequant + bias)),
+ * and then, per row, the first half of the down-projection's
+ * _prep_activation (_ops.py:337-365):
+ *   x = RN_dt(h / RN_dt(f[n]))            (SmoothRot divide; sr_rcp = RN32(1/f),
+ *                                          sr_f = RN_dt(f) as ic_smoothrot_prepare
+ *                                          makes them; both NULL: no divide)
+ *   y = RN_dt(H_R x) per block of rot_size columns   (_quant_utils.py:117-147)
+ * written to out [M, N] in out_dtype (f16/bf16), bit-identical to
+ * ic_gemm_*_ex followed by ic_prepare_activation with the same factors and
+ * rot_size and no pad or perm.  The rest of the down-projection's prep -- pad
+ * to K_w, PermuQuant gather and the per-row INT8 scale over the whole row --
+ * needs every column of a row, so it follows as ic_rotate_quantize(y,
+ * rot_size 0, no factors, perm) (the reference's chained-GEMM kernel,
+ * int8_gemm_int8out, kernels/triton_int8_gemm.py:392-536, quantizes inside
+ * each N-tile with that tile's own abs-max instead).  rot_size is 16, 64 or
+ * 256 and divides N; K is a multiple of 128; num_groups is 1 or gives a
+ * group size that is a multiple of 128; operands, row strides and out are
+ * 16-byte aligned and ldo is a multiple of 8.
+ */
+int ic_gemm_w8a8_chain(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8_t* w, int64_t N,
+                       int64_t ldw, const float* s_a, const float* s_w, const void* bias, int bias_dtype,
+                       int activation, const float* sr_rcp, const float* sr_f, int rot_size, void* out,
+                       int out_dtype, int64_t ldo, void* stream);
+int ic_gemm_w4a8_chain(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed,
+                       int64_t N, int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a,
+                       const void* bias, int bias_dtype, int activation, const float* sr_rcp,
+                       const float* sr_f, int rot_size, void* out, int out_dtype, int64_t ldo, void* stream);
+
+/*
  * W4A16: out = x . RN_dt(q * RN_dt(s))^T (+ bias), fp32 accumulation, dtype f16/bf16.
  * Replaces unpack_int4_to_float16 (kernels/triton_int4_unpack.py:62-88) + F.linear
  * of _ops.py:466-481.
