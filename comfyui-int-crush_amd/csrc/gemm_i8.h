@@ -284,6 +284,8 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
           xs[2 * i] = rq::bits16_f32<OUT_DT>((u16)(hw[i] & 0xffffu));
           xs[2 * i + 1] = rq::bits16_f32<OUT_DT>((u16)(hw[i] >> 16));
         }
+        rq::Bf16RunStats fst{0u, 0.0f};
+        bool fst_ok = false;
         if (has_sr) {
           float rc[16], xo[16];
 #pragma unroll
@@ -292,22 +294,32 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
             rc[4 * i] = r.x; rc[4 * i + 1] = r.y; rc[4 * i + 2] = r.z; rc[4 * i + 3] = r.w;
           }
           float hmin = __builtin_huge_valf();
-          bool nonfinite = false;
+          uint32_t hmax_bits = 0u;
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
             xo[j] = xs[j];
             xs[j] = round_to_dt<OUT_DT>(xs[j] * rc[j]);
             hmin = __builtin_fminf(hmin, __builtin_fabsf(xs[j]));
-            if constexpr (OUT_DT == IC_DTYPE_BF16) nonfinite |= !__builtin_isfinite(xs[j]);
+            if constexpr (OUT_DT == IC_DTYPE_BF16) {
+              const uint32_t a = __float_as_uint(xs[j]) & 0x7fffffffu;
+              hmax_bits = hmax_bits > a ? hmax_bits : a;
+            }
           }
+          const bool nonfinite = OUT_DT == IC_DTYPE_BF16 && hmax_bits >= 0x7f800000u;
+          fst = rq::Bf16RunStats{hmax_bits, hmin};
+          fst_ok = true;
           if (__builtin_expect(!(hmin > dt_min_normal<OUT_DT>()) || nonfinite, 0)) {
+            fst_ok = false;
             // columns of a partial last tile read a valid factor and are never stored
             const int kc = min(n0 + col, N - 16);
 #pragma unroll
             for (int j = 0; j < 16; ++j) xs[j] = div_round_dt<OUT_DT>(xo[j], rc[j], epi.sr_f, kc + j);
           }
         }
-        if constexpr (OUT_DT == IC_DTYPE_BF16) rq::bf16_flush_small<ROT, kNT>(xs, nullptr);
+        if constexpr (OUT_DT == IC_DTYPE_BF16) {
+          if (!fst_ok) fst = rq::bf16_run_stats(xs);
+          rq::bf16_flush_small<ROT, kNT>(xs, nullptr, fst);
+        }
         double v[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j) v[j] = (double)xs[j];

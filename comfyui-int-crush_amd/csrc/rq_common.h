@@ -88,29 +88,79 @@ constexpr int kFastMaxTiles = 4;  // fast path: K_w <= 16384
 // range) are always exact and never flushed.
 template <int LOG4R> constexpr int kFlushSpan() { return 43 - 2 * LOG4R; }
 
+// Per-run statistics the bf16 flush rule needs, over a thread's 16 values:
+// the largest |x| as bits (integer maximum of the bits without the sign, so
+// NaN > inf > any finite value) and the smallest |x| (f32 minimum, which
+// ignores NaN; zero when the run holds a zero).  Callers that already form
+// them while rounding the run pass them in.
+struct Bf16RunStats {
+  uint32_t amax_bits;
+  float amin;
+};
+IC_DEV Bf16RunStats bf16_run_stats(const float* xs) {
+  Bf16RunStats st{0u, __builtin_huge_valf()};
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const uint32_t a = __float_as_uint(xs[j]) & 0x7fffffffu;
+    st.amax_bits = st.amax_bits > a ? st.amax_bits : a;
+    st.amin = __builtin_fminf(st.amin, __builtin_fabsf(xs[j]));
+  }
+  return st;
+}
+
+// Maximum / minimum of an unsigned value over aligned groups of G lanes (G a
+// power of 4 up to 64), in every lane of the group: DPP moves inside rows of
+// 16 lanes (quad permutations, then the half-row and row mirrors), lane
+// shuffles across rows.
+template <int G, bool MAX> IC_DEV uint32_t group_reduce_u32(uint32_t v) {
+  auto op = [](uint32_t a, uint32_t b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
+  auto dpp = [](uint32_t x, int ctrl) -> uint32_t {
+    switch (ctrl) {
+      case 0: return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xB1, 0xf, 0xf, false);   // quad_perm [1,0,3,2]
+      case 1: return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x4E, 0xf, 0xf, false);   // quad_perm [2,3,0,1]
+      case 2: return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x141, 0xf, 0xf, false);  // row_half_mirror
+      default: return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x140, 0xf, 0xf, false); // row_mirror
+    }
+  };
+  if constexpr (G >= 4) {
+    v = op(v, dpp(v, 0));
+    v = op(v, dpp(v, 1));
+  }
+  if constexpr (G >= 16) {
+    v = op(v, dpp(v, 2));
+    v = op(v, dpp(v, 3));
+  }
+  if constexpr (G >= 64) {
+    v = op(v, (uint32_t)__shfl_xor((int)v, 16, 64));
+    v = op(v, (uint32_t)__shfl_xor((int)v, 32, 64));
+  }
+  return v;
+}
+
 // xs: the 16 consecutive input positions of this thread (after the SmoothRot
 // divide); a block of R positions is the R/16 consecutive threads of one
 // aligned group (R = 4096: the four waves of the workgroup, reduced through
 // xred, 2 * TH / 64 words of LDS, with one workgroup barrier).  e_max is the
 // f32 exponent field of the block's largest |x|; bf16 subnormals have field 0.
+// The smallest nonzero |x| is the run's smallest |x| unless the run holds a
+// zero, when it is searched for.
 template <int LOG4R, int TH>
-IC_DEV void bf16_flush_small(float* xs, uint32_t* xred) {
+IC_DEV void bf16_flush_small(float* xs, uint32_t* xred, Bf16RunStats st) {
   constexpr int G = (1 << (2 * LOG4R)) / 16;  // threads per block
-  uint32_t mx = 0u, mn = 0xffffffffu;         // max |x| bits, min nonzero |x| bits - 1
+  uint32_t mx = st.amax_bits;                 // max |x| bits
+  uint32_t mn;                                // min nonzero |x| bits - 1 (none: 0xffffffff)
+  if (st.amin > 0.0f) {
+    mn = __float_as_uint(st.amin) - 1u;
+  } else {
+    mn = 0xffffffffu;
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const uint32_t a = __float_as_uint(xs[j]) & 0x7fffffffu;
-    mx = mx > a ? mx : a;
-    const uint32_t am1 = a - 1u;  // zero wraps to the maximum
-    mn = mn < am1 ? mn : am1;
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t am1 = (__float_as_uint(xs[j]) & 0x7fffffffu) - 1u;  // zero wraps to the maximum
+      mn = mn < am1 ? mn : am1;
+    }
   }
-#pragma unroll
-  for (int o = 1; o < (G < 64 ? G : 64); o <<= 1) {
-    const uint32_t a = (uint32_t)__shfl_xor((int)mx, o, 64);
-    const uint32_t b = (uint32_t)__shfl_xor((int)mn, o, 64);
-    mx = mx > a ? mx : a;
-    mn = mn < b ? mn : b;
-  }
+  mx = group_reduce_u32<(G < 64 ? G : 64), true>(mx);
+  mn = group_reduce_u32<(G < 64 ? G : 64), false>(mn);
   if constexpr (G > 64) {
     static_assert(G == TH, "a block of more than one wave spans the whole workgroup");
     if ((threadIdx.x & 63) == 0) {
@@ -132,6 +182,10 @@ IC_DEV void bf16_flush_small(float* xs, uint32_t* xred) {
     for (int j = 0; j < 16; ++j)
       if ((__float_as_uint(xs[j]) & 0x7fffffffu) < thr) xs[j] = 0.0f;
   }
+}
+template <int LOG4R, int TH>
+IC_DEV void bf16_flush_small(float* xs, uint32_t* xred) {
+  bf16_flush_small<LOG4R, TH>(xs, xred, bf16_run_stats(xs));
 }
 
 // Global -> LDS DMA of 16 bytes per lane (global_load_lds_dwordx4): lane i

@@ -309,20 +309,31 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
 #pragma unroll
           for (int j = 0; j < 16; ++j) xn[j] = xs[j];
         }
+        // bf16: the run's |x| extremes for the flush rule, formed with the
+        // divide's own range test where there is one
+        Bf16RunStats fst{0u, 0.0f};
+        bool fst_ok = false;
         if (has_sr) {
           // fast path valid for products p = RN32(x * rcp) in DT's normal
           // range, which |RN_dt(p)| > min normal guarantees (RN_dt moves p by
           // at most half a DT ulp); zeros, pad runs and non-finite values
           // take the exact path, which returns the same signed zero
           float hmin = __builtin_huge_valf();
-          bool nonfinite = false;
+          uint32_t hmax_bits = 0u;  // bf16: largest |x| as bits (NaN > inf > finite)
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
             xs[j] = round_to_dt<DT>(xs[j] * rc[PLAIN ? 0 : c][j]);
             hmin = __builtin_fminf(hmin, __builtin_fabsf(xs[j]));
-            if constexpr (DT == IC_DTYPE_BF16) nonfinite |= !__builtin_isfinite(xs[j]);
+            if constexpr (DT == IC_DTYPE_BF16) {
+              const uint32_t a = __float_as_uint(xs[j]) & 0x7fffffffu;
+              hmax_bits = hmax_bits > a ? hmax_bits : a;
+            }
           }
+          const bool nonfinite = DT == IC_DTYPE_BF16 && hmax_bits >= 0x7f800000u;
+          fst = Bf16RunStats{hmax_bits, hmin};
+          fst_ok = true;
           if (__builtin_expect(!(hmin > dt_min_normal<DT>()) || nonfinite, 0)) {
+            fst_ok = false;  // the exact path below replaces the run
             if (p0 < K_in) {
               float xo[16];
               if constexpr (NORM != 0) {
@@ -340,7 +351,10 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
             }
           }
         }
-        if constexpr (DT == IC_DTYPE_BF16 && LOG4R >= 2) bf16_flush_small<LOG4R, TH>(xs, xred);
+        if constexpr (DT == IC_DTYPE_BF16 && LOG4R >= 2) {
+          if (!fst_ok) fst = bf16_run_stats(xs);
+          bf16_flush_small<LOG4R, TH>(xs, xred, fst);
+        }
 #pragma unroll
         for (int j = 0; j < 16; ++j) v[j] = (double)xs[j];
       } else {
