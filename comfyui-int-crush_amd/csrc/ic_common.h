@@ -152,7 +152,11 @@ IC_DEV int quant_code(float v, double rs) {
 // to the reference rule (tests/numerics_quant_check.c); a single rounding of
 // v r (+- 0.5) is not (thousands of pairs per type differ).  v = +-inf or NaN gives 0 as the fp64 form does.
 IC_DEV int quant_code_mk(float v, float s, float r) {
-  const float q0 = v * r;
+  // q0 = RN32(v r), as an FMA with a +0 addend: for a 16-bit v widened from
+  // fp16 the compiler then reads v in its fp16 form (v_fma_mix_f32) and needs
+  // no conversion.  Only a zero product can change (-0 becomes +0), and it
+  // gives code 0 either way.
+  const float q0 = __builtin_fmaf(v, r, 0.0f);
   const float e = __builtin_fmaf(-q0, s, v);
   const float q = __builtin_fmaf(e, r, q0);
   return (int)(q + __builtin_copysignf(0.5f, q));

@@ -34,6 +34,18 @@ template <int DT> IC_DEV u16 f32_bits16(float v) {
   if constexpr (DT == IC_DTYPE_F16) return f32_to_f16(v);
   else return f32_to_bf16(v);
 }
+// Two f32 values rounded to DT (RN-even) in one packed conversion
+// (v_cvt_pk_f16_f32 / v_cvt_pk_bf16_f32), a in the low half.
+template <int DT> IC_DEV uint32_t pack2_bits16(float a, float b) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  if constexpr (DT == IC_DTYPE_F16) {
+    typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, h16x2));
+  } else {
+    typedef __bf16 b16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, b16x2));
+  }
+}
 template <int DT> IC_DEV float bits16_f32(u16 b) {
   if constexpr (DT == IC_DTYPE_F16) return f16_to_f32(b);
   else return bf16_to_f32(b);

@@ -320,13 +320,30 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
           // take the exact path, which returns the same signed zero
           float hmin = __builtin_huge_valf();
           uint32_t hmax_bits = 0u;  // bf16: largest |x| as bits (NaN > inf > finite)
+          if constexpr (DT == IC_DTYPE_BF16) {
+            // pairs rounded by one packed conversion; the extremes of |x| as
+            // packed 16-bit integers (bf16 bits without the sign order as the
+            // values, NaN above inf; a NaN minimum sends the run to the exact
+            // path, as the non-finite test would)
+            typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+            u16x2 hmx = {0, 0}, hmn = {0xffff, 0xffff};
 #pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            xs[j] = round_to_dt<DT>(xs[j] * rc[PLAIN ? 0 : c][j]);
-            hmin = __builtin_fminf(hmin, __builtin_fabsf(xs[j]));
-            if constexpr (DT == IC_DTYPE_BF16) {
-              const uint32_t a = __float_as_uint(xs[j]) & 0x7fffffffu;
-              hmax_bits = hmax_bits > a ? hmax_bits : a;
+            for (int i = 0; i < 8; ++i) {
+              const uint32_t w = pack2_bits16<DT>(xs[2 * i] * rc[PLAIN ? 0 : c][2 * i],
+                                                  xs[2 * i + 1] * rc[PLAIN ? 0 : c][2 * i + 1]);
+              xs[2 * i] = __uint_as_float(w << 16);
+              xs[2 * i + 1] = __uint_as_float(w & 0xffff0000u);
+              const u16x2 a = __builtin_bit_cast(u16x2, w & 0x7fff7fffu);
+              hmx = __builtin_elementwise_max(hmx, a);
+              hmn = __builtin_elementwise_min(hmn, a);
+            }
+            hmax_bits = (uint32_t)(hmx.x > hmx.y ? hmx.x : hmx.y) << 16;
+            hmin = __uint_as_float((uint32_t)(hmn.x < hmn.y ? hmn.x : hmn.y) << 16);
+          } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+              xs[j] = round_to_dt<DT>(xs[j] * rc[PLAIN ? 0 : c][j]);
+              hmin = __builtin_fminf(hmin, __builtin_fabsf(xs[j]));
             }
           }
           const bool nonfinite = DT == IC_DTYPE_BF16 && hmax_bits >= 0x7f800000u;
@@ -438,7 +455,7 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
         // 16 contiguous positions per thread: two 16-byte stores
         uint32_t w[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) w[i] = (uint32_t)f32_bits16<DT>(z[2 * i]) | ((uint32_t)f32_bits16<DT>(z[2 * i + 1]) << 16);
+        for (int i = 0; i < 8; ++i) w[i] = pack2_bits16<DT>(z[2 * i], z[2 * i + 1]);
         v4u* dst = (v4u*)(rowbuf + rbaddr(base + 16 * t));
         dst[0] = v4u{w[0], w[1], w[2], w[3]};
         dst[1] = v4u{w[4], w[5], w[6], w[7]};
@@ -446,13 +463,18 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
         // elements b, 4+b, 8+b, 12+b are four consecutive positions: one 8-byte store
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-          const uint32_t lo = (uint32_t)f32_bits16<DT>(z[b]) | ((uint32_t)f32_bits16<DT>(z[4 + b]) << 16);
-          const uint32_t hi = (uint32_t)f32_bits16<DT>(z[8 + b]) | ((uint32_t)f32_bits16<DT>(z[12 + b]) << 16);
+          const uint32_t lo = pack2_bits16<DT>(z[b], z[4 + b]);
+          const uint32_t hi = pack2_bits16<DT>(z[8 + b], z[12 + b]);
           *(v2u*)(rowbuf + rbaddr(base + tile_pos<3>(t, b))) = v2u{lo, hi};
         }
       } else {
+        // pairs rounded by one packed conversion, stored as two 16-bit halves
 #pragma unroll
-        for (int j = 0; j < 16; ++j) rowbuf[rbaddr(base + tile_pos<RC>(t, j))] = f32_bits16<DT>(z[j]);
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t w = pack2_bits16<DT>(z[2 * i], z[2 * i + 1]);
+          rowbuf[rbaddr(base + tile_pos<RC>(t, 2 * i))] = (u16)w;
+          rowbuf[rbaddr(base + tile_pos<RC>(t, 2 * i + 1))] = (u16)(w >> 16);
+        }
       }
     }
 
