@@ -44,7 +44,7 @@ static int reference_code(float v, float s) {
 }
 
 static int kernel_code(float v, float s, float r) {
-  const float q0 = v * r;
+  const float q0 = fmaf(v, r, 0.0f); /* RN32(v r); a zero product becomes +0 */
   const float e = fmaf(-q0, s, v);
   const float q = fmaf(e, r, q0);
   return (int)(q + copysignf(0.5f, q));
