@@ -222,8 +222,12 @@ def gpu_bench(cfg, inp, steps, warmup, rt):
     t0 = time.perf_counter()
     step_ms = _time_loop(step, steps)
     wall = time.perf_counter() - t0
-    gemm_ms = _time_loop(gemm, steps)
-    prep_ms = _time_loop(prep, steps) if cfg["fmt"] != "w4a16" else None
+    # kernels alone: a GEMV lasts ~10 us, so one replay's fixed launch cost is
+    # spread over more launches there (the per-dispatch kernel-trace average
+    # and this figure then agree)
+    reps = steps if M > rt.GEMV_MAX_M else max(steps, 400)
+    gemm_ms = _time_loop(gemm, reps)
+    prep_ms = _time_loop(prep, reps) if cfg["fmt"] != "w4a16" else None
     return step_ms, wall, gemm_ms, prep_ms, copies
 
 
