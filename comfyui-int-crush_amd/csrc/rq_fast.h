@@ -584,7 +584,9 @@ __global__ __launch_bounds__(kThreads) void quant_wave_kernel(
                                        quant_code_mk(v[2], s, rcp_s), quant_code_mk(v[3], s, rcp_s));
     const uint32_t w1 = pack4_lo_bytes(quant_code_mk(v[4], s, rcp_s), quant_code_mk(v[5], s, rcp_s),
                                        quant_code_mk(v[6], s, rcp_s), quant_code_mk(v[7], s, rcp_s));
-    if (e < K) *(v2u*)(qrow + e) = v2u{w0, w1};
+    // streaming stores (measured 9.5 -> 8.3 us at 4096 x 3072; the same for
+    // the rotating prep's codes gained nothing)
+    if (e < K) __builtin_nontemporal_store(v2u{w0, w1}, (v2u*)(qrow + e));
   };
   if constexpr (MAXCH <= 8) {
 #pragma unroll
