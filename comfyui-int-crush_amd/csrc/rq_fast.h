@@ -106,7 +106,14 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
   constexpr int kTile = TH * 16;  // positions per tile
   static_assert(TH == 256 || (TH % 64 == 0 && LOG4R <= 5), "cross-wave rotation needs four waves");
   __shared__ double xbuf[XCH ? xbuf_doubles<kTile>() : 2];
-  __shared__ __attribute__((aligned(16))) u16 rowbuf[rowbuf_len<NT, kTile>()];
+  // WLR: rows without a perm whose rotation stays inside each wave's 1024
+  // positions (R = 64..1024 with the DMA-staged slices, at most two tiles)
+  // keep their rounded values in the upper half of the wave's own exchange
+  // slice instead of a row buffer: the quantization then reads only what
+  // its own wave wrote, and the workgroup needs no row-sized buffer (the
+  // Wan FFN-down rows fit two workgroups per CU instead of one).
+  constexpr bool WLR = VAR == kRqPlain && XCH && LOG4R <= 5 && NT <= 2;
+  __shared__ __attribute__((aligned(16))) u16 rowbuf[WLR ? 8 : rowbuf_len<NT, kTile>()];
   __shared__ float red[TH / 64];
   __shared__ double red_d[NORM != 0 ? 2 * (TH / 64) : 1];
   __shared__ uint32_t xred[DT == IC_DTYPE_BF16 && LOG4R == 6 ? 2 * (TH / 64) : 1];
@@ -189,6 +196,10 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
       dma16_lds(voff + 16u, rb, slice_lds + (uint32_t)(c * 2048 + 1024));
     }
   };
+  // WLR: byte offset in the slice of wave-local position q of tile c (tiles
+  // of 1024 + 64 values from byte 4096; the slice holds 1216 doubles)
+  auto wlr_off = [](int c, int q) { return 4096 + 2176 * c + 2 * (q + 16 * (q >> 8)); };
+  static_assert(!WLR || 4096 + 2176 * NT <= 8 * 1216, "WLR rows fit the exchange slice");
   // Vector-memory operations each wave issues after its DMA of a row: one
   // 16-byte code store per tile that every lane of every wave stores (plus,
   // on some waves, pad-tile stores and the scale store, which only add).
@@ -275,6 +286,7 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
       }
     }
     float amax = 0.0f;
+    uint32_t zs[WLR ? NT : 1][8];  // WLR: this lane's rounded values, packed as they are written
 #pragma unroll
     for (int c = 0; c < NT; ++c) {
       const int base = c * kTile;
@@ -451,7 +463,15 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
         }
       }
       amax = __builtin_fmaxf(amax, zmax);
-      if constexpr (LOG4R == 0 || RC == 0) {
+      if constexpr (WLR) {
+        // kept until every exchange of the row is done (the next tile's
+        // exchange reuses the whole slice); pairs in the store order below
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          if constexpr (RC == 3) zs[c][i] = pack2_bits16<DT>(z[(i & 1) * 8 + (i >> 1)], z[(i & 1) * 8 + (i >> 1) + 4]);
+          else zs[c][i] = pack2_bits16<DT>(z[2 * i], z[2 * i + 1]);
+        }
+      } else if constexpr (LOG4R == 0 || RC == 0) {
         // 16 contiguous positions per thread: two 16-byte stores
         uint32_t w[8];
 #pragma unroll
@@ -478,6 +498,29 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
       }
     }
 
+    if constexpr (WLR) {
+      // into the slice's upper part (the next row's DMA fills bytes 0..4095):
+      // wave-local position q of tile c at byte wlr_off(c, q), 16 values of
+      // padding per 256 as in the row buffer
+#pragma unroll
+      for (int c = 0; c < NT; ++c) {
+        if (c * kTile >= K_w) break;  // uniform
+        if constexpr (RC == 3) {
+          // elements b, 4+b, 8+b, 12+b: positions 256 b + 4 lane + 0..3
+#pragma unroll
+          for (int b = 0; b < 4; ++b)
+            *(v2u*)(slice + wlr_off(c, 256 * b + 4 * lane)) = v2u{zs[c][2 * b], zs[c][2 * b + 1]};
+        } else {
+          // element j: position 256 (lane / 16) + 16 j + lane % 16
+          const int q0 = 256 * (lane >> 4) + (lane & 15);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            *(u16*)(slice + wlr_off(c, q0 + 32 * i)) = (u16)zs[c][i];
+            *(u16*)(slice + wlr_off(c, q0 + 32 * i + 16)) = (u16)(zs[c][i] >> 16);
+          }
+        }
+      }
+    }
     __builtin_amdgcn_s_setprio(0);
     if constexpr (kDma) {
       if (next < M) stage_row(next);  // every exchange read of this row has returned
@@ -508,6 +551,11 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
           vv[2 * i] = bits16_f32<DT>(*(const u16*)(rb + (po[PLAIN ? 0 : c][i] & 0xffffu)));
           vv[2 * i + 1] = bits16_f32<DT>(*(const u16*)(rb + (po[PLAIN ? 0 : c][i] >> 16)));
         }
+      } else if constexpr (WLR) {
+        // this lane's 16 consecutive positions are wave-local 16 lane .. 16 lane + 15
+        const char* wl = slice + wlr_off(c, 16 * lane);
+        unpack8<DT>(*(const v4u*)wl, vv);
+        unpack8<DT>(*(const v4u*)(wl + 16), vv + 8);
       } else {
         unpack8<DT>(*(const v4u*)(rowbuf + rbaddr(o0)), vv);
         unpack8<DT>(*(const v4u*)(rowbuf + rbaddr(o0) + 8), vv + 8);
