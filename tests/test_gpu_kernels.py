@@ -124,6 +124,8 @@ ROT_CASES = [
     (4200, 1024, None, False, True, False),     # the same, rotation pad 4200 -> 5120
     (2500, 1024, None, True, False, False),     # three one-block waves, pad 2500 -> 3072
     (6000, 1024, 6400, True, True, False),      # three-wave workgroups, two tiles, then w_in pad
+    (2048, 64, None, False, False, False),      # no perm: rows kept in the waves' exchange slices, one tile
+    (6144, 64, None, False, False, False),      # the same with two three-wave tiles
     (9216, 256, None, True, True, False),       # one twelve-wave tile, 3072 positions of it padding
     (10000, 1024, 11008, False, True, False),   # the same tile with one-block waves, pads to 10240 and 11008
     (15360, 256, None, True, True, False),      # two eight-wave tiles (Flux single-block output projection)
