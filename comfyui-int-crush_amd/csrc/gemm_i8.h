@@ -35,6 +35,7 @@
 #include <type_traits>
 
 #include "gemm_common.h"
+#include "gemm_i8_big.h"
 #include "rq_common.h"
 
 namespace ic_gemm {
@@ -787,9 +788,39 @@ hipError_t launch_mfma(const GemmArgs& g, hipStream_t st) {
   return launch_kernel<TL, OUT_DT, ACC, false, EPI>(g, 1, st);
 }
 
+// Grouped INT4 on 288 x 192 tiles (gemm_w4g_big_kernel) where their rounds of
+// workgroups cost less than 256 x 128's: 4608 x 3072 (the Flux MLP-down and
+// attention-projection shapes) fills the 256 CUs in one round of 256 tiles
+// instead of two of 432.  That kernel writes 16-bit outputs through its LDS
+// staging tile only, so the output (and a residual) must be 16-byte aligned
+// with row strides and N multiples of 8.
+bool big_tile_ok(const GemmArgs& g) {
+  if (g.M <= 128 || (((uintptr_t)g.C) & 15) != 0 || (g.ldc & 7) != 0 || (g.N & 7) != 0) return false;
+  if (g.epi.res != nullptr &&
+      (g.epi.res_dt == IC_DTYPE_F32 || (((uintptr_t)g.epi.res) & 15) != 0 || (g.epi.ldr & 7) != 0))
+    return false;
+  // per output the 288 x 192 tile costs ~0.93 of 256 x 128 (Wan FFN-down,
+  // 32760 x 5120 x 14336: 13 rounds of it took as long as 20 of 256 x 128)
+  return tiling_cost(g, big::BM, big::BN, 93) < tiling_cost(g, 256, 128);
+}
+
+template <int OUT_DT, bool EPI>
+hipError_t launch_big(const GemmArgs& g, hipStream_t st) {
+  const int tiles = ((g.M + big::BM - 1) / big::BM) * ((g.N + big::BN - 1) / big::BN);
+  auto kern = gemm_w4g_big_kernel<OUT_DT, EPI>;
+  static unsigned char lds_set[64];  // per device
+  if (hipError_t e = ic_set_lds_limit((const void*)kern, (int)big::lds_bytes, lds_set)) return e;
+  kern<<<dim3(tiles), dim3(kNT), big::lds_bytes, st>>>(g.A, g.lda, g.B, g.ldb, g.s_a, g.s_w, g.G, g.bias,
+                                                       g.bias_dt, g.C, g.ldc, g.M, g.N, g.K, g.epi);
+  return hipGetLastError();
+}
+
 template <bool INT4, int GS, int OUT_DT, bool ACC, bool EPI>
 hipError_t pick_tile(const GemmArgs& g, hipStream_t st) {
   const TileShape t = tile_choice(g, GS != 0);
+  if constexpr (INT4 && GS != 0 && !ACC && OUT_DT != IC_DTYPE_F32) {
+    if (big_tile_ok(g)) return launch_big<OUT_DT, EPI>(g, st);
+  }
   if constexpr (!INT4 && GS == 0) {
     if (t.bm == 256 && t.bn == 192) return launch_mfma<Tile<256, 192, 4, 2, false, 0>, OUT_DT, ACC, EPI>(g, st);
     if (t.bm == 256) return launch_mfma<Tile<256, 256, 2, 2, false, 0>, OUT_DT, ACC, EPI>(g, st);

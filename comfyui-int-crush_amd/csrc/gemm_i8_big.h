@@ -1,0 +1,302 @@
+// Grouped W4A8 GEMM on 288 x 192 output tiles (gfx950), for shapes whose
+// 256 x 128 tiling ends in a partly filled round of workgroups.
+//
+// Same arithmetic as gemm_i8_kernel's grouped INT4 path (triton_w4a8_gemm.py:40-108
+// with the per-group scales of _quant_utils.py:237-270): per 128-column stage
+// an exact int32 block sum of 16*q weights, folded in group order as
+// facc = fma(f32(acc_g), s_w[n, g] / 16, facc); out = facc * s_a[m] (+ bias),
+// rounded once.  Outputs are bit-identical to the 256 x 128 kernel.
+//
+// Why this tile: a round of workgroups costs the same whether all CUs are busy
+// or a few, and 4608 x 3072 (the Flux MLP-down / C3 shape) makes 432 tiles of
+// 256 x 128 on 256 CUs, 1.69 rounds paid as two.  4608 x 3072 / 256 CUs is
+// 2^11 * 27 outputs per CU, and 288 x 192 is the one tile of that area whose
+// sides divide M and N with 16-row / 16-column blocks: 16 x 16 tiles, one
+// round.  Its operands per 128-K stage (36 KB of activations, 12 KB of packed
+// weights) are 0.87 bytes per output against 1.22 for 256 x 128.
+//
+// The price is registers: 288 x 192 outputs over 512 lanes are 108 per lane.
+// Holding an int32 group sum and an fp32 running sum for each (216 VGPRs)
+// leaves too little for the operands, so here only the fp32 sums are
+// resident: each 16 x 16 block runs both 64-K steps of a stage back to back
+// and is folded right after, its group sum held only meanwhile.
+//
+// Layout: 8 waves in 2 (rows) x 4 (columns), each owning 144 x 48 = 9 x 3
+// blocks of v_mfma_i32_16x16x64_i8.  Operand lane l holds 16 K-bytes (chunk
+// l/16 of the 64-K step) of row / column l%16, the same chunk for both
+// operands, so the K order inside the instruction does not matter; result
+// lane l holds rows 4*(l/16) + r (r = 0..3) of column l%16.  Activations,
+// packed weights and scales reach LDS by DMA through a two-slot ring (the
+// activation rows swizzled as in gemm_i8_kernel).  Each wave expands its own
+// weight fragments from the packed slot into registers (8 packed bytes per
+// lane and fragment), so no expanded tile is written to LDS and a stage needs
+// one barrier, not two; the two waves of a column group expand the same
+// fragments (60 VALU instructions per wave and stage against 30 for a shared
+// expansion, which measured 4 % slower with its extra barrier and LDS
+// round trip).  Measured at C3 (4608 x 3072 x 12288): 256 x 128 tiles 273 us,
+// this tile with a shared expansion 227 us, with register expansion 217 us,
+// plus the priority ramp below 208 us.
+//
+// Wave priorities: the two waves on a SIMD (one per wave row) run the same
+// instruction mix, MFMAs and the fold's VALU work, and the arbiter favours the
+// older one, which finished its rows of a stage in ~2700 shader clocks while
+// the younger took ~3900 and the older idled at the barrier.  Each wave
+// therefore steps its priority down over the block rows (3 3 2 2 1 1 0 0 0):
+// a wave that runs ahead yields the SIMD to the one behind.
+#pragma once
+#include <type_traits>
+
+#include "gemm_common.h"
+
+namespace {
+namespace big {
+constexpr int BM = 288, BN = 192, NS = 2;
+constexpr int TMB = 9, TNB = 3;              // 16 x 16 blocks per wave
+constexpr int WROWS = TMB * 16, WCOLS = TNB * 16;
+constexpr int A_BYTES = BM * kBK;            // 36864
+constexpr int B_BYTES = BN * kBK / 2;        // 12288, packed nibbles
+constexpr int S_BYTES = BN * 4;              // one fp32 scale per column
+constexpr int SLOT = A_BYTES + B_BYTES + S_BYTES;
+constexpr int A_BLOCKS = BM / 8;             // 1 KB DMA blocks: 8 rows of 128 bytes
+constexpr int B_BLOCKS = BN / 16;            // 1 KB DMA blocks: 16 rows of 64 bytes
+constexpr int A_PER = (A_BLOCKS + 7) / 8;    // blocks per wave (waves 0-3 take one more)
+constexpr int B_PER = (B_BLOCKS + 7) / 8;
+constexpr int S_WAVES = BN / 64;             // waves issuing a scale DMA
+constexpr int EPI_RS = BN + 8;               // 16-bit output staging row stride
+constexpr size_t ring_bytes = (size_t)NS * SLOT;
+constexpr size_t epi_bytes = (size_t)BM * EPI_RS * 2 + (size_t)(BM + BN) * 4;
+constexpr size_t lds_bytes = ring_bytes > epi_bytes ? ring_bytes : epi_bytes;
+constexpr int kPrio[TMB] = {3, 3, 2, 2, 1, 1, 0, 0, 0};  // wave priority per block row
+static_assert(SLOT % 16 == 0 && lds_bytes <= 160 * 1024, "LDS layout");
+static_assert(2 * WROWS == BM && 4 * WCOLS == BN, "wave grid");
+static_assert(A_PER + B_PER + 1 <= TMB, "one DMA slot per block row");
+}  // namespace big
+
+template <int OUT_DT, bool EPI>
+__global__ __launch_bounds__(kNT, 1) void gemm_w4g_big_kernel(
+    const int8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
+    const float* __restrict__ s_a, const float* __restrict__ s_w, int G,
+    const void* __restrict__ bias, int bias_dt, void* __restrict__ C, int64_t ldc, int M, int N,
+    int K, ic_epi epi) {
+  using namespace big;
+  static_assert(OUT_DT != IC_DTYPE_F32, "16-bit outputs only");
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_char*)smem;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = wave >> 2, wc = wave & 3;
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  int tm, tn;
+  tile_coords(blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int KT = K / kBK;
+  const int spg = (K / G) / kBK;  // stages per scale group
+
+  // ---- DMA addressing (rows past M or N re-read the last row; never stored).
+  // A block b: LDS rows 8b + l/8, chunk slot l%8 holding global chunk
+  // (l%8) ^ swz(row).  Packed B block b: rows 16b + l/4, 16-byte parts.
+  uint32_t a_off[A_PER], b_off[B_PER];
+#pragma unroll
+  for (int c = 0; c < A_PER; ++c) {
+    const int row = 8 * (wave + 8 * c) + (lane >> 3);
+    a_off[c] = (uint32_t)(min(row, M - 1 - m0) * lda + (((lane & 7) ^ swz(row)) << 4));
+  }
+#pragma unroll
+  for (int c = 0; c < B_PER; ++c) {
+    // packed row n (64 bytes) holds its 16-byte part p at part p ^ ((n >> 2) & 3):
+    // the fragment reads of 16 consecutive rows then spread over all banks
+    const int row = 16 * (wave + 8 * c) + (lane >> 2);
+    const int part = (lane & 3) ^ ((lane >> 4) & 3);
+    b_off[c] = (uint32_t)(min(row, N - 1 - n0) * ldb + (part << 4));
+  }
+  const uint32_t s_off = (uint32_t)(min(64 * wave + lane, N - 1 - n0) * G * 4);
+  const int8_t* a_base = A + (int64_t)m0 * lda;
+  const uint8_t* b_base = B + (int64_t)n0 * ldb;
+  const float* s_base = s_w + (int64_t)n0 * G;
+
+  auto slot_of = [&](int kt) { return lds0 + (uint32_t)((kt % NS) * SLOT); };
+  auto dma_a = [&](int kt, int c) {
+    const int blk = wave + 8 * c;  // wave-uniform
+    if (blk < A_BLOCKS) dma16(a_off[c], a_base + (int64_t)kt * kBK, slot_of(kt) + (uint32_t)(blk * 1024));
+  };
+  auto dma_b = [&](int kt, int c) {
+    const int blk = wave + 8 * c;
+    if (blk < B_BLOCKS)
+      dma16(b_off[c], b_base + (int64_t)kt * (kBK / 2), slot_of(kt) + (uint32_t)(A_BYTES + blk * 1024));
+  };
+  auto dma_s = [&](int kt) {
+    if (wave < S_WAVES) dma4(s_off, s_base + kt / spg, slot_of(kt) + (uint32_t)(A_BYTES + B_BYTES + wave * 256));
+  };
+
+  // ---- weight fragments of stage kt, expanded from the packed slot: column
+  // n = wc*48 + 16j + l%16, K chunk c = l/16 of each 64-K step, i.e. packed
+  // bytes 8c .. 8c+7 of the first (f0) and second (f1) 32-byte half of row n;
+  // INT4 -> 16*q int8 in natural K order.
+  const int fr_n = wc * WCOLS + (lane & 15), fr_c = lane >> 4;
+  const uint32_t fr0 = (uint32_t)(fr_n * 64 + 8 * (fr_c & 1) + (((fr_c >> 1) ^ ((fr_n >> 2) & 3)) << 4));
+  const uint32_t fr1 = (uint32_t)(fr_n * 64 + 8 * (fr_c & 1) + (((2 + (fr_c >> 1)) ^ ((fr_n >> 2) & 3)) << 4));
+  auto load_b = [&](int kt, int j, v4i& f0, v4i& f1) {
+    const char* pb = smem + (kt % NS) * SLOT + A_BYTES + j * 16 * 64;
+    const v2u q0 = *(const v2u*)(pb + fr0);
+    const v2u q1 = *(const v2u*)(pb + fr1);
+    uint32_t w[8];
+    unpack8_x16(q0.x, w[0], w[1]);
+    unpack8_x16(q0.y, w[2], w[3]);
+    unpack8_x16(q1.x, w[4], w[5]);
+    unpack8_x16(q1.y, w[6], w[7]);
+    f0 = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+    f1 = v4i{(int)w[4], (int)w[5], (int)w[6], (int)w[7]};
+  };
+
+  // scales of stage kt for this lane's three columns; the MFMAs sum 16 * q
+  auto read_scales = [&](int kt, float* sw) {
+    const float* sS = (const float*)(smem + (kt % NS) * SLOT + A_BYTES + B_BYTES);
+#pragma unroll
+    for (int j = 0; j < TNB; ++j) sw[j] = sS[wc * WCOLS + 16 * j + (lane & 15)] * 0.0625f;
+  };
+
+  v4f facc[TMB][TNB];
+#pragma unroll
+  for (int i = 0; i < TMB; ++i)
+#pragma unroll
+    for (int j = 0; j < TNB; ++j) facc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // One stage.  Each 16 x 16 block takes both 64-K steps back to back (the
+  // second MFMA adds to the first), so its int32 group sum lives only until
+  // it is folded: facc = fma(f32(acc), s_w / 16, facc).  Only the fp32 sums
+  // stay resident; the group sums of two block rows are in flight, and the
+  // fold of row i-1 is issued among the MFMAs of row i, whose results it does
+  // not read.  A scheduling barrier per block row keeps the compiler from
+  // hoisting later rows' fragment loads (registers) above it.  Fragment rows
+  // 16 apart share their swizzle, so each operand and K-step needs one LDS
+  // address.  The next stage's DMAs are spread over the rows.
+  auto mfma_stage = [&](int kt) {
+    const bool more = kt + 1 < KT;  // uniform
+    float sw[TNB];
+    read_scales(kt, sw);
+    const char* aR0 = smem + (kt % NS) * SLOT + lds_off(wr * WROWS + (lane & 15), lane >> 4);
+    const char* aR1 = smem + (kt % NS) * SLOT + lds_off(wr * WROWS + (lane & 15), 4 + (lane >> 4));
+    v4i b0[TNB], b1[TNB];
+#pragma unroll
+    for (int j = 0; j < TNB; ++j) load_b(kt, j, b0[j], b1[j]);
+    v4i n0f = *(const v4i*)aR0, n1f = *(const v4i*)aR1;
+    v4i t[2][TNB];
+    // Empty volatile asm statements on the group sums before the fold and on
+    // the fp32 sums after it pin the fold to its block row: without them the
+    // compiler sinks every fold to the end of the stage and holds all 27
+    // group sums at once.
+    auto fold_row = [&](int i, v4i* tr) {
+#pragma unroll
+      for (int j = 0; j < TNB; ++j) {
+        asm volatile("" : "+v"(tr[j]));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) facc[i][j][r] = __builtin_fmaf((float)tr[j][r], sw[j], facc[i][j][r]);
+        asm volatile("" : "+v"(facc[i][j]));
+      }
+    };
+#pragma unroll
+    for (int i = 0; i < TMB; ++i) {
+      if (i == 0 || kPrio[i] != kPrio[i - 1]) {
+        switch (kPrio[i]) {
+          case 3: __builtin_amdgcn_s_setprio(3); break;
+          case 2: __builtin_amdgcn_s_setprio(2); break;
+          case 1: __builtin_amdgcn_s_setprio(1); break;
+          default: __builtin_amdgcn_s_setprio(0); break;
+        }
+      }
+      const v4i a0 = n0f, a1 = n1f;
+      if (i + 1 < TMB) {
+        n0f = *(const v4i*)(aR0 + (i + 1) * 16 * kBK);
+        n1f = *(const v4i*)(aR1 + (i + 1) * 16 * kBK);
+      }
+      v4i* tc = t[i & 1];
+#pragma unroll
+      for (int j = 0; j < TNB; ++j) tc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0[j], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < TNB; ++j) tc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1[j], tc[j], 0, 0, 0);
+      if (i > 0) fold_row(i - 1, t[(i - 1) & 1]);
+      if (more) {
+        if (i < A_PER) dma_a(kt + 1, i);
+        else if (i < A_PER + B_PER) dma_b(kt + 1, i - A_PER);
+        else if (i == A_PER + B_PER) dma_s(kt + 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    fold_row(TMB - 1, t[(TMB - 1) & 1]);
+  };
+
+  // ---- prologue: stage 0 in flight
+#pragma unroll
+  for (int c = 0; c < A_PER; ++c) dma_a(0, c);
+#pragma unroll
+  for (int c = 0; c < B_PER; ++c) dma_b(0, c);
+  dma_s(0);
+
+  for (int s = 0; s < KT; ++s) {
+    wait_vm<0>();
+    lds_barrier();  // stage s resident; every wave is done with stage s-1
+    mfma_stage(s);
+  }
+
+  // ---- epilogue: finish in registers, stage the tile through LDS row-major,
+  // write whole rows with 16-byte stores (the host picks this kernel only for
+  // 16-byte aligned outputs and residuals).
+  constexpr int RS = EPI_RS;
+  constexpr int CPR = BN / 8;
+  lds_barrier();
+  u16* ot = (u16*)smem;
+  float* sa_l = (float*)(smem + BM * RS * 2);
+  float* b_l = sa_l + BM;
+  bool res_lds = false;
+  if constexpr (EPI) {
+    res_lds = epi.res != nullptr;
+    if (res_lds) {
+      for (int c = tid; c < BM * CPR; c += kNT) {
+        const int row = c / CPR, col = (c % CPR) * 8;
+        const int m = m0 + row, n = n0 + col;
+        if (m < M && n < N)
+          *(v4u*)(ot + row * RS + col) = *(const v4u*)((const u16*)epi.res + (int64_t)m * epi.ldr + n);
+      }
+    }
+  }
+  for (int t = tid; t < BM; t += kNT) sa_l[t] = s_a[min(m0 + t, M - 1)];
+  for (int t = tid; t < BN; t += kNT) b_l[t] = bias != nullptr ? ld_any_f32(bias, bias_dt, min(n0 + t, N - 1)) : 0.0f;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < TNB; ++j) {
+    const int nl = wc * WCOLS + 16 * j + (lane & 15);
+    const float b = b_l[nl];
+#pragma unroll
+    for (int i = 0; i < TMB; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int ml = wr * WROWS + 16 * i + 4 * (lane >> 4) + r;
+        float v = facc[i][j][r] * sa_l[ml];
+        if (bias != nullptr) v = v + b;
+        if constexpr (EPI) {
+          v = epi_act(v, epi.act);
+          if (res_lds) {
+            const u16 rv = ot[ml * RS + nl];
+            v = v + (epi.res_dt == IC_DTYPE_F16 ? f16_to_f32(rv) : bf16_to_f32(rv));
+          }
+        }
+        u16 h;
+        if constexpr (OUT_DT == IC_DTYPE_F16) h = f32_to_f16(v);
+        else h = f32_to_bf16(v);
+        ot[ml * RS + nl] = h;
+      }
+      if constexpr (EPI) __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  __syncthreads();
+#pragma unroll 4
+  for (int c = tid; c < BM * CPR; c += kNT) {
+    const int row = c / CPR, col = (c % CPR) * 8;
+    const int m = m0 + row, n = n0 + col;
+    if (m < M && n < N) *(v4u*)((u16*)C + (int64_t)m * ldc + n) = *(const v4u*)(ot + row * RS + col);
+  }
+}
+
+}  // namespace

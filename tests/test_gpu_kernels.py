@@ -644,6 +644,36 @@ def test_wide_rows_prep_f32_and_old_smooth(rt, oracle, dev):
     assert np.abs(q.cpu().numpy().astype(int) - q_ref.astype(int)).max() <= 1
 
 
+# ------------------------------------------------------------------ 288 x 192 grouped INT4 tiles
+# Shapes whose 256 x 128 tiling ends in a partly filled round of workgroups
+# on 256 CUs and whose 288 x 192 tiling takes fewer rounds: the library runs
+# them on gemm_w4g_big_kernel (16-bit outputs).  C3 itself, and a shape
+# partial in both M and N with 128- and 256-column groups.
+BIG_TILE_CASES = [(4608, 3072, 12288, 128), (4600, 3064, 1024, 128), (4600, 3064, 1024, 256)]
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,N,K,gs", BIG_TILE_CASES)
+def test_w4a8_big_tile_sampled_rows(rt, oracle, dev, out_dtype, M, N, K, gs):
+    """Grouped W4A8 on the 288 x 192 tiles: every column of sampled rows
+    (first and last rows of tiles, the partial last tile row) bit-exact
+    against the oracle's accumulators and epilogue."""
+    G = K // gs
+    a = _int8((M, K), 91, -127, 128)
+    w = torch.randint(0, 256, (N, K // 2), generator=_gen(92), dtype=torch.uint8)
+    s_a = torch.rand(M, generator=_gen(93)) * 0.05 + 1e-3
+    s_w = (torch.rand(N, G, generator=_gen(94)) * 2e-2 + 1e-3).to(torch.float16).float()
+    bias = torch.randn(N, generator=_gen(95)).to(out_dtype)
+    assert rt.lib().ic_gemm_splitk_bytes(M, N, K, G, 1) == 0
+    out = rt.gemm_w4a8(a.to(dev), w.to(dev), s_w.to(dev), s_a.to(dev), bias=bias.to(dev), out_dtype=out_dtype)
+    out = out.float().cpu()
+    rows = torch.tensor(sorted({0, 1, 143, 144, 287, 288, 2 * 288 + 77, M // 2, (M - 1) // 288 * 288, M - 2, M - 1}))
+    acc = oracle.gemm_acc(a[rows].numpy(), oracle.unpack_int4(w.numpy(), K), K // 128)
+    sw = np.repeat(s_w.numpy(), gs // 128, axis=1)
+    ref = torch.from_numpy(oracle.epilogue(acc, s_a[rows].numpy(), sw, bias.float().numpy(), DT[out_dtype]))
+    assert torch.equal(out[rows], ref)
+
+
 # ------------------------------------------------------------------ group sizes other than 128
 @pytest.mark.parametrize("gs", [256, 512, 64])
 @pytest.mark.parametrize("M,N,K", [(300, 384, 2048), (64, 3072, 4096), (4608, 3072, 1024)])
