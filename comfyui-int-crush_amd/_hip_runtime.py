@@ -600,13 +600,15 @@ def fused_w4a8_gemm_dequant(x_int8, w_int8, s_w, s_a, bias=None, out_dtype=torch
 _SCALAR_WARNED: set = set()
 
 
-def _warn_if_scalar_gemm(who: str, K: int, G: int, *tensors: torch.Tensor) -> None:
+def _warn_if_scalar_gemm(who: str, K: int, G: int, *tensors: torch.Tensor, out64: bool = False) -> None:
     """The INT8 / W4A8 GEMMs run MFMA tiles only for K a multiple of 128,
-    group sizes that are multiples of 128 and 16-byte aligned operands and
-    row strides; anything else takes the scalar kernel (one thread per output,
-    ~100x slower).  Log that once per shape instead of running it silently."""
+    group sizes that are multiples of 128 (W4A8 also odd multiples of 64 when
+    out64: a 16-bit output whose rows and residual suit the 288 x 192 tile's
+    staged stores) and 16-byte aligned operands and row strides; anything else
+    takes the scalar kernel (one thread per output, ~100x slower).  Log that
+    once per shape instead of running it silently."""
     gs = K // G
-    ok = K % 128 == 0 and (G == 1 or gs % 128 == 0)
+    ok = K % 128 == 0 and (G == 1 or gs % 128 == 0 or (out64 and gs % 128 == 64))
     for t in tensors:
         ok = ok and t.data_ptr() % 16 == 0 and (t.dim() < 2 or (t.stride(0) * t.element_size()) % 16 == 0)
     key = (who, K, G)
@@ -643,7 +645,9 @@ def gemm_w4a8(x_int8: torch.Tensor, w_packed: torch.Tensor, s_w: torch.Tensor, s
     bp, bdt, _keep = _bias_args(bias, N)
     act, rp, rdt, ldr, _rkeep = _epilogue_args(activation, residual, M, N)
     c = _out_buffer(out, M, N, out_dtype, xq.device)
-    _warn_if_scalar_gemm("gemm_w4a8", K, G, xq, w)
+    out64 = (c.dtype != torch.float32 and N % 8 == 0 and c.data_ptr() % 16 == 0 and c.stride(0) % 8 == 0
+             and (rp is None or (rdt != 2 and (rp.value or 0) % 16 == 0 and ldr % 8 == 0)))
+    _warn_if_scalar_gemm("gemm_w4a8", K, G, xq, w, out64=out64)
     with torch.cuda.device(xq.device):
         ws, nb = _splitk_workspace(M, N, K, G, True, xq.device)
         _call("ic_gemm_w4a8_ex", _ptr(xq), M, K, xq.stride(0), _ptr(w), N, w.stride(0), _ptr(sw), G,

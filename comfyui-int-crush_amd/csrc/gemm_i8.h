@@ -653,8 +653,12 @@ __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(
   if (n >= N || m >= M) return;
   const int8_t* a = A + (int64_t)m * lda;
   const uint8_t* b = B + (int64_t)n * ldb;
+  // grouped scales fold once per block of gcd(group, 128) columns, as the
+  // MFMA kernels do (once per 128-column stage, or per 64-K step)
+  int fb = gsize, r128 = 128;
+  while (r128 != 0) { const int t = fb % r128; fb = r128; r128 = t; }
   float facc = 0.0f;
-  int acc = 0;
+  int acc = 0, acc_g = 0;
   for (int k = 0; k < K; ++k) {
     int w;
     if constexpr (INT4) {
@@ -663,12 +667,19 @@ __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(
     } else {
       w = (int8_t)b[k];
     }
-    acc += (int)a[k] * w;
-    if (G > 1 && ((k + 1) % gsize == 0 || k + 1 == K)) {
+    const int p = (int)a[k] * w;
+    acc += p;
+    if (G > 1) {
+      acc_g += p;
       const int g = k / gsize;
-      if (acc_out) acc_out[((int64_t)g * M + m) * N + n] = acc;
-      facc = __builtin_fmaf((float)acc, s_w[(int64_t)n * G + g], facc);
-      acc = 0;
+      if ((k + 1) % fb == 0 || k + 1 == K) {
+        facc = __builtin_fmaf((float)acc, s_w[(int64_t)n * G + g], facc);
+        acc = 0;
+      }
+      if ((k + 1) % gsize == 0 || k + 1 == K) {
+        if (acc_out) acc_out[((int64_t)g * M + m) * N + n] = acc_g;
+        acc_g = 0;
+      }
     }
   }
   if (G <= 1 && acc_out) acc_out[(int64_t)m * N + n] = acc;
@@ -788,6 +799,14 @@ hipError_t launch_mfma(const GemmArgs& g, hipStream_t st) {
   return launch_kernel<TL, OUT_DT, ACC, false, EPI>(g, 1, st);
 }
 
+// Staged 16-bit output path of gemm_w4g_big_kernel: output (and residual)
+// 16-byte aligned, row strides and N multiples of 8.
+bool big_out_ok(const GemmArgs& g) {
+  if (g.out_dt == IC_DTYPE_F32 || (((uintptr_t)g.C) & 15) != 0 || (g.ldc & 7) != 0 || (g.N & 7) != 0) return false;
+  return g.epi.res == nullptr ||
+         (g.epi.res_dt != IC_DTYPE_F32 && (((uintptr_t)g.epi.res) & 15) == 0 && (g.epi.ldr & 7) == 0);
+}
+
 // Grouped INT4 on 288 x 192 tiles (gemm_w4g_big_kernel) where their rounds of
 // workgroups cost less than 256 x 128's: 4608 x 3072 (the Flux MLP-down and
 // attention-projection shapes) fills the 256 CUs in one round of 256 tiles
@@ -795,23 +814,21 @@ hipError_t launch_mfma(const GemmArgs& g, hipStream_t st) {
 // staging tile only, so the output (and a residual) must be 16-byte aligned
 // with row strides and N multiples of 8.
 bool big_tile_ok(const GemmArgs& g) {
-  if (g.M <= 128 || (((uintptr_t)g.C) & 15) != 0 || (g.ldc & 7) != 0 || (g.N & 7) != 0) return false;
-  if (g.epi.res != nullptr &&
-      (g.epi.res_dt == IC_DTYPE_F32 || (((uintptr_t)g.epi.res) & 15) != 0 || (g.epi.ldr & 7) != 0))
-    return false;
+  if (g.M <= 128 || !big_out_ok(g)) return false;
   // per output the 288 x 192 tile costs ~0.93 of 256 x 128 (Wan FFN-down,
   // 32760 x 5120 x 14336: 13 rounds of it took as long as 20 of 256 x 128)
   return tiling_cost(g, big::BM, big::BN, 93) < tiling_cost(g, 256, 128);
 }
 
-template <int OUT_DT, bool EPI>
+template <int OUT_DT, bool EPI, bool F64>
 hipError_t launch_big(const GemmArgs& g, hipStream_t st) {
   const int tiles = ((g.M + big::BM - 1) / big::BM) * ((g.N + big::BN - 1) / big::BN);
-  auto kern = gemm_w4g_big_kernel<OUT_DT, EPI>;
+  auto kern = gemm_w4g_big_kernel<OUT_DT, EPI, F64>;
+  constexpr size_t shm = big::lds_bytes(F64);
   static unsigned char lds_set[64];  // per device
-  if (hipError_t e = ic_set_lds_limit((const void*)kern, (int)big::lds_bytes, lds_set)) return e;
-  kern<<<dim3(tiles), dim3(kNT), big::lds_bytes, st>>>(g.A, g.lda, g.B, g.ldb, g.s_a, g.s_w, g.G, g.bias,
-                                                       g.bias_dt, g.C, g.ldc, g.M, g.N, g.K, g.epi);
+  if (hipError_t e = ic_set_lds_limit((const void*)kern, (int)shm, lds_set)) return e;
+  kern<<<dim3(tiles), dim3(kNT), shm, st>>>(g.A, g.lda, g.B, g.ldb, g.s_a, g.s_w, g.G, g.bias, g.bias_dt, g.C,
+                                            g.ldc, g.M, g.N, g.K, g.epi);
   return hipGetLastError();
 }
 
@@ -819,7 +836,7 @@ template <bool INT4, int GS, int OUT_DT, bool ACC, bool EPI>
 hipError_t pick_tile(const GemmArgs& g, hipStream_t st) {
   const TileShape t = tile_choice(g, GS != 0);
   if constexpr (INT4 && GS != 0 && !ACC && OUT_DT != IC_DTYPE_F32) {
-    if (big_tile_ok(g)) return launch_big<OUT_DT, EPI>(g, st);
+    if (big_tile_ok(g)) return launch_big<OUT_DT, EPI, false>(g, st);
   }
   if constexpr (!INT4 && GS == 0) {
     if (t.bm == 256 && t.bn == 192) return launch_mfma<Tile<256, 192, 4, 2, false, 0>, OUT_DT, ACC, EPI>(g, st);
@@ -868,6 +885,16 @@ bool mfma_shape_ok(const GemmArgs& g, int gsize) {
   // rows are read 8 or 16 bytes at a time
   if (((uintptr_t)g.A & 15) || ((uintptr_t)g.B & 15) || (g.lda & 15) || (g.ldb & 15)) return false;
   return true;
+}
+
+// Packed INT4 with groups of 64 or an odd multiple of 64 columns (the
+// 128-column stages of the other MFMA kernels would straddle groups): the
+// 288 x 192 kernel in its 64-block mode, when its operand and output layouts
+// hold.  The debug accumulator output is not written by it.
+bool big64_ok(const GemmArgs& g, int gsize) {
+  if (!g.int4 || g.G <= 1 || gsize % 128 != 64 || g.K % kBK != 0 || g.acc_out != nullptr) return false;
+  if (((uintptr_t)g.A & 15) || ((uintptr_t)g.B & 15) || (g.lda & 15) || (g.ldb & 15)) return false;
+  return big_out_ok(g);
 }
 
 // Chained MLP epilogue launches (gemm_i8_chain.hip): 128 x 256 tiles, whose
@@ -924,7 +951,12 @@ int run_gemm_t(GemmArgs g, hipStream_t st, const char* who, bool force_generic) 
     return ic_set_error(IC_ERR_INVALID_ARG, "%s: null pointer argument", who);
   const int gsize = g.K / g.G;
   hipError_t e;
-  if (!force_generic && mfma_shape_ok(g, gsize)) {
+  if (!force_generic && big64_ok(g, gsize)) {
+    // groups of 64 (or an odd multiple of 64) columns: the 288 x 192 kernel
+    // folding each 64-K step, at any M
+    if (g.out_dt == IC_DTYPE_F16) e = launch_big<IC_DTYPE_F16, EPI, true>(g, st);
+    else e = launch_big<IC_DTYPE_BF16, EPI, true>(g, st);
+  } else if (!force_generic && mfma_shape_ok(g, gsize)) {
     if constexpr (EPI) {
       // the epilogue options never come with the debug accumulator output
       if (g.int4) e = g.G > 1 ? pick_out<true, 128, false, true>(g, st) : pick_out<true, 0, false, true>(g, st);

@@ -55,24 +55,31 @@ constexpr int TMB = 9, TNB = 3;              // 16 x 16 blocks per wave
 constexpr int WROWS = TMB * 16, WCOLS = TNB * 16;
 constexpr int A_BYTES = BM * kBK;            // 36864
 constexpr int B_BYTES = BN * kBK / 2;        // 12288, packed nibbles
-constexpr int S_BYTES = BN * 4;              // one fp32 scale per column
-constexpr int SLOT = A_BYTES + B_BYTES + S_BYTES;
+constexpr int S_BYTES = BN * 4;              // one fp32 scale per column and scale block
 constexpr int A_BLOCKS = BM / 8;             // 1 KB DMA blocks: 8 rows of 128 bytes
 constexpr int B_BLOCKS = BN / 16;            // 1 KB DMA blocks: 16 rows of 64 bytes
 constexpr int A_PER = (A_BLOCKS + 7) / 8;    // blocks per wave (waves 0-3 take one more)
 constexpr int B_PER = (B_BLOCKS + 7) / 8;
 constexpr int S_WAVES = BN / 64;             // waves issuing a scale DMA
 constexpr int EPI_RS = BN + 8;               // 16-bit output staging row stride
-constexpr size_t ring_bytes = (size_t)NS * SLOT;
+// ring slot: activations, packed weights, then one (scale blocks of 128
+// columns) or two (of 64) scale rows
+constexpr int slot_bytes(bool f64) { return A_BYTES + B_BYTES + (f64 ? 2 : 1) * S_BYTES; }
 constexpr size_t epi_bytes = (size_t)BM * EPI_RS * 2 + (size_t)(BM + BN) * 4;
-constexpr size_t lds_bytes = ring_bytes > epi_bytes ? ring_bytes : epi_bytes;
+constexpr size_t lds_bytes(bool f64) {
+  return (size_t)NS * slot_bytes(f64) > epi_bytes ? (size_t)NS * slot_bytes(f64) : epi_bytes;
+}
 constexpr int kPrio[TMB] = {3, 3, 2, 2, 1, 1, 0, 0, 0};  // wave priority per block row
-static_assert(SLOT % 16 == 0 && lds_bytes <= 160 * 1024, "LDS layout");
+static_assert(slot_bytes(true) % 16 == 0 && lds_bytes(true) <= 160 * 1024, "LDS layout");
 static_assert(2 * WROWS == BM && 4 * WCOLS == BN, "wave grid");
-static_assert(A_PER + B_PER + 1 <= TMB, "one DMA slot per block row");
+static_assert(A_PER + B_PER <= TMB, "one DMA slot per block row");
 }  // namespace big
 
-template <int OUT_DT, bool EPI>
+// F64: groups of 64 columns, or of an odd multiple of 64 (gcd(group, 128)
+// = 64): each 64-K step is folded by itself, with the scale of its group, so
+// a stage folds twice.  Otherwise (group sizes that are multiples of 128)
+// each 128-column stage is folded once with its group's scale.
+template <int OUT_DT, bool EPI, bool F64>
 __global__ __launch_bounds__(kNT, 1) void gemm_w4g_big_kernel(
     const int8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
     const float* __restrict__ s_a, const float* __restrict__ s_w, int G,
@@ -80,6 +87,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4g_big_kernel(
     int K, ic_epi epi) {
   using namespace big;
   static_assert(OUT_DT != IC_DTYPE_F32, "16-bit outputs only");
+  constexpr int SLOT = slot_bytes(F64);
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_char*)smem;
 
@@ -92,7 +100,8 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4g_big_kernel(
   tile_coords(blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int KT = K / kBK;
-  const int spg = (K / G) / kBK;  // stages per scale group
+  // scale blocks (of 128 or 64 columns) per group
+  const int bpg = (K / G) / (F64 ? 64 : kBK);
 
   // ---- DMA addressing (rows past M or N re-read the last row; never stored).
   // A block b: LDS rows 8b + l/8, chunk slot l%8 holding global chunk
@@ -127,7 +136,14 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4g_big_kernel(
       dma16(b_off[c], b_base + (int64_t)kt * (kBK / 2), slot_of(kt) + (uint32_t)(A_BYTES + blk * 1024));
   };
   auto dma_s = [&](int kt) {
-    if (wave < S_WAVES) dma4(s_off, s_base + kt / spg, slot_of(kt) + (uint32_t)(A_BYTES + B_BYTES + wave * 256));
+    if (wave < S_WAVES) {
+      if constexpr (F64) {
+        dma4(s_off, s_base + (2 * kt) / bpg, slot_of(kt) + (uint32_t)(A_BYTES + B_BYTES + wave * 256));
+        dma4(s_off, s_base + (2 * kt + 1) / bpg, slot_of(kt) + (uint32_t)(A_BYTES + B_BYTES + S_BYTES + wave * 256));
+      } else {
+        dma4(s_off, s_base + kt / bpg, slot_of(kt) + (uint32_t)(A_BYTES + B_BYTES + wave * 256));
+      }
+    }
   };
 
   // ---- weight fragments of stage kt, expanded from the packed slot: column
@@ -151,8 +167,8 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4g_big_kernel(
   };
 
   // scales of stage kt for this lane's three columns; the MFMAs sum 16 * q
-  auto read_scales = [&](int kt, float* sw) {
-    const float* sS = (const float*)(smem + (kt % NS) * SLOT + A_BYTES + B_BYTES);
+  auto read_scales = [&](int kt, int h, float* sw) {
+    const float* sS = (const float*)(smem + (kt % NS) * SLOT + A_BYTES + B_BYTES + h * S_BYTES);
 #pragma unroll
     for (int j = 0; j < TNB; ++j) sw[j] = sS[wc * WCOLS + 16 * j + (lane & 15)] * 0.0625f;
   };
@@ -174,25 +190,31 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4g_big_kernel(
   // address.  The next stage's DMAs are spread over the rows.
   auto mfma_stage = [&](int kt) {
     const bool more = kt + 1 < KT;  // uniform
-    float sw[TNB];
-    read_scales(kt, sw);
+    float sw[TNB], sw1[TNB];
+    read_scales(kt, 0, sw);
+    if constexpr (F64) read_scales(kt, 1, sw1);
     const char* aR0 = smem + (kt % NS) * SLOT + lds_off(wr * WROWS + (lane & 15), lane >> 4);
     const char* aR1 = smem + (kt % NS) * SLOT + lds_off(wr * WROWS + (lane & 15), 4 + (lane >> 4));
     v4i b0[TNB], b1[TNB];
 #pragma unroll
     for (int j = 0; j < TNB; ++j) load_b(kt, j, b0[j], b1[j]);
     v4i n0f = *(const v4i*)aR0, n1f = *(const v4i*)aR1;
-    v4i t[2][TNB];
+    v4i t[2][TNB], t1[F64 ? 2 : 1][TNB];
     // Empty volatile asm statements on the group sums before the fold and on
     // the fp32 sums after it pin the fold to its block row: without them the
     // compiler sinks every fold to the end of the stage and holds all 27
     // group sums at once.
-    auto fold_row = [&](int i, v4i* tr) {
+    auto fold_row = [&](int i, v4i* tr, v4i* tr1) {
 #pragma unroll
       for (int j = 0; j < TNB; ++j) {
         asm volatile("" : "+v"(tr[j]));
 #pragma unroll
         for (int r = 0; r < 4; ++r) facc[i][j][r] = __builtin_fmaf((float)tr[j][r], sw[j], facc[i][j][r]);
+        if constexpr (F64) {
+          asm volatile("" : "+v"(tr1[j]));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) facc[i][j][r] = __builtin_fmaf((float)tr1[j][r], sw1[j], facc[i][j][r]);
+        }
         asm volatile("" : "+v"(facc[i][j]));
       }
     };
@@ -212,19 +234,25 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4g_big_kernel(
         n1f = *(const v4i*)(aR1 + (i + 1) * 16 * kBK);
       }
       v4i* tc = t[i & 1];
+      v4i* tc1 = t1[F64 ? (i & 1) : 0];
 #pragma unroll
       for (int j = 0; j < TNB; ++j) tc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0[j], v4i{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-      for (int j = 0; j < TNB; ++j) tc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1[j], tc[j], 0, 0, 0);
-      if (i > 0) fold_row(i - 1, t[(i - 1) & 1]);
+      for (int j = 0; j < TNB; ++j) {
+        if constexpr (F64) tc1[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1[j], v4i{0, 0, 0, 0}, 0, 0, 0);
+        else tc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1[j], tc[j], 0, 0, 0);
+      }
+      if (i > 0) fold_row(i - 1, t[(i - 1) & 1], t1[F64 ? ((i - 1) & 1) : 0]);
       if (more) {
+        // scales first: issued last, their wait at the next stage showed
+        // (~180 clocks per stage on the three waves that fetch them)
+        if (i == 0) dma_s(kt + 1);
         if (i < A_PER) dma_a(kt + 1, i);
         else if (i < A_PER + B_PER) dma_b(kt + 1, i - A_PER);
-        else if (i == A_PER + B_PER) dma_s(kt + 1);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    fold_row(TMB - 1, t[(TMB - 1) & 1]);
+    fold_row(TMB - 1, t[(TMB - 1) & 1], t1[F64 ? ((TMB - 1) & 1) : 0]);
   };
 
   // ---- prologue: stage 0 in flight

@@ -7,6 +7,8 @@ fp32 dequant -> F.linear fallback.
 """
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -675,14 +677,18 @@ def test_w4a8_big_tile_sampled_rows(rt, oracle, dev, out_dtype, M, N, K, gs):
 
 
 # ------------------------------------------------------------------ group sizes other than 128
-@pytest.mark.parametrize("gs", [256, 512, 64])
-@pytest.mark.parametrize("M,N,K", [(300, 384, 2048), (64, 3072, 4096), (4608, 3072, 1024)])
+@pytest.mark.parametrize("gs", [256, 512, 64, 192])
+@pytest.mark.parametrize("M,N,K", [(300, 384, 2048), (64, 3072, 4096), (4608, 3072, 1024), (600, 1000, 1536)])
 def test_w4a8_group_sizes(rt, oracle, dev, gs, M, N, K):
-    """Group sizes 256 / 512 run the MFMA kernels (tiled and split-K), folding
-    each 128-column part with its group's scale: bit-exact against the
-    oracle's epilogue over 128-column accumulators with the scales repeated.
-    Group size 64 runs the scalar kernel: bit-exact against the 64-group fold."""
+    """Group sizes other than 128 run the MFMA kernels: multiples of 128
+    (tiled and split-K) fold each 128-column stage, odd multiples of 64 (the
+    288 x 192 kernel's 64-block mode) each 64-K step, with the scale of the
+    step's group.  Bit-exact against the oracle's epilogue over accumulators
+    of gcd(group, 128) columns with the scales repeated."""
+    if K % gs:
+        pytest.skip("K not a multiple of the group size")
     G = K // gs
+    fb = math.gcd(gs, 128)
     a = _int8((M, K), 81, -127, 128)
     w = torch.randint(0, 256, (N, K // 2), generator=_gen(82), dtype=torch.uint8)
     s_a = torch.rand(M, generator=_gen(83)) * 0.05 + 1e-3
@@ -692,12 +698,8 @@ def test_w4a8_group_sizes(rt, oracle, dev, gs, M, N, K):
     out = out.float().cpu()
     wq = oracle.unpack_int4(w.numpy(), K)
     rows = torch.tensor(sorted({0, 1, M // 2, M - 1}))
-    if gs >= 128:
-        acc = oracle.gemm_acc(a[rows].numpy(), wq, K // 128)
-        sw = np.repeat(s_w.numpy(), gs // 128, axis=1)
-    else:
-        acc = oracle.gemm_acc(a[rows].numpy(), wq, G)
-        sw = s_w.numpy()
+    acc = oracle.gemm_acc(a[rows].numpy(), wq, K // fb)
+    sw = np.repeat(s_w.numpy(), gs // fb, axis=1)
     ref = torch.from_numpy(oracle.epilogue(acc, s_a[rows].numpy(), sw, bias.float().numpy(), 1))
     split = rt.lib().ic_gemm_splitk_bytes(M, N, K, G, 1) > 0
     if not split:
@@ -705,6 +707,27 @@ def test_w4a8_group_sizes(rt, oracle, dev, gs, M, N, K):
     else:  # slices of the fold added in slice order (bounded in test_splitk_grouped_w4a8)
         assert _cos(out[rows], ref) >= 0.99999
         assert torch.allclose(out[rows], ref, rtol=1e-2, atol=1e-2 * ref.abs().max().item())
+
+
+@pytest.mark.parametrize("gs", [256, 64, 96])
+def test_w4a8_scalar_kernel_fold_blocks(rt, oracle, dev, gs):
+    """Operands the MFMA tiles cannot take (a 1-byte offset activation view)
+    run the scalar kernel, which folds per gcd(group, 128) columns like the
+    MFMA kernels: bit-exact against the oracle's blocked epilogue."""
+    M, N, K = 40, 200, 768
+    G = K // gs
+    fb = math.gcd(gs, 128)
+    base = _int8((M, K + 1), 86, -127, 128)
+    a = base[:, 1:]
+    w = torch.randint(0, 256, (N, K // 2), generator=_gen(87), dtype=torch.uint8)
+    s_a = torch.rand(M, generator=_gen(88)) * 0.05 + 1e-3
+    s_w = (torch.rand(N, G, generator=_gen(89)) * 2e-2 + 1e-3).to(torch.float16).float()
+    xa = base.to(dev)[:, 1:]
+    assert xa.data_ptr() % 16 != 0
+    out = rt.gemm_w4a8(xa, w.to(dev), s_w.to(dev), s_a.to(dev), out_dtype=torch.float32).cpu()
+    acc = oracle.gemm_acc(np.ascontiguousarray(a.numpy()), oracle.unpack_int4(w.numpy(), K), K // fb)
+    ref = oracle.epilogue(acc, s_a.numpy(), np.repeat(s_w.numpy(), gs // fb, axis=1), None, 2)
+    assert np.array_equal(out.numpy(), ref)
 
 
 @pytest.mark.parametrize("G", [48, 12])  # group sizes 64 and 256 at K = 3072
