@@ -67,12 +67,16 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4a16_kernel(
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int A_DMA = BM / 64;         // 1 KB DMA blocks of A per wave per stage
-  constexpr int B_DMA = BN * 32 / 8192;  // same for the packed weights
+  constexpr int B_BLK = BN * 32 / 1024;  // 1 KB blocks of packed weights per stage
+  constexpr int B_DMA = (B_BLK + 7) / 8; // per wave (the first B_BLK % 8 waves take one more)
   constexpr int S_WAVES = BN / 64;       // waves issuing one scale DMA per stage
   constexpr int D = A_DMA + B_DMA;
   constexpr int kParts = 4;              // DMA slices per stage (one per MFMA K-step)
-  static_assert(TM >= 1 && TN >= 1 && A_DMA >= 1 && B_DMA >= 1 && BN * 32 % 8192 == 0, "tile shape");
-  static_assert(BN * 32 == kNT * 16, "one packed 16-byte chunk per thread and stage");
+  constexpr int PKC = BN * 2;            // packed 16-byte chunks dequantized per stage
+  static_assert(TM >= 1 && TN >= 1 && A_DMA >= 1 && BM % 64 == 0 && BN % 32 == 0, "tile shape");
+  static_assert(PKC % kNT == 0 || (B_BLK % 8 != 0 && NS == 2 && PKC % 64 == 0 && PKC < 2 * kNT),
+                "dequant split: whole chunks per thread, or whole waves of chunks with a two-slot ring "
+                "(the waits are then vmcnt(0))");
   static_assert(NS >= 2 && S_WAVES <= 8, "ring depth");
 
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -123,7 +127,8 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4a16_kernel(
     const uint8_t* bb = b_base + (int64_t)kt * 32;
 #pragma unroll
     for (int c = 0; c < B_DMA; ++c)
-      if ((A_DMA + c) % kParts == part) dma16(b_off[c], bb, slot + (uint32_t)(TL::A_BYTES + (wave + 8 * c) * 1024));
+      if ((A_DMA + c) % kParts == part && (B_BLK % 8 == 0 || wave + 8 * c < B_BLK))  // wave-uniform
+        dma16(b_off[c], bb, slot + (uint32_t)(TL::A_BYTES + (wave + 8 * c) * 1024));
     if (part == kParts - 1 && s_wave) {
       const int g = G > 1 ? (kt * 64) / gsize : 0;
       dma4(s_off, s_base + g, slot + (uint32_t)(TL::A_BYTES + TL::B_BYTES + wave * 256));
@@ -147,16 +152,21 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4a16_kernel(
   // the dequantization of step s)
   auto dequant = [&](int kt) {
     const char* slot = smem + (kt % NS) * TL::SLOT;
-    const int row = tid >> 1, part = tid & 1;
-    const v4u p = *(const v4u*)(slot + TL::A_BYTES + tid * 16);
-    const DeqScale d = deq_scale<DT>(((const float*)(slot + TL::A_BYTES + TL::B_BYTES))[row]);
     char* bu = smem + NS * TL::SLOT;
-    const uint32_t pw[4] = {p.x, p.y, p.z, p.w};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint32_t o[4];
-      deq8<DT>(pw[i], d, o);
-      *(v4u*)(bu + lds_off(row, 4 * part + i)) = v4u{o[0], o[1], o[2], o[3]};
+    for (int h = 0; h < (PKC + kNT - 1) / kNT; ++h) {
+      const int idx = tid + kNT * h;  // packed chunk: row idx/2, half idx%2
+      if (PKC % kNT != 0 && idx >= PKC) break;  // wave-uniform (whole waves past the end)
+      const int row = idx >> 1, part = idx & 1;
+      const v4u p = *(const v4u*)(slot + TL::A_BYTES + idx * 16);
+      const DeqScale d = deq_scale<DT>(((const float*)(slot + TL::A_BYTES + TL::B_BYTES))[row]);
+      const uint32_t pw[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t o[4];
+        deq8<DT>(pw[i], d, o);
+        *(v4u*)(bu + lds_off(row, 4 * part + i)) = v4u{o[0], o[1], o[2], o[3]};
+      }
     }
   };
 
@@ -297,7 +307,21 @@ hipError_t run_w4a16(const u16* A, int64_t lda, const uint8_t* B, int64_t ldb, c
                      int gsize, const void* bias, int bias_dt, u16* C, int64_t ldc, int M, int N, int K,
                      bool mfma_ok, hipStream_t st) {
   if (mfma_ok) {
-    if (M > 128) return launch_w4a16<WTile<256, 256, 2, 3>, DT>(A, lda, B, ldb, s_w, G, gsize, bias, bias_dt, C, ldc, M, N, K, st);
+    if (M > 128) {
+      // rounds of workgroups x tile area x relative cost per output: 384 x 192 tiles (wave tiles of
+      // 96 x 96, a two-slot ring) where they fill the CUs in fewer rounds, e.g. 4608 x 12288: 768
+      // tiles, three rounds, against 864 of 256 x 256 (four).  Per output they cost ~5 % more than
+      // 256 x 256 (more activation bytes per stage), but dequantize fewer weights per output than
+      // the 192 x 384 tile of the same area, which measured 11 % slower at that shape.
+      const int64_t cus = ic_num_cus();
+      auto cost = [&](int bm, int bn, int pct) {
+        const int64_t t = (int64_t)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+        return (t + cus - 1) / cus * bm * bn * pct;
+      };
+      if (cost(384, 192, 105) < cost(256, 256, 100))
+        return launch_w4a16<WTile<384, 192, 4, 2>, DT>(A, lda, B, ldb, s_w, G, gsize, bias, bias_dt, C, ldc, M, N, K, st);
+      return launch_w4a16<WTile<256, 256, 2, 3>, DT>(A, lda, B, ldb, s_w, G, gsize, bias, bias_dt, C, ldc, M, N, K, st);
+    }
     return launch_w4a16<WTile<128, 256, 2, 4>, DT>(A, lda, B, ldb, s_w, G, gsize, bias, bias_dt, C, ldc, M, N, K, st);
   }
   dim3 grid((unsigned)((N + 255) / 256), (unsigned)M);
