@@ -813,23 +813,34 @@ bool big_out_ok(const GemmArgs& g) {
 // instead of two of 432.  That kernel writes 16-bit outputs through its LDS
 // staging tile only, so the output (and a residual) must be 16-byte aligned
 // with row strides and N multiples of 8.
+// Its two row counts: 288 (9 blocks of 16 rows per wave) and 256 (8), whichever
+// takes fewer rounds x area (4096 rows: 16 tiles of 256 instead of 15 of 288).
+int big_rows(const GemmArgs& g) {
+  return tiling_cost(g, 256, big::BN) < tiling_cost(g, 288, big::BN) ? 8 : 9;
+}
 bool big_tile_ok(const GemmArgs& g) {
   if (g.M <= 128 || !big_out_ok(g)) return false;
   // per output the 288 x 192 tile costs ~0.93 of 256 x 128 (Wan FFN-down,
   // 32760 x 5120 x 14336: 13 rounds of it took as long as 20 of 256 x 128)
-  return tiling_cost(g, big::BM, big::BN, 93) < tiling_cost(g, 256, 128);
+  const int bm = 16 * 2 * big_rows(g);
+  return tiling_cost(g, bm, big::BN, 93) < tiling_cost(g, 256, 128);
 }
 
-template <int OUT_DT, bool EPI, bool F64>
-hipError_t launch_big(const GemmArgs& g, hipStream_t st) {
-  const int tiles = ((g.M + big::BM - 1) / big::BM) * ((g.N + big::BN - 1) / big::BN);
-  auto kern = gemm_w4g_big_kernel<OUT_DT, EPI, F64>;
-  constexpr size_t shm = big::lds_bytes(F64);
+template <int OUT_DT, bool EPI, bool F64, int TMB>
+hipError_t launch_big_t(const GemmArgs& g, hipStream_t st) {
+  using RT = big::Rows<TMB>;
+  const int tiles = ((g.M + RT::BM - 1) / RT::BM) * ((g.N + big::BN - 1) / big::BN);
+  auto kern = gemm_w4g_big_kernel<OUT_DT, EPI, F64, TMB>;
+  constexpr size_t shm = RT::lds_bytes(F64);
   static unsigned char lds_set[64];  // per device
   if (hipError_t e = ic_set_lds_limit((const void*)kern, (int)shm, lds_set)) return e;
   kern<<<dim3(tiles), dim3(kNT), shm, st>>>(g.A, g.lda, g.B, g.ldb, g.s_a, g.s_w, g.G, g.bias, g.bias_dt, g.C,
                                             g.ldc, g.M, g.N, g.K, g.epi);
   return hipGetLastError();
+}
+template <int OUT_DT, bool EPI, bool F64>
+hipError_t launch_big(const GemmArgs& g, hipStream_t st) {
+  return big_rows(g) == 8 ? launch_big_t<OUT_DT, EPI, F64, 8>(g, st) : launch_big_t<OUT_DT, EPI, F64, 9>(g, st);
 }
 
 template <bool INT4, int GS, int OUT_DT, bool ACC, bool EPI>

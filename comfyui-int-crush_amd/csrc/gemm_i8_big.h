@@ -7,6 +7,9 @@
 // facc = fma(f32(acc_g), s_w[n, g] / 16, facc); out = facc * s_a[m] (+ bias),
 // rounded once.  Outputs are bit-identical to the 256 x 128 kernel.
 //
+// The row count is a template parameter: 288 (9 blocks of 16 rows per wave)
+// or 256 (8), whichever tiles M in fewer rounds (4096 rows: 16 tiles of 256).
+//
 // Why this tile: a round of workgroups costs the same whether all CUs are busy
 // or a few, and 4608 x 3072 (the Flux MLP-down / C3 shape) makes 432 tiles of
 // 256 x 128 on 256 CUs, 1.69 rounds paid as two.  4608 x 3072 / 256 CUs is
@@ -50,44 +53,55 @@
 
 namespace {
 namespace big {
-constexpr int BM = 288, BN = 192, NS = 2;
-constexpr int TMB = 9, TNB = 3;              // 16 x 16 blocks per wave
-constexpr int WROWS = TMB * 16, WCOLS = TNB * 16;
-constexpr int A_BYTES = BM * kBK;            // 36864
+constexpr int BN = 192, NS = 2;
+constexpr int TNB = 3;                       // 16 x 16 blocks per wave in N
+constexpr int WCOLS = TNB * 16;
 constexpr int B_BYTES = BN * kBK / 2;        // 12288, packed nibbles
 constexpr int S_BYTES = BN * 4;              // one fp32 scale per column and scale block
-constexpr int A_BLOCKS = BM / 8;             // 1 KB DMA blocks: 8 rows of 128 bytes
 constexpr int B_BLOCKS = BN / 16;            // 1 KB DMA blocks: 16 rows of 64 bytes
-constexpr int A_PER = (A_BLOCKS + 7) / 8;    // blocks per wave (waves 0-3 take one more)
 constexpr int B_PER = (B_BLOCKS + 7) / 8;
 constexpr int S_WAVES = BN / 64;             // waves issuing a scale DMA
 constexpr int EPI_RS = BN + 8;               // 16-bit output staging row stride
-// ring slot: activations, packed weights, then one (scale blocks of 128
-// columns) or two (of 64) scale rows
-constexpr int slot_bytes(bool f64) { return A_BYTES + B_BYTES + (f64 ? 2 : 1) * S_BYTES; }
-constexpr size_t epi_bytes = (size_t)BM * EPI_RS * 2 + (size_t)(BM + BN) * 4;
-constexpr size_t lds_bytes(bool f64) {
-  return (size_t)NS * slot_bytes(f64) > epi_bytes ? (size_t)NS * slot_bytes(f64) : epi_bytes;
-}
-constexpr int kPrio[TMB] = {3, 3, 2, 2, 1, 1, 0, 0, 0};  // wave priority per block row
-static_assert(slot_bytes(true) % 16 == 0 && lds_bytes(true) <= 160 * 1024, "LDS layout");
-static_assert(2 * WROWS == BM && 4 * WCOLS == BN, "wave grid");
-static_assert(A_PER + B_PER <= TMB, "one DMA slot per block row");
+// Tile rows: TMB 16-row blocks per wave, two wave rows (288 rows for TMB = 9,
+// 256 for TMB = 8)
+template <int TMB_>
+struct Rows {
+  static constexpr int TMB = TMB_;
+  static constexpr int BM = 32 * TMB, WROWS = 16 * TMB;
+  static constexpr int A_BYTES = BM * kBK;
+  static constexpr int A_BLOCKS = BM / 8;             // 1 KB DMA blocks: 8 rows of 128 bytes
+  static constexpr int A_PER = (A_BLOCKS + 7) / 8;    // blocks per wave
+  // ring slot: activations, packed weights, then one (scale blocks of 128
+  // columns) or two (of 64) scale rows
+  static constexpr int slot_bytes(bool f64) { return A_BYTES + B_BYTES + (f64 ? 2 : 1) * S_BYTES; }
+  static constexpr size_t epi_bytes = (size_t)BM * EPI_RS * 2 + (size_t)(BM + BN) * 4;
+  static constexpr size_t lds_bytes(bool f64) {
+    return (size_t)NS * slot_bytes(f64) > epi_bytes ? (size_t)NS * slot_bytes(f64) : epi_bytes;
+  }
+  // wave priority per block row: 3 3 2 2 1 1 0 0 ...
+  static constexpr int prio(int i) { return i < 6 ? 3 - i / 2 : 0; }
+  static_assert(slot_bytes(true) % 16 == 0 && lds_bytes(true) <= 160 * 1024, "LDS layout");
+  static_assert(4 * WCOLS == BN, "wave grid");
+  static_assert(A_PER + B_PER <= TMB, "one DMA slot per block row");
+};
 }  // namespace big
 
 // F64: groups of 64 columns, or of an odd multiple of 64 (gcd(group, 128)
 // = 64): each 64-K step is folded by itself, with the scale of its group, so
 // a stage folds twice.  Otherwise (group sizes that are multiples of 128)
 // each 128-column stage is folded once with its group's scale.
-template <int OUT_DT, bool EPI, bool F64>
+template <int OUT_DT, bool EPI, bool F64, int TMB>
 __global__ __launch_bounds__(kNT, 1) void gemm_w4g_big_kernel(
     const int8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
     const float* __restrict__ s_a, const float* __restrict__ s_w, int G,
     const void* __restrict__ bias, int bias_dt, void* __restrict__ C, int64_t ldc, int M, int N,
     int K, ic_epi epi) {
   using namespace big;
+  using RT = Rows<TMB>;
+  constexpr int BM = RT::BM, WROWS = RT::WROWS, A_BYTES = RT::A_BYTES, A_BLOCKS = RT::A_BLOCKS;
+  constexpr int A_PER = RT::A_PER;
   static_assert(OUT_DT != IC_DTYPE_F32, "16-bit outputs only");
-  constexpr int SLOT = slot_bytes(F64);
+  constexpr int SLOT = RT::slot_bytes(F64);
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_char*)smem;
 
@@ -220,8 +234,8 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4g_big_kernel(
     };
 #pragma unroll
     for (int i = 0; i < TMB; ++i) {
-      if (i == 0 || kPrio[i] != kPrio[i - 1]) {
-        switch (kPrio[i]) {
+      if (i == 0 || RT::prio(i) != RT::prio(i - 1)) {
+        switch (RT::prio(i)) {
           case 3: __builtin_amdgcn_s_setprio(3); break;
           case 2: __builtin_amdgcn_s_setprio(2); break;
           case 1: __builtin_amdgcn_s_setprio(1); break;
