@@ -120,6 +120,21 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
   int tm, tn;
   tile_coords(blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
+  // Operands of the staged 16-bit epilogue (activation scale of row m0 + tid,
+  // bias and per-row weight scale of column n0 + tid), loaded now so that
+  // their latency passes under the main loop instead of after it.
+  static_assert(BM <= kNT && BN <= kNT, "one epilogue operand per thread");
+  float pre_sa = 0.0f, pre_b = 0.0f, pre_sw = 0.0f;
+  if constexpr (OUT_DT != IC_DTYPE_F32 && !PART) {
+    if (C != nullptr) {
+      if (tid < BM) pre_sa = s_a[min(m0 + tid, M - 1)];
+      if (tid < BN) {
+        const int n = min(n0 + tid, N - 1);
+        if (bias != nullptr) pre_b = ld_any_f32(bias, bias_dt, n);
+        if constexpr (GS == 0) pre_sw = s_w[n];
+      }
+    }
+  }
   const int KT_all = K / kBK;
   const int kt0 = PART ? (int)((int64_t)blockIdx.y * KT_all / gridDim.y) : 0;
   const int KT = PART ? (int)((int64_t)(blockIdx.y + 1) * KT_all / gridDim.y) - kt0 : KT_all;
@@ -545,12 +560,11 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
             *(v4u*)(ot + row * RS + col) = *(const v4u*)((const u16*)epi.res + (int64_t)m * epi.ldr + n);
         }
       }
-      for (int t = tid; t < BM; t += kNT) sa_l[t] = s_a[min(m0 + t, M - 1)];
-      for (int t = tid; t < BN; t += kNT) {
-        const int n = min(n0 + t, N - 1);
-        b_l[t] = bias != nullptr ? ld_any_f32(bias, bias_dt, n) : 0.0f;
-        if constexpr (GS == 0) sw_l[t] = s_w[n];
-        if constexpr (ROT != 0) rc_l[t] = epi.sr_rcp != nullptr ? epi.sr_rcp[n] : 1.0f;
+      if (tid < BM) sa_l[tid] = pre_sa;
+      if (tid < BN) {
+        b_l[tid] = pre_b;
+        if constexpr (GS == 0) sw_l[tid] = pre_sw;
+        if constexpr (ROT != 0) rc_l[tid] = epi.sr_rcp != nullptr ? epi.sr_rcp[min(n0 + tid, N - 1)] : 1.0f;
       }
       __syncthreads();
 #pragma unroll

@@ -113,6 +113,11 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4g_big_kernel(
   int tm, tn;
   tile_coords(blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
+  // epilogue operands (activation scale of row m0 + tid, bias of column
+  // n0 + tid), loaded now so that their latency passes under the main loop
+  static_assert(BM <= kNT && BN <= kNT, "one epilogue operand per thread");
+  const float pre_sa = tid < BM ? s_a[min(m0 + tid, M - 1)] : 0.0f;
+  const float pre_b = tid < BN && bias != nullptr ? ld_any_f32(bias, bias_dt, min(n0 + tid, N - 1)) : 0.0f;
   const int KT = K / kBK;
   // scale blocks (of 128 or 64 columns) per group
   const int bpg = (K / G) / (F64 ? 64 : kBK);
@@ -303,8 +308,8 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4g_big_kernel(
       }
     }
   }
-  for (int t = tid; t < BM; t += kNT) sa_l[t] = s_a[min(m0 + t, M - 1)];
-  for (int t = tid; t < BN; t += kNT) b_l[t] = bias != nullptr ? ld_any_f32(bias, bias_dt, min(n0 + t, N - 1)) : 0.0f;
+  if (tid < BM) sa_l[tid] = pre_sa;
+  if (tid < BN) b_l[tid] = pre_b;
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < TNB; ++j) {
