@@ -747,7 +747,7 @@ int64_t tiling_cost(const GemmArgs& g, int bm, int bn, int pct = 100) {
 // Tile choice by tile-area rounds (tiling_cost).  Per-row W8A8 takes
 // 256 x 192 where that fills the CUs in fewer rounds than 256 x 256
 // (4096 x 3072: 256 tiles instead of 192 on 256 CUs).  INT4 / grouped:
-// 256 x 128 unless 128 x 128 is cheaper; a 128 x 128 tile costs 1.44x more
+// 256 x 128 (per-row INT4 also 256 x 256) unless 128 x 128 is cheaper; a 128 x 128 tile costs 1.44x more
 // per output (measured on the Flux shapes), so it wins only when it fills CUs
 // that 256 x 128 leaves idle (512 x 3072: 48 tiles of 256 x 128, 96 of
 // 128 x 128 on 256 CUs).
@@ -758,7 +758,13 @@ TileShape tile_choice(const GemmArgs& g, bool grouped) {
       return tiling_cost(g, 256, 192) < tiling_cost(g, 256, 256) ? TileShape{256, 192} : TileShape{256, 256};
     return {128, 128};
   }
-  if (g.M > 128 && tiling_cost(g, 256, 128) <= tiling_cost(g, 128, 128, 144)) return {256, 128};
+  if (g.M > 128 && tiling_cost(g, 256, 128) <= tiling_cost(g, 128, 128, 144)) {
+    // per-row INT4 (no fold, int32 accumulators only) also fits 256 x 256,
+    // ~0.9 of 256 x 128's cost per output (4608 x 3072: one round of 216
+    // tiles, 195-200 us, against two of 432, 212 us)
+    if (!grouped && g.N > 128 && tiling_cost(g, 256, 256, 90) < tiling_cost(g, 256, 128)) return {256, 256};
+    return {256, 128};
+  }
   return {128, 128};
 }
 
@@ -868,6 +874,9 @@ hipError_t pick_tile(const GemmArgs& g, hipStream_t st) {
     if (t.bm == 256) return launch_mfma<Tile<256, 256, 2, 2, false, 0>, OUT_DT, ACC, EPI>(g, st);
     return launch_mfma<Tile<128, 128, 2, 4, false, 0>, OUT_DT, ACC, EPI>(g, st);
   } else {
+    if constexpr (INT4 && GS == 0) {
+      if (t.bm == 256 && t.bn == 256) return launch_mfma<Tile<256, 256, 2, 2, true, 0>, OUT_DT, ACC, EPI>(g, st);
+    }
     if (t.bm == 256) return launch_mfma<Tile<256, 128, 4, 3, INT4, GS>, OUT_DT, ACC, EPI>(g, st);
     return launch_mfma<Tile<128, 128, 2, 4, INT4, GS>, OUT_DT, ACC, EPI>(g, st);
   }

@@ -312,7 +312,7 @@ def test_w8a8_output_formula(rt, oracle, dev, out_dtype, with_bias, M, N, K):
 
 @pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("grouped", [False, True])
-@pytest.mark.parametrize("M,N,K", [(256, 256, 512), (260, 136, 384)])
+@pytest.mark.parametrize("M,N,K", [(256, 256, 512), (260, 136, 384), (4608, 3072, 1024)])
 def test_w4a8_output_formula(rt, oracle, dev, out_dtype, grouped, M, N, K):
     G = K // 128 if grouped else 1
     a = _int8((M, K), 11)
