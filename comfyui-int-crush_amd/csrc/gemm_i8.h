@@ -833,16 +833,24 @@ bool big_out_ok(const GemmArgs& g) {
 // instead of two of 432.  That kernel writes 16-bit outputs through its LDS
 // staging tile only, so the output (and a residual) must be 16-byte aligned
 // with row strides and N multiples of 8.
-// Its two row counts: 288 (9 blocks of 16 rows per wave) and 256 (8), whichever
-// takes fewer rounds x area (4096 rows: 16 tiles of 256 instead of 15 of 288).
+// Its row counts: 256, 288 or 320 (8, 9 or 10 blocks of 16 rows per wave),
+// whichever takes the fewest rounds x area (4096 rows: 16 tiles of 256;
+// 4608: 16 of 288; Wan's 32760 x 5120: 103 x 27 tiles of 320, 11 rounds,
+// against 114 x 27 of 288, 13 rounds).
 int big_rows(const GemmArgs& g) {
-  return tiling_cost(g, 256, big::BN) < tiling_cost(g, 288, big::BN) ? 8 : 9;
+  int best = 9;
+  int64_t bc = tiling_cost(g, 288, big::BN);
+  for (int r : {8, 10}) {
+    const int64_t c = tiling_cost(g, 32 * r, big::BN);
+    if (c < bc) { bc = c; best = r; }
+  }
+  return best;
 }
 bool big_tile_ok(const GemmArgs& g) {
   if (g.M <= 128 || !big_out_ok(g)) return false;
   // per output the 288 x 192 tile costs ~0.93 of 256 x 128 (Wan FFN-down,
   // 32760 x 5120 x 14336: 13 rounds of it took as long as 20 of 256 x 128)
-  const int bm = 16 * 2 * big_rows(g);
+  const int bm = 32 * big_rows(g);
   return tiling_cost(g, bm, big::BN, 93) < tiling_cost(g, 256, 128);
 }
 
@@ -860,7 +868,11 @@ hipError_t launch_big_t(const GemmArgs& g, hipStream_t st) {
 }
 template <int OUT_DT, bool EPI, bool F64>
 hipError_t launch_big(const GemmArgs& g, hipStream_t st) {
-  return big_rows(g) == 8 ? launch_big_t<OUT_DT, EPI, F64, 8>(g, st) : launch_big_t<OUT_DT, EPI, F64, 9>(g, st);
+  switch (big_rows(g)) {
+    case 8: return launch_big_t<OUT_DT, EPI, F64, 8>(g, st);
+    case 10: return launch_big_t<OUT_DT, EPI, F64, 10>(g, st);
+    default: return launch_big_t<OUT_DT, EPI, F64, 9>(g, st);
+  }
 }
 
 template <bool INT4, int GS, int OUT_DT, bool ACC, bool EPI>

@@ -7,8 +7,8 @@
 // facc = fma(f32(acc_g), s_w[n, g] / 16, facc); out = facc * s_a[m] (+ bias),
 // rounded once.  Outputs are bit-identical to the 256 x 128 kernel.
 //
-// The row count is a template parameter: 288 (9 blocks of 16 rows per wave)
-// or 256 (8), whichever tiles M in fewer rounds (4096 rows: 16 tiles of 256).
+// The row count is a template parameter: 256, 288 or 320 (8, 9 or 10 blocks of
+// 16 rows per wave), whichever tiles M in the fewest rounds.
 //
 // Why this tile: a round of workgroups costs the same whether all CUs are busy
 // or a few, and 4608 x 3072 (the Flux MLP-down / C3 shape) makes 432 tiles of
@@ -62,8 +62,8 @@ constexpr int B_BLOCKS = BN / 16;            // 1 KB DMA blocks: 16 rows of 64 b
 constexpr int B_PER = (B_BLOCKS + 7) / 8;
 constexpr int S_WAVES = BN / 64;             // waves issuing a scale DMA
 constexpr int EPI_RS = BN + 8;               // 16-bit output staging row stride
-// Tile rows: TMB 16-row blocks per wave, two wave rows (288 rows for TMB = 9,
-// 256 for TMB = 8)
+// Tile rows: TMB 16-row blocks per wave, two wave rows (256, 288 or 320 rows
+// for TMB = 8, 9, 10)
 template <int TMB_>
 struct Rows {
   static constexpr int TMB = TMB_;

@@ -651,9 +651,11 @@ def test_wide_rows_prep_f32_and_old_smooth(rt, oracle, dev):
 # on 256 CUs and whose 288 x 192 (or 256 x 192) tiling takes fewer rounds: the
 # library runs them on gemm_w4g_big_kernel (16-bit outputs).  C3 itself, a
 # shape partial in both M and N with 128- and 256-column groups, and shapes
-# that take the 256-row variant (4096 rows), one of them with 64-column groups.
+# that take the 256-row (4096 rows) and 320-row (5120 rows) variants, with
+# 128- and 64-column groups.
 BIG_TILE_CASES = [(4608, 3072, 12288, 128), (4600, 3064, 1024, 128), (4600, 3064, 1024, 256),
-                  (4096, 3072, 1024, 128), (4000, 3064, 1024, 64)]
+                  (4096, 3072, 1024, 128), (4000, 3064, 1024, 64),
+                  (5120, 3072, 1024, 128), (5100, 3064, 1024, 64)]  # 320-row variant
 
 
 @pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16])
@@ -671,8 +673,9 @@ def test_w4a8_big_tile_sampled_rows(rt, oracle, dev, out_dtype, M, N, K, gs):
     assert rt.lib().ic_gemm_splitk_bytes(M, N, K, G, 1) == 0
     out = rt.gemm_w4a8(a.to(dev), w.to(dev), s_w.to(dev), s_a.to(dev), bias=bias.to(dev), out_dtype=out_dtype)
     out = out.float().cpu()
-    rows = torch.tensor(sorted({0, 1, 127, 128, 143, 144, 255, 256, 287, 288, 2 * 288 + 77, M // 2,
-                                (M - 1) // 288 * 288, (M - 1) // 256 * 256, M - 2, M - 1}))
+    rows = torch.tensor(sorted({0, 1, 127, 128, 143, 144, 159, 160, 255, 256, 287, 288, 319, 320, 2 * 288 + 77,
+                                M // 2, (M - 1) // 288 * 288, (M - 1) // 256 * 256, (M - 1) // 320 * 320,
+                                M - 2, M - 1}))
     fb = math.gcd(gs, 128)
     acc = oracle.gemm_acc(a[rows].numpy(), oracle.unpack_int4(w.numpy(), K), K // fb)
     sw = np.repeat(s_w.numpy(), gs // fb, axis=1)
