@@ -920,6 +920,12 @@ hipError_t launch_generic(const GemmArgs& g, int gsize, hipStream_t st) {
   }
 }
 
+// The tile kernels form each DMA row offset within a tile (up to 320 rows) in
+// 32-bit arithmetic, and each scale offset as n * G * 4.
+bool dma_strides_ok(const GemmArgs& g) {
+  return 320 * g.lda < (1LL << 31) && 320 * g.ldb < (1LL << 31) && (int64_t)g.N * g.G * 4 < (1LL << 31);
+}
+
 // Grouped scales take the MFMA kernels for group sizes that are multiples of
 // 128: the fold runs once per 128-column stage with that stage's group scale
 // (for 256, 384, ... each group's two or more stages fold separately).  The
@@ -930,7 +936,7 @@ bool mfma_shape_ok(const GemmArgs& g, int gsize) {
   // 16-byte DMA / vector loads need aligned bases and strides; packed INT4
   // rows are read 8 or 16 bytes at a time
   if (((uintptr_t)g.A & 15) || ((uintptr_t)g.B & 15) || (g.lda & 15) || (g.ldb & 15)) return false;
-  return true;
+  return dma_strides_ok(g);
 }
 
 // Packed INT4 with groups of 64 or an odd multiple of 64 columns (the
@@ -940,7 +946,7 @@ bool mfma_shape_ok(const GemmArgs& g, int gsize) {
 bool big64_ok(const GemmArgs& g, int gsize) {
   if (!g.int4 || g.G <= 1 || gsize % 128 != 64 || g.K % kBK != 0 || g.acc_out != nullptr) return false;
   if (((uintptr_t)g.A & 15) || ((uintptr_t)g.B & 15) || (g.lda & 15) || (g.ldb & 15)) return false;
-  return big_out_ok(g);
+  return dma_strides_ok(g) && big_out_ok(g);
 }
 
 // Chained MLP epilogue launches (gemm_i8_chain.hip): 128 x 256 tiles, whose

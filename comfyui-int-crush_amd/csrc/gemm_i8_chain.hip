@@ -42,9 +42,10 @@ int run_chain(GemmArgs g, int rot_size, hipStream_t st, const char* who) {
     return ic_set_error(IC_ERR_UNSUPPORTED, "%s: num_groups %d: group sizes must be multiples of 128", who, g.G);
   // the tile kernel's operand rules and its staged (16-byte row) output path
   if (g.K % kBK != 0 || ((uintptr_t)g.A & 15) || ((uintptr_t)g.B & 15) || (g.lda & 15) || (g.ldb & 15) ||
-      ((uintptr_t)g.C & 15) || (g.ldc & 7) || g.ldc >= (1LL << 24))
+      ((uintptr_t)g.C & 15) || (g.ldc & 7) || g.ldc >= (1LL << 24) || !dma_strides_ok(g))
     return ic_set_error(IC_ERR_UNSUPPORTED, "%s: K a multiple of 128, 16-byte aligned operands, row strides and "
-                        "output, output row stride a multiple of 8 elements are required", who);
+                        "output, output row stride a multiple of 8 elements (and row strides below 2^31 / 320 "
+                        "bytes) are required", who);
   if (g.M == 0) return IC_OK;
   if (!g.A || !g.B || !g.s_a || !g.s_w || !g.C) return ic_set_error(IC_ERR_INVALID_ARG, "%s: null pointer argument", who);
   hipError_t e;

@@ -716,6 +716,26 @@ def test_w4a8_group_sizes(rt, oracle, dev, gs, M, N, K):
         assert torch.allclose(out[rows], ref, rtol=1e-2, atol=1e-2 * ref.abs().max().item())
 
 
+def test_w4a8_huge_row_stride(rt, oracle, dev):
+    """An activation view whose row stride times the tile's 320 rows passes
+    2^31 bytes runs the scalar kernel (the tile kernels form row offsets in
+    32 bits): correct outputs, no out-of-range DMA."""
+    M, N, K, ld = 400, 64, 256, 6_800_000
+    big = torch.randint(-127, 128, (M, ld), dtype=torch.int8, device=dev)
+    xa = big[:, :K]
+    assert xa.stride(0) * 320 >= 2 ** 31
+    w = torch.randint(0, 256, (N, K // 2), generator=_gen(97), dtype=torch.uint8)
+    s_a = torch.rand(M, generator=_gen(98)) * 0.05 + 1e-3
+    s_w = (torch.rand(N, 2, generator=_gen(99)) * 2e-2 + 1e-3).to(torch.float16).float()
+    out = rt.gemm_w4a8(xa, w.to(dev), s_w.to(dev), s_a.to(dev), out_dtype=torch.bfloat16).float().cpu()
+    rows = [0, 1, 200, 319, 320, 399]
+    a = xa[rows].cpu().numpy()
+    del big, xa
+    acc = oracle.gemm_acc(a, oracle.unpack_int4(w.numpy(), K), 2)
+    ref = oracle.epilogue(acc, s_a[rows].numpy(), s_w.numpy(), None, 1)
+    assert np.array_equal(out[rows].numpy(), ref)
+
+
 @pytest.mark.parametrize("gs", [256, 64, 96])
 def test_w4a8_scalar_kernel_fold_blocks(rt, oracle, dev, gs):
     """Operands the MFMA tiles cannot take (a 1-byte offset activation view)
