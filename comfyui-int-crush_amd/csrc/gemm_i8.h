@@ -819,7 +819,7 @@ hipError_t launch_mfma(const GemmArgs& g, hipStream_t st) {
   return launch_kernel<TL, OUT_DT, ACC, false, EPI>(g, 1, st);
 }
 
-// Staged 16-bit output path of gemm_w4g_big_kernel: output (and residual)
+// Staged 16-bit output path of gemm_i8_big_kernel: output (and residual)
 // 16-byte aligned, row strides and N multiples of 8.
 bool big_out_ok(const GemmArgs& g) {
   if (g.out_dt == IC_DTYPE_F32 || (((uintptr_t)g.C) & 15) != 0 || (g.ldc & 7) != 0 || (g.N & 7) != 0) return false;
@@ -827,7 +827,7 @@ bool big_out_ok(const GemmArgs& g) {
          (g.epi.res_dt != IC_DTYPE_F32 && (((uintptr_t)g.epi.res) & 15) == 0 && (g.epi.ldr & 7) == 0);
 }
 
-// Grouped INT4 on 288 x 192 tiles (gemm_w4g_big_kernel) where their rounds of
+// Grouped INT4 on 288 x 192 tiles (gemm_i8_big_kernel) where their rounds of
 // workgroups cost less than 256 x 128's: 4608 x 3072 (the Flux MLP-down and
 // attention-projection shapes) fills the 256 CUs in one round of 256 tiles
 // instead of two of 432.  That kernel writes 16-bit outputs through its LDS
@@ -854,24 +854,40 @@ bool big_tile_ok(const GemmArgs& g) {
   return tiling_cost(g, bm, big::BN, 93) < tiling_cost(g, 256, 128);
 }
 
-template <int OUT_DT, bool EPI, bool F64, int TMB>
+// Per-row weights (W8A8, per-row INT4) on the big tile where its rounds cost
+// less than those of the tile_choice shape.  Per output it runs at ~0.96 of
+// the W8A8 256 x 192 / 256 x 256 tiles (C1 4096 x 3072: 39.8 against 41.1 us
+// on the same 256 x 192 tiling; 4608 x 3072 x 12288: 146 against 173 us,
+// one round of 288 x 192 against one of 256 x 256) and ~0.8 of the per-row
+// INT4 256 x 128 tile (4608 x 3072 x 12288: 141-148 against 192-198 us for
+// 256 x 256): no fold, and the per-wave INT4 expansion runs beside 54 MFMAs a
+// stage.  Not where a K split is planned (few tiles).
+bool big_row_ok(const GemmArgs& g) {
+  if (g.M <= 128 || g.N <= 128 || !big_out_ok(g)) return false;
+  if (g.ws != nullptr && splitk_plan(g, false) > 1) return false;
+  const TileShape t = tile_choice(g, false);
+  const int tpct = t.bm == 128 ? (g.int4 ? 144 : 100) : (g.int4 && t.bn == 256 ? 90 : 100);
+  return tiling_cost(g, 32 * big_rows(g), big::BN, g.int4 ? 80 : 96) < tiling_cost(g, t.bm, t.bn, tpct);
+}
+
+template <int OUT_DT, bool EPI, int MODE, int TMB>
 hipError_t launch_big_t(const GemmArgs& g, hipStream_t st) {
-  using RT = big::Rows<TMB>;
+  using RT = big::Rows<TMB, MODE>;
   const int tiles = ((g.M + RT::BM - 1) / RT::BM) * ((g.N + big::BN - 1) / big::BN);
-  auto kern = gemm_w4g_big_kernel<OUT_DT, EPI, F64, TMB>;
-  constexpr size_t shm = RT::lds_bytes(F64);
+  auto kern = gemm_i8_big_kernel<OUT_DT, EPI, MODE, TMB>;
+  constexpr size_t shm = RT::lds_bytes;
   static unsigned char lds_set[64];  // per device
   if (hipError_t e = ic_set_lds_limit((const void*)kern, (int)shm, lds_set)) return e;
   kern<<<dim3(tiles), dim3(kNT), shm, st>>>(g.A, g.lda, g.B, g.ldb, g.s_a, g.s_w, g.G, g.bias, g.bias_dt, g.C,
                                             g.ldc, g.M, g.N, g.K, g.epi);
   return hipGetLastError();
 }
-template <int OUT_DT, bool EPI, bool F64>
+template <int OUT_DT, bool EPI, int MODE>
 hipError_t launch_big(const GemmArgs& g, hipStream_t st) {
   switch (big_rows(g)) {
-    case 8: return launch_big_t<OUT_DT, EPI, F64, 8>(g, st);
-    case 10: return launch_big_t<OUT_DT, EPI, F64, 10>(g, st);
-    default: return launch_big_t<OUT_DT, EPI, F64, 9>(g, st);
+    case 8: return launch_big_t<OUT_DT, EPI, MODE, 8>(g, st);
+    case 10: return launch_big_t<OUT_DT, EPI, MODE, 10>(g, st);
+    default: return launch_big_t<OUT_DT, EPI, MODE, 9>(g, st);
   }
 }
 
@@ -879,7 +895,10 @@ template <bool INT4, int GS, int OUT_DT, bool ACC, bool EPI>
 hipError_t pick_tile(const GemmArgs& g, hipStream_t st) {
   const TileShape t = tile_choice(g, GS != 0);
   if constexpr (INT4 && GS != 0 && !ACC && OUT_DT != IC_DTYPE_F32) {
-    if (big_tile_ok(g)) return launch_big<OUT_DT, EPI, false>(g, st);
+    if (big_tile_ok(g)) return launch_big<OUT_DT, EPI, big::G128>(g, st);
+  }
+  if constexpr (GS == 0 && !ACC && OUT_DT != IC_DTYPE_F32) {
+    if (big_row_ok(g)) return launch_big<OUT_DT, EPI, INT4 ? big::ROW4 : big::ROW8>(g, st);
   }
   if constexpr (!INT4 && GS == 0) {
     if (t.bm == 256 && t.bn == 192) return launch_mfma<Tile<256, 192, 4, 2, false, 0>, OUT_DT, ACC, EPI>(g, st);
@@ -1006,8 +1025,8 @@ int run_gemm_t(GemmArgs g, hipStream_t st, const char* who, bool force_generic) 
   if (!force_generic && big64_ok(g, gsize)) {
     // groups of 64 (or an odd multiple of 64) columns: the 288 x 192 kernel
     // folding each 64-K step, at any M
-    if (g.out_dt == IC_DTYPE_F16) e = launch_big<IC_DTYPE_F16, EPI, true>(g, st);
-    else e = launch_big<IC_DTYPE_BF16, EPI, true>(g, st);
+    if (g.out_dt == IC_DTYPE_F16) e = launch_big<IC_DTYPE_F16, EPI, big::G64>(g, st);
+    else e = launch_big<IC_DTYPE_BF16, EPI, big::G64>(g, st);
   } else if (!force_generic && mfma_shape_ok(g, gsize)) {
     if constexpr (EPI) {
       // the epilogue options never come with the debug accumulator output

@@ -1,11 +1,14 @@
-// Grouped W4A8 GEMM on 288 x 192 output tiles (gfx950), for shapes whose
-// 256 x 128 tiling ends in a partly filled round of workgroups.
-//
-// Same arithmetic as gemm_i8_kernel's grouped INT4 path (triton_w4a8_gemm.py:40-108
-// with the per-group scales of _quant_utils.py:237-270): per 128-column stage
-// an exact int32 block sum of 16*q weights, folded in group order as
-// facc = fma(f32(acc_g), s_w[n, g] / 16, facc); out = facc * s_a[m] (+ bias),
-// rounded once.  Outputs are bit-identical to the 256 x 128 kernel.
+// INT8-MFMA GEMM on 256/288/320 x 192 output tiles (gfx950), for shapes whose
+// 256 x 128 / 256 x 256 tilings end in a partly filled round of workgroups.
+// Four weight modes share the tile, the DMA ring and the epilogue:
+//  * grouped INT4, the arithmetic of gemm_i8_kernel's grouped path
+//    (triton_w4a8_gemm.py:40-108 with the per-group scales of
+//    _quant_utils.py:237-270): per 128-column stage (or 64-column step) an
+//    exact int32 block sum of 16*q weights, folded in group order as
+//    facc = fma(f32(acc_g), s_w[n, g] / 16, facc); out = facc * s_a[m] (+ bias);
+//  * per-row INT4 and per-row INT8 (triton_int8_gemm.py:46-205): int32 sums
+//    over all of K, out = f32(acc) [/ 16] * (s_a[m] * s_w[n]) (+ bias).
+// Every mode rounds once and is bit-identical to gemm_i8_kernel.
 //
 // The row count is a template parameter: 256, 288 or 320 (8, 9 or 10 blocks of
 // 16 rows per wave), whichever tiles M in the fewest rounds.
@@ -53,34 +56,39 @@
 
 namespace {
 namespace big {
+// Weight modes: grouped INT4 folded per 128-column stage, grouped INT4 folded
+// per 64-column step, per-row INT4, per-row INT8 (no fold: int32 sums across K)
+enum { G128 = 0, G64 = 1, ROW4 = 2, ROW8 = 3 };
 constexpr int BN = 192, NS = 2;
 constexpr int TNB = 3;                       // 16 x 16 blocks per wave in N
 constexpr int WCOLS = TNB * 16;
-constexpr int B_BYTES = BN * kBK / 2;        // 12288, packed nibbles
 constexpr int S_BYTES = BN * 4;              // one fp32 scale per column and scale block
-constexpr int B_BLOCKS = BN / 16;            // 1 KB DMA blocks: 16 rows of 64 bytes
-constexpr int B_PER = (B_BLOCKS + 7) / 8;
 constexpr int S_WAVES = BN / 64;             // waves issuing a scale DMA
 constexpr int EPI_RS = BN + 8;               // 16-bit output staging row stride
 // Tile rows: TMB 16-row blocks per wave, two wave rows (256, 288 or 320 rows
 // for TMB = 8, 9, 10)
-template <int TMB_>
+template <int TMB_, int MODE_>
 struct Rows {
-  static constexpr int TMB = TMB_;
+  static constexpr int TMB = TMB_, MODE = MODE_;
+  static constexpr bool GROUPED = MODE <= G64, F64 = MODE == G64, INT8W = MODE == ROW8;
   static constexpr int BM = 32 * TMB, WROWS = 16 * TMB;
   static constexpr int A_BYTES = BM * kBK;
   static constexpr int A_BLOCKS = BM / 8;             // 1 KB DMA blocks: 8 rows of 128 bytes
   static constexpr int A_PER = (A_BLOCKS + 7) / 8;    // blocks per wave
-  // ring slot: activations, packed weights, then one (scale blocks of 128
+  // weights per stage: packed nibbles (1 KB DMA blocks of 16 rows of 64
+  // bytes) or int8 (blocks of 8 rows of 128 bytes, swizzled as the activations)
+  static constexpr int B_BYTES = INT8W ? BN * kBK : BN * kBK / 2;
+  static constexpr int B_BLOCKS = B_BYTES / 1024;
+  static constexpr int B_PER = (B_BLOCKS + 7) / 8;
+  // ring slot: activations, weights, then none, one (scale blocks of 128
   // columns) or two (of 64) scale rows
-  static constexpr int slot_bytes(bool f64) { return A_BYTES + B_BYTES + (f64 ? 2 : 1) * S_BYTES; }
-  static constexpr size_t epi_bytes = (size_t)BM * EPI_RS * 2 + (size_t)(BM + BN) * 4;
-  static constexpr size_t lds_bytes(bool f64) {
-    return (size_t)NS * slot_bytes(f64) > epi_bytes ? (size_t)NS * slot_bytes(f64) : epi_bytes;
-  }
+  static constexpr int SLOT = A_BYTES + B_BYTES + (GROUPED ? (F64 ? 2 : 1) * S_BYTES : 0);
+  // staging tile, activation scales, bias and per-row weight scales
+  static constexpr size_t epi_bytes = (size_t)BM * EPI_RS * 2 + (size_t)(BM + 2 * BN) * 4;
+  static constexpr size_t lds_bytes = (size_t)NS * SLOT > epi_bytes ? (size_t)NS * SLOT : epi_bytes;
   // wave priority per block row: 3 3 2 2 1 1 0 0 ...
   static constexpr int prio(int i) { return i < 6 ? 3 - i / 2 : 0; }
-  static_assert(slot_bytes(true) % 16 == 0 && lds_bytes(true) <= 160 * 1024, "LDS layout");
+  static_assert(SLOT % 16 == 0 && lds_bytes <= 160 * 1024, "LDS layout");
   static_assert(4 * WCOLS == BN, "wave grid");
   static_assert(A_PER + B_PER <= TMB, "one DMA slot per block row");
 };
@@ -90,18 +98,23 @@ struct Rows {
 // = 64): each 64-K step is folded by itself, with the scale of its group, so
 // a stage folds twice.  Otherwise (group sizes that are multiples of 128)
 // each 128-column stage is folded once with its group's scale.
-template <int OUT_DT, bool EPI, bool F64, int TMB>
-__global__ __launch_bounds__(kNT, 1) void gemm_w4g_big_kernel(
+//
+// ROW4 / ROW8: one scale per output column; the int32 sums run across all of K
+// in the MFMAs (16 * q for INT4) and the epilogue forms
+// f32(acc) [/ 16] * (s_a[m] * s_w[n]), as gemm_i8_kernel's per-row path.
+template <int OUT_DT, bool EPI, int MODE, int TMB>
+__global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
     const int8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
     const float* __restrict__ s_a, const float* __restrict__ s_w, int G,
     const void* __restrict__ bias, int bias_dt, void* __restrict__ C, int64_t ldc, int M, int N,
     int K, ic_epi epi) {
   using namespace big;
-  using RT = Rows<TMB>;
+  using RT = Rows<TMB, MODE>;
   constexpr int BM = RT::BM, WROWS = RT::WROWS, A_BYTES = RT::A_BYTES, A_BLOCKS = RT::A_BLOCKS;
-  constexpr int A_PER = RT::A_PER;
+  constexpr int A_PER = RT::A_PER, B_BYTES = RT::B_BYTES, B_BLOCKS = RT::B_BLOCKS, B_PER = RT::B_PER;
+  constexpr bool GROUPED = RT::GROUPED, F64 = RT::F64, INT8W = RT::INT8W;
   static_assert(OUT_DT != IC_DTYPE_F32, "16-bit outputs only");
-  constexpr int SLOT = RT::slot_bytes(F64);
+  constexpr int SLOT = RT::SLOT;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_char*)smem;
 
@@ -118,13 +131,14 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4g_big_kernel(
   static_assert(BM <= kNT && BN <= kNT, "one epilogue operand per thread");
   const float pre_sa = tid < BM ? s_a[min(m0 + tid, M - 1)] : 0.0f;
   const float pre_b = tid < BN && bias != nullptr ? ld_any_f32(bias, bias_dt, min(n0 + tid, N - 1)) : 0.0f;
+  const float pre_sw = !GROUPED && tid < BN ? s_w[min(n0 + tid, N - 1)] : 0.0f;
   const int KT = K / kBK;
   // scale blocks (of 128 or 64 columns) per group
   const int bpg = (K / G) / (F64 ? 64 : kBK);
 
   // ---- DMA addressing (rows past M or N re-read the last row; never stored).
-  // A block b: LDS rows 8b + l/8, chunk slot l%8 holding global chunk
-  // (l%8) ^ swz(row).  Packed B block b: rows 16b + l/4, 16-byte parts.
+  // A (and int8 B) block b: LDS rows 8b + l/8, chunk slot l%8 holding global
+  // chunk (l%8) ^ swz(row).  Packed B block b: rows 16b + l/4, 16-byte parts.
   uint32_t a_off[A_PER], b_off[B_PER];
 #pragma unroll
   for (int c = 0; c < A_PER; ++c) {
@@ -133,6 +147,11 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4g_big_kernel(
   }
 #pragma unroll
   for (int c = 0; c < B_PER; ++c) {
+    if constexpr (INT8W) {
+      const int row = 8 * (wave + 8 * c) + (lane >> 3);
+      b_off[c] = (uint32_t)(min(row, N - 1 - n0) * ldb + (((lane & 7) ^ swz(row)) << 4));
+      continue;
+    }
     // packed row n (64 bytes) holds its 16-byte part p at part p ^ ((n >> 2) & 3):
     // the fragment reads of 16 consecutive rows then spread over all banks
     const int row = 16 * (wave + 8 * c) + (lane >> 2);
@@ -152,10 +171,10 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4g_big_kernel(
   auto dma_b = [&](int kt, int c) {
     const int blk = wave + 8 * c;
     if (blk < B_BLOCKS)
-      dma16(b_off[c], b_base + (int64_t)kt * (kBK / 2), slot_of(kt) + (uint32_t)(A_BYTES + blk * 1024));
+      dma16(b_off[c], b_base + (int64_t)kt * (INT8W ? kBK : kBK / 2), slot_of(kt) + (uint32_t)(A_BYTES + blk * 1024));
   };
   auto dma_s = [&](int kt) {
-    if (wave < S_WAVES) {
+    if (GROUPED && wave < S_WAVES) {
       if constexpr (F64) {
         dma4(s_off, s_base + (2 * kt) / bpg, slot_of(kt) + (uint32_t)(A_BYTES + B_BYTES + wave * 256));
         dma4(s_off, s_base + (2 * kt + 1) / bpg, slot_of(kt) + (uint32_t)(A_BYTES + B_BYTES + S_BYTES + wave * 256));
@@ -172,7 +191,15 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4g_big_kernel(
   const int fr_n = wc * WCOLS + (lane & 15), fr_c = lane >> 4;
   const uint32_t fr0 = (uint32_t)(fr_n * 64 + 8 * (fr_c & 1) + (((fr_c >> 1) ^ ((fr_n >> 2) & 3)) << 4));
   const uint32_t fr1 = (uint32_t)(fr_n * 64 + 8 * (fr_c & 1) + (((2 + (fr_c >> 1)) ^ ((fr_n >> 2) & 3)) << 4));
+  // int8 weights: rows as the activation fragments, 16 bytes per lane
+  const uint32_t fq0 = (uint32_t)lds_off(fr_n, fr_c), fq1 = (uint32_t)lds_off(fr_n, 4 + fr_c);
   auto load_b = [&](int kt, int j, v4i& f0, v4i& f1) {
+    if constexpr (INT8W) {
+      const char* pb = smem + (kt % NS) * SLOT + A_BYTES + j * 16 * kBK;
+      f0 = *(const v4i*)(pb + fq0);
+      f1 = *(const v4i*)(pb + fq1);
+      return;
+    }
     const char* pb = smem + (kt % NS) * SLOT + A_BYTES + j * 16 * 64;
     const v2u q0 = *(const v2u*)(pb + fr0);
     const v2u q1 = *(const v2u*)(pb + fr1);
@@ -192,11 +219,13 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4g_big_kernel(
     for (int j = 0; j < TNB; ++j) sw[j] = sS[wc * WCOLS + 16 * j + (lane & 15)] * 0.0625f;
   };
 
-  v4f facc[TMB][TNB];
+  // fp32 running sums (grouped) or int32 sums (per row)
+  using AccT = std::conditional_t<GROUPED, v4f, v4i>;
+  AccT facc[TMB][TNB];
 #pragma unroll
   for (int i = 0; i < TMB; ++i)
 #pragma unroll
-    for (int j = 0; j < TNB; ++j) facc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < TNB; ++j) facc[i][j] = AccT{0, 0, 0, 0};
 
   // One stage.  Each 16 x 16 block takes both 64-K steps back to back (the
   // second MFMA adds to the first), so its int32 group sum lives only until
@@ -210,7 +239,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4g_big_kernel(
   auto mfma_stage = [&](int kt) {
     const bool more = kt + 1 < KT;  // uniform
     float sw[TNB], sw1[TNB];
-    read_scales(kt, 0, sw);
+    if constexpr (GROUPED) read_scales(kt, 0, sw);
     if constexpr (F64) read_scales(kt, 1, sw1);
     const char* aR0 = smem + (kt % NS) * SLOT + lds_off(wr * WROWS + (lane & 15), lane >> 4);
     const char* aR1 = smem + (kt % NS) * SLOT + lds_off(wr * WROWS + (lane & 15), 4 + (lane >> 4));
@@ -224,6 +253,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4g_big_kernel(
     // compiler sinks every fold to the end of the stage and holds all 27
     // group sums at once.
     auto fold_row = [&](int i, v4i* tr, v4i* tr1) {
+      if constexpr (!GROUPED) return;
 #pragma unroll
       for (int j = 0; j < TNB; ++j) {
         asm volatile("" : "+v"(tr[j]));
@@ -252,16 +282,23 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4g_big_kernel(
         n0f = *(const v4i*)(aR0 + (i + 1) * 16 * kBK);
         n1f = *(const v4i*)(aR1 + (i + 1) * 16 * kBK);
       }
-      v4i* tc = t[i & 1];
-      v4i* tc1 = t1[F64 ? (i & 1) : 0];
+      if constexpr (GROUPED) {
+        v4i* tc = t[i & 1];
+        v4i* tc1 = t1[F64 ? (i & 1) : 0];
 #pragma unroll
-      for (int j = 0; j < TNB; ++j) tc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0[j], v4i{0, 0, 0, 0}, 0, 0, 0);
+        for (int j = 0; j < TNB; ++j) tc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0[j], v4i{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-      for (int j = 0; j < TNB; ++j) {
-        if constexpr (F64) tc1[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1[j], v4i{0, 0, 0, 0}, 0, 0, 0);
-        else tc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1[j], tc[j], 0, 0, 0);
+        for (int j = 0; j < TNB; ++j) {
+          if constexpr (F64) tc1[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1[j], v4i{0, 0, 0, 0}, 0, 0, 0);
+          else tc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1[j], tc[j], 0, 0, 0);
+        }
+        if (i > 0) fold_row(i - 1, t[(i - 1) & 1], t1[F64 ? ((i - 1) & 1) : 0]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < TNB; ++j) facc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0[j], facc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < TNB; ++j) facc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1[j], facc[i][j], 0, 0, 0);
       }
-      if (i > 0) fold_row(i - 1, t[(i - 1) & 1], t1[F64 ? ((i - 1) & 1) : 0]);
       if (more) {
         // scales first: issued last, their wait at the next stage showed
         // (~180 clocks per stage on the three waves that fetch them)
@@ -296,6 +333,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4g_big_kernel(
   u16* ot = (u16*)smem;
   float* sa_l = (float*)(smem + BM * RS * 2);
   float* b_l = sa_l + BM;
+  float* sw_l = b_l + BN;
   bool res_lds = false;
   if constexpr (EPI) {
     res_lds = epi.res != nullptr;
@@ -309,18 +347,29 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4g_big_kernel(
     }
   }
   if (tid < BM) sa_l[tid] = pre_sa;
-  if (tid < BN) b_l[tid] = pre_b;
+  if (tid < BN) {
+    b_l[tid] = pre_b;
+    sw_l[tid] = pre_sw;
+  }
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < TNB; ++j) {
     const int nl = wc * WCOLS + 16 * j + (lane & 15);
     const float b = b_l[nl];
+    const float sw = sw_l[nl];
 #pragma unroll
     for (int i = 0; i < TMB; ++i) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int ml = wr * WROWS + 16 * i + 4 * (lane >> 4) + r;
-        float v = facc[i][j][r] * sa_l[ml];
+        float v;
+        if constexpr (GROUPED) {
+          v = facc[i][j][r] * sa_l[ml];
+        } else {
+          float a = (float)facc[i][j][r];
+          if constexpr (!INT8W) a *= 0.0625f;
+          v = a * (sa_l[ml] * sw);
+        }
         if (bias != nullptr) v = v + b;
         if constexpr (EPI) {
           v = epi_act(v, epi.act);

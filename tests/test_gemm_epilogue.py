@@ -136,7 +136,7 @@ SHAPES = [
     (100, 1000, 3072, "splitk"),
     (384, 512, 512, "tiles"),
     (260, 250, 384, "ragged"),
-    (1400, 5752, 256, "big"),  # grouped INT4, 16-bit out: 288 x 192 tiles, partial in M and N
+    (1400, 5752, 256, "big"),  # 16-bit out: 256 x 192 tiles, partial in M and N (every format)
 ]
 FMTS = ["int8", "int4", "int4g"]
 
@@ -191,8 +191,8 @@ def _residuals(M, N, out_dtype, seed, dev):
 def test_gemm_epilogue_matches_oracle(rt, oracle, dev, M, N, K, route, fmt, out_dtype):
     if fmt == "int4g" and K % 128:
         pytest.skip("grouped scales need K % 128 == 0")
-    if route == "big" and (fmt != "int4g" or out_dtype == torch.float32):
-        pytest.skip("the 288 x 192 tiles run grouped INT4 with 16-bit outputs only")
+    if route == "big" and out_dtype == torch.float32:
+        pytest.skip("the big tiles write 16-bit outputs only")
     G = K // 128 if fmt == "int4g" else 1
     if route == "splitk":
         assert rt.lib().ic_gemm_splitk_bytes(M, N, K, G, int(fmt != "int8")) > 0

@@ -649,7 +649,7 @@ def test_wide_rows_prep_f32_and_old_smooth(rt, oracle, dev):
 # ------------------------------------------------------------------ 288 x 192 grouped INT4 tiles
 # Shapes whose 256 x 128 tiling ends in a partly filled round of workgroups
 # on 256 CUs and whose 288 x 192 (or 256 x 192) tiling takes fewer rounds: the
-# library runs them on gemm_w4g_big_kernel (16-bit outputs).  C3 itself, a
+# library runs them on gemm_i8_big_kernel (16-bit outputs).  C3 itself, a
 # shape partial in both M and N with 128- and 256-column groups, and shapes
 # that take the 256-row (4096 rows) and 320-row (5120 rows) variants, with
 # 128- and 64-column groups.
@@ -680,6 +680,46 @@ def test_w4a8_big_tile_sampled_rows(rt, oracle, dev, out_dtype, M, N, K, gs):
     acc = oracle.gemm_acc(a[rows].numpy(), oracle.unpack_int4(w.numpy(), K), K // fb)
     sw = np.repeat(s_w.numpy(), gs // fb, axis=1)
     ref = torch.from_numpy(oracle.epilogue(acc, s_a[rows].numpy(), sw, bias.float().numpy(), DT[out_dtype]))
+    assert torch.equal(out[rows], ref)
+
+
+# 256-, 288- and 320-row tiles (4096, 4608, 5120 rows), ragged in M and N
+ROW_BIG_CASES = [(4096, 3072, 1024), (4608, 3072, 1024), (5120, 3072, 1024), (4600, 3064, 1024),
+                 (5100, 3064, 1024)]
+
+
+@pytest.mark.parametrize("int4", [False, True])
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,N,K", ROW_BIG_CASES)
+def test_per_row_big_tile_sampled_rows(rt, oracle, dev, out_dtype, M, N, K, int4):
+    """Per-row W8A8 and per-row W4A8 on the big tiles (int32 sums over all of
+    K, one scale per column): every column of sampled rows (first and last
+    rows of tiles and wave rows, the partial last tile row) bit-exact against
+    the oracle's accumulators and epilogue."""
+    a = _int8((M, K), 71, -127, 128)
+    if int4:
+        w = torch.randint(0, 256, (N, K // 2), generator=_gen(72), dtype=torch.uint8)
+        wq = oracle.unpack_int4(w.numpy(), K)
+        s_w = (torch.rand(N, 1, generator=_gen(74)) * 2e-2 + 1e-3).to(torch.float16).float()
+    else:
+        w = _int8((N, K), 72, -127, 128)
+        wq = w.numpy()
+        s_w = (torch.rand(N, generator=_gen(74)) * 2e-3 + 1e-4).to(torch.float16).float()
+    s_a = torch.rand(M, generator=_gen(73)) * 0.05 + 1e-3
+    bias = torch.randn(N, generator=_gen(75)).to(out_dtype)
+    assert rt.lib().ic_gemm_splitk_bytes(M, N, K, 1, int(int4)) == 0
+    if int4:
+        out = rt.gemm_w4a8(a.to(dev), w.to(dev), s_w.to(dev), s_a.to(dev), bias=bias.to(dev), out_dtype=out_dtype)
+    else:
+        out = rt.fused_int8_gemm_dequant(a.to(dev), w.to(dev), s_w.to(dev), s_a.to(dev), bias=bias.to(dev),
+                                         out_dtype=out_dtype)
+    out = out.float().cpu()
+    rows = torch.tensor(sorted({0, 1, 127, 128, 143, 144, 159, 160, 255, 256, 287, 288, 319, 320, 2 * 288 + 77,
+                                M // 2, (M - 1) // 288 * 288, (M - 1) // 256 * 256, (M - 1) // 320 * 320,
+                                M - 2, M - 1}))
+    acc = oracle.gemm_acc(a[rows].numpy(), wq)
+    ref = torch.from_numpy(oracle.epilogue(acc, s_a[rows].numpy(), s_w.numpy(), bias.float().numpy(),
+                                           DT[out_dtype]))
     assert torch.equal(out[rows], ref)
 
 
