@@ -834,31 +834,36 @@ bool big_out_ok(const GemmArgs& g) {
 // staging tile only, so the output (and a residual) must be 16-byte aligned
 // with row strides and N multiples of 8.
 // Its row counts: 256, 288 or 320 (8, 9 or 10 blocks of 16 rows per wave),
-// whichever takes the fewest rounds x area (4096 rows: 16 tiles of 256;
-// 4608: 16 of 288; Wan's 32760 x 5120: 103 x 27 tiles of 320, 11 rounds,
-// against 114 x 27 of 288, 13 rounds).
-int big_rows(const GemmArgs& g) {
-  int best = 9;
-  int64_t bc = tiling_cost(g, 288, big::BN);
-  for (int r : {8, 10}) {
-    const int64_t c = tiling_cost(g, 32 * r, big::BN);
-    if (c < bc) { bc = c; best = r; }
+// whichever takes the fewest rounds x area, weighted per output against the
+// 288-row tile by the operand bytes each reads (256 rows 1.05, 320 rows 0.99:
+// at Wan's M = 32760 the per-row W8A8 288- and 320-row tiles took ~5 % less
+// time per output than the 256-row one).  4096 rows: 16 tiles of 256; 4608:
+// 16 of 288; Wan's 32760 x 5120: 103 x 27 tiles of 320, 11 rounds, against
+// 114 x 27 of 288, 13 rounds.
+struct BigPick { int tmb; int64_t cost; };
+BigPick big_pick(const GemmArgs& g) {
+  BigPick best{9, tiling_cost(g, 288, big::BN)};
+  const int rows[2] = {8, 10}, pct[2] = {105, 99};
+  for (int i = 0; i < 2; ++i) {
+    const int64_t c = tiling_cost(g, 32 * rows[i], big::BN, pct[i]);
+    if (c < best.cost) best = {rows[i], c};
   }
   return best;
 }
+int big_rows(const GemmArgs& g) { return big_pick(g).tmb; }
 bool big_tile_ok(const GemmArgs& g) {
   if (g.M <= 128 || !big_out_ok(g)) return false;
   // per output the 288 x 192 tile costs ~0.93 of 256 x 128 (Wan FFN-down,
   // 32760 x 5120 x 14336: 13 rounds of it took as long as 20 of 256 x 128)
-  const int bm = 32 * big_rows(g);
-  return tiling_cost(g, bm, big::BN, 93) < tiling_cost(g, 256, 128);
+  return big_pick(g).cost * 93 / 100 < tiling_cost(g, 256, 128);
 }
 
 // Per-row weights (W8A8, per-row INT4) on the big tile where its rounds cost
-// less than those of the tile_choice shape.  Per output it runs at ~0.96 of
-// the W8A8 256 x 192 / 256 x 256 tiles (C1 4096 x 3072: 39.8 against 41.1 us
-// on the same 256 x 192 tiling; 4608 x 3072 x 12288: 146 against 173 us,
-// one round of 288 x 192 against one of 256 x 256) and ~0.8 of the per-row
+// less than those of the tile_choice shape.  Per output of the 288-row tile
+// it runs at ~0.9 of the W8A8 256 x 192 / 256 x 256 tiles (C1 4096 x 3072:
+// 39.4 against 42.3 us on the same 256 x 192 tiling; 4608 x 3072 x 12288:
+// 146 against 173 us, one round of 288 x 192 against one of 256 x 256; Wan
+// qkv 32760 x 15360 x 5120: 2.60 against 2.81 ms) and ~0.8 of the per-row
 // INT4 256 x 128 tile (4608 x 3072 x 12288: 141-148 against 192-198 us for
 // 256 x 256): no fold, and the per-wave INT4 expansion runs beside 54 MFMAs a
 // stage.  Not where a K split is planned (few tiles).
@@ -867,7 +872,7 @@ bool big_row_ok(const GemmArgs& g) {
   if (g.ws != nullptr && splitk_plan(g, false) > 1) return false;
   const TileShape t = tile_choice(g, false);
   const int tpct = t.bm == 128 ? (g.int4 ? 144 : 100) : (g.int4 && t.bn == 256 ? 90 : 100);
-  return tiling_cost(g, 32 * big_rows(g), big::BN, g.int4 ? 80 : 96) < tiling_cost(g, t.bm, t.bn, tpct);
+  return big_pick(g).cost * (g.int4 ? 80 : 90) / 100 < tiling_cost(g, t.bm, t.bn, tpct);
 }
 
 template <int OUT_DT, bool EPI, int MODE, int TMB>
