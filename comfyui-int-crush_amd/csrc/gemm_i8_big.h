@@ -219,6 +219,29 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
     for (int j = 0; j < TNB; ++j) sw[j] = sS[wc * WCOLS + 16 * j + (lane & 15)] * 0.0625f;
   };
 
+  // The next stage's DMAs, issued from block row i of stage kt.
+  auto dma_next = [&](int kt, int i) {
+    if constexpr (INT8W) {
+      // int8 weights: the next stage's weights in block row 0 and its
+      // activations in row 1, so that the last DMA has most of the stage
+      // to land (spread over rows 0-6 as below: C1 40.1 against 38.4 us,
+      // 4096 x 3072 x 12288 137-142 against 127-133 us)
+      if (i == 0) {
+#pragma unroll
+        for (int c = 0; c < B_PER; ++c) dma_b(kt + 1, c);
+      } else if (i == 1) {
+#pragma unroll
+        for (int c = 0; c < A_PER; ++c) dma_a(kt + 1, c);
+      }
+    } else {
+      // scales first: issued last, their wait at the next stage showed
+      // (~180 clocks per stage on the three waves that fetch them)
+      if (i == 0) dma_s(kt + 1);
+      if (i < A_PER) dma_a(kt + 1, i);
+      else if (i < A_PER + B_PER) dma_b(kt + 1, i - A_PER);
+    }
+  };
+
   // fp32 running sums (grouped) or int32 sums (per row)
   using AccT = std::conditional_t<GROUPED, v4f, v4i>;
   AccT facc[TMB][TNB];
@@ -299,30 +322,54 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
 #pragma unroll
         for (int j = 0; j < TNB; ++j) facc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1[j], facc[i][j], 0, 0, 0);
       }
-      if (more) {
-        if constexpr (INT8W) {
-          // int8 weights: the next stage's weights in block row 0 and its
-          // activations in row 1, so that the last DMA has most of the stage
-          // to land (spread over rows 0-6 as below: C1 40.1 against 38.4 us,
-          // 4096 x 3072 x 12288 137-142 against 127-133 us)
-          if (i == 0) {
-#pragma unroll
-            for (int c = 0; c < B_PER; ++c) dma_b(kt + 1, c);
-          } else if (i == 1) {
-#pragma unroll
-            for (int c = 0; c < A_PER; ++c) dma_a(kt + 1, c);
-          }
-        } else {
-          // scales first: issued last, their wait at the next stage showed
-          // (~180 clocks per stage on the three waves that fetch them)
-          if (i == 0) dma_s(kt + 1);
-          if (i < A_PER) dma_a(kt + 1, i);
-          else if (i < A_PER + B_PER) dma_b(kt + 1, i - A_PER);
-        }
-      }
+      if (more) dma_next(kt, i);
       __builtin_amdgcn_sched_barrier(0);
     }
     fold_row(TMB - 1, t[(TMB - 1) & 1], t1[F64 ? ((TMB - 1) & 1) : 0]);
+  };
+
+  // Int8 weights: the last block row's MFMAs of each stage are issued after
+  // the next stage's barrier, behind that stage's first fragment reads, so the
+  // MFMA pipes have work while those reads are in flight.  Their operands stay
+  // in registers: the activation row in pa0 / pa1, the weight fragments in
+  // the set the stage loaded (two sets, alternating by stage).  4096 x 3072 x
+  // 12288: 133-137 against 125-130 us; C1 38.4 against 38.1 us.  With INT4
+  // weights (expanded in registers) the same order was 1-4 % slower.
+  v4i pa0, pa1;
+  auto row_mfma = [&](int i, const v4i& a0, const v4i& a1, const v4i* b0, const v4i* b1) {
+#pragma unroll
+    for (int j = 0; j < TNB; ++j) facc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0[j], facc[i][j], 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < TNB; ++j) facc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1[j], facc[i][j], 0, 0, 0);
+  };
+  auto row_stage = [&](int kt, v4i* b0, v4i* b1, const v4i* pb0, const v4i* pb1) {
+    const bool more = kt + 1 < KT;  // uniform
+    const char* aR0 = smem + (kt % NS) * SLOT + lds_off(wr * WROWS + (lane & 15), lane >> 4);
+    const char* aR1 = smem + (kt % NS) * SLOT + lds_off(wr * WROWS + (lane & 15), 4 + (lane >> 4));
+#pragma unroll
+    for (int j = 0; j < TNB; ++j) load_b(kt, j, b0[j], b1[j]);
+    v4i n0f = *(const v4i*)aR0, n1f = *(const v4i*)aR1;
+    __builtin_amdgcn_s_setprio(3);
+    if (kt > 0) row_mfma(TMB - 1, pa0, pa1, pb0, pb1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < TMB - 1; ++i) {
+      if (i > 0 && RT::prio(i) != RT::prio(i - 1)) {
+        switch (RT::prio(i)) {
+          case 2: __builtin_amdgcn_s_setprio(2); break;
+          case 1: __builtin_amdgcn_s_setprio(1); break;
+          default: __builtin_amdgcn_s_setprio(0); break;
+        }
+      }
+      const v4i a0 = n0f, a1 = n1f;
+      n0f = *(const v4i*)(aR0 + (i + 1) * 16 * kBK);
+      n1f = *(const v4i*)(aR1 + (i + 1) * 16 * kBK);
+      row_mfma(i, a0, a1, b0, b1);
+      if (more) dma_next(kt, i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    pa0 = n0f;
+    pa1 = n1f;
   };
 
   // ---- prologue: stage 0 in flight
@@ -332,10 +379,27 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
   for (int c = 0; c < B_PER; ++c) dma_b(0, c);
   dma_s(0);
 
-  for (int s = 0; s < KT; ++s) {
-    wait_vm<0>();
-    lds_barrier();  // stage s resident; every wave is done with stage s-1
-    mfma_stage(s);
+  if constexpr (!INT8W) {
+    for (int s = 0; s < KT; ++s) {
+      wait_vm<0>();
+      lds_barrier();  // stage s resident; every wave is done with stage s-1
+      mfma_stage(s);
+    }
+  } else {
+    v4i bA0[TNB], bA1[TNB], bB0[TNB], bB1[TNB];
+    for (int s = 0; s < KT; s += 2) {
+      wait_vm<0>();
+      lds_barrier();
+      row_stage(s, bA0, bA1, bB0, bB1);
+      if (s + 1 < KT) {
+        wait_vm<0>();
+        lds_barrier();
+        row_stage(s + 1, bB0, bB1, bA0, bA1);
+      }
+    }
+    __builtin_amdgcn_s_setprio(0);
+    if ((KT - 1) & 1) row_mfma(TMB - 1, pa0, pa1, bB0, bB1);
+    else row_mfma(TMB - 1, pa0, pa1, bA0, bA1);
   }
 
   // ---- epilogue: finish in registers, stage the tile through LDS row-major,
