@@ -683,9 +683,11 @@ def test_w4a8_big_tile_sampled_rows(rt, oracle, dev, out_dtype, M, N, K, gs):
     assert torch.equal(out[rows], ref)
 
 
-# 256-, 288- and 320-row tiles (4096, 4608, 5120 rows), ragged in M and N
+# 256-, 288- and 320-row tiles (4096, 4608, 5120 rows), ragged in M and N; one
+# and nine 128-K stages (the int8-weight loop alternates two fragment sets by
+# stage and finishes the last stage's deferred block row after the loop)
 ROW_BIG_CASES = [(4096, 3072, 1024), (4608, 3072, 1024), (5120, 3072, 1024), (4600, 3064, 1024),
-                 (5100, 3064, 1024)]
+                 (5100, 3064, 1024), (4608, 3072, 128), (4096, 3072, 1152)]
 
 
 @pytest.mark.parametrize("int4", [False, True])
