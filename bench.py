@@ -42,15 +42,25 @@ PEAK_SCLK_MHZ = 2400.0        # MI355X peak engine clock the published MFMA peak
 
 
 def cpu_model():
-    """The host CPU's model name, from /proc/cpuinfo (None where absent)."""
+    """The host CPU's model name from /proc/cpuinfo (what `lscpu` prints as
+    "Model name"), followed by its CPUID family / model / stepping, which name
+    the part where a virtualised host reports only a generic brand string
+    ("AMD EPYC").  None where /proc/cpuinfo is absent."""
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for ln in f:
-                if ln.startswith("model name"):
-                    return ln.split(":", 1)[1].strip()
+                if not ln.strip():
+                    break  # first processor's block only
+                k, _, v = ln.partition(":")
+                fields.setdefault(k.strip(), v.strip())
     except OSError:
-        pass
-    return None
+        return None
+    name = fields.get("model name")
+    if name is None:
+        return None
+    ids = [f"{k.split()[-1]} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields]
+    return f"{name} ({', '.join(ids)})" if ids else name
 
 CONFIGS = {
     "c1": dict(name="C1 W8A8 linear 3072->3072, M=4096, rot 0", fmt="int8", M=4096, K=3072, N=3072,
