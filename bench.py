@@ -103,7 +103,7 @@ def _parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS) + sorted(SETS) + [STEP_CONFIG, MLP_CONFIG])
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS) + sorted(SETS) + [STEP_CONFIG, MLP_CONFIG, F6_CONFIG])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (PMC calibration)")
@@ -668,6 +668,76 @@ def mlp_chain_main(args, rt):
     print(json.dumps(line), flush=True)
 
 
+# ------------------------------------------- C3 GEMM on e3m2 operands (fp6)
+# The grouped W4A8 GEMM of C3 two ways in one process: the int8 MFMA kernel
+# (gemm_w4a8, what the library routes to) and the f8f6f4 MFMA kernel on
+# e3m2 operands (gemm_w4a8_f6: no group-sum converts, no INT4 expansion, 1.5x
+# the operand bytes), on the C3 prep's own codes.  Alternating rounds; the
+# outputs are compared bit for bit.
+F6_CONFIG = "c3f6"
+
+
+def f6_main(args, rt):
+    import torch
+
+    cfg = CONFIGS["c3"]
+    inp = make_inputs(cfg)
+    dev = torch.device("cuda:0")
+    M, K, N = cfg["M"], cfg["K"], cfg["N"]
+    act = inp["x"].dtype
+    per_copy = inp["w"].numel() * 3 // 2  # e3m2 weight bytes per copy
+    copies = max(2, min(64, math.ceil(640e6 / per_copy)))
+    ws = [inp["w"].to(dev) for _ in range(copies)]
+    w6s = [rt.f6_repack_weights(w, K) for w in ws]
+    s_w = inp["s_w"].to(dev)
+    sr = rt.prepare_factors(inp["smoothrot"].to(dev), act)
+    perm = rt.prepare_perm(inp["perm"].to(dev), K)
+    q, s_a = rt.rotate_quantize(inp["x"].to(dev), rot_size=cfg["rot"], w_in=K, smoothrot=sr, perm=perm)
+    a6 = rt.f6_split_activations(q)
+    out_i8 = torch.empty(M, N, dtype=act, device=dev)
+    out_f6 = torch.empty_like(out_i8)
+
+    def i8(i):
+        rt.gemm_w4a8(q, ws[i % copies], s_w, s_a, out_dtype=act, out=out_i8)
+
+    def f6(i):
+        rt.gemm_w4a8_f6(a6, M, K, w6s[i % copies], N, s_w, s_a, out_dtype=act, out=out_f6)
+
+    def split(i):
+        rt.f6_split_activations(q)
+
+    for i in range(max(1, args.warmup)):
+        i8(i)
+        f6(i)
+    torch.cuda.synchronize()
+    same = bool(torch.equal(out_i8, out_f6))
+    t = {"int8": [], "f6": []}
+    for _ in range(3):
+        t["int8"].append(_time_loop(i8, args.steps))
+        t["f6"].append(_time_loop(f6, args.steps))
+    split_ms = _time_loop(split, args.steps)
+    ops, _gb, _pb = algorithmic(cfg)
+    med = {k: statistics.median(v) for k, v in t.items()}
+    tops = {k: ops / (v * 1e-3) / 1e12 for k, v in med.items()}
+    line = {
+        "metric": "C3 grouped W4A8 GEMM: int8 MFMA kernel against the e3m2 f8f6f4 MFMA kernel",
+        "value": round(tops["f6"], 2), "unit": "TOPS", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(med["f6"], 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "C3 GEMM 4608 x 12288 -> 3072, g128, on the C3 prep's codes", "input_copies": copies,
+                   "parallelism": "single GPU"},
+        "int8_kernel": {"ms": [round(v, 5) for v in t["int8"]], "tops": round(tops["int8"], 1),
+                        "frac": round(tops["int8"] / PEAK_INT8_TOPS, 4)},
+        "f6_kernel": {"ms": [round(v, 5) for v in t["f6"]], "tops": round(tops["f6"], 1),
+                      "frac": round(tops["f6"] / PEAK_INT8_TOPS, 4)},
+        "outputs_bit_identical": same,
+        "split_activations_ms": round(split_ms, 5),
+        "note": "the e3m2 route would also need the prep to write the split activations "
+                "(1.5 bytes per code instead of 1), or the split pass timed here",
+    }
+    print(json.dumps(line), flush=True)
+
+
 def traffic_for(workload_key):
     """HBM bytes per launch of the dominant kernel from committed rocprofv3 counters."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
@@ -701,6 +771,9 @@ def main():
         return
     if args.config == MLP_CONFIG:
         mlp_chain_main(args, rt)
+        return
+    if args.config == F6_CONFIG:
+        f6_main(args, rt)
         return
     cfg = CONFIGS[args.config]
     inp = make_inputs(cfg)

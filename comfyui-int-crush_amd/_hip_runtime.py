@@ -83,6 +83,11 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "ic_gemm_w4a16": ([_P, _I, _L, _L, _L, _P, _L, _L, _P, _L, _P, _I, _P, _L, _P], _I),
     "ic_unpack_int4_to_int8": ([_P, _L, _L, _L, _P, _L, _P], _I),
     "ic_unpack_int4_to_float": ([_P, _P, _L, _L, _L, _L, _P, _I, _L, _P], _I),
+    "ic_f6_activation_bytes": ([_L, _L], _L),
+    "ic_f6_weight_bytes": ([_L, _L], _L),
+    "ic_f6_split_activations": ([_P, _L, _L, _L, _P, _P], _I),
+    "ic_f6_repack_weights": ([_P, _L, _L, _L, _P, _P], _I),
+    "ic_gemm_w4a8_f6": ([_P, _L, _L, _P, _L, _P, _L, _P, _P, _I, _P, _I, _L, _P], _I),
     "ic_gemm_w8a8_acc_i32": ([_P, _L, _L, _L, _P, _L, _L, _P, _I, _P], _I),
     "ic_gemm_w4a8_acc_i32": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _I, _P], _I),
     "ic_gemm_w8a8_generic": ([_P, _L, _L, _L, _P, _L, _L, _P, _P, _P, _I, _P, _I, _L, _P], _I),
@@ -653,6 +658,56 @@ def gemm_w4a8(x_int8: torch.Tensor, w_packed: torch.Tensor, s_w: torch.Tensor, s
         _call("ic_gemm_w4a8_ex", _ptr(xq), M, K, xq.stride(0), _ptr(w), N, w.stride(0), _ptr(sw), G,
               _ptr(sa), bp, bdt, act, rp, rdt, ldr, _ptr(c), _dt(c.dtype, "out"), c.stride(0), _ptr(ws), nb,
               _stream(xq))
+    return c
+
+
+def f6_split_activations(x_int8: torch.Tensor) -> torch.Tensor:
+    """int8 codes [M, K] -> the e3m2 activation buffer of gemm_w4a8_f6
+    (x = 16 h + l per code, blocked by 16 rows; ic_f6_split_activations)."""
+    assert x_int8.dtype == torch.int8, f"x_int8 must be int8, got {x_int8.dtype}"
+    _need_cuda(x_int8)
+    xq = _rows(x_int8)
+    M, K = xq.shape
+    nb = lib().ic_f6_activation_bytes(M, K)
+    if nb <= 0:
+        raise ValueError(f"f6_split_activations: K={K} must be a positive multiple of 128")
+    a6 = torch.empty(nb, dtype=torch.uint8, device=xq.device)
+    with torch.cuda.device(xq.device):
+        _call("ic_f6_split_activations", _ptr(xq), M, K, xq.stride(0), _ptr(a6), _stream(xq))
+    return a6
+
+
+def f6_repack_weights(w_packed: torch.Tensor, K: int) -> torch.Tensor:
+    """Packed INT4 [N, K/2] -> the e3m2 weight buffer of gemm_w4a8_f6
+    (blocked by 16 columns; ic_f6_repack_weights).  Once per layer."""
+    assert w_packed.dtype == torch.uint8, f"w_packed must be uint8, got {w_packed.dtype}"
+    _need_cuda(w_packed)
+    w = _rows(w_packed)
+    N = w.shape[0]
+    nb = lib().ic_f6_weight_bytes(N, K)
+    if nb <= 0:
+        raise ValueError(f"f6_repack_weights: K={K} must be a positive multiple of 128")
+    w6 = torch.zeros(nb, dtype=torch.uint8, device=w.device)
+    with torch.cuda.device(w.device):
+        _call("ic_f6_repack_weights", _ptr(w), N, K, w.stride(0), _ptr(w6), _stream(w))
+    return w6
+
+
+def gemm_w4a8_f6(a6: torch.Tensor, M: int, K: int, w6: torch.Tensor, N: int, s_w: torch.Tensor,
+                 s_a: torch.Tensor, bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """Grouped W4A8 on e3m2 operands (ic_gemm_w4a8_f6): the outputs of
+    gemm_w4a8 for the same codes, weights and group scales, bit for bit."""
+    _need_cuda(a6, w6, s_w, s_a, bias)
+    if a6.numel() < lib().ic_f6_activation_bytes(M, K) or w6.numel() < lib().ic_f6_weight_bytes(N, K):
+        raise ValueError("gemm_w4a8_f6: operand buffers smaller than the M x K / N x K formats")
+    sw = s_w.detach().reshape(N, -1).to(torch.float32).contiguous()
+    sa = s_a.detach().reshape(-1).to(torch.float32).contiguous()
+    bp, bdt, _keep = _bias_args(bias, N)
+    c = _out_buffer(out, M, N, out_dtype, a6.device)
+    with torch.cuda.device(a6.device):
+        _call("ic_gemm_w4a8_f6", _ptr(a6), M, K, _ptr(w6), N, _ptr(sw), sw.shape[1], _ptr(sa), bp, bdt, _ptr(c),
+              _dt(c.dtype, "out"), c.stride(0), _stream(a6))
     return c
 
 

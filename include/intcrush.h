@@ -298,6 +298,28 @@ int ic_unpack_int4_to_int8(const uint8_t* packed, int64_t N, int64_t K, int64_t 
 int ic_unpack_int4_to_float(const uint8_t* packed, const float* s_w, int64_t num_groups, int64_t N,
                             int64_t K, int64_t ldp, void* out, int out_dtype, int64_t ldo, void* stream);
 
+/*
+ * Grouped W4A8 on gfx950's f8f6f4 MFMA with 6-bit (e3m2) operands: the same
+ * function as ic_gemm_w4a8 with num_groups > 1 (fused_w4a8_gemm_dequant,
+ * kernels/triton_w4a8_gemm.py:111-169, with the group layout of
+ * _quant_utils.py:237-270), bit-identical outputs, on operands converted once:
+ *   ic_f6_split_activations: int8 codes x [M, K] -> a6 (ic_f6_activation_bytes),
+ *     each code split as x = 16 h + l with h in [-8, 8], l in [-8, 7];
+ *   ic_f6_repack_weights: packed INT4 [N, K/2] -> w6 (ic_f6_weight_bytes).
+ * Both buffers are blocked by 16 rows / columns (layout in csrc/gemm_f6.h) and
+ * must be 16-byte aligned.  K a multiple of 128, groups of a multiple of 128
+ * columns, at least two; N and ldo multiples of 8; f16 / bf16 output.  An
+ * alternative path: the library's own routing keeps the int8 kernel, which
+ * measured as fast.
+ */
+int64_t ic_f6_activation_bytes(int64_t M, int64_t K);
+int64_t ic_f6_weight_bytes(int64_t N, int64_t K);
+int ic_f6_split_activations(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, uint8_t* a6, void* stream);
+int ic_f6_repack_weights(const uint8_t* w_packed, int64_t N, int64_t K, int64_t ldw, uint8_t* w6, void* stream);
+int ic_gemm_w4a8_f6(const uint8_t* a6, int64_t M, int64_t K, const uint8_t* w6, int64_t N, const float* s_w,
+                    int64_t num_groups, const float* s_a, const void* bias, int bias_dtype, void* out,
+                    int out_dtype, int64_t ldo, void* stream);
+
 /* Debug: raw int32 accumulators of the production GEMM kernels (generic != 0
  * selects the shape-generic kernel instead).  W8A8: acc [M,N].  W4A8: acc
  * [num_groups, M, N], one slab per group.  Pins the integer stage of
