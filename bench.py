@@ -111,6 +111,8 @@ def _parse():
                     help="skip the hipBLASLt reference GEMM on the same shape")
     ap.add_argument("--eager", action="store_true",
                     help="launch eagerly instead of replaying a captured graph (for counter collection)")
+    ap.add_argument("--no-step", action="store_true",
+                    help="skip the denoise-step times the default (c3) line carries")
     return ap.parse_args()
 
 
@@ -338,12 +340,67 @@ def flux_step_bench(args, rt):
     torch.cuda.synchronize()
     d_eager = dropin.forward().clone()
     torch.cuda.synchronize()
+    d_eager_ms, d_eager_wall = _time_eager(dropin.forward, reps)
     d_ms, d_out = _time_graph(dropin.forward, reps)
     torch.cuda.synchronize()
     a, b = d_out.double().reshape(-1), eager.double().reshape(-1)
-    r.update(dropin_step_ms=d_ms, dropin_replay_equal=bool(torch.equal(d_out, d_eager)),
+    r.update(dropin_step_ms=d_ms, dropin_eager_ms=d_eager_ms, dropin_eager_wall_ms=d_eager_wall,
+             dropin_replay_equal=bool(torch.equal(d_out, d_eager)),
              dropin_cos_vs_fused=float((a @ b) / (a.norm() * b.norm())))
     return r
+
+
+def _time_eager(fn, reps):
+    """Average ms (HIP events) and host wall ms of reps eager calls of fn."""
+    import torch
+
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) / reps, (time.perf_counter() - t0) * 1e3 / reps
+
+
+def denoise_step_times(rt, reps=5, warmup=2):
+    """The C4 denoise step three ways: the fused model
+    (FluxStep: hand-fused norms and epilogues) replayed as one hipGraph; the
+    drop-in model (DropInFluxStep: every quantized linear an
+    IntCrushOps.Linear, torch glue between them) replayed as one hipGraph; and
+    the drop-in model launched eagerly, layer by layer, the way ComfyUI calls
+    IntCrushOps.Linear.forward (reference _ops.py:817-862)."""
+    import torch
+
+    import bench_flux
+
+    dev = torch.device("cuda:0")
+    fused = bench_flux.FluxStep(rt, dev)
+    for _ in range(warmup):
+        fused.forward()
+    fused_ms, _ = _time_graph(fused.forward, reps)
+    del fused
+    torch.cuda.empty_cache()
+    dropin = bench_flux.DropInFluxStep(rt, dev)
+    for _ in range(warmup):
+        dropin.forward()
+    eager_ms, eager_wall = _time_eager(dropin.forward, reps)
+    graph_ms, _ = _time_graph(dropin.forward, reps)
+    del dropin
+    torch.cuda.empty_cache()
+    return {"fused_graph_ms": round(fused_ms, 3), "dropin_graph_ms": round(graph_ms, 3),
+            "dropin_eager_ms": round(eager_ms, 3), "dropin_eager_host_wall_ms": round(eager_wall, 3),
+            "dropin_eager_over_graph": round(eager_ms / graph_ms, 4), "reps": reps,
+            "workload": "C4 Flux-dev denoise step, batch 1, bf16, random init: 19 double + 38 single blocks, "
+                        "4096 image + 512 text tokens, W4A8 R=256 g128 block linears, M=1 modulation GEMVs, "
+                        "attention in torch SDPA",
+            "note": "fused: FluxStep (adaLN fused into the preps, GELU-tanh and residual in GEMM epilogues), one "
+                    "hipGraph; dropin: every quantized linear an IntCrushOps.Linear (make_intcrush_ops("
+                    "'int4_crush', 256), ComfyUI stand-in from tests/fake_comfy), torch glue between them, "
+                    "as one hipGraph and eagerly (per-layer forward calls, no whole-step capture)"}
 
 
 def flux_step_cpu_baseline(rows=512):
@@ -406,13 +463,14 @@ def flux_step_main(args, rt):
                           "other_torch_ops = step minus the timed parts (norms, modulation, RoPE, GELU, "
                           "residuals, embedders, final layer, concatenations)",
         "graph_replay_equals_eager": r["replay_equal"], "output_finite": r["finite"],
-        "dropin_step": {"ms": round(r["dropin_step_ms"], 4),
+        "dropin_step": {"ms": round(r["dropin_step_ms"], 4), "eager_ms": round(r["dropin_eager_ms"], 4),
+                        "eager_host_wall_ms": round(r["dropin_eager_wall_ms"], 4),
                         "graph_replay_equals_eager": r["dropin_replay_equal"],
                         "output_cosine_vs_fused_step": round(r["dropin_cos_vs_fused"], 7),
                         "note": "the same model with every quantized linear an IntCrushOps.Linear "
                                 "(make_intcrush_ops('int4_crush', 256), ComfyUI stand-in from tests/fake_comfy): "
                                 "per linear prep + W4A8 GEMM, adaLN / GELU-tanh / residuals as torch ops, "
-                                "whole step in one hipGraph"},
+                                "whole step in one hipGraph (ms) and launched eagerly layer by layer (eager_ms)"},
     }
     peaks = measure_peaks()
     line["peak_measured"] = peaks
@@ -824,6 +882,10 @@ def main():
                               "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(pach / PEAK_HBM_GBPS, 4)}
     if M > rt.GEMV_MAX_M and not args.no_vendor:
         line["vendor_gemm"] = vendor_reference(cfg)
+    if args.config == "c3" and not args.no_step:
+        # the metric's second half ("denoise step ms"), on the same box and run
+        torch.cuda.empty_cache()
+        line["denoise_step"] = denoise_step_times(rt)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(cfg, inp)
     print(json.dumps(line), flush=True)
