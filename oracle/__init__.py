@@ -203,6 +203,41 @@ def flush_small_bf16(blk: np.ndarray, k: int) -> np.ndarray:
     return blk
 
 
+def inexact_block_rows(x, dtype: int, *, smoothrot=None, rot_size: int = 0) -> np.ndarray:
+    """Rows of `prepare`'s input whose Hadamard blocks include one whose double
+    sum is not provably exact (after the SmoothRot divide and, for bf16, the
+    flush rule): the rows _prepare_exact_rows recomputes.  Boolean [M]; all
+    False for fp16 inputs and without rotation."""
+    L = lib()
+    R = int(rot_size)
+    xv = np.ascontiguousarray(to_dtype_values(x, dtype), dtype=np.float32)
+    M, K_in = xv.shape
+    flags = np.zeros(M, bool)
+    if R <= 1:
+        return flags
+    k = (R.bit_length() - 1) // 2
+    K_r = ((K_in + R - 1) // R) * R
+    p = {DT_F16: 11, DT_BF16: 8, DT_F32: 24}[dtype]
+    srf = None if smoothrot is None else round_dtype(np.asarray(to_dtype_values(smoothrot, DT_F32), np.float64), dtype)
+    for m in range(M):
+        a = np.zeros(K_r, np.float64)
+        a[:K_in] = xv[m]
+        if srf is not None:
+            a[:K_in] = [L.oc_round(float(v) / float(f), dtype) for v, f in zip(xv[m], srf)]
+        for b0 in range(0, K_r, R):
+            blk = a[b0:b0 + R]
+            if dtype == DT_BF16:
+                blk = flush_small_bf16(blk, k)
+            nz = blk[blk != 0]
+            if nz.size:
+                emax = int(np.max(np.frexp(np.abs(nz))[1])) - 1
+                qmin = int(np.min(np.frexp(np.abs(nz))[1])) - p
+                if (emax + 1 + 2 * k) - qmin > 53:
+                    flags[m] = True
+                    break
+    return flags
+
+
 def _prepare_exact_rows(xv, dtype, srf, R, K_w, pm, smf, out):
     """Recompute rows containing a block whose double sum is not provably exact."""
     L = lib()

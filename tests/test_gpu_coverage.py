@@ -1,0 +1,179 @@
+"""GPU parity at the remaining full BASELINE shapes, run-twice determinism of
+every GEMM route, and the exact bound of the f32 prep.
+
+* C5 (Wan2.1-14B, M = 32760): qkv 5120->15360, proj 5120->5120 and FFN-up
+  5120->13824 in both formats (INT4 g128 W4A8, W8A8), one production launch
+  each; sampled rows at tile edges (256/288/320-row tiles) and in the last
+  partial tile equal the oracle's accumulators and epilogue bit for bit.
+  (FFN-down runs in test_gpu_kernels.py.)
+* C1's exact launch: 4096 x 3072 -> 3072 W8A8 on the codes of its own
+  quantizer (N(0,1) fp16 activations), codes and sampled output rows
+  bit-exact.
+* Every GEMM route (big tiles in each weight mode, the 256 x 128 tile, split
+  K per-row and grouped, GEMVs, W4A16 tiled and GEMV, the scalar kernel, the
+  e3m2 kernel, the epilogue options) gives bit-identical outputs when run
+  twice on the same inputs.
+* f32 activations: rows whose Hadamard blocks all have provably exact fp64
+  sums are bit-exact; in the other rows each prepared value lies within one
+  f32 ulp plus k * 2^-51 * max|x| of its block (R = 4^k) of the exact value,
+  and each code within one of the exact code.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DT = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _dgen(seed):
+    return torch.Generator(device="cuda").manual_seed(seed)
+
+
+# tile edges of the 256-, 288- and 320-row tiles, a middle row, the last partial tile
+C5_ROWS = [0, 1, 255, 256, 287, 288, 319, 320, 12345, 32511, 32512, 32639, 32640, 32759]
+C5_LINEARS = [("qkv", 5120, 15360), ("proj", 5120, 5120), ("up", 5120, 13824)]
+
+
+@pytest.mark.parametrize("fmt", ["int4_g128", "int8"])
+@pytest.mark.parametrize("name,K,N", C5_LINEARS)
+def test_c5_linears_full_size_sampled_rows(rt, oracle, dev, fmt, name, K, N):
+    M = 32760
+    a = torch.randint(-127, 128, (M, K), generator=_dgen(K + N), device=dev, dtype=torch.int8)
+    s_a = torch.rand(M, generator=_gen(2)) * 0.05 + 1e-3
+    if fmt == "int8":
+        w = torch.randint(-127, 128, (N, K), generator=_gen(3), dtype=torch.int8)
+        s_w = (torch.rand(N, generator=_gen(4)) * 2e-3 + 1e-4).to(torch.float16).float()
+        out = rt.fused_int8_gemm_dequant(a, w.to(dev), s_w.to(dev), s_a.to(dev), out_dtype=torch.float16)
+        wq, G = w.numpy(), 1
+    else:
+        G = K // 128
+        w = torch.randint(0, 256, (N, K // 2), generator=_gen(5), dtype=torch.uint8)
+        s_w = (torch.rand(N, G, generator=_gen(6)) * 2e-2 + 1e-3).to(torch.float16).float()
+        out = rt.gemm_w4a8(a, w.to(dev), s_w.to(dev), s_a.to(dev), out_dtype=torch.float16)
+        wq = oracle.unpack_int4(w.numpy(), K)
+    rows = torch.tensor(C5_ROWS)
+    got = out[rows.to(dev)].float().cpu().numpy()
+    arows = a[rows.to(dev)].cpu().numpy()
+    del out, a
+    ref = oracle.epilogue(oracle.gemm_acc(arows, wq, G), s_a[rows].numpy(), s_w.numpy(), None, DT[torch.float16])
+    assert np.array_equal(got, ref)
+
+
+def test_c1_exact_launch(rt, oracle, dev):
+    """BASELINE config 1 as launched: N(0,1) fp16 activations quantized per
+    token, W8A8 GEMM 4096 x 3072 -> 3072, fp16 per-channel scales."""
+    M, K, N = 4096, 3072, 3072
+    x = torch.randn(M, K, generator=_gen(11)).to(torch.float16)
+    w = torch.randint(-127, 128, (N, K), generator=_gen(12), dtype=torch.int8)
+    s_w = (torch.rand(N, 1, generator=_gen(13)) * (2e-3 - 1e-4) + 1e-4).to(torch.float16).float()
+    q, s_a = rt.dynamic_quantize_activation(x.to(dev))
+    out = rt.fused_int8_gemm_dequant(q, w.to(dev), s_w.to(dev), s_a, out_dtype=torch.float16)
+    q_ref, s_ref = oracle.quantize(x.float().numpy())
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+    assert np.array_equal(s_a.cpu().numpy(), s_ref)
+    rows = np.array(sorted({0, 1, 127, 128, 255, 256, 511, 512, 2047, 2048, 3839, 3840, 4094, 4095}))
+    ref = oracle.epilogue(oracle.gemm_acc(q_ref[rows], w.numpy()), s_ref[rows], s_w.numpy(), None, 0)
+    assert np.array_equal(out.float().cpu().numpy()[rows], ref)
+
+
+# (route, weights, M, N, K, group size or 0 for per-row)
+ROUTES = [
+    ("big tile, grouped INT4 g128", "int4", 4608, 3072, 1024, 128),
+    ("big tile, grouped INT4 g64", "int4", 4000, 3064, 1024, 64),
+    ("big tile, per-row INT8", "int8", 4096, 3072, 1024, 0),
+    ("big tile, per-row INT4", "int4", 4608, 3072, 1024, 0),
+    ("256 x 128 tile, grouped INT4", "int4", 2048, 2048, 768, 128),
+    ("W8A8 tile", "int8", 1024, 1024, 768, 0),
+    ("split K, per-row INT8", "int8", 64, 3072, 12288, 0),
+    ("split K, grouped INT4", "int4", 512, 3072, 12288, 128),
+    ("GEMV W8A8", "int8", 1, 2304, 3072, 0),
+    ("GEMV W4A8 g128", "int4", 5, 2304, 3072, 128),
+    ("W4A16 tile", "w4a16", 1024, 2048, 1024, 128),
+    ("W4A16 GEMV", "w4a16", 3, 2048, 1024, 128),
+    ("scalar kernel", "int4-unaligned", 40, 200, 768, 256),
+    ("e3m2 kernel", "f6", 4608, 3072, 1024, 128),
+    ("big tile with GELU and residual", "int4-epi", 4608, 3072, 1024, 128),
+]
+
+
+@pytest.mark.parametrize("route,kind,M,N,K,gs", ROUTES, ids=[r[0] for r in ROUTES])
+def test_gemm_routes_run_twice_identical(rt, dev, route, kind, M, N, K, gs):
+    G = K // gs if gs else 1
+    s_a = (torch.rand(M, generator=_gen(21)) * 0.05 + 1e-3).to(dev)
+    bias = torch.randn(N, generator=_gen(22)).to(torch.bfloat16).to(dev)
+    if kind == "w4a16":
+        x = torch.randn(M, K, generator=_gen(23)).to(torch.bfloat16).to(dev)
+    else:
+        base = torch.randint(-127, 128, (M, K + 1), generator=_gen(23), dtype=torch.int8).to(dev)
+        x = base[:, 1:] if kind == "int4-unaligned" else base[:, :K].contiguous()
+    if kind == "int8":
+        w = torch.randint(-127, 128, (N, K), generator=_gen(24), dtype=torch.int8).to(dev)
+        s_w = (torch.rand(N, generator=_gen(25)) * 2e-3 + 1e-4).to(dev)
+    else:
+        w = torch.randint(0, 256, (N, K // 2), generator=_gen(24), dtype=torch.uint8).to(dev)
+        s_w = (torch.rand(N, G, generator=_gen(25)) * 2e-2 + 1e-3).to(torch.float16).float().to(dev)
+    res = torch.randn(M, N, generator=_gen(26)).to(torch.bfloat16).to(dev) if kind == "int4-epi" else None
+
+    def run():
+        if kind == "int8":
+            return rt.fused_int8_gemm_dequant(x, w, s_w, s_a, bias=bias, out_dtype=torch.bfloat16)
+        if kind == "w4a16":
+            return rt.gemm_w4a16(x, w, s_w)
+        if kind == "f6":
+            return rt.gemm_w4a8_f6(rt.f6_split_activations(x), M, K, rt.f6_repack_weights(w, K), N, s_w, s_a,
+                                   bias=bias, out_dtype=torch.bfloat16)
+        if kind == "int4-epi":
+            return rt.gemm_w4a8(x, w, s_w, s_a, bias=bias, out_dtype=torch.bfloat16,
+                                activation=rt.ACT_GELU_TANH, residual=res)
+        return rt.gemm_w4a8(x, w, s_w, s_a, bias=bias, out_dtype=torch.bfloat16)
+
+    a = run()
+    b = run()
+    torch.cuda.synchronize()
+    assert torch.isfinite(a.float()).all()
+    assert torch.equal(a, b), route
+
+
+@pytest.mark.parametrize("R", [64, 256, 1024])
+def test_f32_prep_bound(rt, oracle, dev, R):
+    M, K = 12, 2048
+    g = _gen(R)
+    x = torch.randn(M, K, generator=g)
+    # rows with tiny values beside large ones: block sums beyond 53 bits
+    x[3, 5] = 3e-30
+    x[7, ::97] = 1e-25
+    x[9] = x[9] * 1e6
+    x[9, 1] = 1e-20
+    fac = torch.exp(torch.randn(K, generator=g) * 0.5)
+    srp = rt.prepare_factors(fac.to(dev), torch.float32)
+    y = rt.prepare_activation(x.to(dev), rot_size=R, smoothrot=srp).cpu().numpy().astype(np.float64)
+    q, s = rt.rotate_quantize(x.to(dev), rot_size=R, smoothrot=srp)
+    y_ref = oracle.prepare(x, 2, smoothrot=fac, rot_size=R).astype(np.float64)
+    q_ref, s_ref = oracle.quantize(y_ref)
+    flagged = oracle.inexact_block_rows(x, 2, smoothrot=fac, rot_size=R)
+    assert flagged[[3, 7, 9]].all()
+    exact = ~flagged
+    assert np.array_equal(y[exact], y_ref[exact])
+    assert np.array_equal(q.cpu().numpy()[exact], q_ref[exact])
+    assert np.array_equal(s.cpu().numpy()[exact], s_ref[exact])
+    # flagged rows: the bound of the fp64 butterflies (k stages, relative
+    # rounding error <= 2^-53 each, on partial sums below 2 max|x| of the
+    # block) plus the final f32 rounding
+    k = (R.bit_length() - 1) // 2
+    xd = oracle.prepare(x, 2, smoothrot=fac, rot_size=0).astype(np.float64)  # the divided row
+    blkmax = np.abs(xd).reshape(M, K // R, R).max(-1).repeat(R, axis=1)
+    ulp = np.spacing(np.abs(y_ref).astype(np.float32)).astype(np.float64)
+    err = np.abs(y - y_ref)
+    assert (err[flagged] <= ulp[flagged] + k * 2.0 ** -51 * blkmax[flagged]).all()
+    assert np.abs(q.cpu().numpy().astype(int) - q_ref.astype(int))[flagged].max() <= 1
+    assert np.allclose(s.cpu().numpy()[flagged], s_ref[flagged], rtol=2e-7)
