@@ -74,6 +74,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "ic_gemm_splitk_bytes": ([_L, _L, _L, _L, _I], _L),
     "ic_gemm_w8a8_ws": ([_P, _L, _L, _L, _P, _L, _L, _P, _P, _P, _I, _P, _I, _L, _P, _L, _P], _I),
     "ic_gemm_w4a8_ws": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _P, _I, _P, _I, _L, _P, _L, _P], _I),
+    "ic_init_device": ([], _I),
     "ic_gemm_w4a8_noalloc": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _P, _I, _P, _I, _L, _P], _I),
     "ic_gemm_w8a8_ex": ([_P, _L, _L, _L, _P, _L, _L, _P, _P, _P, _I, _I, _P, _I, _L, _P, _I, _L, _P, _L, _P], _I),
     "ic_gemm_w4a8_ex": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _P, _I, _I, _P, _I, _L, _P, _I, _L, _P, _L,
@@ -659,6 +660,14 @@ def gemm_w4a8(x_int8: torch.Tensor, w_packed: torch.Tensor, s_w: torch.Tensor, s
               _ptr(sa), bp, bdt, act, rp, rdt, ldr, _ptr(c), _dt(c.dtype, "out"), c.stride(0), _ptr(ws), nb,
               _stream(xq))
     return c
+
+
+def init_device(device=None) -> None:
+    """Per-device set-up (ic_init_device) for `device` (default: the current
+    one): resolves the no-alloc scratch address, so that code capturing
+    ic_gemm_w4a8_noalloc into a graph does no lookup inside the capture."""
+    with torch.cuda.device(device if device is not None else torch.cuda.current_device()):
+        _call("ic_init_device")
 
 
 def f6_split_activations(x_int8: torch.Tensor) -> torch.Tensor:

@@ -46,6 +46,11 @@ int run_gemm(GemmArgs g, hipStream_t st, const char* who, bool force_generic) {
 
 extern "C" {
 
+int ic_init_device(void) {
+  void* p = nullptr;
+  return scratch_for_current_device(&p, "ic_init_device");
+}
+
 int64_t ic_gemm_splitk_bytes(int64_t M, int64_t N, int64_t K, int64_t num_groups, int int4) {
   if (M <= IC_GEMV_MAX_M || N <= 0 || K <= 0 || K % kBK != 0 || num_groups < 1) return 0;
   if (num_groups > 1 && (K % num_groups != 0 || (K / num_groups) % 128 != 0)) return 0;

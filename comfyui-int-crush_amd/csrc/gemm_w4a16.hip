@@ -372,10 +372,11 @@ int ic_gemm_w4a16(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, c
     return ic_gemv_w4a16(x, dtype, M, K, ldx, w_packed, N, ldw, s_w, num_groups, bias, bias_dtype, out, ldo, stream);
   const int G = (int)num_groups, gsize = (int)(K / num_groups);
   // DMA pipeline: 64-K stages, scale groups of whole stages, 16-byte aligned
-  // rows; 32-bit DMA offsets within one tile
+  // rows; 32-bit DMA offsets within one tile (activation tiles of up to 384
+  // rows, weight tiles of up to 256 columns)
   const bool mfma_ok = (K % 64 == 0) && (G == 1 || gsize % 64 == 0) && !((uintptr_t)x & 15) &&
                        !((uintptr_t)w_packed & 15) && !((ldx * 2) & 15) && !(ldw & 15) &&
-                       256 * ldx * 2 < (1LL << 31) && 256 * ldw < (1LL << 31) && N * G * 4 < (1LL << 31);
+                       384 * ldx * 2 < (1LL << 31) && 256 * ldw < (1LL << 31) && N * G * 4 < (1LL << 31);
   hipStream_t st = (hipStream_t)stream;
   hipError_t e = dtype == IC_DTYPE_F16
                      ? run_w4a16<IC_DTYPE_F16>((const u16*)x, ldx, w_packed, ldw, s_w, G, gsize, bias, bias_dtype,

@@ -149,11 +149,16 @@ int ic_gemm_w8a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8
  *   num_groups == 1: out = f32(acc) * (s_a[m] * s_w[n]) + bias[n]
  *   num_groups  > 1: out = (sum_g f32(acc_g) * s_w[n,g]) * s_a[m] + bias[n],
  *                    the sum an fma chain in g order, groups of K/num_groups.
- *                    Group sizes that are multiples of 128 fold once per 128
- *                    columns (acc_g of each 128-column part with its group's
- *                    scale) on the MFMA kernels; other group sizes, K not a
- *                    multiple of 128 and unaligned operands run a scalar
- *                    kernel (one thread per output, about 100x slower).
+ *                    Every kernel folds once per block of gcd(group, 128)
+ *                    columns in K order (acc_g of each block with its group's
+ *                    scale), so the result does not depend on the kernel:
+ *                    - multiples of 128: MFMA kernels, per 128 columns;
+ *                    - odd multiples of 64 with a 16-bit output whose rows are
+ *                      16-byte aligned: the 288 x 192 MFMA kernel, per 64;
+ *                    - anything else (other group sizes, K not a multiple of
+ *                      128, f32 or unaligned outputs with groups of 64,
+ *                      unaligned operands): a scalar kernel, one thread per
+ *                      output, about 100x slower.
  */
 int ic_gemm_w4a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed,
                  int64_t N, int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a,
@@ -197,6 +202,12 @@ int ic_gemm_w4a8_ws(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const u
  * Nothing in it needs clearing: every partial is written before it is read.
  */
 #define IC_NOALLOC_SCRATCH_BYTES (32LL << 20)
+/* Per-device set-up for the current device: looks up the device address of
+ * the no-alloc scratch (a code-object symbol, which the lookup may load).
+ * Call it once per device before capturing ic_gemm_w4a8_noalloc into a
+ * hipGraph; otherwise the entry point does it on its first call on a device.
+ * No reference counterpart. */
+int ic_init_device(void);
 int ic_gemm_w4a8_noalloc(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed,
                          int64_t N, int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a,
                          const void* bias, int bias_dtype, void* out, int out_dtype, int64_t ldo,

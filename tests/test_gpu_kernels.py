@@ -811,3 +811,23 @@ def test_w4a16_group_sizes(rt, oracle, dev, G):
     ref = x.float() @ w.t()
     assert torch.allclose(out, ref, rtol=2e-2, atol=2e-2 * ref.abs().max().item() * 1e-2)
     assert _cos(out, ref) >= 0.9999
+
+
+def test_w4a16_row_stride_past_the_384_row_tile(rt, oracle, dev):
+    """An activation row stride whose 384-row tile offsets pass 2^31 bytes
+    (while 256 rows stay below) runs the scalar W4A16 kernel: correct
+    outputs, no out-of-range DMA."""
+    M, N, K, ld = 400, 64, 256, 3_500_000  # 7.0 MB rows: 256 * 7.0 MB < 2^31 <= 384 * 7.0 MB
+    assert 256 * ld * 2 < 2 ** 31 <= 384 * ld * 2
+    big = torch.zeros(M, ld, dtype=torch.bfloat16, device=dev)
+    x = _acts(M, K, torch.bfloat16, seed=101)
+    big[:, :K] = x.to(dev)
+    xa = big[:, :K]
+    packed = torch.randint(0, 256, (N, K // 2), generator=_gen(102), dtype=torch.uint8)
+    s_w = (torch.rand(N, 2, generator=_gen(103)) * 2e-2 + 1e-3).to(torch.float16).float()
+    out = rt.gemm_w4a16(xa, packed.to(dev), s_w.to(dev)).float().cpu()
+    del big, xa
+    w = torch.from_numpy(oracle.dequant_w4a16(packed.numpy(), s_w.numpy(), K, 1))
+    ref = x.float() @ w.t()
+    assert _cos(out, ref) >= 0.9999
+    assert torch.allclose(out, ref, rtol=2e-2, atol=2e-2 * ref.abs().max().item() * 1e-2)

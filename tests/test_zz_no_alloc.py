@@ -78,3 +78,37 @@ def test_noalloc_rejects_plans_beyond_the_scratch(rt, dev):
                                 rt.IC_DTYPE_BF16, N, None)
     assert rc == 2
     assert "static" in L.ic_last_error().decode()
+
+
+def test_noalloc_captured_in_a_graph(rt, dev):
+    """ic_init_device resolves the scratch outside the capture; the captured
+    no-alloc GEMM, replayed three times with eager work and synchronizations
+    between the replays, matches ic_gemm_w4a8_ws every time."""
+    M, N, K = 64, 3072, 12288
+    need = rt.lib().ic_gemm_splitk_bytes(M, N, K, K // 128, 1)
+    assert 0 < need <= SCRATCH
+    ops = _operands(M, N, K, 300, dev)
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    ref = _run(rt, "ic_gemm_w4a8_ws", M, N, K, ops, ws)
+    rt.init_device(dev)
+    xq, packed, s_w, s_a, bias = ops
+    out = torch.zeros(M, N, dtype=torch.bfloat16, device=dev)
+    L = rt.lib()
+    args = [rt._ptr(xq), M, K, K, rt._ptr(packed), N, K // 2, rt._ptr(s_w), K // 128, rt._ptr(s_a),
+            rt._ptr(bias), rt.IC_DTYPE_F16, rt._ptr(out), rt.IC_DTYPE_BF16, N]
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            rc = L.ic_gemm_w4a8_noalloc(*args, ctypes.c_void_p(s.cuda_stream))
+    assert rc == 0, L.ic_last_error().decode()
+    torch.cuda.current_stream().wait_stream(s)
+    for i in range(3):
+        out.fill_(float("nan"))
+        other = _run(rt, "ic_gemm_w4a8_noalloc", 24, 1024, 4096, _operands(24, 1024, 4096, 301 + i, dev))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"replay {i}"
+        assert not torch.isnan(other.float()).any()
