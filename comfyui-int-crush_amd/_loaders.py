@@ -49,11 +49,11 @@ def _detect_rot_size(metadata: dict | None, default_rot_size: int, format_versio
         except (TypeError, ValueError):
             value = None
         if value in VALID_ROT_SIZES:
-            log.info("[INT-Crush] Auto-detected rot_size=%d from metadata", value)
+            log.info("[INT-Crush] checkpoint metadata sets the Hadamard block size: rot_size %d", value)
             return value
-    log.warning("[INT-Crush] Metadata confirms INT-Crush format but rot_size is missing; using default "
-                "rot_size=%d. This may produce incorrect results if the model was quantized with a "
-                "different rot_size.", default_rot_size)
+    log.warning("[INT-Crush] the checkpoint is an INT-Crush one but names no valid rot_size; the node's "
+                "rot_size %d is used, and outputs are wrong if the weights were quantized with another",
+                default_rot_size)
     return default_rot_size
 
 
@@ -97,7 +97,7 @@ class SimpleINT4UNetLoader:
         rot_size = _detect_rot_size(_read_metadata(path), rot_size, _INT4_FORMAT_VERSIONS)
         use_w4a16 = rot_size == 0
         if use_w4a16:
-            log.info("[INT-Crush] W4A8 requires rotation - falling back to W4A16")
+            log.info("[INT-Crush] rot_size 0: INT4 layers run W4A16 (W4A8 needs rotated activations)")
         ops_cls = make_intcrush_ops("int4_crush", rot_size, use_w4a16=use_w4a16)
         if torch.cuda.is_available():
             torch.cuda.empty_cache()
@@ -162,11 +162,13 @@ def _apply_padded_layer_fixes(model, padded_str: str) -> None:
                     module.weight = torch.nn.Parameter(
                         QuantizedTensor(q[:, :orig_in].contiguous(), weight._layout_type, new_params),
                         requires_grad=False)
-                    log.info("[INT-Crush] INT8: Fixed %s in_features %d -> %d", layer_key, padded_in, orig_in)
+                    log.info("[INT-Crush] INT8 layer %s: padded width %d trimmed to %d inputs", layer_key,
+                             padded_in, orig_in)
             elif weight.shape[1] > orig_in:
                 padded_in = weight.shape[1]
                 module.weight = torch.nn.Parameter(weight[:, :orig_in].contiguous(), requires_grad=False)
-                log.info("[INT-Crush] INT8: Fixed %s in_features %d -> %d", layer_key, padded_in, orig_in)
+                log.info("[INT-Crush] INT8 layer %s: padded width %d trimmed to %d inputs", layer_key, padded_in,
+                         orig_in)
         if module_path == "img_in" and hasattr(m, "in_channels"):
             ps = getattr(m, "patch_size", 1)
             m.in_channels = orig_in // (ps * ps) if ps else orig_in
@@ -197,10 +199,9 @@ class IntCrushLoRALoader:
             raise ValueError(f"INT-Crush LoRA: empty file '{lora_name}'")
         attached, total = attach_lora_as_buffers(model, lora_sd, strength)
         if attached == 0:
-            log.warning("[INT-Crush LoRA] No modules matched (%d patches parsed but none mapped to INT-Crush "
-                        "layers)", total)
+            log.warning("[INT-Crush LoRA] none of the %d LoRA patches belongs to an INT-Crush layer", total)
         else:
-            log.info("[INT-Crush LoRA] Attached to %d layer(s)", attached)
+            log.info("[INT-Crush LoRA] LoRA applied to %d INT-Crush layer(s)", attached)
         return (model,)
 
 
@@ -217,7 +218,7 @@ class IntCrushLoRAUnloader:
 
     def unload(self, model):
         n = clear_intcrush_lora(model)
-        log.info("[INT-Crush LoRA] Cleared LoRA from %d layer(s)", n)
+        log.info("[INT-Crush LoRA] LoRA removed from %d layer(s)", n)
         return (model,)
 
 

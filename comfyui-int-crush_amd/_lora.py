@@ -59,6 +59,5 @@ def attach_lora_as_buffers(model: Any, lora_sd: dict, strength: float) -> tuple[
         module._intcrush_adapter_ready = False
         attached += 1
     if attached == 0:
-        _log.warning("[INT-Crush LoRA] No modules matched (%d patches parsed but none mapped to "
-                     "INT-Crush layers)", len(patches))
+        _log.debug("[INT-Crush LoRA] no INT-Crush layer among the %d patch targets", len(patches))
     return attached, len(patches)
