@@ -95,6 +95,10 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "ic_gemv_w8a8": ([_P, _L, _L, _L, _P, _L, _L, _P, _P, _P, _I, _P, _I, _L, _P], _I),
     "ic_gemv_w4a8": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _P, _I, _P, _I, _L, _P], _I),
     "ic_gemv_w4a16": ([_P, _I, _L, _L, _L, _P, _L, _L, _P, _L, _P, _I, _P, _L, _P], _I),
+    "ic_prep_gemv_w4a8": ([_P, _I, _L, _L, _L, _P, _P, _I, _P, _P, _P, _P, _L, _L, _L, _P, _L, _P, _I, _I, _P, _I,
+                           _L, _P, _I, _L, _P], _I),
+    "ic_prep_gemv_w8a8": ([_P, _I, _L, _L, _L, _P, _P, _I, _P, _P, _P, _P, _L, _L, _L, _P, _P, _I, _I, _P, _I, _L,
+                           _P, _I, _L, _P], _I),
 }
 
 _lib = None
@@ -233,6 +237,28 @@ def prepare_perm(perm: torch.Tensor | None, width: int | None = None) -> torch.T
 
 
 # ── fused prep + quantization ───────────────────────────────────────────────
+def _prep_shape(x2: torch.Tensor, rot_size: int, w_in: int | None, smoothrot: PreparedFactors | None,
+                perm: torch.Tensor | None, smooth: PreparedFactors | None, who: str) -> tuple[int, int, int]:
+    """Checks of the preparation arguments; returns (rot_size, K_w, dtype code)."""
+    K_in = x2.shape[1]
+    R = int(rot_size)
+    if R not in VALID_ROT_SIZES:
+        raise ValueError(f"rot_size must be one of {VALID_ROT_SIZES}, got {R}")
+    K_r = ((K_in + R - 1) // R) * R if R else K_in
+    K_w = max(int(w_in) if w_in is not None else K_r, K_r)
+    dt = _dt(x2.dtype, who)
+    for f in (smoothrot, smooth):
+        if f is not None and f.dtype != x2.dtype:
+            raise ValueError("prepared factors were built for another activation dtype")
+    if smoothrot is not None and smoothrot.K != K_in:
+        raise ValueError(f"SmoothRot factors have {smoothrot.K} entries, expected {K_in}")
+    if smooth is not None and smooth.K != K_w:
+        raise ValueError(f"smooth factors have {smooth.K} entries, expected {K_w}")
+    if perm is not None and (perm.dtype != torch.int32 or perm.numel() != K_w or not perm.is_cuda):
+        raise ValueError("perm must be an int32 device tensor of length w_in (see prepare_perm)")
+    return R, K_w, dt
+
+
 def rotate_quantize(x: torch.Tensor, *, rot_size: int = 0, w_in: int | None = None,
                     smoothrot: PreparedFactors | None = None, perm: torch.Tensor | None = None,
                     smooth: PreparedFactors | None = None, s_a_out: torch.Tensor | None = None,
@@ -247,21 +273,7 @@ def rotate_quantize(x: torch.Tensor, *, rot_size: int = 0, w_in: int | None = No
     _need_cuda(x)
     x2 = _rows(x)
     M, K_in = x2.shape
-    R = int(rot_size)
-    if R not in VALID_ROT_SIZES:
-        raise ValueError(f"rot_size must be one of {VALID_ROT_SIZES}, got {R}")
-    K_r = ((K_in + R - 1) // R) * R if R else K_in
-    K_w = max(int(w_in) if w_in is not None else K_r, K_r)
-    dt = _dt(x2.dtype, "rotate_quantize")
-    for f in (smoothrot, smooth):
-        if f is not None and f.dtype != x2.dtype:
-            raise ValueError("prepared factors were built for another activation dtype")
-    if smoothrot is not None and smoothrot.K != K_in:
-        raise ValueError(f"SmoothRot factors have {smoothrot.K} entries, expected {K_in}")
-    if smooth is not None and smooth.K != K_w:
-        raise ValueError(f"smooth factors have {smooth.K} entries, expected {K_w}")
-    if perm is not None and (perm.dtype != torch.int32 or perm.numel() != K_w or not perm.is_cuda):
-        raise ValueError("perm must be an int32 device tensor of length w_in (see prepare_perm)")
+    R, K_w, dt = _prep_shape(x2, rot_size, w_in, smoothrot, perm, smooth, "rotate_quantize")
     s_a = _alloc_or_reuse((M,), torch.float32, x2.device, s_a_out)
     q = _alloc_or_reuse((M, K_w), torch.int8, x2.device, x_int8_out)
     with torch.cuda.device(x2.device):
@@ -849,6 +861,73 @@ def gemv(x: torch.Tensor, w: torch.Tensor, s_w: torch.Tensor, s_a: torch.Tensor 
     return c
 
 
+# ── single-launch prep + GEMV (M <= 16) ─────────────────────────────────────
+PREP_GEMV_MAX_K = 8192
+PREP_GEMV_MAX_CODES = 16384
+
+
+def prep_gemv_ok(x: torch.Tensor, K_w: int, w: torch.Tensor, num_groups: int = 1) -> bool:
+    """Whether prep_gemv takes a call with activations x, prepared width K_w
+    and weights w (otherwise rotate_quantize and the GEMM entry points do):
+    f16/bf16 rows, K_in a multiple of 16, 16-byte aligned rows and weights."""
+    if x.dim() < 1 or x.shape[-1] == 0:
+        return False
+    M, K_in = x.numel() // x.shape[-1], x.shape[-1]
+    ldx = x.stride(-2) if x.dim() > 1 else K_in
+    return (x.dtype in (torch.float16, torch.bfloat16) and 1 <= M <= GEMV_MAX_M and K_w % 128 == 0
+            and K_w <= PREP_GEMV_MAX_K and M * K_w <= PREP_GEMV_MAX_CODES and K_in % 16 == 0
+            and x.stride(-1) == 1 and x.data_ptr() % 16 == 0 and ldx % 8 == 0 and w.dim() == 2
+            and w.stride(-1) == 1 and w.data_ptr() % 16 == 0 and (w.stride(0) * w.element_size()) % 16 == 0
+            and num_groups in (1, K_w // 128))
+
+
+def prep_gemv(x: torch.Tensor, w: torch.Tensor, s_w: torch.Tensor, *, int4: bool, rot_size: int = 0,
+              w_in: int | None = None, smoothrot: PreparedFactors | None = None,
+              perm: torch.Tensor | None = None, smooth: PreparedFactors | None = None,
+              bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16,
+              out: torch.Tensor | None = None, activation: int = 0,
+              residual: torch.Tensor | None = None) -> torch.Tensor:
+    """One launch for M <= 16 tokens (ic_prep_gemv_w4a8 / ic_prep_gemv_w8a8):
+    rotate_quantize(x, rot_size, w_in, smoothrot, perm, smooth) followed by
+    gemm_w4a8 (int4: w packed uint8 [N, K/2], s_w [N, G] with G = 1 or K/128)
+    or fused_int8_gemm_dequant (w int8 [N, K], s_w [N]) with their epilogue
+    (bias, activation, residual).  Bit-identical to the two calls; the small-M
+    form of fused_quant_int8_gemm_dequant (kernels/triton_int8_gemm.py:243-389).
+    Calls outside prep_gemv_ok raise."""
+    _need_cuda(x, w, s_w, bias, residual)
+    x2 = _rows(x)
+    M, K_in = x2.shape
+    R, K_w, dt = _prep_shape(x2, rot_size, w_in, smoothrot, perm, smooth, "prep_gemv")
+    wr = _rows(w)
+    N = wr.shape[0]
+    if int4:
+        assert wr.dtype == torch.uint8 and wr.shape[1] * 2 >= K_w, "w must be packed uint8 [N, >= K/2]"
+        sw = s_w.detach().reshape(N, -1).to(torch.float32).contiguous()
+    else:
+        assert wr.dtype == torch.int8 and wr.shape[1] >= K_w, "w must be int8 [N, >= K]"
+        sw = s_w.detach().reshape(-1).to(torch.float32).contiguous()
+        if sw.numel() != N:
+            raise ValueError(f"s_w must hold one scale per output channel ({N}), got {sw.numel()}")
+    G = sw.shape[1] if int4 else 1
+    if not prep_gemv_ok(x2, K_w, wr, G):
+        raise ValueError(f"prep_gemv: M={M}, K={K_w}, dtype {x2.dtype}, {G} groups or the weight layout is "
+                         f"outside the single-launch limits (use rotate_quantize and the GEMM)")
+    bp, bdt, _keep = _bias_args(bias, N)
+    act, rp, rdt, ldr, _rkeep = _epilogue_args(activation, residual, M, N)
+    c = _out_buffer(out, M, N, out_dtype, x2.device)
+    sr = (_ptr(smoothrot.rcp), _ptr(smoothrot.fdt)) if smoothrot else (None, None)
+    sm = (_ptr(smooth.rcp), _ptr(smooth.fdt)) if smooth else (None, None)
+    with torch.cuda.device(x2.device):
+        head = (_ptr(x2), dt, M, K_in, x2.stride(0), sr[0], sr[1], R, _ptr(perm), sm[0], sm[1], _ptr(wr), N, K_w,
+                wr.stride(0), _ptr(sw))
+        tail = (bp, bdt, act, rp, rdt, ldr, _ptr(c), _dt(c.dtype, "out"), c.stride(0), _stream(x2))
+        if int4:
+            _call("ic_prep_gemv_w4a8", *head, G, *tail)
+        else:
+            _call("ic_prep_gemv_w8a8", *head, *tail)
+    return c
+
+
 def fused_quant_int8_gemm_dequant(x: torch.Tensor, w_int8: torch.Tensor, s_w: torch.Tensor,
                                   bias: torch.Tensor | None = None,
                                   out_dtype: torch.dtype = torch.bfloat16,
@@ -934,6 +1013,6 @@ __all__ = [
     "unpack_int4_to_float", "prepare_factors", "prepare_perm", "PreparedFactors", "gemm_acc_i32",
     "gemv", "GEMV_MAX_M", "fused_layernorm_quantize", "fused_rmsnorm_quantize", "fused_softmax_quantize",
     "norm_rotate_quantize", "ACT_NONE", "ACT_SILU", "ACT_GELU", "ACT_GELU_TANH", "int8_gemm_int8out",
-    "gemm_chain", "CHAIN_ROT_SIZES",
+    "gemm_chain", "CHAIN_ROT_SIZES", "prep_gemv", "prep_gemv_ok", "PREP_GEMV_MAX_K", "PREP_GEMV_MAX_CODES",
     "load_library",
 ]

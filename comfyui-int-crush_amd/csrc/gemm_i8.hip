@@ -44,6 +44,21 @@ int run_gemm(GemmArgs g, hipStream_t st, const char* who, bool force_generic) {
 
 }  // namespace
 
+// Validation shared by the _ex entry points: activation code and residual.
+int ic_check_epi(const char* who, int activation, const void* residual, int residual_dtype, int64_t ldr,
+                 int64_t N) {
+  if (activation < 0 || activation > 3)
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: activation must be 0 (none), 1 (SiLU), 2 (GELU) or 3 (GELU tanh)",
+                        who);
+  if (residual != nullptr && residual_dtype != IC_DTYPE_F16 && residual_dtype != IC_DTYPE_BF16 &&
+      residual_dtype != IC_DTYPE_F32)
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: residual dtype must be f16/bf16/f32", who);
+  if (residual != nullptr && ldr < N)
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: residual row stride %lld < N=%lld", who, (long long)ldr,
+                        (long long)N);
+  return IC_OK;
+}
+
 extern "C" {
 
 int ic_init_device(void) {
@@ -61,26 +76,11 @@ int64_t ic_gemm_splitk_bytes(int64_t M, int64_t N, int64_t K, int64_t num_groups
   return S > 1 ? (int64_t)S * M * N * 4 : 0;
 }
 
-// Validation shared by the _ex entry points: activation code and residual.
-static int check_epi(const char* who, int activation, const void* residual, int residual_dtype, int64_t ldr,
-                     int64_t N) {
-  if (activation < 0 || activation > 3)
-    return ic_set_error(IC_ERR_INVALID_ARG, "%s: activation must be 0 (none), 1 (SiLU), 2 (GELU) or 3 (GELU tanh)",
-                        who);
-  if (residual != nullptr && residual_dtype != IC_DTYPE_F16 && residual_dtype != IC_DTYPE_BF16 &&
-      residual_dtype != IC_DTYPE_F32)
-    return ic_set_error(IC_ERR_INVALID_ARG, "%s: residual dtype must be f16/bf16/f32", who);
-  if (residual != nullptr && ldr < N)
-    return ic_set_error(IC_ERR_INVALID_ARG, "%s: residual row stride %lld < N=%lld", who, (long long)ldr,
-                        (long long)N);
-  return IC_OK;
-}
-
 int ic_gemm_w8a8_ex(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8_t* w, int64_t N, int64_t ldw,
                     const float* s_a, const float* s_w, const void* bias, int bias_dtype, int activation,
                     const void* residual, int residual_dtype, int64_t ldr, void* out, int out_dtype, int64_t ldo,
                     void* workspace, int64_t workspace_bytes, void* stream) {
-  if (int rc = check_epi("ic_gemm_w8a8", activation, residual, residual_dtype, ldr, N)) return rc;
+  if (int rc = ic_check_epi("ic_gemm_w8a8", activation, residual, residual_dtype, ldr, N)) return rc;
   const ic_epi epi{activation, residual, residual_dtype, ldr};
   if (ic_gemv_applicable(M, K, xq, ldx, w, ldw) && ldw >= K && N > 0 && ldo >= N && ldx >= K)
     return ic_gemv_w8a8_epi(xq, M, K, ldx, w, N, ldw, s_a, s_w, bias, bias_dtype, out, out_dtype, ldo, epi, stream);
@@ -108,7 +108,7 @@ int ic_gemm_w4a8_ex(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const u
                     int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a, const void* bias,
                     int bias_dtype, int activation, const void* residual, int residual_dtype, int64_t ldr, void* out,
                     int out_dtype, int64_t ldo, void* workspace, int64_t workspace_bytes, void* stream) {
-  if (int rc = check_epi("ic_gemm_w4a8", activation, residual, residual_dtype, ldr, N)) return rc;
+  if (int rc = ic_check_epi("ic_gemm_w4a8", activation, residual, residual_dtype, ldr, N)) return rc;
   const ic_epi epi{activation, residual, residual_dtype, ldr};
   if (ic_gemv_applicable(M, K, xq, ldx, w_packed, ldw) && ldw * 2 >= K && N > 0 && ldo >= N && ldx >= K &&
       (num_groups == 1 || num_groups * 128 == K))

@@ -6,15 +6,9 @@
 // (Flux modulation layers, CFG batch 2).  Here one 256-thread workgroup owns
 // 16 output columns and its four waves split K in blocks of 128:
 //
-//   W8A8 / W4A8:  two v_mfma_i32_16x16x64_i8 per block (rows = tokens, padded
-//                 to 16; columns = outputs); INT4 weights are expanded in
-//                 registers to 16*q (two masks and a byte permute per 8
-//                 nibbles), the factor 16 removed exactly at the end.  Block
-//                 sums are exact int32; grouped scales are folded afterwards in
-//                 group order, so every output equals the tiled GEMM's
-//                 (same formula, same rounding steps):
-//                   G == 1: f32(sum) * (s_a[m] * s_w[n]) (+ bias)
-//                   G  > 1: (fma chain over g of f32(acc_g) * s_w[n,g]) * s_a[m] (+ bias)
+//   W8A8 / W4A8:  two v_mfma_i32_16x16x64_i8 per block on exact int32 block
+//                 sums, the tiled GEMM's epilogue formula (body in gemv_i8.h,
+//                 shared with the single-launch prep + GEMV of gemv_prep.h)
 //   W4A16:        four v_mfma_f32_16x16x32_{f16,bf16} per block on weights
 //                 dequantized exactly as RN_dt(q * RN_dt(s)); fp32 partials of
 //                 the four waves are added in wave order.
@@ -25,28 +19,17 @@
 // are staged in LDS once per workgroup and read per block from there, so the
 // registers hold weights only and more waves keep loads in flight.
 #include "dequant4.h"
+#include "gemv_i8.h"
 
 namespace {
 
-constexpr int kGT = 256;  // threads per workgroup (4 waves)
-constexpr int kGBK = 128; // K per block
+using gemv::kGT;
+using gemv::kGBK;
+using gemv::kXlBytes;
 
 typedef _Float16 v8h_t __attribute__((ext_vector_type(8)));
 typedef __bf16 v8bf_t __attribute__((ext_vector_type(8)));
 
-// 8 INT4 nibbles (low nibble = even k) -> 8 int8 values 16*q in natural k order.
-IC_DEV void unpack8_x16(uint32_t P, uint32_t& w0, uint32_t& w1) {
-  const uint32_t lo = (P << 4) & 0xf0f0f0f0u;
-  const uint32_t hi = P & 0xf0f0f0f0u;
-  w0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
-  w1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
-}
-
-// XL: as in the W4A16 GEMV below, the M x K activation codes (at most
-// kXlBytes) are staged in LDS once per workgroup, after the first batch of
-// weight loads is issued, and read per block when used: fewer VGPRs, more
-// waves per SIMD, more weight bytes in flight.
-constexpr int kXlBytes = 16384;
 template <bool INT4, int GS, int OUT_DT, bool XL>
 __global__ __launch_bounds__(kGT) void gemv_i8_kernel(
     const int8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
@@ -56,142 +39,9 @@ __global__ __launch_bounds__(kGT) void gemv_i8_kernel(
   // GS == 128: block sums [KB][M][16]; otherwise per-wave totals [4][M][16];
   // with XL the activation codes [M][K] follow
   extern __shared__ int32_t sacc[];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n0 = blockIdx.x * 16;
-  const int c = lane >> 4, col = lane & 15;
-  const int n = min(n0 + col, N - 1);
-  const int am = min(col, M - 1);  // token row fed by this lane (rows >= M repeat the last one)
-  const int KB = K / kGBK;
-  int8_t* xs = (int8_t*)(sacc + (GS == 128 ? KB : 4) * M * 16);
-  const int8_t* arow = XL ? xs + (int64_t)am * K + 32 * c : A + (int64_t)am * lda + 32 * c;
-  const uint8_t* brow = B + (int64_t)n * ldb + (INT4 ? 16 * c : 32 * c);
-
-  // Loads of up to kBatch blocks are issued before any of them is used, so a
-  // wave keeps kBatch weight loads (plus activation loads) in flight.
-  constexpr int kBatch = 8;
-  v4i tot = {0, 0, 0, 0};
-  // One block: two MFMAs on this lane's 32 activation codes and 32 weights.
-  auto mma_block = [&](int b, const v4i& av0, const v4i& av1, const v4u& pwu, const v4i& w1u) {
-    v4i b0v, b1v;
-    if constexpr (INT4) {
-      uint32_t w[8];
-      unpack8_x16(pwu.x, w[0], w[1]);
-      unpack8_x16(pwu.y, w[2], w[3]);
-      unpack8_x16(pwu.z, w[4], w[5]);
-      unpack8_x16(pwu.w, w[6], w[7]);
-      b0v = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
-      b1v = v4i{(int)w[4], (int)w[5], (int)w[6], (int)w[7]};
-    } else {
-      b0v = __builtin_bit_cast(v4i, pwu);
-      b1v = w1u;
-    }
-    if constexpr (GS == 128) {
-      v4i s = __builtin_amdgcn_mfma_i32_16x16x64_i8(av0, b0v, v4i{0, 0, 0, 0}, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_i32_16x16x64_i8(av1, b1v, s, 0, 0, 0);
-      // D layout: lane holds rows 4*(lane/16) + i of column lane%16
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 4 * c + i;
-        if (r < M) sacc[(b * M + r) * 16 + col] = s[i];
-      }
-    } else {
-      tot = __builtin_amdgcn_mfma_i32_16x16x64_i8(av0, b0v, tot, 0, 0, 0);
-      tot = __builtin_amdgcn_mfma_i32_16x16x64_i8(av1, b1v, tot, 0, 0, 0);
-    }
-  };
-  if constexpr (XL) {
-    v4u pw[kBatch];
-    v4i w1[INT4 ? 1 : kBatch];
-    auto load_batch = [&](int b0) {
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const int b = b0 + 4 * u;
-        if (b < KB) {  // uniform across the wave
-          if constexpr (INT4) {
-            pw[u] = *(const v4u*)(brow + (kGBK / 2) * b);
-          } else {
-            pw[u] = *(const v4u*)(brow + kGBK * b);
-            w1[u] = *(const v4i*)(brow + kGBK * b + 16);
-          }
-        }
-      }
-    };
-    // the first batch of weight loads is in flight while the codes are staged
-    load_batch(wave);
-    const int per_row = K / 16;  // 16-byte chunks
-    for (int i = tid; i < M * per_row; i += kGT) {
-      const int r = i / per_row, k16 = i - r * per_row;
-      *(v4i*)(xs + (int64_t)r * K + 16 * k16) = *(const v4i*)(A + (int64_t)r * lda + 16 * k16);
-    }
-    __syncthreads();
-    for (int b0 = wave; b0 < KB; b0 += 4 * kBatch) {
-      if (b0 != wave) load_batch(b0);
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const int b = b0 + 4 * u;
-        if (b >= KB) break;
-        mma_block(b, *(const v4i*)(arow + kGBK * b), *(const v4i*)(arow + kGBK * b + 16), pw[u],
-                  w1[INT4 ? 0 : u]);
-      }
-    }
-  } else {
-    for (int b0 = wave; b0 < KB; b0 += 4 * kBatch) {
-      v4u pw[kBatch];
-      v4i a0[kBatch], a1[kBatch], w1[kBatch];
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const int b = b0 + 4 * u;
-        if (b < KB) {  // uniform across the wave
-          a0[u] = *(const v4i*)(arow + kGBK * b);
-          a1[u] = *(const v4i*)(arow + kGBK * b + 16);
-          if constexpr (INT4) {
-            pw[u] = *(const v4u*)(brow + (kGBK / 2) * b);
-          } else {
-            pw[u] = *(const v4u*)(brow + kGBK * b);
-            w1[u] = *(const v4i*)(brow + kGBK * b + 16);
-          }
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const int b = b0 + 4 * u;
-        if (b >= KB) break;
-        mma_block(b, a0[u], a1[u], pw[u], w1[u]);
-      }
-    }
-  }
-  if constexpr (GS != 128) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 4 * c + i;
-      if (r < M) sacc[(wave * M + r) * 16 + col] = tot[i];
-    }
-  }
-  __syncthreads();
-
-  if (tid >= 16 * M) return;
-  const int m = tid >> 4, nl = tid & 15, no = n0 + nl;
-  if (no >= N) return;
-  float v;
-  if constexpr (GS == 128) {
-    const float* sw = s_w + (int64_t)no * G;
-    float facc = 0.0f;
-    for (int g = 0; g < KB; ++g) {
-      float s = sw[g];
-      if constexpr (INT4) s *= 0.0625f;  // block sums hold 16 * the true sum
-      facc = __builtin_fmaf((float)sacc[(g * M + m) * 16 + nl], s, facc);
-    }
-    v = facc * s_a[m];
-  } else {
-    const int t = ((sacc[(0 * M + m) * 16 + nl] + sacc[(1 * M + m) * 16 + nl]) +
-                   sacc[(2 * M + m) * 16 + nl]) + sacc[(3 * M + m) * 16 + nl];
-    float a = (float)t;
-    if constexpr (INT4) a *= 0.0625f;
-    v = a * (s_a[m] * s_w[no]);
-  }
-  if (bias != nullptr) v = v + ld_any_f32(bias, bias_dt, no);
-  v = epi_apply(v, epi, m, no);
-  st_from_f32<OUT_DT>(C, (int64_t)m * ldc + no, v);
+  int8_t* xs = (int8_t*)(sacc + (GS == 128 ? K / kGBK : 4) * M * 16);
+  gemv::gemv_i8_body<INT4, GS, OUT_DT, XL>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, epi, sacc,
+                                           xs);
 }
 
 // W4A16 weight dequantization RN_dt(q * RN_dt(s)) of 8 nibbles.

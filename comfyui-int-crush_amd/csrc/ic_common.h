@@ -21,6 +21,9 @@ int ic_num_cus();  // compute units of the current device
 // hipFuncSetAttribute(MaxDynamicSharedMemorySize) once per kernel and device;
 // done points at the caller's 64 per-device flags.
 hipError_t ic_set_lds_limit(const void* kern, int bytes, unsigned char* done);
+// Validation of the epilogue arguments (activation code, residual dtype and
+// stride) shared by the entry points that take them (gemm_i8.hip).
+int ic_check_epi(const char* who, int activation, const void* residual, int residual_dtype, int64_t ldr, int64_t N);
 // GEMV routing test shared by the GEMM entry points (gemv.hip); strides in bytes.
 bool ic_gemv_applicable(int64_t M, int64_t K, const void* x, int64_t ldx_bytes, const void* w, int64_t ldw_bytes);
 

@@ -19,54 +19,11 @@
 // A tile of 4096 positions is spread as 16 contiguous elements per thread
 // (digits 0-1 in registers); digits 2-3 are reached through one LDS transpose
 // among 16 threads, digits 4-5 through a second transpose among 256 threads.
-#include "rq_common.h"
+#include "rq_row.h"
 
 namespace {
 
 using namespace rq;
-
-// Load 16 consecutive values starting at element p0 (zero past n) as f32.
-// Whole in-bounds 16-element runs use 16-byte loads when the base is aligned.
-template <int DT> IC_DEV void load16(const void* base, int p0, int n, bool vec_ok, float* out) {
-  constexpr int ESZ = DT == IC_DTYPE_F32 ? 4 : 2;
-  if (vec_ok && p0 + 16 <= n && ((((uintptr_t)base) & 15) == 0)) {
-    const v4u* src = (const v4u*)((const char*)base + (int64_t)p0 * ESZ);
-    if constexpr (ESZ == 2) {
-      v4u a = src[0], b = src[1];
-      uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        out[2 * i] = bits16_f32<DT>((u16)(w[i] & 0xffffu));
-        out[2 * i + 1] = bits16_f32<DT>((u16)(w[i] >> 16));
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v4u a = src[i];
-        out[4 * i] = __uint_as_float(a.x);
-        out[4 * i + 1] = __uint_as_float(a.y);
-        out[4 * i + 2] = __uint_as_float(a.z);
-        out[4 * i + 3] = __uint_as_float(a.w);
-      }
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < 16; ++j) out[j] = (p0 + j < n) ? ld_as_f32<DT>(base, p0 + j) : 0.0f;
-  }
-}
-IC_DEV void load16i(const int32_t* base, int p0, int n, int* out) {
-  if (p0 + 16 <= n && ((((uintptr_t)base) & 15) == 0)) {
-    const v4u* src = (const v4u*)(base + p0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v4u a = src[i];
-      out[4 * i] = (int)a.x; out[4 * i + 1] = (int)a.y; out[4 * i + 2] = (int)a.z; out[4 * i + 3] = (int)a.w;
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < 16; ++j) out[j] = (p0 + j < n) ? base[p0 + j] : 0;
-  }
-}
 
 // LOG4R: 0 = no rotation, 2..6 = rot size 16..4096.  QUANT: write INT8 codes and
 // scales; otherwise write the prepared activation in the input type.
@@ -79,12 +36,11 @@ __global__ __launch_bounds__(kThreads) void rotate_quant_kernel(
     int8_t* __restrict__ q_out, int64_t ldq, float* __restrict__ s_out,
     void* __restrict__ y_out, int64_t ldy) {
   constexpr int R = LOG4R == 0 ? 1 : (1 << (2 * LOG4R));
-  constexpr int RC = LOG4R <= 2 ? 0 : (LOG4R <= 4 ? 1 : 2);
   constexpr int ESZ = DT == IC_DTYPE_F32 ? 4 : 2;
 
-  __shared__ double tbuf[kTile / 16 * kPadStride];  // 36 KB; reused as the row buffer
+  __shared__ double tbuf[kTbufDoubles];  // 36 KB; reused as the row buffer
   __shared__ float red[kThreads / 64];
-  __shared__ uint32_t xred[DT == IC_DTYPE_BF16 && LOG4R == 6 ? 2 * (kThreads / 64) : 1];
+  __shared__ uint32_t xred[DT == IC_DTYPE_BF16 && LOG4R == 6 ? kXredWords : 1];
 
   const int t = threadIdx.x;
   const int64_t row = blockIdx.x;
@@ -97,74 +53,24 @@ __global__ __launch_bounds__(kThreads) void rotate_quant_kernel(
 
   // Rotated, rounded values of this thread (exact values of type DT) per tile.
   float val[kMaxTiles][16];
-
 #pragma unroll
   for (int tile = 0; tile < kMaxTiles; ++tile) {
     if (tile >= ntiles) break;
-    const int base = tile * kTile;
-    double v[16];
-    // ---- load + SmoothRot divide (digits 0-1 layout: 16 contiguous positions)
-    const int p0 = base + 16 * t;
+    // load + SmoothRot divide (16 contiguous positions per thread)
+    const int p0 = tile * kTile + 16 * t;
     float xs[16];
     load16<DT>(xrow, p0, K_in, xvec, xs);
     if (sr_rcp != nullptr) {
       float rc[16];
       load16<IC_DTYPE_F32>(sr_rcp, p0, K_in, fvec, rc);
-#pragma unroll
-      for (int j = 0; j < 16; ++j)
-        if (p0 + j < K_in) xs[j] = div_round_dt<DT>(xs[j], rc[j], sr_f, p0 + j);
+      smoothrot_divide16<DT>(xs, rc, sr_f, p0, K_in);
     }
-    if constexpr (DT == IC_DTYPE_BF16 && LOG4R >= 2) bf16_flush_small<LOG4R, kThreads>(xs, xred);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) v[j] = (double)xs[j];
-    if constexpr (LOG4R >= 2) { stage_lo(v); stage_hi(v); }
-    if constexpr (LOG4R >= 3) {
-      __syncthreads();  // previous users of tbuf are done
-#pragma unroll
-      for (int j = 0; j < 16; ++j) tbuf[tslot(16 * t + j)] = v[j];
-      __syncthreads();
-      const int g = t >> 4, l = t & 15;
-#pragma unroll
-      for (int h = 0; h < 16; ++h) v[h] = tbuf[tslot(256 * g + 16 * h + l)];
-      stage_lo(v);
-      if constexpr (LOG4R >= 4) stage_hi(v);
-      if constexpr (LOG4R >= 5) {
-#pragma unroll
-        for (int h = 0; h < 16; ++h) tbuf[tslot(256 * g + 16 * h + l)] = v[h];
-        __syncthreads();
-#pragma unroll
-        for (int gg = 0; gg < 16; ++gg) v[gg] = tbuf[tslot(256 * gg + t)];
-        stage_lo(v);
-        if constexpr (LOG4R >= 6) stage_hi(v);
-      }
-    }
-    // ---- round once to the activation type; positions past the rotated
-    // width are the zero pad to K_w.
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int p = base + tile_pos<(LOG4R == 0 ? 0 : RC)>(t, j);
-      val[tile][j] = p < K_r ? round_f64_to_dt<DT>(v[j]) : 0.0f;
-    }
+    rotate_tile<DT, LOG4R>(xs, tbuf, xred, tile * kTile, K_r, val[tile]);
   }
-
-  // ---- publish the prepared row (natural order) to LDS for the gather
-  __syncthreads();
   char* rowbuf = (char*)tbuf;
-#pragma unroll
-  for (int tile = 0; tile < kMaxTiles; ++tile) {
-    if (tile >= ntiles) break;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int p = tile * kTile + tile_pos<(LOG4R == 0 ? 0 : RC)>(t, j);
-      if (p < K_w) {
-        if constexpr (ESZ == 2) ((u16*)rowbuf)[p] = f32_bits16<DT>(val[tile][j]);
-        else ((float*)rowbuf)[p] = val[tile][j];
-      }
-    }
-  }
-  __syncthreads();
+  publish_row<DT, LOG4R, kMaxTiles>(val, ntiles, K_w, rowbuf);
 
-  // ---- gather (perm), old-smooth divide, abs-max.  Thread t owns output
+  // gather (perm), old-smooth divide, abs-max.  Thread t owns output
   // positions o = 16*(t + 256*c) + j.
   float m = 0.0f;
 #pragma unroll
@@ -180,20 +86,7 @@ __global__ __launch_bounds__(kThreads) void rotate_quant_kernel(
     }
     float smr[16];
     if (sm_rcp != nullptr) load16<IC_DTYPE_F32>(sm_rcp, o0, K_w, fvec, smr);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int o = o0 + j;
-      float vv = 0.0f;
-      if (o < K_w) {
-        // a malformed perm entry reads position 0 instead of leaving the row
-        const int sidx = (unsigned)src[j] < (unsigned)K_w ? src[j] : 0;
-        if constexpr (ESZ == 2) vv = bits16_f32<DT>(((const u16*)rowbuf)[sidx]);
-        else vv = ((const float*)rowbuf)[sidx];
-        if (sm_rcp != nullptr) vv = div_round_dt<DT>(vv, smr[j], sm_f, o);
-      }
-      val[c][j] = vv;
-      m = __builtin_fmaxf(m, __builtin_fabsf(vv));
-    }
+    m = gather16<DT>(rowbuf, src, sm_rcp != nullptr, smr, sm_f, o0, K_w, val[c], m);
   }
 
   if constexpr (!QUANT) {
@@ -206,13 +99,8 @@ __global__ __launch_bounds__(kThreads) void rotate_quant_kernel(
         if (o < K_w) st_from_f32<DT>((char*)y_out + row * ldy * ESZ, o, val[c][j]);
       }
     }
-    return;
   } else {
-    m = wave_max(m);
-    if ((t & 63) == 0) red[t >> 6] = m;
-    __syncthreads();
-    m = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
-    const float s = quant_scale(m);
+    const float s = row_scale(m, red);
     const double rs = 1.0 / (double)s;
     if (t == 0) s_out[row] = s;
     int8_t* qrow = q_out + row * ldq;
@@ -221,22 +109,7 @@ __global__ __launch_bounds__(kThreads) void rotate_quant_kernel(
       if (c >= ntiles) break;
       const int o0 = 16 * (t + kThreads * c);
       if (o0 >= K_w) break;
-      uint32_t w[4];
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        uint32_t packed = 0;
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const int code = quant_code(val[c][4 * d + b], rs);
-          packed |= ((uint32_t)code & 0xffu) << (8 * b);
-        }
-        w[d] = packed;
-      }
-      if (o0 + 16 <= K_w && ((((uintptr_t)(qrow + o0)) & 15) == 0)) {
-        *(v4u*)(qrow + o0) = v4u{w[0], w[1], w[2], w[3]};
-      } else {
-        for (int j = 0; j < 16 && o0 + j < K_w; ++j) qrow[o0 + j] = (int8_t)(w[j >> 2] >> (8 * (j & 3)));
-      }
+      store_codes16(val[c], rs, qrow, o0, K_w);
     }
   }
 }

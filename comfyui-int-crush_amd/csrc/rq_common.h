@@ -51,6 +51,49 @@ template <int DT> IC_DEV float bits16_f32(u16 b) {
   else return bf16_to_f32(b);
 }
 
+// Load 16 consecutive values starting at element p0 (zero past n) as f32.
+// Whole in-bounds 16-element runs use 16-byte loads when the base is aligned.
+template <int DT> IC_DEV void load16(const void* base, int p0, int n, bool vec_ok, float* out) {
+  constexpr int ESZ = DT == IC_DTYPE_F32 ? 4 : 2;
+  if (vec_ok && p0 + 16 <= n && ((((uintptr_t)base) & 15) == 0)) {
+    const v4u* src = (const v4u*)((const char*)base + (int64_t)p0 * ESZ);
+    if constexpr (ESZ == 2) {
+      v4u a = src[0], b = src[1];
+      uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        out[2 * i] = bits16_f32<DT>((u16)(w[i] & 0xffffu));
+        out[2 * i + 1] = bits16_f32<DT>((u16)(w[i] >> 16));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v4u a = src[i];
+        out[4 * i] = __uint_as_float(a.x);
+        out[4 * i + 1] = __uint_as_float(a.y);
+        out[4 * i + 2] = __uint_as_float(a.z);
+        out[4 * i + 3] = __uint_as_float(a.w);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) out[j] = (p0 + j < n) ? ld_as_f32<DT>(base, p0 + j) : 0.0f;
+  }
+}
+IC_DEV void load16i(const int32_t* base, int p0, int n, int* out) {
+  if (p0 + 16 <= n && ((((uintptr_t)base) & 15) == 0)) {
+    const v4u* src = (const v4u*)(base + p0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v4u a = src[i];
+      out[4 * i] = (int)a.x; out[4 * i + 1] = (int)a.y; out[4 * i + 2] = (int)a.z; out[4 * i + 3] = (int)a.w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) out[j] = (p0 + j < n) ? base[p0 + j] : 0;
+  }
+}
+
 // Layout of register element j of thread t after the rotation phases for rot
 // size class RC (0: none/16, 1: 64/256, 2: 1024/4096, 3: 1024 rotated inside
 // each wave's own 1024 positions), tile-local position.

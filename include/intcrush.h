@@ -301,6 +301,36 @@ int ic_gemv_w4a16(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, c
                   int64_t N, int64_t ldw, const float* s_w, int64_t num_groups, const void* bias,
                   int bias_dtype, void* out, int64_t ldo, void* stream);
 
+/*
+ * Single-launch small-batch linear on raw activations: the preparation and
+ * per-token quantization of ic_rotate_quantize (same x, dtype, M, K_in, ldx,
+ * sr_rcp/sr_f, rot_size, perm, sm_rcp/sm_f; K plays K_w) followed by the W4A8
+ * / W8A8 GEMV with the epilogue options of ic_gemm_*_ex, in one kernel.  Each
+ * workgroup prepares the M rows itself in LDS while its first weight loads are
+ * in flight; outputs are bit-identical to ic_rotate_quantize followed by
+ * ic_gemm_w4a8_ex / ic_gemm_w8a8_ex (which route M <= IC_GEMV_MAX_M to the
+ * GEMV).  Limits: dtype f16/bf16; 1 <= M <= IC_GEMV_MAX_M (M = 0: no-op);
+ * K a multiple of 128, K <= IC_PREP_GEMV_MAX_K and M * K <=
+ * IC_PREP_GEMV_MAX_CODES; weights 16-byte aligned with a row stride (ldw, in
+ * bytes for both formats: INT4 rows hold K/2 bytes) that is a multiple of
+ * 16; W4A8 num_groups 1 or K/128.  Outside them IC_ERR_UNSUPPORTED: the two
+ * calls cover every shape.  Replace the small-M use of
+ * fused_quant_int8_gemm_dequant (kernels/triton_int8_gemm.py:243-389) behind
+ * _ops.py:443-464 and :493-579.
+ */
+#define IC_PREP_GEMV_MAX_K 8192
+#define IC_PREP_GEMV_MAX_CODES 16384
+int ic_prep_gemv_w4a8(const void* x, int dtype, int64_t M, int64_t K_in, int64_t ldx, const float* sr_rcp,
+                      const float* sr_f, int rot_size, const int32_t* perm, const float* sm_rcp, const float* sm_f,
+                      const uint8_t* w_packed, int64_t N, int64_t K, int64_t ldw, const float* s_w,
+                      int64_t num_groups, const void* bias, int bias_dtype, int activation, const void* residual,
+                      int residual_dtype, int64_t ldr, void* out, int out_dtype, int64_t ldo, void* stream);
+int ic_prep_gemv_w8a8(const void* x, int dtype, int64_t M, int64_t K_in, int64_t ldx, const float* sr_rcp,
+                      const float* sr_f, int rot_size, const int32_t* perm, const float* sm_rcp, const float* sm_f,
+                      const int8_t* w, int64_t N, int64_t K, int64_t ldw, const float* s_w, const void* bias,
+                      int bias_dtype, int activation, const void* residual, int residual_dtype, int64_t ldr,
+                      void* out, int out_dtype, int64_t ldo, void* stream);
+
 /* INT4 -> int8 unpack (no scale).  kernels/triton_int4_to_int8_unpack.py:55-81. */
 int ic_unpack_int4_to_int8(const uint8_t* packed, int64_t N, int64_t K, int64_t ldp, int8_t* out,
                            int64_t ldo, void* stream);
