@@ -620,13 +620,13 @@ _SCALAR_WARNED: set = set()
 
 def _warn_if_scalar_gemm(who: str, K: int, G: int, *tensors: torch.Tensor, out64: bool = False) -> None:
     """The INT8 / W4A8 GEMMs run MFMA tiles only for K a multiple of 128,
-    group sizes that are multiples of 128 (W4A8 also odd multiples of 64 when
-    out64: a 16-bit output whose rows and residual suit the 288 x 192 tile's
-    staged stores) and 16-byte aligned operands and row strides; anything else
-    takes the scalar kernel (one thread per output, ~100x slower).  Log that
-    once per shape instead of running it silently."""
+    group sizes that are multiples of 128 (W4A8 also odd multiples of 64 or
+    of 32 when out64: a 16-bit output whose rows and residual suit the
+    288 x 192 tile's staged stores) and 16-byte aligned operands and row
+    strides; anything else takes the scalar kernel (one thread per output,
+    ~100x slower).  Log that once per shape instead of running it silently."""
     gs = K // G
-    ok = K % 128 == 0 and (G == 1 or gs % 128 == 0 or (out64 and gs % 128 == 64))
+    ok = K % 128 == 0 and (G == 1 or gs % 128 == 0 or (out64 and gs % 32 == 0))
     for t in tensors:
         ok = ok and t.data_ptr() % 16 == 0 and (t.dim() < 2 or (t.stride(0) * t.element_size()) % 16 == 0)
     key = (who, K, G)

@@ -973,6 +973,14 @@ bool big64_ok(const GemmArgs& g, int gsize) {
   return dma_strides_ok(g) && big_out_ok(g);
 }
 
+// Packed INT4 with groups of 32 or an odd multiple of 32 columns: the same
+// kernel in its 32-column mode (two half-masked MFMAs per 64-K step).
+bool big32_ok(const GemmArgs& g, int gsize) {
+  if (!g.int4 || g.G <= 1 || gsize % 64 != 32 || g.K % kBK != 0 || g.acc_out != nullptr) return false;
+  if (((uintptr_t)g.A & 15) || ((uintptr_t)g.B & 15) || (g.lda & 15) || (g.ldb & 15)) return false;
+  return dma_strides_ok(g) && big_out_ok(g);
+}
+
 // Chained MLP epilogue launches (gemm_i8_chain.hip): 128 x 256 tiles, whose
 // 256 columns hold whole R-blocks for R <= 256 and whose staging tile and
 // fp64 exchange slices fit the LDS together.  The caller has checked the
@@ -1032,6 +1040,11 @@ int run_gemm_t(GemmArgs g, hipStream_t st, const char* who, bool force_generic) 
     // folding each 64-K step, at any M
     if (g.out_dt == IC_DTYPE_F16) e = launch_big<IC_DTYPE_F16, EPI, big::G64>(g, st);
     else e = launch_big<IC_DTYPE_BF16, EPI, big::G64>(g, st);
+  } else if (!force_generic && big32_ok(g, gsize)) {
+    // groups of 32 (or an odd multiple of 32) columns: the same kernel folding
+    // each 32-column half step
+    if (g.out_dt == IC_DTYPE_F16) e = launch_big<IC_DTYPE_F16, EPI, big::G32>(g, st);
+    else e = launch_big<IC_DTYPE_BF16, EPI, big::G32>(g, st);
   } else if (!force_generic && mfma_shape_ok(g, gsize)) {
     if constexpr (EPI) {
       // the epilogue options never come with the debug accumulator output

@@ -3,8 +3,8 @@
 // Four weight modes share the tile, the DMA ring and the epilogue:
 //  * grouped INT4, the arithmetic of gemm_i8_kernel's grouped path
 //    (triton_w4a8_gemm.py:40-108 with the per-group scales of
-//    _quant_utils.py:237-270): per 128-column stage (or 64-column step) an
-//    exact int32 block sum of 16*q weights, folded in group order as
+//    _quant_utils.py:237-270): per 128-column stage (or 64- or 32-column
+//    step) an exact int32 block sum of 16*q weights, folded in group order as
 //    facc = fma(f32(acc_g), s_w[n, g] / 16, facc); out = facc * s_a[m] (+ bias);
 //  * per-row INT4 and per-row INT8 (triton_int8_gemm.py:46-205): int32 sums
 //    over all of K, out = f32(acc) [/ 16] * (s_a[m] * s_w[n]) (+ bias).
@@ -57,8 +57,9 @@
 namespace {
 namespace big {
 // Weight modes: grouped INT4 folded per 128-column stage, grouped INT4 folded
-// per 64-column step, per-row INT4, per-row INT8 (no fold: int32 sums across K)
-enum { G128 = 0, G64 = 1, ROW4 = 2, ROW8 = 3 };
+// per 64-column step, per-row INT4, per-row INT8 (no fold: int32 sums across
+// K), grouped INT4 folded per 32-column half step
+enum { G128 = 0, G64 = 1, ROW4 = 2, ROW8 = 3, G32 = 4 };
 constexpr int BN = 192, NS = 2;
 constexpr int TNB = 3;                       // 16 x 16 blocks per wave in N
 constexpr int WCOLS = TNB * 16;
@@ -70,7 +71,9 @@ constexpr int EPI_RS = BN + 8;               // 16-bit output staging row stride
 template <int TMB_, int MODE_>
 struct Rows {
   static constexpr int TMB = TMB_, MODE = MODE_;
-  static constexpr bool GROUPED = MODE <= G64, F64 = MODE == G64, INT8W = MODE == ROW8;
+  static constexpr bool GROUPED = MODE <= G64 || MODE == G32, F64 = MODE == G64, F32 = MODE == G32;
+  static constexpr bool INT8W = MODE == ROW8;
+  static constexpr int NSC = F32 ? 4 : (F64 ? 2 : 1);  // scale rows per stage (grouped)
   static constexpr int BM = 32 * TMB, WROWS = 16 * TMB;
   static constexpr int A_BYTES = BM * kBK;
   static constexpr int A_BLOCKS = BM / 8;             // 1 KB DMA blocks: 8 rows of 128 bytes
@@ -81,8 +84,8 @@ struct Rows {
   static constexpr int B_BLOCKS = B_BYTES / 1024;
   static constexpr int B_PER = (B_BLOCKS + 7) / 8;
   // ring slot: activations, weights, then none, one (scale blocks of 128
-  // columns) or two (of 64) scale rows
-  static constexpr int SLOT = A_BYTES + B_BYTES + (GROUPED ? (F64 ? 2 : 1) * S_BYTES : 0);
+  // columns), two (of 64) or four (of 32) scale rows
+  static constexpr int SLOT = A_BYTES + B_BYTES + (GROUPED ? NSC * S_BYTES : 0);
   // staging tile, activation scales, bias and per-row weight scales
   static constexpr size_t epi_bytes = (size_t)BM * EPI_RS * 2 + (size_t)(BM + 2 * BN) * 4;
   static constexpr size_t lds_bytes = (size_t)NS * SLOT > epi_bytes ? (size_t)NS * SLOT : epi_bytes;
@@ -96,8 +99,12 @@ struct Rows {
 
 // F64: groups of 64 columns, or of an odd multiple of 64 (gcd(group, 128)
 // = 64): each 64-K step is folded by itself, with the scale of its group, so
-// a stage folds twice.  Otherwise (group sizes that are multiples of 128)
-// each 128-column stage is folded once with its group's scale.
+// a stage folds twice.  F32: groups of an odd multiple of 32 columns: each
+// 64-K step runs as two MFMAs on the activation fragments with the lanes of
+// the other 32-column half zeroed (lanes 0-31 hold K 0-31 of the step, lanes
+// 32-63 K 32-63), so a stage folds four sums.  Otherwise (group sizes that
+// are multiples of 128) each 128-column stage is folded once with its
+// group's scale.
 //
 // ROW4 / ROW8: one scale per output column; the int32 sums run across all of K
 // in the MFMAs (16 * q for INT4) and the epilogue forms
@@ -112,7 +119,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
   using RT = Rows<TMB, MODE>;
   constexpr int BM = RT::BM, WROWS = RT::WROWS, A_BYTES = RT::A_BYTES, A_BLOCKS = RT::A_BLOCKS;
   constexpr int A_PER = RT::A_PER, B_BYTES = RT::B_BYTES, B_BLOCKS = RT::B_BLOCKS, B_PER = RT::B_PER;
-  constexpr bool GROUPED = RT::GROUPED, F64 = RT::F64, INT8W = RT::INT8W;
+  constexpr bool GROUPED = RT::GROUPED, F64 = RT::F64, F32 = RT::F32, INT8W = RT::INT8W;
   static_assert(OUT_DT != IC_DTYPE_F32, "16-bit outputs only");
   constexpr int SLOT = RT::SLOT;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -133,8 +140,8 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
   const float pre_b = tid < BN && bias != nullptr ? ld_any_f32(bias, bias_dt, min(n0 + tid, N - 1)) : 0.0f;
   const float pre_sw = !GROUPED && tid < BN ? s_w[min(n0 + tid, N - 1)] : 0.0f;
   const int KT = K / kBK;
-  // scale blocks (of 128 or 64 columns) per group
-  const int bpg = (K / G) / (F64 ? 64 : kBK);
+  // scale blocks (of 128, 64 or 32 columns) per group
+  const int bpg = (K / G) / (F32 ? 32 : (F64 ? 64 : kBK));
 
   // ---- DMA addressing (rows past M or N re-read the last row; never stored).
   // A (and int8 B) block b: LDS rows 8b + l/8, chunk slot l%8 holding global
@@ -175,7 +182,12 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
   };
   auto dma_s = [&](int kt) {
     if (GROUPED && wave < S_WAVES) {
-      if constexpr (F64) {
+      if constexpr (F32) {
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+          dma4(s_off, s_base + (4 * kt + h) / bpg,
+               slot_of(kt) + (uint32_t)(A_BYTES + B_BYTES + h * S_BYTES + wave * 256));
+      } else if constexpr (F64) {
         dma4(s_off, s_base + (2 * kt) / bpg, slot_of(kt) + (uint32_t)(A_BYTES + B_BYTES + wave * 256));
         dma4(s_off, s_base + (2 * kt + 1) / bpg, slot_of(kt) + (uint32_t)(A_BYTES + B_BYTES + S_BYTES + wave * 256));
       } else {
@@ -328,6 +340,76 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
     fold_row(TMB - 1, t[(TMB - 1) & 1], t1[F64 ? ((TMB - 1) & 1) : 0]);
   };
 
+  // One stage of the 32-column fold (F32).  Per block row, the two 64-K steps
+  // each run as two MFMAs on half-masked activation fragments: sums qa, qb
+  // (K 0-31, 32-63 of the stage) and qc, qd (K 64-95, 96-127), folded in K
+  // order.  The fold of a row's qc, qd is issued among the next row's MFMAs
+  // (as in the other grouped modes), so four half sums of 16 x 16 x 3 blocks
+  // are live at a time, as many as the 64-column fold holds.
+  const bool lo_half = (lane >> 4) < 2;
+  auto half_frag = [&](const v4i& a, bool lo) {
+    const bool keep = lo ? lo_half : !lo_half;
+    return v4i{keep ? a[0] : 0, keep ? a[1] : 0, keep ? a[2] : 0, keep ? a[3] : 0};
+  };
+  auto mfma_stage32 = [&](int kt) {
+    const bool more = kt + 1 < KT;  // uniform
+    float s0[TNB], s1[TNB], s2[TNB], s3[TNB];
+    read_scales(kt, 0, s0);
+    read_scales(kt, 1, s1);
+    read_scales(kt, 2, s2);
+    read_scales(kt, 3, s3);
+    const char* aR0 = smem + (kt % NS) * SLOT + lds_off(wr * WROWS + (lane & 15), lane >> 4);
+    const char* aR1 = smem + (kt % NS) * SLOT + lds_off(wr * WROWS + (lane & 15), 4 + (lane >> 4));
+    v4i b0[TNB], b1[TNB];
+#pragma unroll
+    for (int j = 0; j < TNB; ++j) load_b(kt, j, b0[j], b1[j]);
+    v4i n0f = *(const v4i*)aR0, n1f = *(const v4i*)aR1;
+    v4i qa[TNB], qb[TNB], qc[TNB], qd[TNB];
+    auto fold2 = [&](int i, v4i* x, v4i* y, const float* sx, const float* sy) {
+#pragma unroll
+      for (int j = 0; j < TNB; ++j) {
+        asm volatile("" : "+v"(x[j]));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) facc[i][j][r] = __builtin_fmaf((float)x[j][r], sx[j], facc[i][j][r]);
+        asm volatile("" : "+v"(y[j]));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) facc[i][j][r] = __builtin_fmaf((float)y[j][r], sy[j], facc[i][j][r]);
+        asm volatile("" : "+v"(facc[i][j]));
+      }
+    };
+#pragma unroll
+    for (int i = 0; i < TMB; ++i) {
+      if (i == 0 || RT::prio(i) != RT::prio(i - 1)) {
+        switch (RT::prio(i)) {
+          case 3: __builtin_amdgcn_s_setprio(3); break;
+          case 2: __builtin_amdgcn_s_setprio(2); break;
+          case 1: __builtin_amdgcn_s_setprio(1); break;
+          default: __builtin_amdgcn_s_setprio(0); break;
+        }
+      }
+      const v4i a0 = n0f, a1 = n1f;
+      if (i + 1 < TMB) {
+        n0f = *(const v4i*)(aR0 + (i + 1) * 16 * kBK);
+        n1f = *(const v4i*)(aR1 + (i + 1) * 16 * kBK);
+      }
+      const v4i a0l = half_frag(a0, true), a0h = half_frag(a0, false);
+#pragma unroll
+      for (int j = 0; j < TNB; ++j) qa[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0l, b0[j], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < TNB; ++j) qb[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0h, b0[j], v4i{0, 0, 0, 0}, 0, 0, 0);
+      if (i > 0) fold2(i - 1, qc, qd, s2, s3);
+      const v4i a1l = half_frag(a1, true), a1h = half_frag(a1, false);
+#pragma unroll
+      for (int j = 0; j < TNB; ++j) qc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1l, b1[j], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < TNB; ++j) qd[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1h, b1[j], v4i{0, 0, 0, 0}, 0, 0, 0);
+      fold2(i, qa, qb, s0, s1);
+      if (more) dma_next(kt, i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    fold2(TMB - 1, qc, qd, s2, s3);
+  };
+
   // Int8 weights: the last block row's MFMAs of each stage are issued after
   // the next stage's barrier, behind that stage's first fragment reads, so the
   // MFMA pipes have work while those reads are in flight.  Their operands stay
@@ -383,7 +465,8 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
     for (int s = 0; s < KT; ++s) {
       wait_vm<0>();
       lds_barrier();  // stage s resident; every wave is done with stage s-1
-      mfma_stage(s);
+      if constexpr (F32) mfma_stage32(s);
+      else mfma_stage(s);
     }
   } else {
     v4i bA0[TNB], bA1[TNB], bB0[TNB], bB1[TNB];

@@ -90,6 +90,7 @@ def test_c1_exact_launch(rt, oracle, dev):
 ROUTES = [
     ("big tile, grouped INT4 g128", "int4", 4608, 3072, 1024, 128),
     ("big tile, grouped INT4 g64", "int4", 4000, 3064, 1024, 64),
+    ("big tile, grouped INT4 g32", "int4", 4000, 3064, 1024, 32),
     ("big tile, per-row INT8", "int8", 4096, 3072, 1024, 0),
     ("big tile, per-row INT4", "int4", 4608, 3072, 1024, 0),
     ("256 x 128 tile, grouped INT4", "int4", 2048, 2048, 768, 128),

@@ -727,12 +727,14 @@ def test_per_row_big_tile_sampled_rows(rt, oracle, dev, out_dtype, M, N, K, int4
 
 
 # ------------------------------------------------------------------ group sizes other than 128
-@pytest.mark.parametrize("gs", [256, 512, 64, 192])
-@pytest.mark.parametrize("M,N,K", [(300, 384, 2048), (64, 3072, 4096), (4608, 3072, 1024), (600, 1000, 1536)])
+@pytest.mark.parametrize("gs", [256, 512, 64, 192, 32, 96])
+@pytest.mark.parametrize("M,N,K", [(300, 384, 2048), (64, 3072, 4096), (4608, 3072, 1024), (600, 1000, 1536),
+                                   (5, 1000, 1536)])
 def test_w4a8_group_sizes(rt, oracle, dev, gs, M, N, K):
     """Group sizes other than 128 run the MFMA kernels: multiples of 128
     (tiled and split-K) fold each 128-column stage, odd multiples of 64 (the
-    288 x 192 kernel's 64-block mode) each 64-K step, with the scale of the
+    288 x 192 kernel's 64-block mode) each 64-K step, odd multiples of 32
+    (its 32-column mode) each 32-column half step, with the scale of the
     step's group.  Bit-exact against the oracle's epilogue over accumulators
     of gcd(group, 128) columns with the scales repeated."""
     if K % gs:
