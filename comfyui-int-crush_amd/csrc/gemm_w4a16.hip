@@ -15,7 +15,8 @@
 // LDS ring filled by inline-assembly global->LDS DMAs issued in slices between
 // the MFMA K-steps, explicit vmcnt waits.  One stage is 64 K values: a 128-byte
 // row of 16-bit activations, 32 bytes of packed weights per output column and
-// the fp32 scale of the stage's group per column.  Once per stage the
+// two fp32 scales per column, those of the groups of the stage's two 32-K
+// halves (group sizes that are multiples of 32).  Once per stage the
 // workgroup dequantizes the packed tile into a 16-bit LDS tile with the same
 // swizzled row layout as the activations (two or three VALU instructions per
 // weight with packed 16-bit math), then every wave runs its MFMAs from LDS.
@@ -48,8 +49,8 @@ struct WTile {
   static constexpr int BM = BM_, BN = BN_, WGM = WGM_, NS = NS_;
   static constexpr int A_BYTES = BM * kBK;  // 64 16-bit activations per row
   static constexpr int B_BYTES = BN * 32;   // 64 packed INT4 weights per column
-  static constexpr int S_BYTES = BN * 4;    // fp32 scale of the stage's group per column
-  static constexpr int SLOT = A_BYTES + B_BYTES + S_BYTES;
+  static constexpr int S_BYTES = BN * 4;    // fp32 scale per column of one 32-K half's group
+  static constexpr int SLOT = A_BYTES + B_BYTES + 2 * S_BYTES;
   static constexpr int BU_BYTES = BN * kBK;  // dequantized 16-bit weights
   static constexpr int EPI_RS = BN + 8;      // output staging row stride (elements)
   static constexpr size_t epi_bytes() { return (size_t)BM * EPI_RS * 2 + (size_t)BN * 4; }
@@ -130,8 +131,11 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4a16_kernel(
       if ((A_DMA + c) % kParts == part && (B_BLK % 8 == 0 || wave + 8 * c < B_BLK))  // wave-uniform
         dma16(b_off[c], bb, slot + (uint32_t)(TL::A_BYTES + (wave + 8 * c) * 1024));
     if (part == kParts - 1 && s_wave) {
-      const int g = G > 1 ? (kt * 64) / gsize : 0;
-      dma4(s_off, s_base + g, slot + (uint32_t)(TL::A_BYTES + TL::B_BYTES + wave * 256));
+      // the groups of the stage's two 32-K halves (the same one unless the
+      // group size is an odd multiple of 32)
+      const int g0 = G > 1 ? (kt * 64) / gsize : 0, g1 = G > 1 ? (kt * 64 + 32) / gsize : 0;
+      dma4(s_off, s_base + g0, slot + (uint32_t)(TL::A_BYTES + TL::B_BYTES + wave * 256));
+      dma4(s_off, s_base + g1, slot + (uint32_t)(TL::A_BYTES + TL::B_BYTES + TL::S_BYTES + wave * 256));
     }
   };
   auto issue_dma = [&](int kt) {
@@ -143,7 +147,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4a16_kernel(
   // before the epilogue), so the stages after s always hold NS-2 steps of DMAs
   // and the DMA issue needs no branch between the MFMA K-steps.
   auto wait_stage = [&](int s) {
-    if (s_wave) wait_vm<(D + 1) * (NS - 2)>();
+    if (s_wave) wait_vm<(D + 2) * (NS - 2)>();
     else wait_vm<D * (NS - 2)>();
   };
 
@@ -159,7 +163,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_w4a16_kernel(
       if (PKC % kNT != 0 && idx >= PKC) break;  // wave-uniform (whole waves past the end)
       const int row = idx >> 1, part = idx & 1;
       const v4u p = *(const v4u*)(slot + TL::A_BYTES + idx * 16);
-      const DeqScale d = deq_scale<DT>(((const float*)(slot + TL::A_BYTES + TL::B_BYTES))[row]);
+      const DeqScale d = deq_scale<DT>(((const float*)(slot + TL::A_BYTES + TL::B_BYTES + part * TL::S_BYTES))[row]);
       const uint32_t pw[4] = {p.x, p.y, p.z, p.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -371,10 +375,10 @@ int ic_gemm_w4a16(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, c
   if (ic_gemv_applicable(M, K, x, ldx * 2, w_packed, ldw) && (num_groups == 1 || (K / num_groups) % 32 == 0))
     return ic_gemv_w4a16(x, dtype, M, K, ldx, w_packed, N, ldw, s_w, num_groups, bias, bias_dtype, out, ldo, stream);
   const int G = (int)num_groups, gsize = (int)(K / num_groups);
-  // DMA pipeline: 64-K stages, scale groups of whole stages, 16-byte aligned
+  // DMA pipeline: 64-K stages, scale groups of whole 32-K halves, 16-byte aligned
   // rows; 32-bit DMA offsets within one tile (activation tiles of up to 384
   // rows, weight tiles of up to 256 columns)
-  const bool mfma_ok = (K % 64 == 0) && (G == 1 || gsize % 64 == 0) && !((uintptr_t)x & 15) &&
+  const bool mfma_ok = (K % 64 == 0) && (G == 1 || gsize % 32 == 0) && !((uintptr_t)x & 15) &&
                        !((uintptr_t)w_packed & 15) && !((ldx * 2) & 15) && !(ldw & 15) &&
                        384 * ldx * 2 < (1LL << 31) && 256 * ldw < (1LL << 31) && N * G * 4 < (1LL << 31);
   hipStream_t st = (hipStream_t)stream;

@@ -802,9 +802,10 @@ def test_w4a8_scalar_kernel_fold_blocks(rt, oracle, dev, gs):
     assert np.array_equal(out.numpy(), ref)
 
 
-@pytest.mark.parametrize("G", [48, 12])  # group sizes 64 and 256 at K = 3072
-def test_w4a16_group_sizes(rt, oracle, dev, G):
-    M, N, K = 200, 256, 3072
+@pytest.mark.parametrize("G", [48, 12, 96, 32])  # group sizes 64, 256, 32 and 96 at K = 3072
+@pytest.mark.parametrize("M", [200, 100])  # 256 x 256 and 128 x 256 tiles
+def test_w4a16_group_sizes(rt, oracle, dev, G, M):
+    N, K = 256, 3072
     x = _acts(M, K, torch.bfloat16, seed=86)
     packed = torch.randint(0, 256, (N, K // 2), generator=_gen(87), dtype=torch.uint8)
     s_w = (torch.rand(N, G, generator=_gen(88)) * 2e-2 + 1e-3).to(torch.float16).float()
