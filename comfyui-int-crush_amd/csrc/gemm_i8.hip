@@ -111,7 +111,7 @@ int ic_gemm_w4a8_ex(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const u
   if (int rc = ic_check_epi("ic_gemm_w4a8", activation, residual, residual_dtype, ldr, N)) return rc;
   const ic_epi epi{activation, residual, residual_dtype, ldr};
   if (ic_gemv_applicable(M, K, xq, ldx, w_packed, ldw) && ldw * 2 >= K && N > 0 && ldo >= N && ldx >= K &&
-      (num_groups == 1 || num_groups * 128 == K))
+      ic_gemv_w4a8_groups_ok(M, K, num_groups))
     return ic_gemv_w4a8_epi(xq, M, K, ldx, w_packed, N, ldw, s_w, num_groups, s_a, bias, bias_dtype, out, out_dtype,
                             ldo, epi, stream);
   GemmArgs g{xq, ldx, w_packed, ldw, s_a, s_w, (int)num_groups, bias, bias_dtype, out, out_dtype,

@@ -18,6 +18,8 @@
 // activations fit 16 KB (M = 1 up to K = 8192 for 16-bit activations) they
 // are staged in LDS once per workgroup and read per block from there, so the
 // registers hold weights only and more waves keep loads in flight.
+#include <type_traits>
+
 #include "dequant4.h"
 #include "gemv_i8.h"
 
@@ -30,18 +32,21 @@ using gemv::kXlBytes;
 typedef _Float16 v8h_t __attribute__((ext_vector_type(8)));
 typedef __bf16 v8bf_t __attribute__((ext_vector_type(8)));
 
+// Ints of block sums: grouped (GS = fold block) [K/GS][M][16], per row
+// [4][M][16].
+constexpr int64_t gemv_sums(int GS, int64_t M, int64_t K) { return (GS ? K / GS : 4) * M * 16; }
+
 template <bool INT4, int GS, int OUT_DT, bool XL>
 __global__ __launch_bounds__(kGT) void gemv_i8_kernel(
     const int8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
-    const float* __restrict__ s_a, const float* __restrict__ s_w, int G,
+    const float* __restrict__ s_a, const float* __restrict__ s_w, int G, int gsize,
     const void* __restrict__ bias, int bias_dt, void* __restrict__ C, int64_t ldc, int M, int N, int K,
     ic_epi epi) {
-  // GS == 128: block sums [KB][M][16]; otherwise per-wave totals [4][M][16];
-  // with XL the activation codes [M][K] follow
+  // the block sums, then with XL the activation codes [M][K]
   extern __shared__ int32_t sacc[];
-  int8_t* xs = (int8_t*)(sacc + (GS == 128 ? K / kGBK : 4) * M * 16);
-  gemv::gemv_i8_body<INT4, GS, OUT_DT, XL>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, epi, sacc,
-                                           xs);
+  int8_t* xs = (int8_t*)(sacc + gemv_sums(GS, M, K));
+  gemv::gemv_i8_body<INT4, GS, OUT_DT, XL>(A, lda, B, ldb, s_a, s_w, G, gsize, bias, bias_dt, C, ldc, M, N, K, epi,
+                                           sacc, xs);
 }
 
 // W4A16 weight dequantization RN_dt(q * RN_dt(s)) of 8 nibbles.
@@ -152,11 +157,11 @@ hipError_t launch_gemv_i8_t(const int8_t* A, int64_t lda, const uint8_t* B, int6
                             const float* s_w, int G, const void* bias, int bias_dt, void* C, int64_t ldc,
                             int M, int N, int K, const ic_epi& epi, hipStream_t st) {
   auto kern = gemv_i8_kernel<INT4, GS, OUT_DT, XL>;
-  const size_t shm = (size_t)(GS == 128 ? K / kGBK : 4) * M * 16 * 4 + (XL ? (size_t)M * K : 0);
+  const size_t shm = (size_t)gemv_sums(GS, M, K) * 4 + (XL ? (size_t)M * K : 0);
   static unsigned char lds_set[64];  // per device
   if (hipError_t e = ic_set_lds_limit((const void*)kern, 160 * 1024, lds_set)) return e;
-  kern<<<dim3((unsigned)((N + 15) / 16)), dim3(kGT), shm, st>>>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C,
-                                                                ldc, M, N, K, epi);
+  kern<<<dim3((unsigned)((N + 15) / 16)), dim3(kGT), shm, st>>>(A, lda, B, ldb, s_a, s_w, G, K / G, bias, bias_dt,
+                                                                C, ldc, M, N, K, epi);
   return hipGetLastError();
 }
 
@@ -164,7 +169,7 @@ template <bool INT4, int GS, int OUT_DT>
 hipError_t launch_gemv_i8(const int8_t* A, int64_t lda, const uint8_t* B, int64_t ldb, const float* s_a,
                           const float* s_w, int G, const void* bias, int bias_dt, void* C, int64_t ldc,
                           int M, int N, int K, const ic_epi& epi, hipStream_t st) {
-  if ((int64_t)M * K <= kXlBytes)
+  if ((int64_t)M * K <= kXlBytes && gemv_sums(GS, M, K) * 4 + (int64_t)M * K <= 160 * 1024)
     return launch_gemv_i8_t<INT4, GS, OUT_DT, true>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, epi, st);
   return launch_gemv_i8_t<INT4, GS, OUT_DT, false>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, epi, st);
 }
@@ -199,6 +204,23 @@ int check_gemv_common(const char* who, int64_t M, int64_t K, int64_t N, int64_t 
 
 }  // namespace
 
+// Grouped W4A8 folds per gcd(group, 128) columns, as the GEMM kernels do.
+static int fold_block(int64_t gsize) {
+  int64_t a = gsize, b = 128;
+  while (b != 0) {
+    const int64_t t = a % b;
+    a = b;
+    b = t;
+  }
+  return (int)a;
+}
+
+// Shared by the GEMM entry points, which route M <= 16 here.
+bool ic_gemv_w4a8_groups_ok(int64_t M, int64_t K, int64_t num_groups) {
+  if (num_groups == 1) return true;
+  if (num_groups < 1 || K % num_groups != 0 || (K / num_groups) % 32 != 0) return false;
+  return gemv_sums(fold_block(K / num_groups), M, K) * 4 <= 128 * 1024;
+}
 // Shared by the GEMM entry points, which route M <= 16 here.
 bool ic_gemv_applicable(int64_t M, int64_t K, const void* x, int64_t ldx_bytes, const void* w, int64_t ldw_bytes) {
   return M >= 1 && M <= IC_GEMV_MAX_M && K % kGBK == 0 && K <= IC_GEMV_MAX_K && ((uintptr_t)x & 15) == 0 &&
@@ -231,8 +253,10 @@ int ic_gemv_w4a8_epi(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const 
   const char* who = "ic_gemv_w4a8";
   int rc = check_gemv_common(who, M, K, N, ldx, ldo, bias, bias_dtype);
   if (rc) return rc;
-  if (num_groups < 1 || (num_groups > 1 && num_groups * kGBK != K))
-    return ic_set_error(IC_ERR_UNSUPPORTED, "%s: num_groups must be 1 or K/128", who);
+  if (!ic_gemv_w4a8_groups_ok(M, K, num_groups))
+    return ic_set_error(IC_ERR_UNSUPPORTED,
+                        "%s: num_groups must be 1 or give groups of a multiple of 32 columns whose %d-column fold "
+                        "sums of M x K fit 128 KB", who, num_groups > 1 ? fold_block(K / num_groups) : 0);
   if (M == 0) return IC_OK;
   if (!xq || !w_packed || !s_a || !s_w || !out) return ic_set_error(IC_ERR_INVALID_ARG, "%s: null pointer", who);
   if (!ic_gemv_applicable(M, K, xq, ldx, w_packed, ldw) || ldw * 2 < K)
@@ -240,11 +264,15 @@ int ic_gemv_w4a8_epi(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const 
   if (out_dtype != IC_DTYPE_F16 && out_dtype != IC_DTYPE_BF16 && out_dtype != IC_DTYPE_F32)
     return ic_set_error(IC_ERR_INVALID_ARG, "%s: out dtype must be f16/bf16/f32", who);
   hipStream_t st = (hipStream_t)stream;
-  hipError_t e = num_groups > 1
-                     ? pick_gemv_out<true, 128>(out_dtype, xq, ldx, w_packed, ldw, s_a, s_w, (int)num_groups, bias,
-                                                bias_dtype, out, ldo, (int)M, (int)N, (int)K, epi, st)
-                     : pick_gemv_out<true, 0>(out_dtype, xq, ldx, w_packed, ldw, s_a, s_w, 1, bias, bias_dtype, out,
-                                              ldo, (int)M, (int)N, (int)K, epi, st);
+  const int fb = num_groups > 1 ? fold_block(K / num_groups) : 0;
+  auto go = [&](auto gs_c) {
+    return pick_gemv_out<true, decltype(gs_c)::value>(out_dtype, xq, ldx, w_packed, ldw, s_a, s_w, (int)num_groups,
+                                                      bias, bias_dtype, out, ldo, (int)M, (int)N, (int)K, epi, st);
+  };
+  hipError_t e = fb == 128 ? go(std::integral_constant<int, 128>{})
+                 : fb == 64 ? go(std::integral_constant<int, 64>{})
+                 : fb == 32 ? go(std::integral_constant<int, 32>{})
+                            : go(std::integral_constant<int, 0>{});
   if (e != hipSuccess) return ic_set_error(IC_ERR_LAUNCH, "%s: %s", who, hipGetErrorString(e));
   return IC_OK;
 }

@@ -36,10 +36,13 @@ IC_DEV void unpack8_x16(uint32_t P, uint32_t& w0, uint32_t& w1) {
   w1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
 }
 
-// One K block of one wave: two MFMAs on the lane's 32 activation codes (av0,
-// av1) and its 32 weights (INT4: the 16 packed bytes pwu; INT8: pwu and w1u).
-// GS == 128 stores the block sums to sacc[b][M][16]; otherwise they
-// accumulate in tot.  c = lane / 16, col = lane % 16.
+// One K block of one wave: MFMAs on the lane's 32 activation codes (av0, av1:
+// K 32c .. 32c+31 of the block, c = lane / 16) and its 32 weights (INT4: the
+// 16 packed bytes pwu; INT8: pwu and w1u).  Grouped (GS = 128, 64 or 32, the
+// fold block gcd(group, 128)): the sums of the block's 128 / GS parts, each
+// from the lanes holding that part's K range (the other lanes' codes zeroed),
+// go to sacc[(b * 128 / GS + part)][M][16].  Per row (GS = 0) they accumulate
+// in tot.  col = lane % 16.
 template <bool INT4, int GS>
 IC_DEV void mma_block(int b, const v4i& av0, const v4i& av1, const v4u& pwu, const v4i& w1u, int M, int c, int col,
                       int32_t* sacc, v4i& tot) {
@@ -56,14 +59,20 @@ IC_DEV void mma_block(int b, const v4i& av0, const v4i& av1, const v4u& pwu, con
     b0v = __builtin_bit_cast(v4i, pwu);
     b1v = w1u;
   }
-  if constexpr (GS == 128) {
-    v4i s = __builtin_amdgcn_mfma_i32_16x16x64_i8(av0, b0v, v4i{0, 0, 0, 0}, 0, 0, 0);
-    s = __builtin_amdgcn_mfma_i32_16x16x64_i8(av1, b1v, s, 0, 0, 0);
-    // D layout: lane holds rows 4*(lane/16) + i of column lane%16
+  if constexpr (GS != 0) {
+    constexpr int NQ = 128 / GS;  // fold blocks per K block
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 4 * c + i;
-      if (r < M) sacc[(b * M + r) * 16 + col] = s[i];
+    for (int q = 0; q < NQ; ++q) {
+      const bool keep = NQ == 1 || (c * NQ) / 4 == q;
+      const v4i a0 = keep ? av0 : v4i{0, 0, 0, 0}, a1 = keep ? av1 : v4i{0, 0, 0, 0};
+      v4i s = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0v, v4i{0, 0, 0, 0}, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1v, s, 0, 0, 0);
+      // D layout: lane holds rows 4*(lane/16) + i of column lane%16
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * c + i;
+        if (r < M) sacc[((b * NQ + q) * M + r) * 16 + col] = s[i];
+      }
     }
   } else {
     tot = __builtin_amdgcn_mfma_i32_16x16x64_i8(av0, b0v, tot, 0, 0, 0);
@@ -82,20 +91,35 @@ IC_DEV void store_wave_totals(const v4i& tot, int wave, int M, int c, int col, i
 
 // Output (m, n0 + nl) from the sums of its 16-column block in sacc (after a
 // barrier): dequant, bias, activation / residual, rounding to the output type.
+// Grouped: the fold blocks of GS columns in K order, each with the scale of
+// its group (gsize columns).
 template <bool INT4, int GS, int OUT_DT>
 IC_DEV void gemv_output(int m, int nl, const int32_t* sacc, int KB, int M, int n0, int N, const float* s_a,
-                        const float* __restrict__ s_w, int G, const void* __restrict__ bias, int bias_dt,
+                        const float* __restrict__ s_w, int G, int gsize, const void* __restrict__ bias, int bias_dt,
                         void* __restrict__ C, int out_dt, int64_t ldc, const ic_epi& epi) {
   const int no = n0 + nl;
   if (no >= N) return;
   float v;
-  if constexpr (GS == 128) {
+  if constexpr (GS != 0) {
     const float* sw = s_w + (int64_t)no * G;
+    const int nf = KB * (128 / GS), bpg = gsize / GS;  // fold blocks; per group
     float facc = 0.0f;
-    for (int g = 0; g < KB; ++g) {
-      float s = sw[g];
-      if constexpr (INT4) s *= 0.0625f;  // block sums hold 16 * the true sum
-      facc = __builtin_fmaf((float)sacc[(g * M + m) * 16 + nl], s, facc);
+    if (bpg == 1) {  // group = fold block: scale addresses affine in the loop
+      for (int f = 0; f < nf; ++f) {
+        float s = sw[f];
+        if constexpr (INT4) s *= 0.0625f;  // block sums hold 16 * the true sum
+        facc = __builtin_fmaf((float)sacc[(f * M + m) * 16 + nl], s, facc);
+      }
+    } else {
+      for (int f = 0, g = 0, r = 0; f < nf; ++f) {
+        float s = sw[g];
+        if constexpr (INT4) s *= 0.0625f;
+        facc = __builtin_fmaf((float)sacc[(f * M + m) * 16 + nl], s, facc);
+        if (++r == bpg) {
+          r = 0;
+          ++g;
+        }
+      }
     }
     v = facc * s_a[m];
   } else {
@@ -117,12 +141,12 @@ IC_DEV void gemv_output(int m, int nl, const int32_t* sacc, int KB, int M, int n
 }
 
 // The GEMV on INT8 codes A [M, K] (row stride lda), one 16-column block per
-// workgroup.  sacc: GS == 128: block sums [K/128][M][16]; otherwise per-wave
+// workgroup.  sacc: grouped: fold-block sums [K/GS][M][16]; per row: per-wave
 // totals [4][M][16].  XL: xs receives the codes, copied after the first batch
 // of weight loads is issued.
 template <bool INT4, int GS, int OUT_DT, bool XL>
 IC_DEV void gemv_i8_body(const int8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
-                         const float* __restrict__ s_a, const float* __restrict__ s_w, int G,
+                         const float* __restrict__ s_a, const float* __restrict__ s_w, int G, int gsize,
                          const void* __restrict__ bias, int bias_dt, void* __restrict__ C, int64_t ldc, int M, int N,
                          int K, const ic_epi& epi, int32_t* sacc, int8_t* xs) {
   const int tid = threadIdx.x, lane = tid & 63;
@@ -200,11 +224,11 @@ IC_DEV void gemv_i8_body(const int8_t* __restrict__ A, int64_t lda, const uint8_
       }
     }
   }
-  if constexpr (GS != 128) store_wave_totals(tot, wave, M, c, col, sacc);
+  if constexpr (GS == 0) store_wave_totals(tot, wave, M, c, col, sacc);
   __syncthreads();
   if (tid < 16 * M)
-    gemv_output<INT4, GS, OUT_DT>(tid >> 4, tid & 15, sacc, KB, M, n0, N, s_a, s_w, G, bias, bias_dt, C, OUT_DT,
-                                  ldc, epi);
+    gemv_output<INT4, GS, OUT_DT>(tid >> 4, tid & 15, sacc, KB, M, n0, N, s_a, s_w, G, gsize, bias, bias_dt, C,
+                                  OUT_DT, ldc, epi);
 }
 
 }  // namespace gemv

@@ -251,7 +251,7 @@ __global__ __launch_bounds__(gemv::kGT) void prep_gemv_kernel(
       if (b < KB)
         gemv::mma_block<INT4, GS>(b, *(const v4i*)(arow + kGBK * b), *(const v4i*)(arow + kGBK * b + 16), pw[i],
                                   w1[INT4 ? 0 : i], M, c, col, sj, tot);
-      if constexpr (GS != 128) {
+      if constexpr (GS == 0) {
         if (u == UB - 1) {
           gemv::store_wave_totals(tot, wave, M, c, col, sj);
           tot = v4i{0, 0, 0, 0};
@@ -263,7 +263,7 @@ __global__ __launch_bounds__(gemv::kGT) void prep_gemv_kernel(
   for (int o = tid; o < ncb * 16 * M; o += kThreads) {
     const int j = o / (16 * M), r = o - j * 16 * M;
     gemv::gemv_output<INT4, GS, gemv::kOutRuntime>(r >> 4, r & 15, sacc + j * sacc_cb, KB, M, (cb_first + j) * 16,
-                                                   N, sa, s_w, G, bias, bias_dt, C, out_dt, ldc, epi);
+                                                   N, sa, s_w, G, K / G, bias, bias_dt, C, out_dt, ldc, epi);
   }
 }
 

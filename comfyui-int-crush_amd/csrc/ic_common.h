@@ -24,8 +24,11 @@ hipError_t ic_set_lds_limit(const void* kern, int bytes, unsigned char* done);
 // Validation of the epilogue arguments (activation code, residual dtype and
 // stride) shared by the entry points that take them (gemm_i8.hip).
 int ic_check_epi(const char* who, int activation, const void* residual, int residual_dtype, int64_t ldr, int64_t N);
-// GEMV routing test shared by the GEMM entry points (gemv.hip); strides in bytes.
+// GEMV routing tests shared by the GEMM entry points (gemv.hip); strides in
+// bytes.  The W4A8 GEMV takes per-row scales and groups of multiples of 32
+// columns whose fold sums fit its LDS.
 bool ic_gemv_applicable(int64_t M, int64_t K, const void* x, int64_t ldx_bytes, const void* w, int64_t ldw_bytes);
+bool ic_gemv_w4a8_groups_ok(int64_t M, int64_t K, int64_t num_groups);
 
 // Arguments of the fused preparation kernels (internal; the ABI is flat).
 struct ic_rotq_args {

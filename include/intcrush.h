@@ -284,6 +284,10 @@ int ic_gemm_w4a16(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, c
  * arithmetic and same results as ic_gemm_w8a8 / ic_gemm_w4a8 (bit-identical)
  * and ic_gemm_w4a16 (fp32 accumulation, tolerance-equal), reading each packed
  * weight byte once.  The GEMM entry points route such calls here themselves.
+ * ic_gemv_w4a8 takes num_groups 1 or groups of a multiple of 32 columns, folded
+ * per gcd(group, 128) columns as the GEMM does, while those fold sums of the
+ * M rows fit 128 KB (K / gcd * M * 64 bytes); the GEMM entry point runs the
+ * tiled kernel otherwise.
  * Replace the M <= 16 use of fused_int8_gemm_dequant / fused_w4a8_gemm_dequant
  * (kernels/triton_int8_gemm.py:135-205, triton_w4a8_gemm.py:111-169) and of
  * F.linear on unpacked weights (_ops.py:466-481), e.g. Flux modulation linears.

@@ -75,6 +75,51 @@ def test_gemv_w4a8_bit_exact(rt, oracle, dev, M, N, K, grouped, via):
     assert np.array_equal(out.float().cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("gs", [32, 64, 96, 256, 384])
+@pytest.mark.parametrize("M", [1, 5, 16])
+@pytest.mark.parametrize("via", ["gemv", "gemm"])
+def test_gemv_w4a8_group_sizes(rt, oracle, dev, gs, M, via):
+    """Groups other than 128 columns: the GEMV folds per gcd(group, 128)
+    columns in K order with each block's group scale, as the GEMM kernels
+    do.  Bit-exact against the oracle's blocked epilogue."""
+    import math
+    N, K = 264, 3072 if gs != 256 else 2048
+    G, fb = K // gs, math.gcd(gs, 128)
+    a = _int8((M, K), 41 + M)
+    packed = torch.randint(0, 256, (N, K // 2), generator=_gen(42), dtype=torch.uint8)
+    s_a = torch.rand(M, generator=_gen(43)) * 0.05 + 1e-3
+    s_w = (torch.rand(N, G, generator=_gen(44)) * 2e-2 + 1e-3).to(torch.float16).float()
+    bias = torch.randn(N, generator=_gen(45)).to(torch.bfloat16)
+    args = (a.to(dev), packed.to(dev), s_w.to(dev), s_a.to(dev))
+    if via == "gemv":
+        out = rt.gemv(*args, bias=bias.to(dev), out_dtype=torch.bfloat16, kind="w4a8")
+    else:
+        out = rt.gemm_w4a8(*args, bias=bias.to(dev), out_dtype=torch.bfloat16)
+    acc = oracle.gemm_acc(a.numpy(), oracle.unpack_int4(packed.numpy(), K), K // fb)
+    sw = np.repeat(s_w.numpy(), gs // fb, axis=1)
+    ref = oracle.epilogue(acc, s_a.numpy(), sw, bias.float().numpy(), DT[torch.bfloat16])
+    assert np.array_equal(out.float().cpu().numpy(), ref)
+
+
+def test_gemv_group_sums_past_the_lds_take_the_gemm(rt, oracle, dev):
+    """M = 16, K = 8192 in groups of 32: the fold sums (256 KB) exceed the
+    GEMV's LDS, so the GEMM entry point runs the tiled kernel -- same
+    numbers -- and the explicit GEMV refuses."""
+    M, N, K, gs = 16, 200, 8192, 32
+    G = K // gs
+    a = _int8((M, K), 51)
+    packed = torch.randint(0, 256, (N, K // 2), generator=_gen(52), dtype=torch.uint8)
+    s_a = torch.rand(M, generator=_gen(53)) * 0.05 + 1e-3
+    s_w = (torch.rand(N, G, generator=_gen(54)) * 2e-2 + 1e-3).to(torch.float16).float()
+    args = (a.to(dev), packed.to(dev), s_w.to(dev), s_a.to(dev))
+    with pytest.raises(RuntimeError, match="fit 128 KB"):
+        rt.gemv(*args, out_dtype=torch.bfloat16, kind="w4a8")
+    out = rt.gemm_w4a8(*args, out_dtype=torch.bfloat16)
+    acc = oracle.gemm_acc(a.numpy(), oracle.unpack_int4(packed.numpy(), K), K // gs)
+    ref = oracle.epilogue(acc, s_a.numpy(), s_w.numpy(), None, DT[torch.bfloat16])
+    assert np.array_equal(out.float().cpu().numpy(), ref)
+
+
 def test_gemv_matches_tiled_gemm_rows(rt, dev):
     """The same rows computed at M = 16 (GEMV) and inside an M = 300 GEMM agree
     bit for bit.  N = 6144 gives the GEMM enough tiles that it does not split
