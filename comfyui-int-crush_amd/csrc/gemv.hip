@@ -55,23 +55,40 @@ __global__ __launch_bounds__(kGT) void gemv_i8_kernel(
 // each block's fragments read from there when used.  Held in registers for a
 // batch of 8 blocks, they were 4x the weight bytes per lane and 128 VGPRs,
 // which left two waves per SIMD and too few weight loads in flight (16.5 us,
-// 1.8 TB/s, at the Flux modulation shape; 12.7 us with the staging).
+// 1.8 TB/s, at the Flux modulation shape; 12.7 us with the staging).  The
+// weight scales are staged too (82 -> 71 VGPRs, no per-block division or
+// scattered scale load): 11.7 us.
 template <int DT, bool XL>
 __global__ __launch_bounds__(kGT) void gemv_w4a16_kernel(
     const u16* __restrict__ X, int64_t ldx, const uint8_t* __restrict__ B, int64_t ldb,
     const float* __restrict__ s_w, int G, int gsize, const void* __restrict__ bias, int bias_dt,
     u16* __restrict__ C, int64_t ldc, int M, int N, int K) {
   __shared__ float sacc[4 * 16 * 16];
-  extern __shared__ __attribute__((aligned(16))) u16 xs[];  // XL: M rows of K values
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the workgroup's 16 x G weight scales, then (XL) M rows of K activations
+  extern __shared__ __attribute__((aligned(16))) float ssc[];
+  u16* xs = (u16*)(ssc + ((16 * G + 3) & ~3));
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n0 = blockIdx.x * 16;
   const int c = lane >> 4, col = lane & 15;
   const int n = min(n0 + col, N - 1);
   const int am = min(col, M - 1);
   const int KB = K / kGBK;
   const uint8_t* brow = B + (int64_t)n * ldb + 16 * c;
-  const float* swrow = s_w + (int64_t)n * G;
   const u16* xrow = XL ? xs + (int64_t)am * K + 32 * c : X + (int64_t)am * ldx + 32 * c;
+  // The scales of the 16 columns are one contiguous run of s_w (rows n0 ..
+  // n0+15); staged once, read per block from LDS.  The lane's 32 values of
+  // block b are quarter q = 4b + c of 32 columns, in group q / (gsize / 32),
+  // formed as trunc((q + 1/2) / gq) in f32 (exact: q < 2^9, and the half
+  // keeps the product clear of the integers).
+  auto stage_scales = [&] {
+    for (int i = tid; i < 16 * G; i += kGT) {
+      const int r = i / G;
+      ssc[i] = s_w[(int64_t)min(n0 + r, N - 1) * G + (i - r * G)];
+    }
+  };
+  const float inv_gq = 32.0f / (float)gsize;
+  const float* sc_col = ssc + col * G;
+  auto scale_of = [&](int b) { return G > 1 ? sc_col[(int)(((float)(4 * b + c) + 0.5f) * inv_gq)] : sc_col[0]; };
 
   constexpr int kBatch = 8;
   v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -92,8 +109,10 @@ __global__ __launch_bounds__(kGT) void gemv_w4a16_kernel(
     }
   };
   if constexpr (XL) {
-    // staged first: holding a batch of weights across the copy costs ~20
-    // VGPRs, and the lower occupancy measured slower than the overlap gained
+    // staged first: issuing the first batch of weight loads ahead of the copy
+    // measured slower (13.1 against 11.7 us at 1 x 3072 -> 18432), as did
+    // holding a batch of weights across it (~20 VGPRs, lower occupancy)
+    stage_scales();
     const int per_row = K / 8;  // 16-byte chunks
     for (int i = tid; i < M * per_row; i += kGT) {
       const int r = i / per_row, k8 = i - r * per_row;
@@ -102,26 +121,23 @@ __global__ __launch_bounds__(kGT) void gemv_w4a16_kernel(
     __syncthreads();
     for (int b0 = wave; b0 < KB; b0 += 4 * kBatch) {
       v4u pw[kBatch];
-      float sv[kBatch];
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
         const int b = b0 + 4 * u;
-        if (b < KB) {  // uniform across the wave
-          pw[u] = *(const v4u*)(brow + (kGBK / 2) * b);
-          sv[u] = swrow[G > 1 ? (kGBK * b + 32 * c) / gsize : 0];
-        }
+        if (b < KB) pw[u] = *(const v4u*)(brow + (kGBK / 2) * b);  // uniform across the wave
       }
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
         const int b = b0 + 4 * u;
         if (b >= KB) break;
-        mma_block(b, nullptr, pw[u], sv[u]);
+        mma_block(b, nullptr, pw[u], scale_of(b));
       }
     }
   } else {
+    stage_scales();
+    __syncthreads();
     for (int b0 = wave; b0 < KB; b0 += 4 * kBatch) {
       v4u xv[kBatch][4], pw[kBatch];
-      float sv[kBatch];
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
         const int b = b0 + 4 * u;
@@ -129,14 +145,13 @@ __global__ __launch_bounds__(kGT) void gemv_w4a16_kernel(
 #pragma unroll
           for (int j = 0; j < 4; ++j) xv[u][j] = *(const v4u*)(xrow + kGBK * b + 8 * j);
           pw[u] = *(const v4u*)(brow + (kGBK / 2) * b);
-          sv[u] = swrow[G > 1 ? (kGBK * b + 32 * c) / gsize : 0];
         }
       }
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
         const int b = b0 + 4 * u;
         if (b >= KB) break;
-        mma_block(b, xv[u], pw[u], sv[u]);
+        mma_block(b, xv[u], pw[u], scale_of(b));
       }
     }
   }
@@ -311,7 +326,7 @@ int ic_gemv_w4a16(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, c
   hipStream_t st = (hipStream_t)stream;
   const int64_t xl_bytes = M * K * 2;
   const bool xl = xl_bytes <= kXlBytes;
-  const size_t shm = xl ? (size_t)xl_bytes : 0;
+  const size_t shm = (size_t)((16 * G + 3) & ~3) * 4 + (xl ? (size_t)xl_bytes : 0);  // at most 48 KB
   auto args = [&](auto kern) {
     kern<<<grid, kGT, shm, st>>>((const u16*)x, ldx, w_packed, ldw, s_w, G, gsize, bias, bias_dtype, (u16*)out, ldo,
                                  (int)M, (int)N, (int)K);
