@@ -879,7 +879,8 @@ def main():
         pach = prep_bytes / (p_ms * 1e-3) / 1e9
         line["prep_quant"] = {"kernel": "rotate_quantize", "bound": "hbm", "kernel_ms": round(p_ms, 5),
                               "algorithmic_bytes": prep_bytes, "achieved": round(pach, 1),
-                              "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(pach / PEAK_HBM_GBPS, 4)}
+                              "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(pach / PEAK_HBM_GBPS, 4),
+                              "frac_of_measured_peak": round(pach / peaks["hbm_copy_gbps"], 4)}
     if M > rt.GEMV_MAX_M and not args.no_vendor:
         line["vendor_gemm"] = vendor_reference(cfg)
     if args.config == "c3" and not args.no_step:
