@@ -62,7 +62,6 @@ class CudaGraphRunner:
         self._s_w: torch.Tensor = layer.weight._params.scale
         self._zp = layer.weight._params.zp
         self._rot_size: int = layer._intcrush_rot_size if layer._intcrush_rot_need else 0
-        self._w_in: int = layer._intcrush_w_in
         self._safe_no_clone = safe_no_clone
         self._max_cached = max_cached_shapes if max_cached_shapes is not None else self._MAX_CACHED_SHAPES
         self._graphs: OrderedDict[tuple, _GraphEntry] = OrderedDict()
@@ -97,10 +96,13 @@ class CudaGraphRunner:
     # ── internals ─────────────────────────────────────────────────────────
     def _prep_and_quantize(self, x_2d, bias, compute_dtype, *, s_a_out=None, x_int8_out=None, out=None):
         st = self._layer._intcrush_state(x_2d)
-        q, s_a = _rt.rotate_quantize(x_2d, rot_size=self._rot_size, w_in=self._w_in, smoothrot=st.smoothrot,
-                                     perm=st.perm, smooth=st.smooth, s_a_out=s_a_out, x_int8_out=x_int8_out)
-        return _rt.fused_int8_gemm_dequant(q, self._w_int8, self._s_w, s_a, bias=bias, out_dtype=compute_dtype,
-                                           out=out)
+        # at the GEMM's width (the layer's prepared width unless it is padded
+        # to a multiple of 128 for the MFMA kernels)
+        q, s_a = _rt.rotate_quantize(x_2d, rot_size=self._rot_size, w_in=st.k_gemm, smoothrot=st.smoothrot,
+                                     perm=st.perm_gemm, smooth=st.smooth_gemm, s_a_out=s_a_out,
+                                     x_int8_out=x_int8_out)
+        wq, ws = st.gemm_weights(self._w_int8, self._s_w)
+        return _rt.fused_int8_gemm_dequant(q, wq, ws, s_a, bias=bias, out_dtype=compute_dtype, out=out)
 
     def _run_eager(self, x_2d, bias, compute_dtype):
         return self._prep_and_quantize(x_2d, bias, compute_dtype)
@@ -110,7 +112,7 @@ class CudaGraphRunner:
         N = self._w_int8.shape[0]
         dev = x_2d.device
         static_x = torch.empty(M, K, dtype=x_2d.dtype, device=dev)
-        static_x_int8 = torch.empty(M, self._w_in, dtype=torch.int8, device=dev)
+        static_x_int8 = torch.empty(M, self._layer._intcrush_state(x_2d).k_gemm, dtype=torch.int8, device=dev)
         static_s_a = torch.empty(M, dtype=torch.float32, device=dev)
         static_out = torch.empty(M, N, dtype=compute_dtype, device=dev)
         static_x.copy_(x_2d)

@@ -35,6 +35,7 @@ Reference behaviours kept on purpose (documented quirks):
 from __future__ import annotations
 
 import logging
+import math
 import os
 from typing import Any, Callable
 
@@ -116,12 +117,39 @@ def _hip_ready(x: torch.Tensor) -> bool:
         "fallback on the GPU (set INTCRUSH_ALLOW_TORCH_FALLBACK=1 to allow it)")
 
 
+def _gemm_width(layer) -> int:
+    """Width the GEMM kernels run a layer at: its prepared width K_w, or, when
+    K_w is not a multiple of 128 (the MFMA kernels' K step; e.g. a 64-wide
+    patch embedding), the next multiple of lcm(128, group size).  The extra
+    columns hold zero weights and zero codes: their products add nothing to
+    the exact int32 sums, and their fold blocks add fma(0, s, f) = f, so the
+    outputs are those of the unpadded product.  Layers with a zero point or an
+    SVD residual, whose corrections are formed over the prepared activation,
+    keep K_w (and the scalar kernel)."""
+    K_w = layer._intcrush_w_in
+    w = layer.weight
+    params = getattr(w, "_params", None)
+    if (K_w is None or K_w % 128 == 0 or params is None or getattr(params, "zp", None) is not None
+            or layer._intcrush_L1 is not None):
+        return K_w
+    sc = params.scale
+    G = sc.shape[1] if sc.dim() > 1 else 1
+    if G > 1 and (K_w % G or (K_w // G) % 32):
+        return K_w  # groups the MFMA kernels do not take at any width
+    step = 128 if G <= 1 else 128 * (K_w // G) // math.gcd(128, K_w // G)
+    return -(-K_w // step) * step
+
+
 class _DeviceState:
     """Per (device, activation dtype) kernel-side copies of a layer's
     preparation tensors: rounded SmoothRot / SmoothQuant factors with their
-    reciprocals, and the int32 PermuQuant indices."""
+    reciprocals, and the int32 PermuQuant indices; and the operands of the
+    GEMM at its width (_gemm_width): the prepared width k_gemm, the perm and
+    old-SmoothQuant factors extended over the extra columns (identity, 1), and
+    the weights and scales padded once (zero weights; scale 1 for the extra
+    groups)."""
 
-    __slots__ = ("smoothrot", "smooth", "perm")
+    __slots__ = ("smoothrot", "smooth", "perm", "k_w", "k_gemm", "perm_gemm", "smooth_gemm", "_wpad")
 
     def __init__(self, layer, device: torch.device, dtype: torch.dtype):
         f = layer._intcrush_smoothrot_factors
@@ -129,7 +157,36 @@ class _DeviceState:
         sm = layer._intcrush_smooth if f is None else None  # old SmoothQuant only without SmoothRot
         self.smooth = _rt.prepare_factors(sm.to(device), dtype) if sm is not None else None
         p = layer._intcrush_perm
-        self.perm = _rt.prepare_perm(p.to(device), layer._intcrush_w_in) if p is not None else None
+        K_w = layer._intcrush_w_in
+        self.perm = _rt.prepare_perm(p.to(device), K_w) if p is not None else None
+        self.k_w = K_w
+        self.k_gemm = _gemm_width(layer)
+        self.perm_gemm, self.smooth_gemm, self._wpad = self.perm, self.smooth, None
+        if self.k_gemm != K_w:
+            if p is not None:
+                ext = torch.arange(K_w, self.k_gemm, device=device, dtype=p.dtype)
+                self.perm_gemm = _rt.prepare_perm(torch.cat([p.to(device), ext]), self.k_gemm)
+            if sm is not None:
+                ones = torch.ones(self.k_gemm - K_w, device=device, dtype=sm.dtype)
+                self.smooth_gemm = _rt.prepare_factors(torch.cat([sm.to(device), ones]), dtype)
+
+    def gemm_weights(self, qdata: torch.Tensor, scale: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """(weights, scales) at k_gemm columns; the layer's own when no pad
+        is needed."""
+        if self.k_gemm == self.k_w:
+            return qdata, scale
+        N = qdata.shape[0]
+        int4 = qdata.dtype == torch.uint8
+        key = (qdata.data_ptr(), scale.data_ptr())
+        if self._wpad is None or self._wpad[0] != key:
+            cols = (self.k_gemm // 2 if int4 else self.k_gemm) - qdata.shape[1]
+            wq = torch.cat([qdata, qdata.new_zeros(N, cols)], dim=1)
+            sc = scale.reshape(N, -1)
+            if sc.shape[1] > 1:
+                extra = self.k_gemm // (self.k_w // sc.shape[1]) - sc.shape[1]
+                sc = torch.cat([sc, sc.new_ones(N, extra)], dim=1)
+            self._wpad = (key, wq, sc.reshape(N) if scale.dim() == 1 else sc)
+        return self._wpad[1], self._wpad[2]
 
 
 # ── ops factory ───────────────────────────────────────────────────────────
@@ -386,10 +443,11 @@ def make_intcrush_ops(quant_format: str, rot_size: int, use_pytorch: bool = Fals
                 need_prep = params.zp is not None or (self._intcrush_L1 is not None and self._intcrush_L2 is not None)
                 x_prep = (_rt.prepare_activation(x2, rot_size=R, w_in=self._intcrush_w_in, smoothrot=st.smoothrot,
                                                  perm=st.perm) if need_prep else None)
-                q, s_a = _rt.rotate_quantize(x2, rot_size=R, w_in=self._intcrush_w_in, smoothrot=st.smoothrot,
-                                             perm=st.perm)
+                q, s_a = _rt.rotate_quantize(x2, rot_size=R, w_in=st.k_gemm, smoothrot=st.smoothrot,
+                                             perm=st.perm_gemm)
                 res, lora = self._fold_linear_residuals(x, x_prep, params, x.dtype, x_prep)
-                out = _rt.gemm_w4a8(q, qdata, params.scale, s_a, bias=bias, out_dtype=x.dtype, residual=res)
+                wq, ws = st.gemm_weights(qdata, params.scale)
+                out = _rt.gemm_w4a8(q, wq, ws, s_a, bias=bias, out_dtype=x.dtype, residual=res)
                 out = self._apply_residuals(x, out, x_prep=x_prep, folded=True, lora_folded=lora)
                 return self._finish_forward(out, x)
 
@@ -398,10 +456,11 @@ def make_intcrush_ops(quant_format: str, rot_size: int, use_pytorch: bool = Fals
                 x2 = x.reshape(-1, x.shape[-1])
                 st = self._intcrush_state(x2)
                 params = weight._params
-                x_prep = _rt.prepare_activation(x2, rot_size=self._kernel_rot(), w_in=self._intcrush_w_in,
-                                                smoothrot=st.smoothrot, perm=st.perm)
+                x_prep = _rt.prepare_activation(x2, rot_size=self._kernel_rot(), w_in=st.k_gemm,
+                                                smoothrot=st.smoothrot, perm=st.perm_gemm)
                 b = bias if _env_flag("INTCRUSH_W4A16_BIAS") else None
-                out = _rt.gemm_w4a16(x_prep, qdata, params.scale, bias=b)
+                wq, ws = st.gemm_weights(qdata, params.scale)
+                out = _rt.gemm_w4a16(x_prep, wq, ws, bias=b)
                 if params.zp is not None:
                     self._zp_correction(out, x_prep, params.scale, params.zp)
                 out = self._apply_residuals(x, out, x_prep=x_prep)
@@ -443,21 +502,20 @@ def make_intcrush_ops(quant_format: str, rot_size: int, use_pytorch: bool = Fals
                 fused = _rt.USE_FUSED_W8A8 and x2.dtype in (torch.float16, torch.bfloat16)
                 x_prep = None
                 if zp is not None or fused:
-                    x_prep = _rt.prepare_activation(x2, rot_size=R, w_in=self._intcrush_w_in, smoothrot=st.smoothrot,
-                                                    perm=st.perm, smooth=st.smooth)
+                    x_prep = _rt.prepare_activation(x2, rot_size=R, w_in=st.k_gemm, smoothrot=st.smoothrot,
+                                                    perm=st.perm_gemm, smooth=st.smooth_gemm)
+                wq, ws = st.gemm_weights(qdata, params.scale)
                 if fused:
-                    out = _rt.fused_quant_int8_gemm_dequant(x_prep, qdata, params.scale, bias=bias,
-                                                            out_dtype=compute_dtype)
+                    out = _rt.fused_quant_int8_gemm_dequant(x_prep, wq, ws, bias=bias, out_dtype=compute_dtype)
                     if zp is not None:
                         self._zp_correction(out, x_prep, params.scale, zp)
                     out = self._apply_residuals(x, out)
                     return self._finish_forward(out, x)
-                q, s_a = _rt.rotate_quantize(x2, rot_size=R, w_in=self._intcrush_w_in, smoothrot=st.smoothrot,
-                                             perm=st.perm, smooth=st.smooth)
+                q, s_a = _rt.rotate_quantize(x2, rot_size=R, w_in=st.k_gemm, smoothrot=st.smoothrot,
+                                             perm=st.perm_gemm, smooth=st.smooth_gemm)
                 # the INT8 path's SVD branch reads the raw input (_ops.py:578)
                 res, lora = self._fold_linear_residuals(x, x_prep, params, compute_dtype, x2)
-                out = _rt.fused_int8_gemm_dequant(q, qdata, params.scale, s_a, bias=bias, out_dtype=compute_dtype,
-                                                  residual=res)
+                out = _rt.fused_int8_gemm_dequant(q, wq, ws, s_a, bias=bias, out_dtype=compute_dtype, residual=res)
                 out = self._apply_residuals(x, out, folded=True, lora_folded=lora)
                 return self._finish_forward(out, x)
 

@@ -328,3 +328,63 @@ def test_w4a8_layer_wider_than_one_workgroup(oracle, dev, dtype, K):
         assert np.array_equal(out.numpy(), ref)
     else:
         assert _cos(out, torch.from_numpy(ref)) >= 0.9999
+
+
+# ------------------------------------------------------------------ K not a multiple of 128
+@pytest.mark.parametrize("K,G,R", [(64, 1, 64), (96, 3, 16), (320, 10, 64), (64, 2, 0)])
+def test_narrow_layers_take_the_mfma_kernels(oracle, dev, K, G, R):
+    """Layers whose prepared width is not a multiple of 128 (e.g. a 64-wide
+    patch embedding) run the MFMA kernels at the next multiple of
+    lcm(128, group size): zero weights, zero codes and scale-1 groups in the
+    extra columns.  Bit-exact against the oracle over the real columns, and no
+    scalar-kernel warning is logged."""
+    rt = __graft_entry__._submodule("_hip_runtime")
+    M, N = 40, 96
+    ops = ops_mod.make_intcrush_ops("int4_crush", R if R else 256)
+    sd = int4_layer(N, K, G=G, seed=120 + K)
+    name = "double_blocks.0.img_mlp.2" if R else "double_blocks.0.img_mod.modulation"
+    lin = _to_dev(load_linear(ops, name, sd, K, N), dev)
+    assert lin._intcrush_rot_need == bool(R)
+    x = _x(M, K, torch.bfloat16, 121)
+    before = set(rt._SCALAR_WARNED)
+    out = lin(x.to(dev)).float().cpu().numpy()
+    st = lin._intcrush_state(x.to(dev))
+    assert st.k_gemm % 128 == 0 and st.k_gemm > K
+    assert set(rt._SCALAR_WARNED) == before
+    if R:  # W4A8
+        y = oracle.prepare(x, 1, smoothrot=sd["weight_smoothrot_factors"], rot_size=R, w_in=K,
+                           perm=sd["weight_perm"])
+        q, s = oracle.quantize(y)
+        acc = oracle.gemm_acc(q, oracle.unpack_int4(sd["weight"].numpy(), K), G)
+        ref = oracle.epilogue(acc, s, sd["weight_scale"].float().numpy(), sd["bias"].float().numpy(), 1)
+        assert np.array_equal(out, ref)
+    else:  # W4A16 (unrotated INT4)
+        y = oracle.prepare(x, 1, smoothrot=sd["weight_smoothrot_factors"], rot_size=0, w_in=K,
+                           perm=sd["weight_perm"])
+        w = oracle.dequant_w4a16(sd["weight"].numpy(), sd["weight_scale"].float().numpy(), K, 1)
+        ref = torch.from_numpy(y) @ torch.from_numpy(w).t()
+        assert _cos(torch.from_numpy(out), ref) >= 0.9999
+
+
+def test_narrow_int8_layer_graph_replays(oracle, dev):
+    """A 64-wide INT8 layer: the hipGraph runner runs prep + GEMM at 128
+    columns; every replay equals the oracle."""
+    rt = __graft_entry__._submodule("_hip_runtime")
+    K, N = 64, 128
+    ops = ops_mod.make_intcrush_ops("int8_crush", 64)
+    sd = int8_layer(N, K, seed=130, perm=True, smoothrot=True)
+    lin = _to_dev(load_linear(ops, "double_blocks.0.img_attn.qkv", sd, K, N), dev)
+    x = _x(48, K, torch.float16, 131).to(dev)
+    before = set(rt._SCALAR_WARNED)
+    first = lin(x).clone()
+    for _ in range(3):
+        y = lin(x)
+        torch.cuda.synchronize()
+        assert torch.equal(y, first)
+    assert set(rt._SCALAR_WARNED) == before
+    yp = oracle.prepare(x.cpu(), 0, smoothrot=sd["weight_smoothrot_factors"], rot_size=64, w_in=K,
+                        perm=sd["weight_perm"])
+    q, s = oracle.quantize(yp)
+    ref = oracle.epilogue(oracle.gemm_acc(q, sd["weight"].numpy()), s, sd["weight_scale"].float().numpy(),
+                          sd["bias"].float().numpy(), 0)
+    assert np.array_equal(first.float().cpu().numpy(), ref)
