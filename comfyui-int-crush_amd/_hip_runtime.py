@@ -79,6 +79,9 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "ic_gemm_w8a8_ex": ([_P, _L, _L, _L, _P, _L, _L, _P, _P, _P, _I, _I, _P, _I, _L, _P, _I, _L, _P, _L, _P], _I),
     "ic_gemm_w4a8_ex": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _P, _I, _I, _P, _I, _L, _P, _I, _L, _P, _L,
                          _P], _I),
+    "ic_int4_interleave_k": ([_P, _L, _L, _L, _P, _L, _P], _I),
+    "ic_gemm_w4a8_kil_ex": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _P, _I, _I, _P, _I, _L, _P, _I, _L, _P, _L,
+                             _P], _I),
     "ic_gemm_w8a8_chain": ([_P, _L, _L, _L, _P, _L, _L, _P, _P, _P, _I, _I, _P, _P, _I, _P, _I, _L, _P], _I),
     "ic_gemm_w4a8_chain": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _P, _I, _I, _P, _P, _I, _P, _I, _L, _P], _I),
     "ic_gemm_w4a16": ([_P, _I, _L, _L, _L, _P, _L, _L, _P, _L, _P, _I, _P, _L, _P], _I),
@@ -636,16 +639,36 @@ def _warn_if_scalar_gemm(who: str, K: int, G: int, *tensors: torch.Tensor, out64
                     "running the scalar fallback kernel (about 100x slower)", who, K, gs)
 
 
+def int4_interleave_k(w_packed: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Packed INT4 rows [N, K/2] (checkpoint nibble order) -> the same weights
+    in the K-interleaved order gemm_w4a8(..., kil=True) takes
+    (ic_int4_interleave_k): byte 4d + j holds k = 8d + j low and 8d + 4 + j
+    high.  out may be w_packed itself."""
+    assert w_packed.dtype == torch.uint8 and w_packed.dim() == 2, "w_packed must be uint8 [N, K/2]"
+    _need_cuda(w_packed)
+    N, half = w_packed.shape
+    if (2 * half) % 8:
+        raise ValueError(f"int4_interleave_k: K={2 * half} must be a multiple of 8")
+    w = w_packed if w_packed.stride(1) == 1 else w_packed.contiguous()
+    o = out if out is not None else torch.empty_like(w, memory_format=torch.contiguous_format)
+    assert o.shape == w.shape and o.dtype == torch.uint8 and o.stride(1) == 1, "out must be uint8 [N, K/2]"
+    with torch.cuda.device(w.device):
+        _call("ic_int4_interleave_k", _ptr(w), N, 2 * half, w.stride(0), _ptr(o), o.stride(0), _stream(w))
+    return o
+
+
 def gemm_w4a8(x_int8: torch.Tensor, w_packed: torch.Tensor, s_w: torch.Tensor, s_a: torch.Tensor,
               bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16,
               out: torch.Tensor | None = None, activation: int = 0,
-              residual: torch.Tensor | None = None) -> torch.Tensor:
+              residual: torch.Tensor | None = None, kil: bool = False) -> torch.Tensor:
     """W4A8 with the INT4 unpack fused into the GEMM.
 
     w_packed [N, K/2] uint8; s_w [N, G] (or [N]) float scales, group size K/G.
     out = (sum_g f32(acc_g) * s_w[n,g]) * s_a[m] + bias  (G > 1)
     out = f32(acc) * (s_a[m] * s_w[n]) + bias           (G == 1)
     then the activation and residual of fused_int8_gemm_dequant, in f32.
+    kil: w_packed is in the K-interleaved nibble order (int4_interleave_k),
+    which the kernels expand with fewer instructions; same outputs.
     """
     assert x_int8.dtype == torch.int8, f"x_int8 must be int8, got {x_int8.dtype}"
     assert w_packed.dtype == torch.uint8, f"w_packed must be uint8, got {w_packed.dtype}"
@@ -668,9 +691,9 @@ def gemm_w4a8(x_int8: torch.Tensor, w_packed: torch.Tensor, s_w: torch.Tensor, s
     _warn_if_scalar_gemm("gemm_w4a8", K, G, xq, w, out64=out64)
     with torch.cuda.device(xq.device):
         ws, nb = _splitk_workspace(M, N, K, G, True, xq.device)
-        _call("ic_gemm_w4a8_ex", _ptr(xq), M, K, xq.stride(0), _ptr(w), N, w.stride(0), _ptr(sw), G,
-              _ptr(sa), bp, bdt, act, rp, rdt, ldr, _ptr(c), _dt(c.dtype, "out"), c.stride(0), _ptr(ws), nb,
-              _stream(xq))
+        _call("ic_gemm_w4a8_kil_ex" if kil else "ic_gemm_w4a8_ex", _ptr(xq), M, K, xq.stride(0), _ptr(w), N,
+              w.stride(0), _ptr(sw), G, _ptr(sa), bp, bdt, act, rp, rdt, ldr, _ptr(c), _dt(c.dtype, "out"),
+              c.stride(0), _ptr(ws), nb, _stream(xq))
     return c
 
 
@@ -1009,8 +1032,8 @@ __all__ = [
     "TRITON_INT4_INT8_UNPACK", "TRITON_DYNQUANT", "TRITON_W4A8_GEMM", "TRITON_FUSED_QGD",
     "USE_FUSED_W8A8", "USE_CUDA_GRAPHS", "dynamic_quantize_activation", "fused_int8_gemm_dequant",
     "fused_quant_int8_gemm_dequant", "fused_w4a8_gemm_dequant", "unpack_int4_to_int8",
-    "unpack_int4_to_float16", "rotate_quantize", "prepare_activation", "gemm_w4a8", "gemm_w4a16",
-    "unpack_int4_to_float", "prepare_factors", "prepare_perm", "PreparedFactors", "gemm_acc_i32",
+    "unpack_int4_to_float16", "rotate_quantize", "prepare_activation", "gemm_w4a8", "int4_interleave_k",
+    "gemm_w4a16", "unpack_int4_to_float", "prepare_factors", "prepare_perm", "PreparedFactors", "gemm_acc_i32",
     "gemv", "GEMV_MAX_M", "fused_layernorm_quantize", "fused_rmsnorm_quantize", "fused_softmax_quantize",
     "norm_rotate_quantize", "ACT_NONE", "ACT_SILU", "ACT_GELU", "ACT_GELU_TANH", "int8_gemm_int8out",
     "gemm_chain", "CHAIN_ROT_SIZES", "prep_gemv", "prep_gemv_ok", "PREP_GEMV_MAX_K", "PREP_GEMV_MAX_CODES",

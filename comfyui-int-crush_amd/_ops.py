@@ -71,8 +71,8 @@ _KNOWN_SUFFIXES = (_SD_KEY_WEIGHT, _SD_KEY_SCALE, _SD_KEY_ZP, _SD_KEY_PERM, _SD_
 _VALID_SCALE_DTYPES = (torch.float16, torch.float32)
 
 
-def _env_flag(name: str) -> bool:
-    return os.environ.get(name, "0") == "1"
+def _env_flag(name: str, default: str = "0") -> bool:
+    return os.environ.get(name, default) == "1"
 
 
 # ── lazy ComfyUI imports (_ops.py:53-72) ──────────────────────────────────
@@ -147,7 +147,10 @@ class _DeviceState:
     GEMM at its width (_gemm_width): the prepared width k_gemm, the perm and
     old-SmoothQuant factors extended over the extra columns (identity, 1), and
     the weights and scales padded once (zero weights; scale 1 for the extra
-    groups)."""
+    groups), for W4A8 layers rewritten once in the K-interleaved nibble order
+    that the W4A8 kernels expand with fewer instructions (a second copy of
+    the packed weights on the device, N x K/2 bytes per layer;
+    INTCRUSH_W4_INTERLEAVE=0 keeps the checkpoint order)."""
 
     __slots__ = ("smoothrot", "smooth", "perm", "k_w", "k_gemm", "perm_gemm", "smooth_gemm", "_wpad")
 
@@ -170,22 +173,30 @@ class _DeviceState:
                 ones = torch.ones(self.k_gemm - K_w, device=device, dtype=sm.dtype)
                 self.smooth_gemm = _rt.prepare_factors(torch.cat([sm.to(device), ones]), dtype)
 
-    def gemm_weights(self, qdata: torch.Tensor, scale: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    def gemm_weights(self, qdata: torch.Tensor, scale: torch.Tensor,
+                     kil: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
         """(weights, scales) at k_gemm columns; the layer's own when no pad
-        is needed."""
-        if self.k_gemm == self.k_w:
+        is needed.  kil (packed INT4, k_gemm a multiple of 8): the weights in
+        the K-interleaved nibble order, for gemm_w4a8(..., kil=True)."""
+        kil = kil and self.k_gemm % 8 == 0
+        if self.k_gemm == self.k_w and not kil:
             return qdata, scale
         N = qdata.shape[0]
         int4 = qdata.dtype == torch.uint8
-        key = (qdata.data_ptr(), scale.data_ptr())
+        key = (qdata.data_ptr(), scale.data_ptr(), kil)
         if self._wpad is None or self._wpad[0] != key:
-            cols = (self.k_gemm // 2 if int4 else self.k_gemm) - qdata.shape[1]
-            wq = torch.cat([qdata, qdata.new_zeros(N, cols)], dim=1)
-            sc = scale.reshape(N, -1)
-            if sc.shape[1] > 1:
-                extra = self.k_gemm // (self.k_w // sc.shape[1]) - sc.shape[1]
-                sc = torch.cat([sc, sc.new_ones(N, extra)], dim=1)
-            self._wpad = (key, wq, sc.reshape(N) if scale.dim() == 1 else sc)
+            wq, sc = qdata, scale
+            if self.k_gemm != self.k_w:
+                cols = (self.k_gemm // 2 if int4 else self.k_gemm) - qdata.shape[1]
+                wq = torch.cat([qdata, qdata.new_zeros(N, cols)], dim=1)
+                sc = scale.reshape(N, -1)
+                if sc.shape[1] > 1:
+                    extra = self.k_gemm // (self.k_w // sc.shape[1]) - sc.shape[1]
+                    sc = torch.cat([sc, sc.new_ones(N, extra)], dim=1)
+                sc = sc.reshape(N) if scale.dim() == 1 else sc
+            if kil:
+                wq = _rt.int4_interleave_k(wq)  # a new tensor: the layer's weights stay as loaded
+            self._wpad = (key, wq, sc)
         return self._wpad[1], self._wpad[2]
 
 
@@ -446,8 +457,9 @@ def make_intcrush_ops(quant_format: str, rot_size: int, use_pytorch: bool = Fals
                 q, s_a = _rt.rotate_quantize(x2, rot_size=R, w_in=st.k_gemm, smoothrot=st.smoothrot,
                                              perm=st.perm_gemm)
                 res, lora = self._fold_linear_residuals(x, x_prep, params, x.dtype, x_prep)
-                wq, ws = st.gemm_weights(qdata, params.scale)
-                out = _rt.gemm_w4a8(q, wq, ws, s_a, bias=bias, out_dtype=x.dtype, residual=res)
+                kil = _env_flag("INTCRUSH_W4_INTERLEAVE", "1") and st.k_gemm % 8 == 0
+                wq, ws = st.gemm_weights(qdata, params.scale, kil=kil)
+                out = _rt.gemm_w4a8(q, wq, ws, s_a, bias=bias, out_dtype=x.dtype, residual=res, kil=kil)
                 out = self._apply_residuals(x, out, x_prep=x_prep, folded=True, lora_folded=lora)
                 return self._finish_forward(out, x)
 

@@ -43,14 +43,6 @@ template <int N> IC_DEV void wait_vm() {
 }
 IC_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// 8 INT4 nibbles (low nibble = even k) -> 8 int8 values 16*q in natural k order.
-IC_DEV void unpack8_x16(uint32_t P, uint32_t& w0, uint32_t& w1) {
-  const uint32_t lo = (P << 4) & 0xf0f0f0f0u;  // bytes: 16*q[k=0,2,4,6]
-  const uint32_t hi = P & 0xf0f0f0f0u;         // bytes: 16*q[k=1,3,5,7]
-  w0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);  // q0 q1 q2 q3
-  w1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // q4 q5 q6 q7
-}
-
 // Logical tile id for hardware block id b.  Consecutive block ids are spread
 // round-robin over the 8 XCDs; renumber so each XCD works on a contiguous run
 // of logical tiles, then walk the run in bands of GM tile rows so neighbouring

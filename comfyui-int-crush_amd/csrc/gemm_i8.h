@@ -46,12 +46,17 @@ struct GemmArgs {
   int32_t* acc_out; bool int4;
   void* ws = nullptr; int64_t ws_bytes = 0;  // split-K workspace (optional)
   ic_epi epi{};                              // activation / residual epilogue
+  bool kil = false;                          // packed INT4 in the K-interleaved nibble order
 };
 }  // namespace ic_gemm
 
 // GEMM launches with the activation / residual epilogue compiled in
 // (gemm_i8_epi.hip).
 int ic_gemm_run_epi(const ic_gemm::GemmArgs& g, hipStream_t st, const char* who, bool force_generic);
+// gemm_i8_big_kernel on packed INT4 in the K-interleaved nibble order, for
+// weight mode `mode` (gemm_i8_kil.hip; its own translation unit, so that
+// these instantiations compile in parallel with the others).
+hipError_t ic_launch_big_kil(const ic_gemm::GemmArgs& g, int out_dt, bool epi, int mode, hipStream_t st);
 
 namespace {
 using ic_gemm::GemmArgs;
@@ -93,7 +98,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
     const int8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
     const float* __restrict__ s_a, const float* __restrict__ s_w, int G,
     const void* __restrict__ bias, int bias_dt, void* __restrict__ C, int64_t ldc, int M, int N,
-    int K, int32_t* __restrict__ acc_out, ic_epi epi) {
+    int K, int32_t* __restrict__ acc_out, ic_epi epi, W4Sel wsel) {
   constexpr int BM = TL::BM, BN = TL::BN, WGM = TL::WGM, NS = TL::NS, GS = TL::GS;
   constexpr bool INT4 = TL::INT4;
   constexpr int WGN = 8 / WGM;
@@ -227,9 +232,9 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
     wait_vm<0>();
   };
 
-  // ---- packed INT4 -> 16*q int8 tile in LDS.  One buffer suffices: the
-  // barrier at the top of each step orders the MFMA reads of step s-1 before
-  // the unpack of step s.
+  // ---- packed INT4 -> 16*q int8 tile in LDS (either nibble order: wsel).
+  // One buffer suffices: the barrier at the top of each step orders the MFMA
+  // reads of step s-1 before the unpack of step s.
   auto unpack = [&](int kt) {
     if constexpr (INT4) {
       const char* bp = smem + (kt % NS) * TL::SLOT + TL::A_BYTES;
@@ -240,10 +245,10 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
         const int row = idx >> 2, part = idx & 3;
         const v4u p = *(const v4u*)(bp + idx * 16);
         uint32_t w[8];
-        unpack8_x16(p.x, w[0], w[1]);
-        unpack8_x16(p.y, w[2], w[3]);
-        unpack8_x16(p.z, w[4], w[5]);
-        unpack8_x16(p.w, w[6], w[7]);
+        unpack8_x16(p.x, w[0], w[1], wsel);
+        unpack8_x16(p.y, w[2], w[3], wsel);
+        unpack8_x16(p.z, w[4], w[5], wsel);
+        unpack8_x16(p.w, w[6], w[7], wsel);
         *(v4u*)(bu + lds_off(row, 2 * part)) = v4u{w[0], w[1], w[2], w[3]};
         *(v4u*)(bu + lds_off(row, 2 * part + 1)) = v4u{w[4], w[5], w[6], w[7]};
       }
@@ -655,13 +660,14 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_kernel(
 }
 
 // Shape-generic fallback (any K, any alignment): one thread per output, exact
-// int32 accumulation; same epilogue arithmetic as the MFMA kernel.
+// int32 accumulation; same epilogue arithmetic as the MFMA kernel.  kil: the
+// packed INT4 rows are in the K-interleaved nibble order.
 template <bool INT4, int OUT_DT>
 __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(
     const int8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
     const float* __restrict__ s_a, const float* __restrict__ s_w, int G, int gsize,
     const void* __restrict__ bias, int bias_dt, void* __restrict__ C, int64_t ldc, int M, int N,
-    int K, int32_t* __restrict__ acc_out, ic_epi epi) {
+    int K, int32_t* __restrict__ acc_out, ic_epi epi, bool kil) {
   const int n = blockIdx.x * blockDim.x + threadIdx.x;
   const int m = blockIdx.y;
   if (n >= N || m >= M) return;
@@ -676,7 +682,8 @@ __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(
   for (int k = 0; k < K; ++k) {
     int w;
     if constexpr (INT4) {
-      const int nib = (b[k >> 1] >> (4 * (k & 1))) & 0xf;
+      const int t = w4_nibble_index(k, kil);
+      const int nib = (b[t >> 1] >> (4 * (t & 1))) & 0xf;
       w = nib >= 8 ? nib - 16 : nib;
     } else {
       w = (int8_t)b[k];
@@ -799,7 +806,8 @@ hipError_t launch_kernel(const GemmArgs& g, int S, hipStream_t st) {
   static unsigned char lds_set[64];  // per device
   if (hipError_t e = ic_set_lds_limit((const void*)kern, (int)shm, lds_set)) return e;
   kern<<<dim3(tiles, S), dim3(kNT), shm, st>>>(g.A, g.lda, g.B, g.ldb, g.s_a, g.s_w, g.G, g.bias, g.bias_dt,
-                                               g.C, g.ldc, g.M, g.N, g.K, PART ? (int32_t*)g.ws : g.acc_out, g.epi);
+                                               g.C, g.ldc, g.M, g.N, g.K, PART ? (int32_t*)g.ws : g.acc_out, g.epi,
+                                               g.kil ? kW4Kil : kW4Plain);
   return hipGetLastError();
 }
 
@@ -875,11 +883,11 @@ bool big_row_ok(const GemmArgs& g) {
   return big_pick(g).cost * (g.int4 ? 80 : 90) / 100 < tiling_cost(g, t.bm, t.bn, tpct);
 }
 
-template <int OUT_DT, bool EPI, int MODE, int TMB>
+template <int OUT_DT, bool EPI, int MODE, int TMB, bool KIL>
 hipError_t launch_big_t(const GemmArgs& g, hipStream_t st) {
   using RT = big::Rows<TMB, MODE>;
   const int tiles = ((g.M + RT::BM - 1) / RT::BM) * ((g.N + big::BN - 1) / big::BN);
-  auto kern = gemm_i8_big_kernel<OUT_DT, EPI, MODE, TMB>;
+  auto kern = gemm_i8_big_kernel<OUT_DT, EPI, MODE, TMB, KIL>;
   constexpr size_t shm = RT::lds_bytes;
   static unsigned char lds_set[64];  // per device
   if (hipError_t e = ic_set_lds_limit((const void*)kern, (int)shm, lds_set)) return e;
@@ -887,12 +895,15 @@ hipError_t launch_big_t(const GemmArgs& g, hipStream_t st) {
                                             g.ldc, g.M, g.N, g.K, g.epi);
   return hipGetLastError();
 }
-template <int OUT_DT, bool EPI, int MODE>
+template <int OUT_DT, bool EPI, int MODE, bool KIL = false>
 hipError_t launch_big(const GemmArgs& g, hipStream_t st) {
+  if constexpr (!KIL && MODE != big::ROW8) {
+    if (g.kil) return ic_launch_big_kil(g, OUT_DT, EPI, MODE, st);
+  }
   switch (big_rows(g)) {
-    case 8: return launch_big_t<OUT_DT, EPI, MODE, 8>(g, st);
-    case 10: return launch_big_t<OUT_DT, EPI, MODE, 10>(g, st);
-    default: return launch_big_t<OUT_DT, EPI, MODE, 9>(g, st);
+    case 8: return launch_big_t<OUT_DT, EPI, MODE, 8, KIL>(g, st);
+    case 10: return launch_big_t<OUT_DT, EPI, MODE, 10, KIL>(g, st);
+    default: return launch_big_t<OUT_DT, EPI, MODE, 9, KIL>(g, st);
   }
 }
 
@@ -932,7 +943,7 @@ hipError_t launch_generic_t(const GemmArgs& g, int gsize, hipStream_t st) {
   dim3 grid((unsigned)((g.N + 255) / 256), (unsigned)g.M);
   gemm_i8_generic_kernel<INT4, OUT_DT><<<grid, dim3(256), 0, st>>>(
       g.A, g.lda, g.B, g.ldb, g.s_a, g.s_w, g.G, gsize, g.bias, g.bias_dt, g.C, g.ldc, g.M, g.N, g.K,
-      g.acc_out, g.epi);
+      g.acc_out, g.epi, g.kil);
   return hipGetLastError();
 }
 template <bool INT4>
@@ -994,7 +1005,7 @@ hipError_t launch_chain_t(const GemmArgs& g, hipStream_t st) {
   static unsigned char lds_set[64];  // per device
   if (hipError_t e = ic_set_lds_limit((const void*)kern, (int)shm, lds_set)) return e;
   kern<<<dim3(tiles), dim3(kNT), shm, st>>>(g.A, g.lda, g.B, g.ldb, g.s_a, g.s_w, g.G, g.bias, g.bias_dt, g.C,
-                                            g.ldc, g.M, g.N, g.K, nullptr, g.epi);
+                                            g.ldc, g.M, g.N, g.K, nullptr, g.epi, kW4Plain);
   return hipGetLastError();
 }
 template <class TL, int OUT_DT>

@@ -42,6 +42,23 @@ int run_gemm(GemmArgs g, hipStream_t st, const char* who, bool force_generic) {
   return run_gemm_t<false>(g, st, who, force_generic);
 }
 
+// W4A8 on either nibble order of the packed weights (kil: K-interleaved);
+// M <= 16 takes the GEMV where its shape and groups allow.
+int gemm_w4a8_any(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w, int64_t N, int64_t ldw,
+                  const float* s_w, int64_t num_groups, const float* s_a, const void* bias, int bias_dtype,
+                  int activation, const void* residual, int residual_dtype, int64_t ldr, void* out, int out_dtype,
+                  int64_t ldo, void* workspace, int64_t workspace_bytes, void* stream, bool kil, const char* who) {
+  if (int rc = ic_check_epi(who, activation, residual, residual_dtype, ldr, N)) return rc;
+  const ic_epi epi{activation, residual, residual_dtype, ldr};
+  if (ic_gemv_applicable(M, K, xq, ldx, w, ldw) && ldw * 2 >= K && N > 0 && ldo >= N && ldx >= K &&
+      ic_gemv_w4a8_groups_ok(M, K, num_groups))
+    return ic_gemv_w4a8_epi(xq, M, K, ldx, w, N, ldw, s_w, num_groups, s_a, bias, bias_dtype, out, out_dtype, ldo, epi,
+                            stream, kil ? kW4Kil : kW4Plain);
+  GemmArgs g{xq, ldx, w, ldw, s_a, s_w, (int)num_groups, bias, bias_dtype, out, out_dtype,
+             ldo, (int)M, (int)N, (int)K, nullptr, true, workspace, workspace_bytes, epi, kil};
+  return run_gemm(g, (hipStream_t)stream, who, false);
+}
+
 }  // namespace
 
 // Validation shared by the _ex entry points: activation code and residual.
@@ -108,15 +125,21 @@ int ic_gemm_w4a8_ex(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const u
                     int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a, const void* bias,
                     int bias_dtype, int activation, const void* residual, int residual_dtype, int64_t ldr, void* out,
                     int out_dtype, int64_t ldo, void* workspace, int64_t workspace_bytes, void* stream) {
-  if (int rc = ic_check_epi("ic_gemm_w4a8", activation, residual, residual_dtype, ldr, N)) return rc;
-  const ic_epi epi{activation, residual, residual_dtype, ldr};
-  if (ic_gemv_applicable(M, K, xq, ldx, w_packed, ldw) && ldw * 2 >= K && N > 0 && ldo >= N && ldx >= K &&
-      ic_gemv_w4a8_groups_ok(M, K, num_groups))
-    return ic_gemv_w4a8_epi(xq, M, K, ldx, w_packed, N, ldw, s_w, num_groups, s_a, bias, bias_dtype, out, out_dtype,
-                            ldo, epi, stream);
-  GemmArgs g{xq, ldx, w_packed, ldw, s_a, s_w, (int)num_groups, bias, bias_dtype, out, out_dtype,
-             ldo, (int)M, (int)N, (int)K, nullptr, true, workspace, workspace_bytes, epi};
-  return run_gemm(g, (hipStream_t)stream, "ic_gemm_w4a8", false);
+  return gemm_w4a8_any(xq, M, K, ldx, w_packed, N, ldw, s_w, num_groups, s_a, bias, bias_dtype, activation, residual,
+                       residual_dtype, ldr, out, out_dtype, ldo, workspace, workspace_bytes, stream, false,
+                       "ic_gemm_w4a8");
+}
+
+int ic_gemm_w4a8_kil_ex(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_kil, int64_t N,
+                        int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a, const void* bias,
+                        int bias_dtype, int activation, const void* residual, int residual_dtype, int64_t ldr,
+                        void* out, int out_dtype, int64_t ldo, void* workspace, int64_t workspace_bytes,
+                        void* stream) {
+  if (K % 8 != 0)
+    return ic_set_error(IC_ERR_INVALID_ARG, "ic_gemm_w4a8_kil_ex: K=%lld must be a multiple of 8", (long long)K);
+  return gemm_w4a8_any(xq, M, K, ldx, w_kil, N, ldw, s_w, num_groups, s_a, bias, bias_dtype, activation, residual,
+                       residual_dtype, ldr, out, out_dtype, ldo, workspace, workspace_bytes, stream, true,
+                       "ic_gemm_w4a8_kil_ex");
 }
 
 int ic_gemm_w4a8_ws(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed,

@@ -41,12 +41,12 @@ __global__ __launch_bounds__(kGT) void gemv_i8_kernel(
     const int8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
     const float* __restrict__ s_a, const float* __restrict__ s_w, int G, int gsize,
     const void* __restrict__ bias, int bias_dt, void* __restrict__ C, int64_t ldc, int M, int N, int K,
-    ic_epi epi) {
+    ic_epi epi, W4Sel sel) {
   // the block sums, then with XL the activation codes [M][K]
   extern __shared__ int32_t sacc[];
   int8_t* xs = (int8_t*)(sacc + gemv_sums(GS, M, K));
   gemv::gemv_i8_body<INT4, GS, OUT_DT, XL>(A, lda, B, ldb, s_a, s_w, G, gsize, bias, bias_dt, C, ldc, M, N, K, epi,
-                                           sacc, xs);
+                                           sacc, xs, sel);
 }
 
 // W4A16 weight dequantization RN_dt(q * RN_dt(s)) of 8 nibbles.
@@ -170,36 +170,41 @@ __global__ __launch_bounds__(kGT) void gemv_w4a16_kernel(
 template <bool INT4, int GS, int OUT_DT, bool XL>
 hipError_t launch_gemv_i8_t(const int8_t* A, int64_t lda, const uint8_t* B, int64_t ldb, const float* s_a,
                             const float* s_w, int G, const void* bias, int bias_dt, void* C, int64_t ldc,
-                            int M, int N, int K, const ic_epi& epi, hipStream_t st) {
+                            int M, int N, int K, const ic_epi& epi, W4Sel sel, hipStream_t st) {
   auto kern = gemv_i8_kernel<INT4, GS, OUT_DT, XL>;
   const size_t shm = (size_t)gemv_sums(GS, M, K) * 4 + (XL ? (size_t)M * K : 0);
   static unsigned char lds_set[64];  // per device
   if (hipError_t e = ic_set_lds_limit((const void*)kern, 160 * 1024, lds_set)) return e;
   kern<<<dim3((unsigned)((N + 15) / 16)), dim3(kGT), shm, st>>>(A, lda, B, ldb, s_a, s_w, G, K / G, bias, bias_dt,
-                                                                C, ldc, M, N, K, epi);
+                                                                C, ldc, M, N, K, epi, sel);
   return hipGetLastError();
 }
 
 template <bool INT4, int GS, int OUT_DT>
 hipError_t launch_gemv_i8(const int8_t* A, int64_t lda, const uint8_t* B, int64_t ldb, const float* s_a,
                           const float* s_w, int G, const void* bias, int bias_dt, void* C, int64_t ldc,
-                          int M, int N, int K, const ic_epi& epi, hipStream_t st) {
+                          int M, int N, int K, const ic_epi& epi, W4Sel sel, hipStream_t st) {
   if ((int64_t)M * K <= kXlBytes && gemv_sums(GS, M, K) * 4 + (int64_t)M * K <= 160 * 1024)
-    return launch_gemv_i8_t<INT4, GS, OUT_DT, true>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, epi, st);
-  return launch_gemv_i8_t<INT4, GS, OUT_DT, false>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, epi, st);
+    return launch_gemv_i8_t<INT4, GS, OUT_DT, true>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, epi,
+                                                    sel, st);
+  return launch_gemv_i8_t<INT4, GS, OUT_DT, false>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, epi,
+                                                   sel, st);
 }
 
 template <bool INT4, int GS>
 hipError_t pick_gemv_out(int out_dt, const int8_t* A, int64_t lda, const uint8_t* B, int64_t ldb,
                          const float* s_a, const float* s_w, int G, const void* bias, int bias_dt, void* C,
-                         int64_t ldc, int M, int N, int K, const ic_epi& epi, hipStream_t st) {
+                         int64_t ldc, int M, int N, int K, const ic_epi& epi, W4Sel sel, hipStream_t st) {
   switch (out_dt) {
     case IC_DTYPE_F16:
-      return launch_gemv_i8<INT4, GS, IC_DTYPE_F16>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, epi, st);
+      return launch_gemv_i8<INT4, GS, IC_DTYPE_F16>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, epi,
+                                                    sel, st);
     case IC_DTYPE_BF16:
-      return launch_gemv_i8<INT4, GS, IC_DTYPE_BF16>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, epi, st);
+      return launch_gemv_i8<INT4, GS, IC_DTYPE_BF16>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, epi,
+                                                     sel, st);
     default:
-      return launch_gemv_i8<INT4, GS, IC_DTYPE_F32>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, epi, st);
+      return launch_gemv_i8<INT4, GS, IC_DTYPE_F32>(A, lda, B, ldb, s_a, s_w, G, bias, bias_dt, C, ldc, M, N, K, epi,
+                                                    sel, st);
   }
 }
 
@@ -257,14 +262,15 @@ int ic_gemv_w8a8_epi(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const 
   if (out_dtype != IC_DTYPE_F16 && out_dtype != IC_DTYPE_BF16 && out_dtype != IC_DTYPE_F32)
     return ic_set_error(IC_ERR_INVALID_ARG, "%s: out dtype must be f16/bf16/f32", who);
   hipError_t e = pick_gemv_out<false, 0>(out_dtype, xq, ldx, (const uint8_t*)w, ldw, s_a, s_w, 1, bias, bias_dtype,
-                                         out, ldo, (int)M, (int)N, (int)K, epi, (hipStream_t)stream);
+                                         out, ldo, (int)M, (int)N, (int)K, epi, kW4Plain, (hipStream_t)stream);
   if (e != hipSuccess) return ic_set_error(IC_ERR_LAUNCH, "%s: %s", who, hipGetErrorString(e));
   return IC_OK;
 }
 
 int ic_gemv_w4a8_epi(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed, int64_t N,
                      int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a, const void* bias,
-                     int bias_dtype, void* out, int out_dtype, int64_t ldo, const ic_epi& epi, void* stream) {
+                     int bias_dtype, void* out, int out_dtype, int64_t ldo, const ic_epi& epi, void* stream,
+                     W4Sel sel) {
   const char* who = "ic_gemv_w4a8";
   int rc = check_gemv_common(who, M, K, N, ldx, ldo, bias, bias_dtype);
   if (rc) return rc;
@@ -282,7 +288,8 @@ int ic_gemv_w4a8_epi(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const 
   const int fb = num_groups > 1 ? fold_block(K / num_groups) : 0;
   auto go = [&](auto gs_c) {
     return pick_gemv_out<true, decltype(gs_c)::value>(out_dtype, xq, ldx, w_packed, ldw, s_a, s_w, (int)num_groups,
-                                                      bias, bias_dtype, out, ldo, (int)M, (int)N, (int)K, epi, st);
+                                                      bias, bias_dtype, out, ldo, (int)M, (int)N, (int)K, epi, sel,
+                                                      st);
   };
   hipError_t e = fb == 128 ? go(std::integral_constant<int, 128>{})
                  : fb == 64 ? go(std::integral_constant<int, 64>{})

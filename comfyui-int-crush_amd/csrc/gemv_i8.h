@@ -28,31 +28,23 @@ constexpr int kGBK = 128;  // K per block
 constexpr int kXlBytes = 16384;
 constexpr int kOutRuntime = -1;  // OUT_DT: output dtype passed at run time
 
-// 8 INT4 nibbles (low nibble = even k) -> 8 int8 values 16*q in natural k order.
-IC_DEV void unpack8_x16(uint32_t P, uint32_t& w0, uint32_t& w1) {
-  const uint32_t lo = (P << 4) & 0xf0f0f0f0u;
-  const uint32_t hi = P & 0xf0f0f0f0u;
-  w0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
-  w1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
-}
-
 // One K block of one wave: MFMAs on the lane's 32 activation codes (av0, av1:
 // K 32c .. 32c+31 of the block, c = lane / 16) and its 32 weights (INT4: the
 // 16 packed bytes pwu; INT8: pwu and w1u).  Grouped (GS = 128, 64 or 32, the
 // fold block gcd(group, 128)): the sums of the block's 128 / GS parts, each
 // from the lanes holding that part's K range (the other lanes' codes zeroed),
 // go to sacc[(b * 128 / GS + part)][M][16].  Per row (GS = 0) they accumulate
-// in tot.  col = lane % 16.
+// in tot.  col = lane % 16.  sel: the nibble order of the packed weights.
 template <bool INT4, int GS>
 IC_DEV void mma_block(int b, const v4i& av0, const v4i& av1, const v4u& pwu, const v4i& w1u, int M, int c, int col,
-                      int32_t* sacc, v4i& tot) {
+                      int32_t* sacc, v4i& tot, W4Sel sel = kW4Plain) {
   v4i b0v, b1v;
   if constexpr (INT4) {
     uint32_t w[8];
-    unpack8_x16(pwu.x, w[0], w[1]);
-    unpack8_x16(pwu.y, w[2], w[3]);
-    unpack8_x16(pwu.z, w[4], w[5]);
-    unpack8_x16(pwu.w, w[6], w[7]);
+    unpack8_x16(pwu.x, w[0], w[1], sel);
+    unpack8_x16(pwu.y, w[2], w[3], sel);
+    unpack8_x16(pwu.z, w[4], w[5], sel);
+    unpack8_x16(pwu.w, w[6], w[7], sel);
     b0v = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
     b1v = v4i{(int)w[4], (int)w[5], (int)w[6], (int)w[7]};
   } else {
@@ -148,7 +140,7 @@ template <bool INT4, int GS, int OUT_DT, bool XL>
 IC_DEV void gemv_i8_body(const int8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
                          const float* __restrict__ s_a, const float* __restrict__ s_w, int G, int gsize,
                          const void* __restrict__ bias, int bias_dt, void* __restrict__ C, int64_t ldc, int M, int N,
-                         int K, const ic_epi& epi, int32_t* sacc, int8_t* xs) {
+                         int K, const ic_epi& epi, int32_t* sacc, int8_t* xs, W4Sel sel) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n0 = blockIdx.x * 16;
@@ -195,7 +187,7 @@ IC_DEV void gemv_i8_body(const int8_t* __restrict__ A, int64_t lda, const uint8_
         const int b = b0 + 4 * u;
         if (b >= KB) break;
         mma_block<INT4, GS>(b, *(const v4i*)(arow + kGBK * b), *(const v4i*)(arow + kGBK * b + 16), pw[u],
-                            w1[INT4 ? 0 : u], M, c, col, sacc, tot);
+                            w1[INT4 ? 0 : u], M, c, col, sacc, tot, sel);
       }
     }
   } else {
@@ -220,7 +212,7 @@ IC_DEV void gemv_i8_body(const int8_t* __restrict__ A, int64_t lda, const uint8_
       for (int u = 0; u < kBatch; ++u) {
         const int b = b0 + 4 * u;
         if (b >= KB) break;
-        mma_block<INT4, GS>(b, a0[u], a1[u], pw[u], w1[u], M, c, col, sacc, tot);
+        mma_block<INT4, GS>(b, a0[u], a1[u], pw[u], w1[u], M, c, col, sacc, tot, sel);
       }
     }
   }

@@ -176,6 +176,39 @@ IC_DEV uint32_t pack4_lo_bytes(int c0, int c1, int c2, int c3) {
   return lo | hi;
 }
 
+// ------------------------------------------------------------ packed INT4
+// Packed INT4 weight rows come in two nibble orders (two's complement nibbles
+// either way):
+//   plain (the checkpoint format, _quant_utils.py:67-80): byte b holds
+//     k = 2b in its low nibble and k = 2b + 1 in its high nibble;
+//   K-interleaved (ic_int4_interleave_k): byte 4d + j holds k = 8d + j in its
+//     low nibble and k = 8d + 4 + j in its high nibble (j = 0..3).
+// A dword of 8 nibbles expands to 8 int8 values 16*q in natural k order from
+// two masked copies, lo = the low nibbles moved up, hi = the high nibbles in
+// place (bytes 16*q, exactly; the factor 16 is removed in the epilogues).
+// The plain order then needs two byte permutes; the K-interleaved one takes
+// lo and hi as they are.  W4Sel holds the permutes' selectors, so that
+// kernels keeping them serve either order with the same instructions.
+struct W4Sel {
+  uint32_t s0, s1;
+};
+constexpr W4Sel kW4Plain{0x05010400u, 0x07030602u};  // q0 q1 q2 q3 | q4 q5 q6 q7 from (hi, lo)
+constexpr W4Sel kW4Kil{0x03020100u, 0x07060504u};    // lo | hi
+IC_DEV void unpack8_x16(uint32_t P, uint32_t& w0, uint32_t& w1, W4Sel sel = kW4Plain) {
+  const uint32_t lo = (P << 4) & 0xf0f0f0f0u;
+  const uint32_t hi = P & 0xf0f0f0f0u;
+  w0 = __builtin_amdgcn_perm(hi, lo, sel.s0);
+  w1 = __builtin_amdgcn_perm(hi, lo, sel.s1);
+}
+IC_DEV void unpack8_x16_kil(uint32_t P, uint32_t& w0, uint32_t& w1) {
+  w0 = (P << 4) & 0xf0f0f0f0u;
+  w1 = P & 0xf0f0f0f0u;
+}
+// Nibble index (byte * 2 + high) of weight k in a packed row.
+IC_DEV int w4_nibble_index(int k, bool kil) {
+  return kil ? ((k & ~7) + 2 * (k & 3) + ((k >> 2) & 1)) : k;
+}
+
 // ------------------------------------------------------------ reductions
 IC_DEV float wave_max(float v) {
 #pragma unroll
@@ -267,4 +300,5 @@ int ic_gemv_w8a8_epi(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const 
                      int64_t ldo, const ic_epi& epi, void* stream);
 int ic_gemv_w4a8_epi(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed, int64_t N,
                      int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a, const void* bias,
-                     int bias_dtype, void* out, int out_dtype, int64_t ldo, const ic_epi& epi, void* stream);
+                     int bias_dtype, void* out, int out_dtype, int64_t ldo, const ic_epi& epi, void* stream,
+                     W4Sel sel = kW4Plain);

@@ -153,10 +153,11 @@ int ic_gemm_w8a8(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8
  *                    columns in K order (acc_g of each block with its group's
  *                    scale), so the result does not depend on the kernel:
  *                    - multiples of 128: MFMA kernels, per 128 columns;
- *                    - odd multiples of 64 with a 16-bit output whose rows are
- *                      16-byte aligned: the 288 x 192 MFMA kernel, per 64;
+ *                    - odd multiples of 64 or of 32 with a 16-bit output
+ *                      whose rows are 16-byte aligned: the 288 x 192 MFMA
+ *                      kernel, per 64 or per 32;
  *                    - anything else (other group sizes, K not a multiple of
- *                      128, f32 or unaligned outputs with groups of 64,
+ *                      128, f32 or unaligned outputs with such groups,
  *                      unaligned operands): a scalar kernel, one thread per
  *                      output, about 100x slower.
  */
@@ -236,6 +237,26 @@ int ic_gemm_w4a8_ex(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const u
                     const void* bias, int bias_dtype, int activation, const void* residual,
                     int residual_dtype, int64_t ldr, void* out, int out_dtype, int64_t ldo, void* workspace,
                     int64_t workspace_bytes, void* stream);
+
+/*
+ * K-interleaved INT4 weights.  No reference counterpart: the reference
+ * unpacks the checkpoint's nibble order (byte b holds k = 2b low, 2b + 1 high;
+ * _quant_utils.py:67-80) inside every GEMM call.  ic_int4_interleave_k
+ * rewrites packed rows once, on the device, so that byte 4d + j holds
+ * k = 8d + j in its low nibble and k = 8d + 4 + j in its high nibble (a
+ * permutation inside each 4-byte word; K a multiple of 8; w_kil may be
+ * w_packed itself with ldo == ldw, else the two must not overlap).  The
+ * W4A8 kernels then expand 8 weights with 3 instructions instead of 5.
+ * ic_gemm_w4a8_kil_ex is ic_gemm_w4a8_ex on such weights: same arguments,
+ * routes and results, bit for bit.
+ */
+int ic_int4_interleave_k(const uint8_t* w_packed, int64_t N, int64_t K, int64_t ldw, uint8_t* w_kil, int64_t ldo,
+                         void* stream);
+int ic_gemm_w4a8_kil_ex(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_kil, int64_t N,
+                        int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a, const void* bias,
+                        int bias_dtype, int activation, const void* residual, int residual_dtype, int64_t ldr,
+                        void* out, int out_dtype, int64_t ldo, void* workspace, int64_t workspace_bytes,
+                        void* stream);
 
 /*
  * Chained MLP epilogue: the up-projection GEMM of an MLP, finished as the

@@ -53,6 +53,10 @@ def test_version_and_limits(rt):
     lambda L: L.ic_gemm_w4a8(None, 1, 100, 100, None, 4, 50, None, 3, None, None, 0, None, 0, 4, None),
     # w4a16 with f32 activations
     lambda L: L.ic_gemm_w4a16(None, 2, 1, 64, 64, None, 4, 32, None, 1, None, 0, None, 4, None),
+    # K-interleaved INT4: K not a multiple of 8
+    lambda L: L.ic_int4_interleave_k(None, 4, 12, 6, None, 6, None),
+    lambda L: L.ic_gemm_w4a8_kil_ex(None, 1, 100, 100, None, 4, 50, None, 1, None, None, 0, 0, None, 0, 0, None, 0,
+                                    4, None, 0, None),
 ])
 def test_argument_validation(rt, call):
     lib = rt.lib()
