@@ -113,6 +113,9 @@ def _parse():
                     help="launch eagerly instead of replaying a captured graph (for counter collection)")
     ap.add_argument("--no-step", action="store_true",
                     help="skip the denoise-step times the default (c3) line carries")
+    ap.add_argument("--w4-order", default="kil", choices=["kil", "plain"],
+                    help="packed INT4 nibble order the W4A8 GEMMs read: K-interleaved (rewritten once per "
+                         "weight, as the drop-in Linear does) or the checkpoint's")
     return ap.parse_args()
 
 
@@ -191,7 +194,7 @@ def _time_loop(fn, n):
     return s.elapsed_time(e) / n
 
 
-def gpu_bench(cfg, inp, steps, warmup, rt):
+def gpu_bench(cfg, inp, steps, warmup, rt, w4_order="kil"):
     import torch
 
     dev = torch.device("cuda:0")
@@ -203,6 +206,9 @@ def gpu_bench(cfg, inp, steps, warmup, rt):
     copies = max(2, min(64, math.ceil(640e6 / per_copy)))
     xs = [inp["x"].to(dev) for _ in range(copies)]
     ws = [inp["w"].to(dev) for _ in range(copies)]
+    kil = cfg["fmt"] == "int4" and w4_order == "kil"
+    if kil:  # the per-layer rewrite the drop-in Linear does once, outside the timed steps
+        ws = [rt.int4_interleave_k(w) for w in ws]
     s_w = inp["s_w"].to(dev)
     sr = rt.prepare_factors(inp["smoothrot"].to(dev), act) if inp["smoothrot"] is not None else None
     perm = rt.prepare_perm(inp["perm"].to(dev), K) if inp["perm"] is not None else None
@@ -221,7 +227,7 @@ def gpu_bench(cfg, inp, steps, warmup, rt):
         elif cfg["fmt"] == "int8":
             rt.fused_int8_gemm_dequant(q, w, s_w, s_a, out_dtype=act, out=out)
         else:
-            rt.gemm_w4a8(q, w, s_w, s_a, out_dtype=act, out=out)
+            rt.gemm_w4a8(q, w, s_w, s_a, out_dtype=act, out=out, kil=kil)
 
     def step(i):
         if cfg["fmt"] != "w4a16":
@@ -603,7 +609,7 @@ def set_main(args, rt):
     for key in st["members"]:
         cfg = CONFIGS[key]
         inp = make_inputs(cfg)
-        s_ms, _wall, g_ms, p_ms, copies = gpu_bench(cfg, inp, args.steps, args.warmup, rt)
+        s_ms, _wall, g_ms, p_ms, copies = gpu_bench(cfg, inp, args.steps, args.warmup, rt, args.w4_order)
         ops, _gb, _pb = algorithmic(cfg)
         tot_ops += ops
         step_ms += s_ms
@@ -841,7 +847,7 @@ def main():
         b.copy_(a)
         torch.cuda.synchronize()
         del a, b
-    step_ms, wall, g_ms, p_ms, copies = gpu_bench(cfg, inp, args.steps, args.warmup, rt)
+    step_ms, wall, g_ms, p_ms, copies = gpu_bench(cfg, inp, args.steps, args.warmup, rt, args.w4_order)
     M, K, N = cfg["M"], cfg["K"], cfg["N"]
     ops, gemv_bytes, prep_bytes = algorithmic(cfg)
     is_fp = cfg["fmt"] == "w4a16"
@@ -867,7 +873,8 @@ def main():
         "config": {"workload": cfg["name"], "M": M, "K_in": cfg.get("K_in", K), "K": K, "N": N,
                    "group_size": K // cfg["G"],
                    "rot_size": cfg["rot"], "smoothrot": cfg["smoothrot"], "perm": cfg["perm"],
-                   "activation": cfg["act"], "input_copies": copies, "parallelism": "single GPU"},
+                   "activation": cfg["act"], "input_copies": copies, "parallelism": "single GPU",
+                   **({"w4_order": args.w4_order} if cfg["fmt"] == "int4" else {})},
         "roofline": roof,
         "host_wall_ms_per_step": round(wall * 1e3 / args.steps, 5),
     }

@@ -51,14 +51,17 @@ BLOCK_LINEARS = (("qkv", HID, 3 * HID), ("proj", HID, HID), ("mlp_up", HID, MLP)
 
 
 class QLinear:
-    """One INT4 W4A8 linear: packed codes [N, K/2], fp32 group scales
-    [N, K/128], bf16 bias, prepared SmoothRot factors and permutation."""
+    """One INT4 W4A8 linear: packed codes [N, K/2] (w, the checkpoint's nibble
+    order, and wk, the K-interleaved copy the GEMM reads, as the drop-in
+    Linear keeps it), fp32 group scales [N, K/128], bf16 bias, prepared
+    SmoothRot factors and permutation."""
 
     def __init__(self, rt, K, N, gen, dev, act, rotated=True):
         import torch
 
         self.K, self.N = K, N
         self.w = torch.randint(0, 256, (N, K // 2), generator=gen, device=dev, dtype=torch.uint8)
+        self.wk = rt.int4_interleave_k(self.w) if rotated else None
         s = torch.rand(N, K // GROUP, generator=gen, device=dev) * (2e-2 - 1e-3) + 1e-3
         self.s_w = s.to(torch.float16).float().contiguous()
         self.b = (torch.randn(N, generator=gen, device=dev) * 0.02).to(act)
@@ -82,7 +85,7 @@ class QLinear:
         return self.gemm(rt, q, s_a, x.dtype, activation=activation)
 
     def gemm(self, rt, q, s_a, act, out=None, activation=0, residual=None):
-        return rt.gemm_w4a8(q, self.w, self.s_w, s_a, bias=self.b, out_dtype=act, out=out,
+        return rt.gemm_w4a8(q, self.wk, self.s_w, s_a, bias=self.b, out_dtype=act, out=out, kil=True,
                             activation=activation, residual=residual)
 
     def __call__(self, rt, x, residual=None):
