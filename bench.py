@@ -535,6 +535,32 @@ def measure_peaks():
     c0, c1, w0, w1 = clk.tolist()
     wall_khz = lib.bp_wall_clock_khz()
     sclk_mhz = (c1 - c0) / (w1 - w0) * wall_khz / 1e3 if w1 > w0 and wall_khz > 0 else None
+    # L2 / Infinity Cache -> LDS by global_load_lds_dwordx4, the GEMMs' operand path
+    lib.bp_lds_delivery.argtypes = [ctypes.c_void_p, ctypes.c_longlong, ctypes.c_int, ctypes.c_void_p,
+                                    ctypes.c_void_p]
+    lib.bp_lds_delivery.restype = ctypes.c_int
+    lib.bp_lds_delivery_bytes.argtypes = [ctypes.c_int]
+    lib.bp_lds_delivery_bytes.restype = ctypes.c_double
+    sink = torch.empty(lib.bp_grid() // 2, dtype=torch.int32, device="cuda:0")
+    deliv = {}
+    for name, size in (("l2", 2 << 20), ("infinity_cache", 64 << 20)):
+        buf = torch.ones(size, dtype=torch.uint8, device="cuda:0")
+        d_iters = 400
+        run = lambda: lib.bp_lds_delivery(ctypes.c_void_p(buf.data_ptr()), size, d_iters,
+                                          ctypes.c_void_p(sink.data_ptr()), stream)
+        for _ in range(2):
+            if run() != 0:
+                raise RuntimeError("LDS delivery probe launch failed")
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(3):
+            run()
+        e.record()
+        e.synchronize()
+        deliv[name] = 3 * lib.bp_lds_delivery_bytes(d_iters) / (s.elapsed_time(e) * 1e-3)
+        del buf
+    cus = lib.bp_grid() // 2
     a = torch.empty(1 << 30, dtype=torch.uint8, device="cuda:0")
     b = torch.empty_like(a)
     b.copy_(a)
@@ -549,13 +575,18 @@ def measure_peaks():
     hbm = 5 * 2 * a.numel() / (s.elapsed_time(e) * 1e-3) / 1e9
     del a, b
     return {"int8_tops": round(rates[0], 1), "fp16_tflops": round(rates[1], 1), "hbm_copy_gbps": round(hbm, 1),
+            "lds_delivery_tbps": {k: round(v / 1e12, 2) for k, v in deliv.items()},
+            "lds_delivery_bytes_per_clk_cu": ({k: round(v / cus / (sclk_mhz * 1e6), 1) for k, v in deliv.items()}
+                                              if sclk_mhz else None),
             "sclk_mhz": round(sclk_mhz) if sclk_mhz else None,
             "int8_peak_at_sclk_tops": round(PEAK_INT8_TOPS * sclk_mhz / PEAK_SCLK_MHZ, 1) if sclk_mhz else None,
             "method": "register-only MFMA loops (v_mfma_i32_32x32x32_i8, v_mfma_f32_32x32x16_f16), "
                       "2 workgroups of 4 waves per CU, 4 independent accumulator chains per wave; "
                       "sclk: shader-clock ticks over wall-clock ticks across one wave's INT8 loop; "
                       f"int8_peak_at_sclk: the published peak scaled by sclk / {PEAK_SCLK_MHZ} MHz; "
-                      "HBM: 1 GiB device copy, read + write bytes"}
+                      "HBM: 1 GiB device copy, read + write bytes; LDS delivery: global_load_lds_dwordx4 "
+                      "into LDS, 56 KB stages per CU with two in flight, from a 2 MB (L2-resident) and a "
+                      "64 MB (Infinity Cache) buffer"}
 
 
 def vendor_reference(cfg, reps=20):

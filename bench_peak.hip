@@ -17,6 +17,15 @@
 // constant-rate wall clock (wall_clock64, bp_wall_clock_khz() ticks per ms)
 // before and after its loop into clk[0..3], so the host can compute the
 // engine clock the MFMA loop actually ran at.
+//
+//   bp_lds_delivery(buf, bytes, iters, sink, stream): the rate at which
+//   global_load_lds_dwordx4 moves data from the memory hierarchy into LDS,
+//   the path the GEMMs stage their operands through.  One 512-thread
+//   workgroup per CU; per iteration each wave issues 7 DMAs of 1 KB (a 56 KB
+//   stage per CU, two stages in flight, as in the tiled GEMMs), from 1 KB
+//   blocks of `buf` spread over the buffer.  A buffer that fits the L2
+//   (2 MB) gives the L2-hit rate, one that does not (64 MB) the Infinity
+//   Cache rate.  Bytes moved per launch: bp_lds_delivery_bytes(iters).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -89,6 +98,37 @@ __global__ __launch_bounds__(kThreads) void mfma_f16_loop(int iters, int* __rest
   out[blockIdx.x * kThreads + threadIdx.x] = (int)s;
 }
 
+constexpr int kDmaPer = 7;                      // 1 KB DMAs per wave and stage
+constexpr int kDmaStage = 8 * kDmaPer * 1024;   // bytes per workgroup and stage
+
+__global__ __launch_bounds__(512, 1) void lds_delivery(const char* __restrict__ buf, long long nblk, int iters,
+                                                       int* __restrict__ sink) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const unsigned lds0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
+  auto issue = [&](int it) {
+#pragma unroll
+    for (int c = 0; c < kDmaPer; ++c) {
+      const long long blk = ((long long)blockIdx.x * 977 + (long long)it * 56 + wave * kDmaPer + c) % nblk;
+      const char* src = buf + blk * 1024;
+      const unsigned dst = lds0 + (unsigned)((it & 1) * kDmaStage + (wave * kDmaPer + c) * 1024);
+      asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(dst), "v"((unsigned)(lane * 16)),
+                   "s"(src) : "m0");
+    }
+  };
+  issue(0);
+  for (int it = 0; it < iters; ++it) {
+    if (it + 1 < iters) {
+      issue(it + 1);
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPer) : "memory");  // stage it has landed
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) sink[blockIdx.x] = smem[lane];
+}
+
 }  // namespace
 
 extern "C" {
@@ -121,6 +161,20 @@ int bp_mfma_i8(int iters, int* out, long long* clk, void* stream) {
   const int grid = bp_grid();
   if (grid <= 0 || iters <= 0 || out == nullptr) return (int)hipErrorInvalidValue;
   mfma_i8_loop<<<dim3(grid), dim3(kThreads), 0, (hipStream_t)stream>>>(iters, out, clk);
+  return (int)hipGetLastError();
+}
+
+// Bytes one bp_lds_delivery launch of `iters` iterations moves into LDS.
+double bp_lds_delivery_bytes(int iters) { return (double)(bp_grid() / 2) * iters * kDmaStage; }
+
+// sink must hold bp_grid() / 2 ints; bytes >= 1 KB.
+int bp_lds_delivery(const void* buf, long long bytes, int iters, int* sink, void* stream) {
+  const int grid = bp_grid() / 2;
+  if (grid <= 0 || iters <= 0 || buf == nullptr || sink == nullptr || bytes < 1024) return (int)hipErrorInvalidValue;
+  const int shm = 2 * kDmaStage;
+  hipError_t e = hipFuncSetAttribute((const void*)lds_delivery, hipFuncAttributeMaxDynamicSharedMemorySize, shm);
+  if (e != hipSuccess) return (int)e;
+  lds_delivery<<<dim3(grid), dim3(512), shm, (hipStream_t)stream>>>((const char*)buf, bytes / 1024, iters, sink);
   return (int)hipGetLastError();
 }
 
