@@ -173,18 +173,22 @@ class _DeviceState:
                 ones = torch.ones(self.k_gemm - K_w, device=device, dtype=sm.dtype)
                 self.smooth_gemm = _rt.prepare_factors(torch.cat([sm.to(device), ones]), dtype)
 
-    def gemm_weights(self, qdata: torch.Tensor, scale: torch.Tensor,
-                     kil: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    def gemm_weights(self, qdata: torch.Tensor, scale: torch.Tensor, kil: bool = False,
+                     cache: bool = True) -> tuple[torch.Tensor, torch.Tensor]:
         """(weights, scales) at k_gemm columns; the layer's own when no pad
         is needed.  kil (packed INT4, k_gemm a multiple of 8): the weights in
-        the K-interleaved nibble order, for gemm_w4a8(..., kil=True)."""
+        the K-interleaved nibble order, for gemm_w4a8(..., kil=True).
+        cache: keep the derived copy for the next call, keyed by the tensors'
+        addresses -- only for the layer's resident weights; a per-call cast
+        copy (offloaded or patched weights) may reuse an address with other
+        contents, so its derived copy is built for that call alone."""
         kil = kil and self.k_gemm % 8 == 0
         if self.k_gemm == self.k_w and not kil:
             return qdata, scale
         N = qdata.shape[0]
         int4 = qdata.dtype == torch.uint8
         key = (qdata.data_ptr(), scale.data_ptr(), kil)
-        if self._wpad is None or self._wpad[0] != key:
+        if not cache or self._wpad is None or self._wpad[0] != key:
             wq, sc = qdata, scale
             if self.k_gemm != self.k_w:
                 cols = (self.k_gemm // 2 if int4 else self.k_gemm) - qdata.shape[1]
@@ -196,6 +200,8 @@ class _DeviceState:
                 sc = sc.reshape(N) if scale.dim() == 1 else sc
             if kil:
                 wq = _rt.int4_interleave_k(wq)  # a new tensor: the layer's weights stay as loaded
+            if not cache:
+                return wq, sc
             self._wpad = (key, wq, sc)
         return self._wpad[1], self._wpad[2]
 
@@ -457,8 +463,10 @@ def make_intcrush_ops(quant_format: str, rot_size: int, use_pytorch: bool = Fals
                 q, s_a = _rt.rotate_quantize(x2, rot_size=R, w_in=st.k_gemm, smoothrot=st.smoothrot,
                                              perm=st.perm_gemm)
                 res, lora = self._fold_linear_residuals(x, x_prep, params, x.dtype, x_prep)
-                kil = _env_flag("INTCRUSH_W4_INTERLEAVE", "1") and st.k_gemm % 8 == 0
-                wq, ws = st.gemm_weights(qdata, params.scale, kil=kil)
+                # resident weights: the cached K-interleaved copy; a per-call cast copy: the checkpoint order
+                own = weight is self.weight
+                kil = own and _env_flag("INTCRUSH_W4_INTERLEAVE", "1") and st.k_gemm % 8 == 0
+                wq, ws = st.gemm_weights(qdata, params.scale, kil=kil, cache=own)
                 out = _rt.gemm_w4a8(q, wq, ws, s_a, bias=bias, out_dtype=x.dtype, residual=res, kil=kil)
                 out = self._apply_residuals(x, out, x_prep=x_prep, folded=True, lora_folded=lora)
                 return self._finish_forward(out, x)
@@ -471,7 +479,7 @@ def make_intcrush_ops(quant_format: str, rot_size: int, use_pytorch: bool = Fals
                 x_prep = _rt.prepare_activation(x2, rot_size=self._kernel_rot(), w_in=st.k_gemm,
                                                 smoothrot=st.smoothrot, perm=st.perm_gemm)
                 b = bias if _env_flag("INTCRUSH_W4A16_BIAS") else None
-                wq, ws = st.gemm_weights(qdata, params.scale)
+                wq, ws = st.gemm_weights(qdata, params.scale, cache=weight is self.weight)
                 out = _rt.gemm_w4a16(x_prep, wq, ws, bias=b)
                 if params.zp is not None:
                     self._zp_correction(out, x_prep, params.scale, params.zp)
@@ -516,7 +524,7 @@ def make_intcrush_ops(quant_format: str, rot_size: int, use_pytorch: bool = Fals
                 if zp is not None or fused:
                     x_prep = _rt.prepare_activation(x2, rot_size=R, w_in=st.k_gemm, smoothrot=st.smoothrot,
                                                     perm=st.perm_gemm, smooth=st.smooth_gemm)
-                wq, ws = st.gemm_weights(qdata, params.scale)
+                wq, ws = st.gemm_weights(qdata, params.scale, cache=weight is self.weight)
                 if fused:
                     out = _rt.fused_quant_int8_gemm_dequant(x_prep, wq, ws, bias=bias, out_dtype=compute_dtype)
                     if zp is not None:

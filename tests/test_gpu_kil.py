@@ -96,3 +96,38 @@ def test_dropin_linear_uses_the_interleaved_copy(dev, monkeypatch):
     assert st._wpad is not None and st._wpad[0][2] is True
     assert st._wpad[1].data_ptr() != lin.weight._qdata.data_ptr()
     assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("K,G", [(1024, 8), (64, 2)])
+def test_cast_weights_are_not_cached(dev, monkeypatch, K, G):
+    """Weights that reach forward as a per-call cast copy (ComfyUI's offload or
+    weight-patch path) are not cached by address -- a later copy may reuse the
+    address with other contents: W4A8 runs them in the checkpoint order, and a
+    narrow layer's zero-padded operands are built for that call.  Outputs equal
+    the resident weights', and the resident cache is left as it was."""
+    import comfy.quant_ops as qo
+
+    ops_mod = __graft_entry__._submodule("_ops")
+    from test_gpu_ops import _to_dev, _x
+
+    N = 192
+    ops = ops_mod.make_intcrush_ops("int4_crush", 64)
+    sd = int4_layer(N, K, G=G, seed=150 + K)
+    lin = _to_dev(load_linear(ops, "double_blocks.0.img_mlp.2", sd, K, N), dev)
+    x = _x(300, K, torch.bfloat16, 151).to(dev)
+    ref = lin(x).clone()
+    st = lin._intcrush_state(x)
+    cached = st._wpad
+    assert cached is not None and cached[0][2] is True
+
+    def cast_copy(s, input=None, dtype=None, device=None, bias_dtype=None, offloadable=False):
+        w = s.weight
+        w2 = qo.QuantizedTensor(w._qdata.clone(), w._layout_type, w._params)
+        return (w2, s.bias, None) if offloadable else (w2, s.bias)
+
+    monkeypatch.setattr(ops_mod, "_cast_fns", (cast_copy, lambda *a: None))
+    monkeypatch.setattr(lin, "comfy_cast_weights", True, raising=False)
+    for _ in range(2):
+        out = lin(x)
+        assert torch.equal(out, ref)
+    assert lin._intcrush_state(x)._wpad is cached
