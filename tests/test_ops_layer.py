@@ -339,3 +339,28 @@ def test_checkpoint_save_rejects_bad_input(tmp_path):
     save_file({"a": torch.zeros(2)}, p)
     _, info = ckpt.load_checkpoint(p)
     assert (info.fmt, info.rot_size, info.padded_layers) == (None, None, {})
+
+
+@pytest.mark.parametrize("K_w,G,zp,svd,expect", [
+    (3072, 24, False, False, 3072),  # already a multiple of 128
+    (64, 1, False, False, 128),      # Flux img_in: per-row scales
+    (96, 3, False, False, 128),      # groups of 32: lcm(128, 32) = 128
+    (320, 10, False, False, 384),
+    (192, 2, False, False, 384),     # groups of 96: lcm(128, 96) = 384
+    (100, 1, False, False, 128),
+    (80, 5, False, False, 80),       # groups of 16: no MFMA width holds them
+    (64, 1, True, False, 64),        # zero point: corrections over the prepared width
+    (64, 1, False, True, 64),        # SVD residual: the same
+])
+def test_gemm_width_of_narrow_layers(K_w, G, zp, svd, expect):
+    """The width the drop-in Linear runs the GEMMs at: K_w, or for widths that
+    are not a multiple of 128 the next multiple of lcm(128, group size)."""
+    from types import SimpleNamespace
+
+    ops_mod = __graft_entry__._submodule("_ops")
+    N = 8
+    scale = torch.ones(N, G) if G > 1 else torch.ones(N)
+    params = SimpleNamespace(scale=scale, zp=torch.zeros(N) if zp else None)
+    layer = SimpleNamespace(_intcrush_w_in=K_w, weight=SimpleNamespace(_params=params),
+                            _intcrush_L1=torch.zeros(4, K_w) if svd else None)
+    assert ops_mod._gemm_width(layer) == expect
