@@ -55,8 +55,9 @@ IC_DEV v4u quant16(const float* v, float s, float r) {
 // 12288, or any width for plain rows); wider rows with factors or a perm keep
 // one.
 // Workgroup sums of two fp64 values (TH/64 waves; red holds 2 * TH/64
-// doubles).  The caller's barrier at the top of the row guarantees red is no
-// longer being read, so one barrier suffices.
+// doubles).  The caller guarantees red is no longer being read (a barrier at
+// the top of the row, or a copy of red per row parity), so one barrier
+// suffices.
 template <int TH>
 IC_DEV void block_sum2_f64(double& a, double& b, double* red) {
 #pragma unroll
@@ -113,9 +114,23 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
   // its own wave wrote, and the workgroup needs no row-sized buffer (the
   // Wan FFN-down rows fit two workgroups per CU instead of one).
   constexpr bool WLR = VAR == kRqPlain && XCH && LOG4R <= 5 && NT <= 2;
-  __shared__ __attribute__((aligned(16))) u16 rowbuf[WLR ? 8 : rowbuf_len<NT, kTile>()];
-  __shared__ float red[TH / 64];
-  __shared__ double red_d[NORM != 0 ? 2 * (TH / 64) : 1];
+  // DBR: the row buffer and the reduction slots alternate between two copies
+  // by row parity, so no barrier is needed at the top of a row: a wave that
+  // writes row r + 2's copy has passed row r + 1's abs-max barrier, which no
+  // wave reaches before it has finished reading row r's.  For rotations that
+  // stay inside each wave (R <= 1024), where the second row buffer leaves the
+  // workgroups the LDS admits per CU unchanged (WLR kernels have none).
+  constexpr int kRowLen = WLR ? 8 : rowbuf_len<NT, kTile>();
+  constexpr int kXbufBytes = XCH ? 8 * xbuf_doubles<kTile>() : 16;
+  constexpr int kWgCap = 1024 / TH;  // ~16 waves per CU at these kernels' register counts
+  constexpr int kLds1 = kXbufBytes + 2 * kRowLen + 4096, kLds2 = kLds1 + 2 * kRowLen;
+  constexpr int kOcc1 = 163840 / kLds1 < kWgCap ? 163840 / kLds1 : kWgCap;
+  constexpr int kOcc2 = 163840 / kLds2 < kWgCap ? 163840 / kLds2 : kWgCap;
+  constexpr bool DBR = LOG4R <= 5 && (WLR || (kOcc2 >= 1 && kOcc2 >= kOcc1));
+  constexpr int NB = DBR ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) u16 rowbuf_all[(DBR && !WLR) ? 2 : 1][kRowLen];
+  __shared__ float red_all[NB][TH / 64];
+  __shared__ double red_d_all[NB][NORM != 0 ? 2 * (TH / 64) : 1];
   __shared__ uint32_t xred[DT == IC_DTYPE_BF16 && LOG4R == 6 ? 2 * (TH / 64) : 1];
 
   constexpr bool PLAIN = VAR == kRqPlain;
@@ -230,10 +245,14 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
     }
   }
   bool first_row = true;
+  int parity = 0;
 
-  for (; row < M; row += gridDim.x) {
+  for (; row < M; row += gridDim.x, parity ^= (DBR ? 1 : 0)) {
     const int next = row + gridDim.x;
-    __syncthreads();  // the previous row's gather is done with rowbuf and red
+    u16* const rowbuf = rowbuf_all[WLR ? 0 : parity];
+    float* const red = red_all[parity];
+    double* const red_d = red_d_all[parity];
+    if constexpr (!DBR) __syncthreads();  // the previous row's gather is done with rowbuf and red
     // Wave priority ramps down over the row (3 after the barrier, 2 in the
     // rotation, 1 in the rounding, 0 from the row scale on).  The SIMDs
     // otherwise issue oldest-wave-first, so each SIMD's youngest wave finished
