@@ -114,6 +114,10 @@ template <int RC> IC_DEV int tile_pos(int t, int j) {
 // groups of a wave use distinct banks.
 IC_DEV int xslot(int p) { return p + 2 * (p >> 4) + 16 * (p >> 8); }
 template <int TILE> constexpr int xbuf_doubles() { return TILE + 2 * (TILE / 16) + 16 * (TILE / 256); }
+// The same buffer without the 16 per 256 (tslot): the fast path's R = 64 /
+// 256 exchange keeps its transposed reads on alternate bank halves instead by
+// letting the odd 16-lane groups read their 16 rows in the order h ^ 8.
+template <int TILE> constexpr int tslot_doubles() { return TILE + 2 * (TILE / 16); }
 IC_DEV int rbaddr(int p) { return p + 16 * (p >> 8); }
 template <int NT, int TILE> constexpr int rowbuf_len() { return NT * TILE + 16 * (NT * TILE / 256); }
 

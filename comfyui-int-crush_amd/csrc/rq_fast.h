@@ -106,7 +106,6 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
   constexpr bool XCH = LOG4R >= 3;
   constexpr int kTile = TH * 16;  // positions per tile
   static_assert(TH == 256 || (TH % 64 == 0 && LOG4R <= 5), "cross-wave rotation needs four waves");
-  __shared__ double xbuf[XCH ? xbuf_doubles<kTile>() : 2];
   // WLR: rows without a perm whose rotation stays inside each wave's 1024
   // positions (R = 64..1024 with the DMA-staged slices, at most two tiles)
   // keep their rounded values in the upper half of the wave's own exchange
@@ -120,13 +119,42 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
   // wave reaches before it has finished reading row r's.  For rotations that
   // stay inside each wave (R <= 1024), where the second row buffer leaves the
   // workgroups the LDS admits per CU unchanged (WLR kernels have none).
+  //
+  // XROT (R = 64 / 256 with a row buffer): the exchange buffer without the
+  // 16 doubles of padding per 256 positions (tslot), where that is what lets
+  // the second row buffer fit and more than one workgroup shares a CU (one
+  // 768-thread workgroup per CU measured slower with it).  The padding put
+  // the four 16-lane groups of a wave 128 bytes apart modulo the 512 bytes of
+  // the LDS banks for the transposed reads.  Without it the groups' blocks
+  // lie 2304 bytes apart (256 mod 512), so groups 0 and 2 (and 1 and 3) would
+  // meet; instead groups 2 and 3 of each wave read their 16 rows in the order
+  // h ^ 8, a further 1152 bytes (128 mod 512) away: the four reads of a row
+  // land at 0, 256, 128 and 384 mod 512.  Those lanes' registers then hold
+  // rows h ^ 8: the radix-4 digit on bits 2-3 maps register a to logical
+  // a ^ 2, and y_i = s/2 - x_(3-i) commutes with that relabeling
+  // (3 - (a ^ 2) = (3 - a) ^ 2), so the butterflies run unchanged and only
+  // the row-buffer stores (and the test of pad positions) use the logical
+  // index j ^ 8.
   constexpr int kRowLen = WLR ? 8 : rowbuf_len<NT, kTile>();
-  constexpr int kXbufBytes = XCH ? 8 * xbuf_doubles<kTile>() : 16;
   constexpr int kWgCap = 1024 / TH;  // ~16 waves per CU at these kernels' register counts
-  constexpr int kLds1 = kXbufBytes + 2 * kRowLen + 4096, kLds2 = kLds1 + 2 * kRowLen;
-  constexpr int kOcc1 = 163840 / kLds1 < kWgCap ? 163840 / kLds1 : kWgCap;
-  constexpr int kOcc2 = 163840 / kLds2 < kWgCap ? 163840 / kLds2 : kWgCap;
-  constexpr bool DBR = LOG4R <= 5 && (WLR || (kOcc2 >= 1 && kOcc2 >= kOcc1));
+  // the reduction slots (NB copies) and 32 bytes of alignment
+  constexpr int kSlots1 = (TH / 64) * 4 + (NORM != 0 ? 2 * (TH / 64) : 1) * 8 +
+                          (DT == IC_DTYPE_BF16 && LOG4R == 6 ? 2 * (TH / 64) : 1) * 4 + 32;
+  constexpr int kSlots2 = kSlots1 + (TH / 64) * 4 + (NORM != 0 ? 2 * (TH / 64) : 1) * 8;
+  // workgroups per CU with one or two row buffers and an exchange buffer of
+  // XB bytes (LDS is allocated in 512-byte granules)
+  constexpr auto occ = [](int xb, int nbuf) {
+    const int lds = (xb + 2 * nbuf * kRowLen + (nbuf == 1 ? kSlots1 : kSlots2) + 511) / 512 * 512;
+    return 163840 / lds < kWgCap ? 163840 / lds : kWgCap;
+  };
+  constexpr auto dbr_fits = [occ](int xb) { return occ(xb, 2) >= 1 && occ(xb, 2) >= occ(xb, 1); };
+  constexpr int kXbPad = XCH ? 8 * xbuf_doubles<kTile>() : 16;
+  constexpr int kXbTight = XCH ? 8 * tslot_doubles<kTile>() : 16;
+  constexpr bool XROT = XCH && (LOG4R == 3 || LOG4R == 4) && !WLR && kWgCap >= 2 && !dbr_fits(kXbPad) &&
+                        dbr_fits(kXbTight);
+  constexpr bool DBR = LOG4R <= 5 && (WLR || dbr_fits(XROT ? kXbTight : kXbPad));
+  __shared__ double xbuf[XCH ? (XROT ? tslot_doubles<kTile>() : xbuf_doubles<kTile>()) : 2];
+  auto xs = [](int p) { return XROT ? tslot(p) : xslot(p); };
   constexpr int NB = DBR ? 2 : 1;
   __shared__ __attribute__((aligned(16))) u16 rowbuf_all[(DBR && !WLR) ? 2 : 1][kRowLen];
   __shared__ float red_all[NB][TH / 64];
@@ -198,7 +226,7 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
   // (first 8 values) and + 1024 (last 8); NT * 2 KB fit the 8 KB slice.
   const int wave_u = __builtin_amdgcn_readfirstlane(t >> 6);
   const int lane = t & 63;
-  char* const slice = (char*)(xbuf + (XCH ? xslot(1024 * wave_u) : 0));
+  char* const slice = (char*)(xbuf + (XCH ? xs(1024 * wave_u) : 0));
   const uint32_t slice_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)slice;
   auto stage_row = [&](int r) {
     const u16* rb = x + (int64_t)r * ldx;
@@ -415,13 +443,21 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
       if constexpr (XCH) {
         // digits 2-3: transpose among 16 lanes of one wave (no workgroup barrier)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) xbuf[xslot(16 * t + j)] = v[j];
+        for (int j = 0; j < 16; ++j) xbuf[xs(16 * t + j)] = v[j];
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         const int g = t >> 4, l = t & 15;
+        if constexpr (XROT) {
+          // row h ^ 8 for groups 2 and 3 of the wave: tslot(256 g + 16 (h ^ 8) + l)
+          const int gp = (g >> 1) & 1;
+          const int r_lo = 288 * g + 144 * gp + l, r_hi = 288 * g - 144 * gp + l;
 #pragma unroll
-        for (int h = 0; h < 16; ++h) v[h] = xbuf[xslot(256 * g + 16 * h + l)];
+          for (int h = 0; h < 16; ++h) v[h] = xbuf[(h < 8 ? r_lo : r_hi) + 18 * h];
+        } else {
+#pragma unroll
+          for (int h = 0; h < 16; ++h) v[h] = xbuf[xslot(256 * g + 16 * h + l)];
+        }
         stage_lo(v);
         if constexpr (LOG4R >= 4) stage_hi(v);
         if constexpr (LOG4R == 5) {
@@ -477,7 +513,8 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
           z[j] = rto24(v[j]);
-          if (base + kTile > K_r && base + tile_pos<(LOG4R == 0 ? 0 : RC)>(t, j) >= K_r) z[j] = 0.0f;
+          const int jl = XROT ? (j ^ (8 * ((t >> 5) & 1))) : j;  // logical index of register j
+          if (base + kTile > K_r && base + tile_pos<(LOG4R == 0 ? 0 : RC)>(t, jl) >= K_r) z[j] = 0.0f;
           zmax = __builtin_fmaxf(zmax, __builtin_fabsf(z[j]));
         }
       }
@@ -505,6 +542,21 @@ __global__ __launch_bounds__(TH, (NT <= 3 || VAR == kRqPlain) ? 2 : 1) void rq_f
           const uint32_t lo = pack2_bits16<DT>(z[b], z[4 + b]);
           const uint32_t hi = pack2_bits16<DT>(z[8 + b], z[12 + b]);
           *(v2u*)(rowbuf + rbaddr(base + tile_pos<3>(t, b))) = v2u{lo, hi};
+        }
+      } else if constexpr (XROT) {
+        // registers 2i, 2i + 1 hold logical elements (2i) ^ 8g', (2i + 1) ^ 8g'
+        // (g' = 1 in groups 2 and 3 of the wave), i.e. 128 positions further
+        // (i < 4) or back (i >= 4) there; all inside the lane's 256-position block
+        static_assert(RC == 1, "XROT stores");
+        const int gp = (t >> 5) & 1;
+        u16* const rl = rowbuf + rbaddr(base + tile_pos<1>(t, 0)) + 128 * gp;
+        u16* const rh = rowbuf + rbaddr(base + tile_pos<1>(t, 0)) - 128 * gp;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t w = pack2_bits16<DT>(z[2 * i], z[2 * i + 1]);
+          u16* const r = i < 4 ? rl : rh;
+          r[32 * i] = (u16)w;
+          r[32 * i + 16] = (u16)(w >> 16);
         }
       } else {
         // pairs rounded by one packed conversion, stored as two 16-bit halves
