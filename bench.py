@@ -113,9 +113,14 @@ def _parse():
                     help="launch eagerly instead of replaying a captured graph (for counter collection)")
     ap.add_argument("--no-step", action="store_true",
                     help="skip the denoise-step times the default (c3) line carries")
-    ap.add_argument("--w4-order", default="kil", choices=["kil", "plain"],
-                    help="packed INT4 nibble order the W4A8 GEMMs read: K-interleaved (rewritten once per "
-                         "weight, as the drop-in Linear does) or the checkpoint's")
+    ap.add_argument("--w4-order", default="kil", choices=["kil", "plain", "unpacked"],
+                    help="INT4 weight form the W4A8 GEMMs read: packed in the K-interleaved order (rewritten "
+                         "once per weight, as the drop-in Linear does), packed in the checkpoint's order, or "
+                         "unpacked to int8 (what the drop-in Linear uses for launches that fill at most half "
+                         "the CUs)")
+    ap.add_argument("--rows", type=int, default=None,
+                    help="override the config's M (GEMM configs; the line then names the override and "
+                         "carries no committed traffic figure)")
     return ap.parse_args()
 
 
@@ -207,8 +212,11 @@ def gpu_bench(cfg, inp, steps, warmup, rt, w4_order="kil"):
     xs = [inp["x"].to(dev) for _ in range(copies)]
     ws = [inp["w"].to(dev) for _ in range(copies)]
     kil = cfg["fmt"] == "int4" and w4_order == "kil"
+    unpacked = cfg["fmt"] == "int4" and w4_order == "unpacked"
     if kil:  # the per-layer rewrite the drop-in Linear does once, outside the timed steps
         ws = [rt.int4_interleave_k(w) for w in ws]
+    elif unpacked:
+        ws = [rt.unpack_int4_to_int8(w, K) for w in ws]
     s_w = inp["s_w"].to(dev)
     sr = rt.prepare_factors(inp["smoothrot"].to(dev), act) if inp["smoothrot"] is not None else None
     perm = rt.prepare_perm(inp["perm"].to(dev), K) if inp["perm"] is not None else None
@@ -226,6 +234,8 @@ def gpu_bench(cfg, inp, steps, warmup, rt, w4_order="kil"):
             rt.gemm_w4a16(xs[i % copies], w, s_w, out=out)
         elif cfg["fmt"] == "int8":
             rt.fused_int8_gemm_dequant(q, w, s_w, s_a, out_dtype=act, out=out)
+        elif unpacked:
+            rt.gemm_w4a8_unpacked(q, w, s_w, s_a, out_dtype=act, out=out)
         else:
             rt.gemm_w4a8(q, w, s_w, s_a, out_dtype=act, out=out, kil=kil)
 
@@ -871,6 +881,8 @@ def main():
         f6_main(args, rt)
         return
     cfg = CONFIGS[args.config]
+    if args.rows is not None:
+        cfg = dict(cfg, M=int(args.rows), name=f"{cfg['name']} (M overridden to {int(args.rows)})")
     inp = make_inputs(cfg)
     if args.calib_copy:
         a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda:0")
@@ -888,14 +900,15 @@ def main():
         achieved = gemv_bytes / (g_ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "kernel": kname, "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS,
                 "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4), "kernel_ms": round(g_ms, 5),
-                "algorithmic_bytes_per_launch": gemv_bytes, "traffic": traffic_for(args.config)}
+                "algorithmic_bytes_per_launch": gemv_bytes,
+                "traffic": traffic_for(args.config) if args.rows is None else None}
     else:
         peak = PEAK_FP16_TFLOPS if is_fp else PEAK_INT8_TOPS
         achieved = ops / (g_ms * 1e-3) / 1e12
         roof = {"bound": "mfma", "kernel": kname, "achieved": round(achieved, 2), "peak": peak,
                 "unit": "TFLOP/s" if is_fp else "TOPS", "frac": round(achieved / peak, 4),
                 "kernel_ms": round(g_ms, 5), "algorithmic_ops_per_launch": ops,
-                "traffic": traffic_for(args.config)}
+                "traffic": traffic_for(args.config) if args.rows is None else None}
     line = {
         "metric": METRIC, "value": round(ops / (step_ms * 1e-3) / 1e12, 3), "unit": "TOPS",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(step_ms, 5),

@@ -37,6 +37,7 @@ holds its own weights, so they stream from HBM as in a real step (about
 from __future__ import annotations
 
 import math
+import os
 
 HID, HEADS, HEAD_DIM, MLP = 3072, 24, 128, 12288
 N_DOUBLE, N_SINGLE = 19, 38
@@ -53,7 +54,9 @@ BLOCK_LINEARS = (("qkv", HID, 3 * HID), ("proj", HID, HID), ("mlp_up", HID, MLP)
 class QLinear:
     """One INT4 W4A8 linear: packed codes [N, K/2] (w, the checkpoint's nibble
     order, and wk, the K-interleaved copy the GEMM reads, as the drop-in
-    Linear keeps it), fp32 group scales [N, K/128], bf16 bias, prepared
+    Linear keeps it; w8, the codes unpacked to int8, made at the first launch
+    that fills at most half the CUs, which reads it instead -- the text
+    stream's 512 rows; INTCRUSH_W4_UNPACKED=0 keeps wk), fp32 group scales [N, K/128], bf16 bias, prepared
     SmoothRot factors and permutation."""
 
     def __init__(self, rt, K, N, gen, dev, act, rotated=True):
@@ -62,6 +65,7 @@ class QLinear:
         self.K, self.N = K, N
         self.w = torch.randint(0, 256, (N, K // 2), generator=gen, device=dev, dtype=torch.uint8)
         self.wk = rt.int4_interleave_k(self.w) if rotated else None
+        self.w8 = None
         s = torch.rand(N, K // GROUP, generator=gen, device=dev) * (2e-2 - 1e-3) + 1e-3
         self.s_w = s.to(torch.float16).float().contiguous()
         self.b = (torch.randn(N, generator=gen, device=dev) * 0.02).to(act)
@@ -85,6 +89,12 @@ class QLinear:
         return self.gemm(rt, q, s_a, x.dtype, activation=activation)
 
     def gemm(self, rt, q, s_a, act, out=None, activation=0, residual=None):
+        if (os.environ.get("INTCRUSH_W4_UNPACKED", "1") != "0"
+                and rt.w4a8_unpacked_pays(q.shape[0], self.N, self.K, self.s_w.shape[1], device=q.device)):
+            if self.w8 is None:
+                self.w8 = rt.unpack_int4_to_int8(self.w, self.K)
+            return rt.gemm_w4a8_unpacked(q, self.w8, self.s_w, s_a, bias=self.b, out_dtype=act, out=out,
+                                         activation=activation, residual=residual)
         return rt.gemm_w4a8(q, self.wk, self.s_w, s_a, bias=self.b, out_dtype=act, out=out, kil=True,
                             activation=activation, residual=residual)
 

@@ -82,6 +82,8 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "ic_int4_interleave_k": ([_P, _L, _L, _L, _P, _L, _P], _I),
     "ic_gemm_w4a8_kil_ex": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _P, _I, _I, _P, _I, _L, _P, _I, _L, _P, _L,
                              _P], _I),
+    "ic_gemm_w4a8_unpacked_ex": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _P, _I, _I, _P, _I, _L, _P, _I, _L, _P,
+                                  _L, _P], _I),
     "ic_gemm_w8a8_chain": ([_P, _L, _L, _L, _P, _L, _L, _P, _P, _P, _I, _I, _P, _P, _I, _P, _I, _L, _P], _I),
     "ic_gemm_w4a8_chain": ([_P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _P, _I, _I, _P, _P, _I, _P, _I, _L, _P], _I),
     "ic_gemm_w4a16": ([_P, _I, _L, _L, _L, _P, _L, _L, _P, _L, _P, _I, _P, _L, _P], _I),
@@ -696,6 +698,54 @@ def gemm_w4a8(x_int8: torch.Tensor, w_packed: torch.Tensor, s_w: torch.Tensor, s
               c.stride(0), _ptr(ws), nb, _stream(xq))
     return c
 
+def w4a8_unpacked_pays(M: int, N: int, K: int, G: int, device=None) -> bool:
+    """Whether a W4A8 launch of M x N outputs over K runs faster on weights
+    unpacked to one byte each (gemm_w4a8_unpacked) than on packed INT4: when
+    its 288 x 192 tiles fill at most half the CUs (and the groups are whole
+    128-column blocks, which the unpacked kernels need for their MFMA tiles).  There the L2 serves the doubled
+    weight bytes without contention and the dropped in-loop INT4 expansion
+    shows (measured on MI355X: 512 x 3072 x 3072 23.9 -> 19.2 us, 1024 x 3072
+    x 12288 85 -> 67 us); on a full launch the two are level (C3 175 us each)
+    or the packed form leads (the Wan FFN-down, 2 %)."""
+    if M <= 16 or K % 128 or K % G or (G > 1 and (K // G) % 128):
+        return False  # the GEMV reads the packed weights; other groups have their own fold modes
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    return ((M + 287) // 288) * ((N + 191) // 192) * 2 <= cus
+
+
+def gemm_w4a8_unpacked(x_int8: torch.Tensor, w_int8: torch.Tensor, s_w: torch.Tensor, s_a: torch.Tensor,
+                       bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16,
+                       out: torch.Tensor | None = None, activation: int = 0,
+                       residual: torch.Tensor | None = None) -> torch.Tensor:
+    """gemm_w4a8 on the INT4 weights unpacked to int8 [N, K] (unpack_int4_to_int8;
+    ic_gemm_w4a8_unpacked_ex): the same outputs bit for bit, without the
+    in-loop INT4 expansion and at twice the weight bytes (see
+    w4a8_unpacked_pays).  s_w [N, G] group scales or [N] per-row scales."""
+    assert x_int8.dtype == torch.int8, f"x_int8 must be int8, got {x_int8.dtype}"
+    assert w_int8.dtype == torch.int8, f"w_int8 must be int8, got {w_int8.dtype}"
+    _need_cuda(x_int8, w_int8, s_w, s_a, bias, residual)
+    xq = _rows(x_int8)
+    M, K = xq.shape
+    N = w_int8.shape[0]
+    assert w_int8.shape[1] >= K, f"unpacked weight too narrow for K={K}"
+    w = _rows(w_int8)
+    sw = s_w.detach().reshape(N, -1).to(torch.float32).contiguous()
+    G = sw.shape[1]
+    if K % G:
+        raise ValueError(f"K={K} is not a multiple of the {G} scale groups")
+    sa = s_a.detach().reshape(-1).to(torch.float32).contiguous()
+    bp, bdt, _keep = _bias_args(bias, N)
+    act, rp, rdt, ldr, _rkeep = _epilogue_args(activation, residual, M, N)
+    c = _out_buffer(out, M, N, out_dtype, xq.device)
+    _warn_if_scalar_gemm("gemm_w4a8_unpacked", K, G, xq, w)
+    with torch.cuda.device(xq.device):
+        ws, nb = _splitk_workspace(M, N, K, G, False, xq.device)
+        _call("ic_gemm_w4a8_unpacked_ex", _ptr(xq), M, K, xq.stride(0), _ptr(w), N, w.stride(0), _ptr(sw), G,
+              _ptr(sa), bp, bdt, act, rp, rdt, ldr, _ptr(c), _dt(c.dtype, "out"), c.stride(0), _ptr(ws), nb,
+              _stream(xq))
+    return c
+
 
 def init_device(device=None) -> None:
     """Per-device set-up (ic_init_device) for `device` (default: the current
@@ -1033,7 +1083,7 @@ __all__ = [
     "USE_FUSED_W8A8", "USE_CUDA_GRAPHS", "dynamic_quantize_activation", "fused_int8_gemm_dequant",
     "fused_quant_int8_gemm_dequant", "fused_w4a8_gemm_dequant", "unpack_int4_to_int8",
     "unpack_int4_to_float16", "rotate_quantize", "prepare_activation", "gemm_w4a8", "int4_interleave_k",
-    "gemm_w4a16", "unpack_int4_to_float", "prepare_factors", "prepare_perm", "PreparedFactors", "gemm_acc_i32",
+    "gemm_w4a8_unpacked", "w4a8_unpacked_pays", "gemm_w4a16", "unpack_int4_to_float", "prepare_factors", "prepare_perm", "PreparedFactors", "gemm_acc_i32",
     "gemv", "GEMV_MAX_M", "fused_layernorm_quantize", "fused_rmsnorm_quantize", "fused_softmax_quantize",
     "norm_rotate_quantize", "ACT_NONE", "ACT_SILU", "ACT_GELU", "ACT_GELU_TANH", "int8_gemm_int8out",
     "gemm_chain", "CHAIN_ROT_SIZES", "prep_gemv", "prep_gemv_ok", "PREP_GEMV_MAX_K", "PREP_GEMV_MAX_CODES",

@@ -150,9 +150,11 @@ class _DeviceState:
     groups), for W4A8 layers rewritten once in the K-interleaved nibble order
     that the W4A8 kernels expand with fewer instructions (a second copy of
     the packed weights on the device, N x K/2 bytes per layer;
-    INTCRUSH_W4_INTERLEAVE=0 keeps the checkpoint order)."""
+    INTCRUSH_W4_INTERLEAVE=0 keeps the checkpoint order), and unpacked once
+    to int8 for the W4A8 launches that fill at most half the CUs (N x K bytes
+    per layer that meets such a launch; INTCRUSH_W4_UNPACKED=0 turns it off)."""
 
-    __slots__ = ("smoothrot", "smooth", "perm", "k_w", "k_gemm", "perm_gemm", "smooth_gemm", "_wpad")
+    __slots__ = ("smoothrot", "smooth", "perm", "k_w", "k_gemm", "perm_gemm", "smooth_gemm", "_wcache")
 
     def __init__(self, layer, device: torch.device, dtype: torch.dtype):
         f = layer._intcrush_smoothrot_factors
@@ -164,7 +166,7 @@ class _DeviceState:
         self.perm = _rt.prepare_perm(p.to(device), K_w) if p is not None else None
         self.k_w = K_w
         self.k_gemm = _gemm_width(layer)
-        self.perm_gemm, self.smooth_gemm, self._wpad = self.perm, self.smooth, None
+        self.perm_gemm, self.smooth_gemm, self._wcache = self.perm, self.smooth, {}
         if self.k_gemm != K_w:
             if p is not None:
                 ext = torch.arange(K_w, self.k_gemm, device=device, dtype=p.dtype)
@@ -174,21 +176,26 @@ class _DeviceState:
                 self.smooth_gemm = _rt.prepare_factors(torch.cat([sm.to(device), ones]), dtype)
 
     def gemm_weights(self, qdata: torch.Tensor, scale: torch.Tensor, kil: bool = False,
-                     cache: bool = True) -> tuple[torch.Tensor, torch.Tensor]:
+                     cache: bool = True, unpack: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
         """(weights, scales) at k_gemm columns; the layer's own when no pad
         is needed.  kil (packed INT4, k_gemm a multiple of 8): the weights in
-        the K-interleaved nibble order, for gemm_w4a8(..., kil=True).
-        cache: keep the derived copy for the next call, keyed by the tensors'
-        addresses -- only for the layer's resident weights; a per-call cast
-        copy (offloaded or patched weights) may reuse an address with other
-        contents, so its derived copy is built for that call alone."""
-        kil = kil and self.k_gemm % 8 == 0
-        if self.k_gemm == self.k_w and not kil:
+        the K-interleaved nibble order, for gemm_w4a8(..., kil=True).  unpack
+        (packed INT4): the weights unpacked to int8 [N, k_gemm], for
+        gemm_w4a8_unpacked.  cache: keep the derived copy for the next call
+        (one per form), keyed by the tensors' addresses -- only for the
+        layer's resident weights; a per-call cast copy (offloaded or patched
+        weights) may reuse an address with other contents, so its derived
+        copy is built for that call alone."""
+        int4 = qdata.dtype == torch.uint8
+        unpack = unpack and int4
+        kil = kil and self.k_gemm % 8 == 0 and not unpack
+        if self.k_gemm == self.k_w and not kil and not unpack:
             return qdata, scale
         N = qdata.shape[0]
-        int4 = qdata.dtype == torch.uint8
-        key = (qdata.data_ptr(), scale.data_ptr(), kil)
-        if not cache or self._wpad is None or self._wpad[0] != key:
+        form = "unpacked" if unpack else ("kil" if kil else "padded")
+        key = (qdata.data_ptr(), scale.data_ptr())
+        hit = self._wcache.get(form) if cache else None
+        if hit is None or hit[0] != key:
             wq, sc = qdata, scale
             if self.k_gemm != self.k_w:
                 cols = (self.k_gemm // 2 if int4 else self.k_gemm) - qdata.shape[1]
@@ -198,12 +205,16 @@ class _DeviceState:
                     extra = self.k_gemm // (self.k_w // sc.shape[1]) - sc.shape[1]
                     sc = torch.cat([sc, sc.new_ones(N, extra)], dim=1)
                 sc = sc.reshape(N) if scale.dim() == 1 else sc
+            # new tensors: the layer's weights stay as loaded
             if kil:
-                wq = _rt.int4_interleave_k(wq)  # a new tensor: the layer's weights stay as loaded
+                wq = _rt.int4_interleave_k(wq)
+            elif unpack:
+                wq = _rt.unpack_int4_to_int8(wq, self.k_gemm)
             if not cache:
                 return wq, sc
-            self._wpad = (key, wq, sc)
-        return self._wpad[1], self._wpad[2]
+            hit = (key, wq, sc)
+            self._wcache[form] = hit
+        return hit[1], hit[2]
 
 
 # ── ops factory ───────────────────────────────────────────────────────────
@@ -463,11 +474,21 @@ def make_intcrush_ops(quant_format: str, rot_size: int, use_pytorch: bool = Fals
                 q, s_a = _rt.rotate_quantize(x2, rot_size=R, w_in=st.k_gemm, smoothrot=st.smoothrot,
                                              perm=st.perm_gemm)
                 res, lora = self._fold_linear_residuals(x, x_prep, params, x.dtype, x_prep)
-                # resident weights: the cached K-interleaved copy; a per-call cast copy: the checkpoint order
+                # resident weights: a cached derived copy -- unpacked to int8 for launches that fill
+                # at most half the CUs, else K-interleaved; a per-call cast copy: the checkpoint order
                 own = weight is self.weight
-                kil = own and _env_flag("INTCRUSH_W4_INTERLEAVE", "1") and st.k_gemm % 8 == 0
-                wq, ws = st.gemm_weights(qdata, params.scale, kil=kil, cache=own)
-                out = _rt.gemm_w4a8(q, wq, ws, s_a, bias=bias, out_dtype=x.dtype, residual=res, kil=kil)
+                N = qdata.shape[0]
+                G = params.scale.reshape(N, -1).shape[1]
+                if G > 1:
+                    G = st.k_gemm // (st.k_w // G)  # groups at the GEMM's (padded) width
+                if (own and _env_flag("INTCRUSH_W4_UNPACKED", "1")
+                        and _rt.w4a8_unpacked_pays(q.shape[0], N, st.k_gemm, G, device=q.device)):
+                    wq, ws = st.gemm_weights(qdata, params.scale, unpack=True)
+                    out = _rt.gemm_w4a8_unpacked(q, wq, ws, s_a, bias=bias, out_dtype=x.dtype, residual=res)
+                else:
+                    kil = own and _env_flag("INTCRUSH_W4_INTERLEAVE", "1") and st.k_gemm % 8 == 0
+                    wq, ws = st.gemm_weights(qdata, params.scale, kil=kil, cache=own)
+                    out = _rt.gemm_w4a8(q, wq, ws, s_a, bias=bias, out_dtype=x.dtype, residual=res, kil=kil)
                 out = self._apply_residuals(x, out, x_prep=x_prep, folded=True, lora_folded=lora)
                 return self._finish_forward(out, x)
 

@@ -897,7 +897,7 @@ hipError_t launch_big_t(const GemmArgs& g, hipStream_t st) {
 }
 template <int OUT_DT, bool EPI, int MODE, bool KIL = false>
 hipError_t launch_big(const GemmArgs& g, hipStream_t st) {
-  if constexpr (!KIL && MODE != big::ROW8) {
+  if constexpr (!KIL && MODE != big::ROW8 && MODE != big::G128I8) {
     if (g.kil) return ic_launch_big_kil(g, OUT_DT, EPI, MODE, st);
   }
   switch (big_rows(g)) {
@@ -910,8 +910,9 @@ hipError_t launch_big(const GemmArgs& g, hipStream_t st) {
 template <bool INT4, int GS, int OUT_DT, bool ACC, bool EPI>
 hipError_t pick_tile(const GemmArgs& g, hipStream_t st) {
   const TileShape t = tile_choice(g, GS != 0);
-  if constexpr (INT4 && GS != 0 && !ACC && OUT_DT != IC_DTYPE_F32) {
-    if (big_tile_ok(g)) return launch_big<OUT_DT, EPI, big::G128>(g, st);
+  if constexpr (GS != 0 && !ACC && OUT_DT != IC_DTYPE_F32) {
+    // grouped packed INT4, or grouped int8 weights (INT4 unpacked to bytes)
+    if (big_tile_ok(g)) return launch_big<OUT_DT, EPI, INT4 ? big::G128 : big::G128I8>(g, st);
   }
   if constexpr (GS == 0 && !ACC && OUT_DT != IC_DTYPE_F32) {
     if (big_row_ok(g)) return launch_big<OUT_DT, EPI, INT4 ? big::ROW4 : big::ROW8>(g, st);

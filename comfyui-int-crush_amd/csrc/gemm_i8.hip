@@ -142,6 +142,19 @@ int ic_gemm_w4a8_kil_ex(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, con
                        "ic_gemm_w4a8_kil_ex");
 }
 
+int ic_gemm_w4a8_unpacked_ex(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8_t* w, int64_t N,
+                             int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a, const void* bias,
+                             int bias_dtype, int activation, const void* residual, int residual_dtype, int64_t ldr,
+                             void* out, int out_dtype, int64_t ldo, void* workspace, int64_t workspace_bytes,
+                             void* stream) {
+  const char* who = "ic_gemm_w4a8_unpacked_ex";
+  if (int rc = ic_check_epi(who, activation, residual, residual_dtype, ldr, N)) return rc;
+  const ic_epi epi{activation, residual, residual_dtype, ldr};
+  GemmArgs g{xq, ldx, (const uint8_t*)w, ldw, s_a, s_w, (int)num_groups, bias, bias_dtype, out, out_dtype,
+             ldo, (int)M, (int)N, (int)K, nullptr, false, workspace, workspace_bytes, epi};
+  return run_gemm(g, (hipStream_t)stream, who, false);
+}
+
 int ic_gemm_w4a8_ws(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_packed,
                     int64_t N, int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a,
                     const void* bias, int bias_dtype, void* out, int out_dtype, int64_t ldo,

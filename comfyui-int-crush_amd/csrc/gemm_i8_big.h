@@ -58,8 +58,10 @@ namespace {
 namespace big {
 // Weight modes: grouped INT4 folded per 128-column stage, grouped INT4 folded
 // per 64-column step, per-row INT4, per-row INT8 (no fold: int32 sums across
-// K), grouped INT4 folded per 32-column half step
-enum { G128 = 0, G64 = 1, ROW4 = 2, ROW8 = 3, G32 = 4 };
+// K), grouped INT4 folded per 32-column half step, grouped int8 folded per
+// 128-column stage (INT4 weights unpacked once to one byte each: no
+// expansion in the main loop, twice the weight bytes per stage)
+enum { G128 = 0, G64 = 1, ROW4 = 2, ROW8 = 3, G32 = 4, G128I8 = 5 };
 constexpr int BN = 192, NS = 2;
 constexpr int TNB = 3;                       // 16 x 16 blocks per wave in N
 constexpr int WCOLS = TNB * 16;
@@ -71,8 +73,8 @@ constexpr int EPI_RS = BN + 8;               // 16-bit output staging row stride
 template <int TMB_, int MODE_>
 struct Rows {
   static constexpr int TMB = TMB_, MODE = MODE_;
-  static constexpr bool GROUPED = MODE <= G64 || MODE == G32, F64 = MODE == G64, F32 = MODE == G32;
-  static constexpr bool INT8W = MODE == ROW8;
+  static constexpr bool GROUPED = MODE <= G64 || MODE == G32 || MODE == G128I8, F64 = MODE == G64, F32 = MODE == G32;
+  static constexpr bool INT8W = MODE == ROW8 || MODE == G128I8;
   static constexpr int NSC = F32 ? 4 : (F64 ? 2 : 1);  // scale rows per stage (grouped)
   static constexpr int BM = 32 * TMB, WROWS = 16 * TMB;
   static constexpr int A_BYTES = BM * kBK;
@@ -236,15 +238,16 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
   };
 
   // scales of stage kt for this lane's three columns; the MFMAs sum 16 * q
+  // for packed INT4 (scaled back exactly by 1/16) and q for int8 weights
   auto read_scales = [&](int kt, int h, float* sw) {
     const float* sS = (const float*)(smem + (kt % NS) * SLOT + A_BYTES + B_BYTES + h * S_BYTES);
 #pragma unroll
-    for (int j = 0; j < TNB; ++j) sw[j] = sS[wc * WCOLS + 16 * j + (lane & 15)] * 0.0625f;
+    for (int j = 0; j < TNB; ++j) sw[j] = sS[wc * WCOLS + 16 * j + (lane & 15)] * (INT8W ? 1.0f : 0.0625f);
   };
 
   // The next stage's DMAs, issued from block row i of stage kt.
   auto dma_next = [&](int kt, int i) {
-    if constexpr (INT8W) {
+    if constexpr (INT8W && !GROUPED) {
       // int8 weights: the next stage's weights in block row 0 and its
       // activations in row 1, so that the last DMA has most of the stage
       // to land (spread over rows 0-6 as below: C1 40.1 against 38.4 us,
@@ -472,7 +475,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
   for (int c = 0; c < B_PER; ++c) dma_b(0, c);
   dma_s(0);
 
-  if constexpr (!INT8W) {
+  if constexpr (!INT8W || GROUPED) {
     for (int s = 0; s < KT; ++s) {
       wait_vm<0>();
       lds_barrier();  // stage s resident; every wave is done with stage s-1

@@ -259,6 +259,23 @@ int ic_gemm_w4a8_kil_ex(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, con
                         void* stream);
 
 /*
+ * W4A8 on INT4 weights unpacked to one int8 byte each (w [N, K], row stride
+ * ldw >= K, as ic_unpack_int4_to_int8 writes them), with the group scales
+ * s_w [N, num_groups] of ic_gemm_w4a8_ex: the same arithmetic and results
+ * (per 128-column block an exact int32 sum, folded facc = fma(f32(sum), s_w,
+ * facc) in K order), without the in-loop INT4 expansion, at twice the weight
+ * bytes.  Any int8 weights are accepted.  No reference counterpart: a
+ * derived copy of the checkpoint's packed weights (as the K-interleaved one),
+ * for the large-M W4A8 launches of callers that can hold N * K bytes more per
+ * layer.  M <= 16 runs the tile kernels, not the GEMV.
+ */
+int ic_gemm_w4a8_unpacked_ex(const int8_t* xq, int64_t M, int64_t K, int64_t ldx, const int8_t* w, int64_t N,
+                             int64_t ldw, const float* s_w, int64_t num_groups, const float* s_a, const void* bias,
+                             int bias_dtype, int activation, const void* residual, int residual_dtype, int64_t ldr,
+                             void* out, int out_dtype, int64_t ldo, void* workspace, int64_t workspace_bytes,
+                             void* stream);
+
+/*
  * Chained MLP epilogue: the up-projection GEMM of an MLP, finished as the
  * next linear's prepared activation.  Each output is first what
  * ic_gemm_*_ex computes with this activation and no residual,

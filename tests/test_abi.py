@@ -57,6 +57,11 @@ def test_version_and_limits(rt):
     lambda L: L.ic_int4_interleave_k(None, 4, 12, 6, None, 6, None),
     lambda L: L.ic_gemm_w4a8_kil_ex(None, 1, 100, 100, None, 4, 50, None, 1, None, None, 0, 0, None, 0, 0, None, 0,
                                     4, None, 0, None),
+    # unpacked INT4: K not divisible by groups; weight rows shorter than K
+    lambda L: L.ic_gemm_w4a8_unpacked_ex(None, 1, 100, 100, None, 4, 100, None, 3, None, None, 0, 0, None, 0, 0, None,
+                                         0, 4, None, 0, None),
+    lambda L: L.ic_gemm_w4a8_unpacked_ex(None, 1, 100, 100, None, 4, 50, None, 1, None, None, 0, 0, None, 0, 0, None,
+                                         0, 4, None, 0, None),
 ])
 def test_argument_validation(rt, call):
     lib = rt.lib()

@@ -1,9 +1,11 @@
-"""GPU parity of the K-interleaved INT4 order (ic_int4_interleave_k,
-ic_gemm_w4a8_kil_ex): the repack kernel equals the numpy restatement in
-tests/_w4.py, and W4A8 on interleaved weights equals W4A8 on the checkpoint
-order bit for bit on every route -- the 288 x 192 kernel in each fold mode,
-the 256 x 128 / split-K tiles, the GEMV, the scalar kernel -- with and without
-the activation / residual epilogue, and through the drop-in Linear."""
+"""GPU parity of the derived INT4 weight forms: the K-interleaved order
+(ic_int4_interleave_k, ic_gemm_w4a8_kil_ex) and the weights unpacked to int8
+(ic_unpack_int4_to_int8, ic_gemm_w4a8_unpacked_ex).  The repack kernel equals
+the numpy restatement in tests/_w4.py, and W4A8 on either form equals W4A8 on
+the checkpoint order bit for bit on every route -- the 288 x 192 kernel in
+each fold mode, the 256 x 128 / split-K tiles, the GEMV, the scalar kernel --
+with and without the activation / residual epilogue, and through the drop-in
+Linear."""
 from __future__ import annotations
 
 import numpy as np
@@ -76,6 +78,44 @@ def test_kil_gemm_equals_plain(rt, dev, M, N, K, G, out_dtype, epi):
     assert torch.isfinite(plain.float()).all()
 
 
+@pytest.mark.parametrize("M,N,K,G,out_dtype", ROUTES)
+@pytest.mark.parametrize("epi", [False, True])
+def test_unpacked_gemm_equals_plain(rt, dev, M, N, K, G, out_dtype, epi):
+    """The unpacked form takes the int8-weight kernels: the 288 x 192 kernel's
+    grouped int8 mode, per-row W8A8, the int8 256 x 128 and split-K tiles, the
+    scalar kernel (the tile kernels also at M <= 16); every one folds in the
+    same order as the packed routes."""
+    print(f"[unpacked] M={M} N={N} K={K} G={G} out={out_dtype} epi={epi}", flush=True)
+    g = _gen(M * 5 + N + K + G)
+    q = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8).to(dev)
+    w = _packed(N, K, 5 + K).to(dev)
+    sw = (torch.rand(N, G, generator=g) * 0.02 + 1e-3).to(dev)
+    sa = (torch.rand(M, generator=g) * 0.05 + 1e-3).to(dev)
+    bias = torch.randn(N, generator=g).to(torch.bfloat16).to(dev)
+    kw = {}
+    if epi:
+        kw = dict(activation=rt.ACT_GELU_TANH, residual=torch.randn(M, N, generator=g).to(torch.float16).to(dev))
+    plain = rt.gemm_w4a8(q, w, sw, sa, bias=bias, out_dtype=out_dtype, **kw)
+    w8 = rt.unpack_int4_to_int8(w, K)
+    un = rt.gemm_w4a8_unpacked(q, w8, sw, sa, bias=bias, out_dtype=out_dtype, **kw)
+    assert torch.equal(plain, un)
+    assert torch.isfinite(plain.float()).all()
+
+
+def test_unpacked_rule(rt, dev):
+    """Unpacked weights for launches whose 288 x 192 tiles fill at most half
+    the CUs and whose groups are whole 128-column blocks; never for the GEMV."""
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    assert rt.w4a8_unpacked_pays(512, 3072, 3072, 24, device=dev)
+    assert not rt.w4a8_unpacked_pays(16, 3072, 3072, 24, device=dev)
+    assert not rt.w4a8_unpacked_pays(512, 3072, 3072, 48, device=dev)  # groups of 64
+    assert rt.w4a8_unpacked_pays(512, 3072, 3072, 1, device=dev)
+    tiles_half = cus // 2  # 288-row tiles x 192-column tiles
+    assert rt.w4a8_unpacked_pays(288, 192 * tiles_half, 3072, 24, device=dev)
+    assert not rt.w4a8_unpacked_pays(288, 192 * (tiles_half + 1), 3072, 24, device=dev)
+    assert not rt.w4a8_unpacked_pays(4608, 3072, 12288, 96, device=dev)
+
+
 def test_dropin_linear_uses_the_interleaved_copy(dev, monkeypatch):
     """W4A8 layers keep one interleaved copy of their weights per device; the
     outputs equal those of the checkpoint order (INTCRUSH_W4_INTERLEAVE=0)."""
@@ -87,14 +127,15 @@ def test_dropin_linear_uses_the_interleaved_copy(dev, monkeypatch):
     sd = int4_layer(N, K, G=8, seed=140)
     lin = _to_dev(load_linear(ops, "double_blocks.0.img_mlp.2", sd, K, N), dev)
     x = _x(300, K, torch.bfloat16, 141).to(dev)
+    monkeypatch.setenv("INTCRUSH_W4_UNPACKED", "0")  # this small launch would take the unpacked copy
     monkeypatch.setenv("INTCRUSH_W4_INTERLEAVE", "0")
     ref = lin(x).clone()
-    assert lin._intcrush_state(x)._wpad is None
+    assert "kil" not in lin._intcrush_state(x)._wcache
     monkeypatch.setenv("INTCRUSH_W4_INTERLEAVE", "1")
     out = lin(x)
     st = lin._intcrush_state(x)
-    assert st._wpad is not None and st._wpad[0][2] is True
-    assert st._wpad[1].data_ptr() != lin.weight._qdata.data_ptr()
+    assert "kil" in st._wcache
+    assert st._wcache["kil"][1].data_ptr() != lin.weight._qdata.data_ptr()
     assert torch.equal(out, ref)
 
 
@@ -115,10 +156,11 @@ def test_cast_weights_are_not_cached(dev, monkeypatch, K, G):
     sd = int4_layer(N, K, G=G, seed=150 + K)
     lin = _to_dev(load_linear(ops, "double_blocks.0.img_mlp.2", sd, K, N), dev)
     x = _x(300, K, torch.bfloat16, 151).to(dev)
+    monkeypatch.setenv("INTCRUSH_W4_UNPACKED", "0")
     ref = lin(x).clone()
     st = lin._intcrush_state(x)
-    cached = st._wpad
-    assert cached is not None and cached[0][2] is True
+    cached = dict(st._wcache)
+    assert "kil" in cached
 
     def cast_copy(s, input=None, dtype=None, device=None, bias_dtype=None, offloadable=False):
         w = s.weight
@@ -130,4 +172,30 @@ def test_cast_weights_are_not_cached(dev, monkeypatch, K, G):
     for _ in range(2):
         out = lin(x)
         assert torch.equal(out, ref)
-    assert lin._intcrush_state(x)._wpad is cached
+    now = lin._intcrush_state(x)._wcache
+    assert now.keys() == cached.keys() and all(now[k] is cached[k] for k in cached)
+
+
+def test_dropin_linear_uses_the_unpacked_copy(dev, monkeypatch):
+    """A W4A8 layer called with few rows runs its unpacked int8 copy (kept per
+    device next to the interleaved one, which larger launches use); outputs
+    equal the packed route's bit for bit, with and without a K pad."""
+    ops_mod = __graft_entry__._submodule("_ops")
+    from test_gpu_ops import _to_dev, _x
+
+    for K, N, G, seed in ((1024, 192, 8, 160), (1000, 192, 1, 161)):
+        ops = ops_mod.make_intcrush_ops("int4_crush", 0 if K % 8 else 256)
+        sd = int4_layer(N, K, G=G, seed=seed)
+        lin = _to_dev(load_linear(ops, "double_blocks.0.txt_mlp.2", sd, K, N), dev)
+        x = _x(300, K, torch.bfloat16, seed + 1).to(dev)
+        monkeypatch.setenv("INTCRUSH_W4_UNPACKED", "0")
+        ref = lin(x).clone()
+        st = lin._intcrush_state(x)
+        assert "unpacked" not in st._wcache
+        monkeypatch.setenv("INTCRUSH_W4_UNPACKED", "1")
+        out = lin(x)
+        assert "unpacked" in st._wcache
+        w8 = st._wcache["unpacked"][1]
+        assert w8.dtype == torch.int8 and w8.shape == (N, st.k_gemm)
+        assert torch.equal(out, ref)
+        assert lin(x) is not None and st._wcache["unpacked"][1] is w8  # built once
