@@ -1,6 +1,7 @@
 // INT8-MFMA GEMM on 256/288/320 x 192 output tiles (gfx950), for shapes whose
 // 256 x 128 / 256 x 256 tilings end in a partly filled round of workgroups.
-// Four weight modes share the tile, the DMA ring and the epilogue:
+// The weight modes share the tile, the DMA ring and the epilogue (the W4A16
+// modes, at the enum below, put fp16 MFMAs on the same layout):
 //  * grouped INT4, the arithmetic of gemm_i8_kernel's grouped path
 //    (triton_w4a8_gemm.py:40-108 with the per-group scales of
 //    _quant_utils.py:237-270): per 128-column stage (or 64- or 32-column
@@ -52,6 +53,7 @@
 #pragma once
 #include <type_traits>
 
+#include "dequant4.h"
 #include "gemm_common.h"
 
 namespace {
@@ -60,8 +62,12 @@ namespace big {
 // per 64-column step, per-row INT4, per-row INT8 (no fold: int32 sums across
 // K), grouped INT4 folded per 32-column half step, grouped int8 folded per
 // 128-column stage (INT4 weights unpacked once to one byte each: no
-// expansion in the main loop, twice the weight bytes per stage)
-enum { G128 = 0, G64 = 1, ROW4 = 2, ROW8 = 3, G32 = 4, G128I8 = 5 };
+// expansion in the main loop, twice the weight bytes per stage), and W4A16:
+// 16-bit activations, INT4 weights dequantized in registers to RN_dt(q *
+// RN_dt(s)) and summed in fp32 by v_mfma_f32_16x16x32_{f16,bf16} (64-K
+// stages: the same 128-byte LDS rows and 16-byte fragments as the int8
+// modes), with a two-slot ring (W16) or a three-slot one (W16L, long K)
+enum { G128 = 0, G64 = 1, ROW4 = 2, ROW8 = 3, G32 = 4, G128I8 = 5, W16 = 6, W16L = 7 };
 constexpr int BN = 192, NS = 2;
 constexpr int TNB = 3;                       // 16 x 16 blocks per wave in N
 constexpr int WCOLS = TNB * 16;
@@ -75,6 +81,15 @@ struct Rows {
   static constexpr int TMB = TMB_, MODE = MODE_;
   static constexpr bool GROUPED = MODE <= G64 || MODE == G32 || MODE == G128I8, F64 = MODE == G64, F32 = MODE == G32;
   static constexpr bool INT8W = MODE == ROW8 || MODE == G128I8;
+  static constexpr bool DEQ = MODE == W16 || MODE == W16L;  // W4A16: one scale row per 64-K stage, no fold
+  static constexpr bool SCALED = GROUPED || DEQ;  // the slot holds scale rows
+  static constexpr int KS = DEQ ? 64 : kBK;       // K values per stage
+  // ring slots: W16L keeps two DMA stages in flight in a three-slot ring
+  // (W4A16's stages are short: one barrier, no fold), the other modes one in
+  // two.  Measured on MI355X: 4608 x 3072 x 12288 (one round, 192 stages)
+  // 359 -> 322 us; C2 4608 x 12288 x 3072 (four rounds of 48 stages, each
+  // tile paying the deeper prologue) 310 -> 319 us.
+  static constexpr int NSL = MODE == W16L ? 3 : NS;
   static constexpr int NSC = F32 ? 4 : (F64 ? 2 : 1);  // scale rows per stage (grouped)
   static constexpr int BM = 32 * TMB, WROWS = 16 * TMB;
   static constexpr int A_BYTES = BM * kBK;
@@ -82,21 +97,32 @@ struct Rows {
   static constexpr int A_PER = (A_BLOCKS + 7) / 8;    // blocks per wave
   // weights per stage: packed nibbles (1 KB DMA blocks of 16 rows of 64
   // bytes) or int8 (blocks of 8 rows of 128 bytes, swizzled as the activations)
-  static constexpr int B_BYTES = INT8W ? BN * kBK : BN * kBK / 2;
+  static constexpr int B_BYTES = INT8W ? BN * kBK : BN * KS / 2;
   static constexpr int B_BLOCKS = B_BYTES / 1024;
   static constexpr int B_PER = (B_BLOCKS + 7) / 8;
   // ring slot: activations, weights, then none, one (scale blocks of 128
   // columns), two (of 64) or four (of 32) scale rows
-  static constexpr int SLOT = A_BYTES + B_BYTES + (GROUPED ? NSC * S_BYTES : 0);
+  static constexpr int SLOT = A_BYTES + B_BYTES + (SCALED ? NSC * S_BYTES : 0);
   // staging tile, activation scales, bias and per-row weight scales
   static constexpr size_t epi_bytes = (size_t)BM * EPI_RS * 2 + (size_t)(BM + 2 * BN) * 4;
-  static constexpr size_t lds_bytes = (size_t)NS * SLOT > epi_bytes ? (size_t)NS * SLOT : epi_bytes;
+  static constexpr size_t lds_bytes = (size_t)NSL * SLOT > epi_bytes ? (size_t)NSL * SLOT : epi_bytes;
   // wave priority per block row: 3 3 2 2 1 1 0 0 ...
   static constexpr int prio(int i) { return i < 6 ? 3 - i / 2 : 0; }
   static_assert(SLOT % 16 == 0 && lds_bytes <= 160 * 1024, "LDS layout");
   static_assert(4 * WCOLS == BN, "wave grid");
   static_assert(A_PER + B_PER <= TMB, "one DMA slot per block row");
 };
+
+typedef _Float16 v8h16 __attribute__((ext_vector_type(8)));
+typedef __bf16 v8bf16 __attribute__((ext_vector_type(8)));
+// fp32 += 16-bit A (rows) x 16-bit B (columns) over 32 K, operands as 16 bytes per lane
+template <int DT> IC_DEV v4f mfma16(const v4i& a, const v4i& b, const v4f& c) {
+  if constexpr (DT == IC_DTYPE_F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h16, a), __builtin_bit_cast(v8h16, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf16, a), __builtin_bit_cast(v8bf16, b), c, 0,
+                                                   0, 0);
+}
 }  // namespace big
 
 // F64: groups of 64 columns, or of an odd multiple of 64 (gcd(group, 128)
@@ -125,6 +151,10 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
   constexpr int BM = RT::BM, WROWS = RT::WROWS, A_BYTES = RT::A_BYTES, A_BLOCKS = RT::A_BLOCKS;
   constexpr int A_PER = RT::A_PER, B_BYTES = RT::B_BYTES, B_BLOCKS = RT::B_BLOCKS, B_PER = RT::B_PER;
   constexpr bool GROUPED = RT::GROUPED, F64 = RT::F64, F32 = RT::F32, INT8W = RT::INT8W;
+  constexpr bool DEQ = RT::DEQ, SCALED = RT::SCALED;
+  constexpr int KS = RT::KS;
+  constexpr int NS = RT::NSL;  // ring slots of this mode (hides big::NS)
+  constexpr int LA = NS - 1;   // stages of DMAs in flight ahead of the one computed
   static_assert(OUT_DT != IC_DTYPE_F32, "16-bit outputs only");
   static_assert(!(KIL && INT8W), "the nibble order applies to packed INT4 weights");
   constexpr int SLOT = RT::SLOT;
@@ -142,12 +172,12 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
   // epilogue operands (activation scale of row m0 + tid, bias of column
   // n0 + tid), loaded now so that their latency passes under the main loop
   static_assert(BM <= kNT && BN <= kNT, "one epilogue operand per thread");
-  const float pre_sa = tid < BM ? s_a[min(m0 + tid, M - 1)] : 0.0f;
+  const float pre_sa = !DEQ && tid < BM ? s_a[min(m0 + tid, M - 1)] : 0.0f;
   const float pre_b = tid < BN && bias != nullptr ? ld_any_f32(bias, bias_dt, min(n0 + tid, N - 1)) : 0.0f;
-  const float pre_sw = !GROUPED && tid < BN ? s_w[min(n0 + tid, N - 1)] : 0.0f;
-  const int KT = K / kBK;
+  const float pre_sw = !GROUPED && !DEQ && tid < BN ? s_w[min(n0 + tid, N - 1)] : 0.0f;
+  const int KT = K / KS;
   // scale blocks (of 128, 64 or 32 columns) per group
-  const int bpg = (K / G) / (F32 ? 32 : (F64 ? 64 : kBK));
+  const int bpg = (K / G) / (F32 ? 32 : (F64 || DEQ ? 64 : kBK));
 
   // ---- DMA addressing (rows past M or N re-read the last row; never stored).
   // A (and int8 B) block b: LDS rows 8b + l/8, chunk slot l%8 holding global
@@ -163,6 +193,14 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
     if constexpr (INT8W) {
       const int row = 8 * (wave + 8 * c) + (lane >> 3);
       b_off[c] = (uint32_t)(min(row, N - 1 - n0) * ldb + (((lane & 7) ^ swz(row)) << 4));
+      continue;
+    }
+    if constexpr (DEQ) {
+      // 32 packed bytes per row and 64-K stage: LDS part p of row n holds
+      // global part p ^ bit 3 of n, so the fragment reads (4 bytes at 4c of
+      // one part, 16 rows) cover all 64 banks
+      const int row = 32 * (wave + 8 * c) + (lane >> 1);
+      b_off[c] = (uint32_t)(min(row, N - 1 - n0) * ldb + (((lane & 1) ^ ((row >> 3) & 1)) << 4));
       continue;
     }
     // packed row n (64 bytes) holds its 16-byte part p at part p ^ ((n >> 2) & 3):
@@ -184,10 +222,10 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
   auto dma_b = [&](int kt, int c) {
     const int blk = wave + 8 * c;
     if (blk < B_BLOCKS)
-      dma16(b_off[c], b_base + (int64_t)kt * (INT8W ? kBK : kBK / 2), slot_of(kt) + (uint32_t)(A_BYTES + blk * 1024));
+      dma16(b_off[c], b_base + (int64_t)kt * (INT8W ? kBK : KS / 2), slot_of(kt) + (uint32_t)(A_BYTES + blk * 1024));
   };
   auto dma_s = [&](int kt) {
-    if (GROUPED && wave < S_WAVES) {
+    if (SCALED && wave < S_WAVES) {
       if constexpr (F32) {
 #pragma unroll
         for (int h = 0; h < 4; ++h)
@@ -211,7 +249,22 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
   const uint32_t fr1 = (uint32_t)(fr_n * 64 + 8 * (fr_c & 1) + (((2 + (fr_c >> 1)) ^ ((fr_n >> 2) & 3)) << 4));
   // int8 weights: rows as the activation fragments, 16 bytes per lane
   const uint32_t fq0 = (uint32_t)lds_off(fr_n, fr_c), fq1 = (uint32_t)lds_off(fr_n, 4 + fr_c);
+  // W4A16: the lane's 8 K values of column fr_n per 32-K step are 4 packed
+  // bytes, at 4c of part h (swizzled by bit 3 of the row, which is bit 3 of
+  // the lane), dequantized with the stage's scale of that column
+  const uint32_t fw = (uint32_t)(fr_n * 32 + 4 * fr_c), fsw = (uint32_t)(((lane >> 3) & 1) << 4);
+  DeqScale dsc[TNB];
   auto load_b = [&](int kt, int j, v4i& f0, v4i& f1) {
+    if constexpr (DEQ) {
+      const char* pb = smem + (kt % NS) * SLOT + A_BYTES + j * 16 * 32 + fw;
+      const uint32_t p0 = *(const uint32_t*)(pb + fsw), p1 = *(const uint32_t*)(pb + (16u ^ fsw));
+      uint32_t w0[4], w1[4];
+      deq8<OUT_DT>(p0, dsc[j], w0);
+      deq8<OUT_DT>(p1, dsc[j], w1);
+      f0 = v4i{(int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3]};
+      f1 = v4i{(int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3]};
+      return;
+    }
     if constexpr (INT8W) {
       const char* pb = smem + (kt % NS) * SLOT + A_BYTES + j * 16 * kBK;
       f0 = *(const v4i*)(pb + fq0);
@@ -245,8 +298,9 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
     for (int j = 0; j < TNB; ++j) sw[j] = sS[wc * WCOLS + 16 * j + (lane & 15)] * (INT8W ? 1.0f : 0.0625f);
   };
 
-  // The next stage's DMAs, issued from block row i of stage kt.
-  auto dma_next = [&](int kt, int i) {
+  // The DMAs of stage kn (the next one, or with a three-slot ring the one
+  // after), issued from block row i of the stage being computed.
+  auto dma_next = [&](int kn, int i) {
     if constexpr (INT8W && !GROUPED) {
       // int8 weights: the next stage's weights in block row 0 and its
       // activations in row 1, so that the last DMA has most of the stage
@@ -254,22 +308,22 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
       // 4096 x 3072 x 12288 137-142 against 127-133 us)
       if (i == 0) {
 #pragma unroll
-        for (int c = 0; c < B_PER; ++c) dma_b(kt + 1, c);
+        for (int c = 0; c < B_PER; ++c) dma_b(kn, c);
       } else if (i == 1) {
 #pragma unroll
-        for (int c = 0; c < A_PER; ++c) dma_a(kt + 1, c);
+        for (int c = 0; c < A_PER; ++c) dma_a(kn, c);
       }
     } else {
       // scales first: issued last, their wait at the next stage showed
       // (~180 clocks per stage on the three waves that fetch them)
-      if (i == 0) dma_s(kt + 1);
-      if (i < A_PER) dma_a(kt + 1, i);
-      else if (i < A_PER + B_PER) dma_b(kt + 1, i - A_PER);
+      if (i == 0) dma_s(kn);
+      if (i < A_PER) dma_a(kn, i);
+      else if (i < A_PER + B_PER) dma_b(kn, i - A_PER);
     }
   };
 
   // fp32 running sums (grouped) or int32 sums (per row)
-  using AccT = std::conditional_t<GROUPED, v4f, v4i>;
+  using AccT = std::conditional_t<GROUPED || DEQ, v4f, v4i>;
   AccT facc[TMB][TNB];
 #pragma unroll
   for (int i = 0; i < TMB; ++i)
@@ -286,10 +340,15 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
   // 16 apart share their swizzle, so each operand and K-step needs one LDS
   // address.  The next stage's DMAs are spread over the rows.
   auto mfma_stage = [&](int kt) {
-    const bool more = kt + 1 < KT;  // uniform
+    const bool more = kt + LA < KT;  // uniform
     float sw[TNB], sw1[TNB];
     if constexpr (GROUPED) read_scales(kt, 0, sw);
     if constexpr (F64) read_scales(kt, 1, sw1);
+    if constexpr (DEQ) {
+      const float* sS = (const float*)(smem + (kt % NS) * SLOT + A_BYTES + B_BYTES);
+#pragma unroll
+      for (int j = 0; j < TNB; ++j) dsc[j] = deq_scale<OUT_DT>(sS[wc * WCOLS + 16 * j + (lane & 15)]);
+    }
     const char* aR0 = smem + (kt % NS) * SLOT + lds_off(wr * WROWS + (lane & 15), lane >> 4);
     const char* aR1 = smem + (kt % NS) * SLOT + lds_off(wr * WROWS + (lane & 15), 4 + (lane >> 4));
     v4i b0[TNB], b1[TNB];
@@ -342,13 +401,18 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
           else tc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1[j], tc[j], 0, 0, 0);
         }
         if (i > 0) fold_row(i - 1, t[(i - 1) & 1], t1[F64 ? ((i - 1) & 1) : 0]);
+      } else if constexpr (DEQ) {
+#pragma unroll
+        for (int j = 0; j < TNB; ++j) facc[i][j] = mfma16<OUT_DT>(a0, b0[j], facc[i][j]);
+#pragma unroll
+        for (int j = 0; j < TNB; ++j) facc[i][j] = mfma16<OUT_DT>(a1, b1[j], facc[i][j]);
       } else {
 #pragma unroll
         for (int j = 0; j < TNB; ++j) facc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0[j], facc[i][j], 0, 0, 0);
 #pragma unroll
         for (int j = 0; j < TNB; ++j) facc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1[j], facc[i][j], 0, 0, 0);
       }
-      if (more) dma_next(kt, i);
+      if (more) dma_next(kt + LA, i);
       __builtin_amdgcn_sched_barrier(0);
     }
     fold_row(TMB - 1, t[(TMB - 1) & 1], t1[F64 ? ((TMB - 1) & 1) : 0]);
@@ -418,7 +482,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
 #pragma unroll
       for (int j = 0; j < TNB; ++j) qd[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1h, b1[j], v4i{0, 0, 0, 0}, 0, 0, 0);
       fold2(i, qa, qb, s0, s1);
-      if (more) dma_next(kt, i);
+      if (more) dma_next(kt + 1, i);
       __builtin_amdgcn_sched_barrier(0);
     }
     fold2(TMB - 1, qc, qd, s2, s3);
@@ -461,23 +525,50 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
       n0f = *(const v4i*)(aR0 + (i + 1) * 16 * kBK);
       n1f = *(const v4i*)(aR1 + (i + 1) * 16 * kBK);
       row_mfma(i, a0, a1, b0, b1);
-      if (more) dma_next(kt, i);
+      if (more) dma_next(kt + 1, i);
       __builtin_amdgcn_sched_barrier(0);
     }
     pa0 = n0f;
     pa1 = n1f;
   };
 
-  // ---- prologue: stage 0 in flight
+  // ---- prologue: stages 0 .. LA-1 in flight
+  for (int s0 = 0; s0 < LA && s0 < KT; ++s0) {
 #pragma unroll
-  for (int c = 0; c < A_PER; ++c) dma_a(0, c);
+    for (int c = 0; c < A_PER; ++c) dma_a(s0, c);
 #pragma unroll
-  for (int c = 0; c < B_PER; ++c) dma_b(0, c);
-  dma_s(0);
+    for (int c = 0; c < B_PER; ++c) dma_b(s0, c);
+    dma_s(s0);
+  }
+  // this wave's DMA instructions per stage (wave-uniform): with two stages in
+  // flight, stage s has landed once no more than those of stage s+1 remain
+  // outstanding (they retire in issue order)
+  int per_stage = (SCALED && wave < S_WAVES) ? RT::NSC : 0;
+#pragma unroll
+  for (int c = 0; c < A_PER; ++c) per_stage += wave + 8 * c < A_BLOCKS;
+#pragma unroll
+  for (int c = 0; c < B_PER; ++c) per_stage += wave + 8 * c < B_BLOCKS;
+  auto wait_stage = [&](int s) {
+    if (LA == 1 || s + 1 >= KT) {
+      wait_vm<0>();
+      return;
+    }
+    switch (per_stage) {
+      case 0: wait_vm<0>(); break;
+      case 1: wait_vm<1>(); break;
+      case 2: wait_vm<2>(); break;
+      case 3: wait_vm<3>(); break;
+      case 4: wait_vm<4>(); break;
+      case 5: wait_vm<5>(); break;
+      case 6: wait_vm<6>(); break;
+      case 7: wait_vm<7>(); break;
+      default: wait_vm<0>(); break;
+    }
+  };
 
   if constexpr (!INT8W || GROUPED) {
     for (int s = 0; s < KT; ++s) {
-      wait_vm<0>();
+      wait_stage(s);
       lds_barrier();  // stage s resident; every wave is done with stage s-1
       if constexpr (F32) mfma_stage32(s);
       else mfma_stage(s);
@@ -540,6 +631,8 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
         float v;
         if constexpr (GROUPED) {
           v = facc[i][j][r] * sa_l[ml];
+        } else if constexpr (DEQ) {
+          v = facc[i][j][r];
         } else {
           float a = (float)facc[i][j][r];
           if constexpr (!INT8W) a *= 0.0625f;

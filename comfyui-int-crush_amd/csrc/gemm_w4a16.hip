@@ -2,8 +2,11 @@
 //
 // Replaces unpack_int4_to_float16 (triton_int4_unpack.py:25-88) followed by the
 // cuBLAS F.linear of _forward_int4_w4a16 (_ops.py:466-481): the dequantized
-// weight w[n,k] = RN_dt(q[n,k] * RN_dt(s[n, k/gs])) is produced in LDS and
-// consumed by v_mfma_f32_32x32x16_{f16,bf16}; it is never written to HBM.  For
+// weight w[n,k] = RN_dt(q[n,k] * RN_dt(s[n, k/gs])) is never written to HBM.
+// Shapes with M > 128, groups of whole 64-column blocks and an aligned 16-bit
+// output run gemm_i8_big_kernel's W4A16 mode (weights dequantized in registers,
+// v_mfma_f32_16x16x32); the kernel below covers the rest: the dequantized tile
+// is produced in LDS and consumed by v_mfma_f32_32x32x16_{f16,bf16}.  For
 // fp16 this is bit-identical to the reference unpack (an fp16 product of two
 // fp16 values); the reference rejects bf16 here and its PyTorch fallback
 // rounds q*s to the activation type, which is what bf16 does.  Accumulation is
@@ -25,6 +28,7 @@
 // triton_int4_to_int8_unpack.py:26-81 and triton_int4_unpack.py:25-88.
 #include "dequant4.h"
 #include "gemm_common.h"
+#include "gemm_i8_big.h"
 
 namespace {
 
@@ -306,11 +310,56 @@ hipError_t launch_w4a16(const u16* A, int64_t lda, const uint8_t* B, int64_t ldb
   return hipGetLastError();
 }
 
+// W4A16 on the 256/288/320 x 192 tiles of gemm_i8_big_kernel (its W16 mode):
+// each wave dequantizes its own weight fragments in registers beside its
+// v_mfma_f32_16x16x32 instructions, so no dequantized tile is written to or
+// read back from LDS and a stage has one barrier.
+template <int DT, int TMB, int MODE>
+hipError_t launch_w4a16_big_t(const u16* A, int64_t lda, const uint8_t* B, int64_t ldb, const float* s_w, int G,
+                              const void* bias, int bias_dt, u16* C, int64_t ldc, int M, int N, int K,
+                              hipStream_t st) {
+  using RT = big::Rows<TMB, MODE>;
+  const int tiles = ((M + RT::BM - 1) / RT::BM) * ((N + big::BN - 1) / big::BN);
+  auto kern = gemm_i8_big_kernel<DT, false, MODE, TMB>;
+  constexpr size_t shm = RT::lds_bytes;
+  static unsigned char lds_set[64];  // per device
+  if (hipError_t e = ic_set_lds_limit((const void*)kern, (int)shm, lds_set)) return e;
+  kern<<<dim3(tiles), dim3(kNT), shm, st>>>((const int8_t*)A, lda * 2, B, ldb, nullptr, s_w, G, bias, bias_dt, C,
+                                            ldc, M, N, K, ic_epi{});
+  return hipGetLastError();
+}
+
+// Rows per tile (256, 288 or 320) by workgroup rounds x tile area, as for the
+// INT8 big tiles.
+template <int DT, int MODE>
+hipError_t launch_w4a16_big_m(const u16* A, int64_t lda, const uint8_t* B, int64_t ldb, const float* s_w, int G,
+                            const void* bias, int bias_dt, u16* C, int64_t ldc, int M, int N, int K, hipStream_t st) {
+  const int64_t cus = ic_num_cus();
+  auto cost = [&](int bm, int pct) {
+    const int64_t t = (int64_t)((M + bm - 1) / bm) * ((N + big::BN - 1) / big::BN);
+    return (t + cus - 1) / cus * bm * pct;
+  };
+  const int64_t c9 = cost(288, 100), c8 = cost(256, 105), c10 = cost(320, 99);
+  if (c8 < c9 && c8 <= c10)
+    return launch_w4a16_big_t<DT, 8, MODE>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
+  if (c10 < c9) return launch_w4a16_big_t<DT, 10, MODE>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
+  return launch_w4a16_big_t<DT, 9, MODE>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
+}
+// the three-slot ring past K = 8192 (128 stages; at 8192 the two-slot ring
+// measured 188 against 192 us for 4096 x 3072, at 12288 316 against 356 us)
+template <int DT>
+hipError_t launch_w4a16_big(const u16* A, int64_t lda, const uint8_t* B, int64_t ldb, const float* s_w, int G,
+                            const void* bias, int bias_dt, u16* C, int64_t ldc, int M, int N, int K, hipStream_t st) {
+  if (K > 8192) return launch_w4a16_big_m<DT, big::W16L>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
+  return launch_w4a16_big_m<DT, big::W16>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
+}
+
 template <int DT>
 hipError_t run_w4a16(const u16* A, int64_t lda, const uint8_t* B, int64_t ldb, const float* s_w, int G,
                      int gsize, const void* bias, int bias_dt, u16* C, int64_t ldc, int M, int N, int K,
-                     bool mfma_ok, hipStream_t st) {
+                     bool mfma_ok, bool big_ok, hipStream_t st) {
   if (mfma_ok) {
+    if (M > 128 && big_ok) return launch_w4a16_big<DT>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
     if (M > 128) {
       // rounds of workgroups x tile area x relative cost per output: 384 x 192 tiles (wave tiles of
       // 96 x 96, a two-slot ring) where they fill the CUs in fewer rounds, e.g. 4608 x 12288: 768
@@ -381,12 +430,17 @@ int ic_gemm_w4a16(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, c
   const bool mfma_ok = (K % 64 == 0) && (G == 1 || gsize % 32 == 0) && !((uintptr_t)x & 15) &&
                        !((uintptr_t)w_packed & 15) && !((ldx * 2) & 15) && !(ldw & 15) &&
                        384 * ldx * 2 < (1LL << 31) && 256 * ldw < (1LL << 31) && N * G * 4 < (1LL << 31);
+  // the big tiles: one scale per column and 64-K stage (groups of whole
+  // stages), 320-row DMA offsets in 32 bits, and the staged output path
+  // (16-byte aligned output, row stride and N multiples of 8)
+  const bool big_ok = mfma_ok && (G == 1 || gsize % 64 == 0) && 320 * ldx * 2 < (1LL << 31) &&
+                      320 * ldw < (1LL << 31) && !((uintptr_t)out & 15) && (ldo & 7) == 0 && (N & 7) == 0;
   hipStream_t st = (hipStream_t)stream;
   hipError_t e = dtype == IC_DTYPE_F16
                      ? run_w4a16<IC_DTYPE_F16>((const u16*)x, ldx, w_packed, ldw, s_w, G, gsize, bias, bias_dtype,
-                                               (u16*)out, ldo, (int)M, (int)N, (int)K, mfma_ok, st)
+                                               (u16*)out, ldo, (int)M, (int)N, (int)K, mfma_ok, big_ok, st)
                      : run_w4a16<IC_DTYPE_BF16>((const u16*)x, ldx, w_packed, ldw, s_w, G, gsize, bias, bias_dtype,
-                                                (u16*)out, ldo, (int)M, (int)N, (int)K, mfma_ok, st);
+                                                (u16*)out, ldo, (int)M, (int)N, (int)K, mfma_ok, big_ok, st);
   if (e != hipSuccess) return ic_set_error(IC_ERR_LAUNCH, "%s: %s", who, hipGetErrorString(e));
   return IC_OK;
 }

@@ -816,6 +816,33 @@ def test_w4a16_group_sizes(rt, oracle, dev, G, M):
     assert _cos(out, ref) >= 0.9999
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("K,G", [(8192, 64), (8256, 129), (12288, 96)])  # 128, 129 and 192 stages of 64 K
+def test_w4a16_long_k_three_slot_ring(rt, oracle, dev, dtype, K, G):
+    """Long K on the big-tile W4A16 modes: K = 8192 with one DMA stage in
+    flight, K > 8192 with two (per-wave vmcnt counts at each stage top, an odd
+    and an even stage count): within fp32-accumulation tolerance of the
+    dequantized-weight product, and one-hot rows return the dequantized
+    weights bit for bit."""
+    print(f"[w4a16 long K] K={K} G={G} {dtype}", flush=True)
+    M, N = 300, 200
+    x = _acts(M, K, dtype, seed=130)
+    packed = torch.randint(0, 256, (N, K // 2), generator=_gen(131), dtype=torch.uint8)
+    s_w = (torch.rand(N, G, generator=_gen(132)) * 2e-2 + 1e-3).to(torch.float16).float()
+    bias = torch.randn(N, generator=_gen(133)).to(dtype)
+    out = rt.gemm_w4a16(x.to(dev), packed.to(dev), s_w.to(dev), bias=bias.to(dev)).float().cpu()
+    w = torch.from_numpy(oracle.dequant_w4a16(packed.numpy(), s_w.numpy(), K, DT[dtype]))
+    ref = x.float() @ w.t() + bias.float()
+    tol = 1e-2 if dtype == torch.float16 else 2e-2
+    assert torch.allclose(out, ref, rtol=tol, atol=tol * ref.abs().max().item() * 1e-2)
+    assert _cos(out, ref) >= 0.9999
+    hot = torch.zeros(M, K, dtype=dtype)
+    cols = (torch.arange(M) * 27) % K  # spread over the stages
+    hot[torch.arange(M), cols] = 1
+    out1 = rt.gemm_w4a16(hot.to(dev), packed.to(dev), s_w.to(dev)).float().cpu().numpy()
+    assert np.array_equal(out1, w.numpy()[:, cols.numpy()].T)
+
+
 def test_w4a16_row_stride_past_the_384_row_tile(rt, oracle, dev):
     """An activation row stride whose 384-row tile offsets pass 2^31 bytes
     (while 256 rows stay below) runs the scalar W4A16 kernel: correct
