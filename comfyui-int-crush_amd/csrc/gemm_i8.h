@@ -777,15 +777,20 @@ TileShape tile_choice(const GemmArgs& g, bool grouped) {
 
 // K slices for `tiles` workgroups over KT stages: minimise rounds of
 // workgroups times stages per slice plus the partials' round trip through
-// HBM (8 bytes per output and slice; ~3.6 MB per stage time).  Only when the
-// unsplit launch would leave more than half the CUs idle; 1 = no split.
-int choose_splits(int64_t tiles, int KT, int64_t M, int64_t N) {
+// HBM (8 bytes per output and slice; ~3.6 MB per stage time) and, for grouped
+// scales, the second kernel that adds the slices (~6 stage times: at M = 512,
+// N = 3072, K = 3072 the unsplit grouped W4A8 took 24.3 us on packed and 19.4
+// us on unpacked weights against 26.2 / 23.3 us split in two, and unsplit its
+// outputs are the single fold chain's).  Only when the unsplit launch would
+// leave more than half the CUs idle; 1 = no split.
+int choose_splits(int64_t tiles, int KT, int64_t M, int64_t N, bool grouped) {
   const int64_t cus = ic_num_cus();
   if (tiles * 2 > cus || KT < 8) return 1;
   double best = (double)((tiles + cus - 1) / cus) * KT;
   int bs = 1;
   for (int S = 2; S <= 16 && KT / S >= 4; ++S) {
-    const double c = (double)((tiles * S + cus - 1) / cus) * ((KT + S - 1) / S) + (double)S * M * N * 8.0 / 3.6e6;
+    const double c = (double)((tiles * S + cus - 1) / cus) * ((KT + S - 1) / S) + (double)S * M * N * 8.0 / 3.6e6 +
+                     (grouped ? 6.0 : 0.0);
     if (c < best) { best = c; bs = S; }
   }
   return bs;
@@ -794,7 +799,7 @@ int choose_splits(int64_t tiles, int KT, int64_t M, int64_t N) {
 int splitk_plan(const GemmArgs& g, bool grouped) {
   const TileShape t = tile_choice(g, grouped);
   const int64_t tiles = (int64_t)((g.M + t.bm - 1) / t.bm) * ((g.N + t.bn - 1) / t.bn);
-  return choose_splits(tiles, g.K / kBK, g.M, g.N);
+  return choose_splits(tiles, g.K / kBK, g.M, g.N, grouped);
 }
 
 template <class TL, int OUT_DT, bool ACC, bool PART, bool EPI>
