@@ -843,6 +843,22 @@ def test_w4a16_long_k_three_slot_ring(rt, oracle, dev, dtype, K, G):
     assert np.array_equal(out1, w.numpy()[:, cols.numpy()].T)
 
 
+@pytest.mark.parametrize("K,G", [(64, 1), (128, 2), (192, 3)])  # one, two and three 64-K stages
+def test_w4a16_big_tiles_short_k(rt, oracle, dev, K, G):
+    """The big-tile W4A16 mode with one to three stages (prologue, first and
+    last stage at once): within fp32-accumulation tolerance of the
+    dequantized-weight product."""
+    M, N = 200, 64
+    x = _acts(M, K, torch.float16, seed=140 + K)
+    packed = torch.randint(0, 256, (N, K // 2), generator=_gen(141), dtype=torch.uint8)
+    s_w = (torch.rand(N, G, generator=_gen(142)) * 2e-2 + 1e-3).to(torch.float16).float()
+    out = rt.gemm_w4a16(x.to(dev), packed.to(dev), s_w.to(dev)).float().cpu()
+    w = torch.from_numpy(oracle.dequant_w4a16(packed.numpy(), s_w.numpy(), K, DT[torch.float16]))
+    ref = x.float() @ w.t()
+    assert torch.allclose(out, ref, rtol=1e-2, atol=1e-2 * ref.abs().max().item() * 1e-2)
+    assert _cos(out, ref) >= 0.9999
+
+
 def test_w4a16_row_stride_past_the_384_row_tile(rt, oracle, dev):
     """An activation row stride whose 384-row tile offsets pass 2^31 bytes
     (while 256 rows stay below) runs the scalar W4A16 kernel: correct
