@@ -38,6 +38,8 @@ CASES = {
     "w4096": (4096, 4096, 4096, 256, True, True, torch.float16, None),
     "c3_noperm_r64": (4608, 12288, 12288, 64, False, True, torch.float16, None),
     "c3_plain_bf16": (4608, 12288, 12288, 256, False, False, torch.bfloat16, None),
+    "flux15360_f16": (4608, 15360, 15360, 256, True, True, torch.float16, None),
+    "flux15360_bf16": (4608, 15360, 15360, 256, True, True, torch.bfloat16, None),
     "wan_down": (32760, 13824, 14336, 1024, False, False, torch.float16, None),
     "wan5120": (32760, 5120, 5120, 1024, False, False, torch.float16, None),
     "norm3072_bf16": (4608, 3072, 3072, 256, True, True, torch.bfloat16, "layer"),

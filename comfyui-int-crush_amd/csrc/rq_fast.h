@@ -96,10 +96,17 @@ IC_DEV void block_sum2_f64(double& a, double& b, double* red) {
 // values are exact in fp64 for any realistic row).  The prep
 // then treats y as its input: the same arithmetic as the chain normalise ->
 // activation tensor -> rotate_quantize, without the tensor.
-// (a 768-thread workgroup's exchange buffer leaves LDS for one per CU, which
-// its launch bounds say)
+// (the 768-thread workgroup, and the two-tile 448 / 512-thread ones with a
+// row buffer, leave LDS for one workgroup per CU, which their launch bounds
+// say)
+template <int DT, int LOG4R, int NT, int VAR, int TH>
+constexpr int rq_fast_min_wgs() {
+  const bool wave_local = VAR == kRqPlain && LOG4R >= 3 && LOG4R <= 5 && NT <= 2;
+  if (TH >= 768 || (TH >= 448 && NT >= 2 && !wave_local)) return 1;
+  return (NT <= 3 || VAR == kRqPlain) ? 2 : 1;
+}
 template <int DT, int LOG4R, int NT, int VAR, int TH, int NORM = 0>
-__global__ __launch_bounds__(TH, (TH < 768 && (NT <= 3 || VAR == kRqPlain)) ? 2 : 1) void rq_fast_kernel(
+__global__ __launch_bounds__(TH, (rq_fast_min_wgs<DT, LOG4R, NT, VAR, TH>())) void rq_fast_kernel(
     const u16* __restrict__ x, int64_t ldx, int M, int K_in, int K_r,
     const float* __restrict__ sr_rcp, const float* __restrict__ sr_f, int K_w,
     const int32_t* __restrict__ perm, int8_t* __restrict__ q_out, int64_t ldq,
