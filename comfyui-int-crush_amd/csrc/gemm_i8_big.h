@@ -253,18 +253,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
   // bytes, at 4c of part h (swizzled by bit 3 of the row, which is bit 3 of
   // the lane), dequantized with the stage's scale of that column
   const uint32_t fw = (uint32_t)(fr_n * 32 + 4 * fr_c), fsw = (uint32_t)(((lane >> 3) & 1) << 4);
-  DeqScale dsc[TNB];
   auto load_b = [&](int kt, int j, v4i& f0, v4i& f1) {
-    if constexpr (DEQ) {
-      const char* pb = smem + (kt % NS) * SLOT + A_BYTES + j * 16 * 32 + fw;
-      const uint32_t p0 = *(const uint32_t*)(pb + fsw), p1 = *(const uint32_t*)(pb + (16u ^ fsw));
-      uint32_t w0[4], w1[4];
-      deq8<OUT_DT>(p0, dsc[j], w0);
-      deq8<OUT_DT>(p1, dsc[j], w1);
-      f0 = v4i{(int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3]};
-      f1 = v4i{(int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3]};
-      return;
-    }
     if constexpr (INT8W) {
       const char* pb = smem + (kt % NS) * SLOT + A_BYTES + j * 16 * kBK;
       f0 = *(const v4i*)(pb + fq0);
@@ -344,11 +333,6 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
     float sw[TNB], sw1[TNB];
     if constexpr (GROUPED) read_scales(kt, 0, sw);
     if constexpr (F64) read_scales(kt, 1, sw1);
-    if constexpr (DEQ) {
-      const float* sS = (const float*)(smem + (kt % NS) * SLOT + A_BYTES + B_BYTES);
-#pragma unroll
-      for (int j = 0; j < TNB; ++j) dsc[j] = deq_scale<OUT_DT>(sS[wc * WCOLS + 16 * j + (lane & 15)]);
-    }
     const char* aR0 = smem + (kt % NS) * SLOT + lds_off(wr * WROWS + (lane & 15), lane >> 4);
     const char* aR1 = smem + (kt % NS) * SLOT + lds_off(wr * WROWS + (lane & 15), 4 + (lane >> 4));
     v4i b0[TNB], b1[TNB];
@@ -401,11 +385,6 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
           else tc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1[j], tc[j], 0, 0, 0);
         }
         if (i > 0) fold_row(i - 1, t[(i - 1) & 1], t1[F64 ? ((i - 1) & 1) : 0]);
-      } else if constexpr (DEQ) {
-#pragma unroll
-        for (int j = 0; j < TNB; ++j) facc[i][j] = mfma16<OUT_DT>(a0, b0[j], facc[i][j]);
-#pragma unroll
-        for (int j = 0; j < TNB; ++j) facc[i][j] = mfma16<OUT_DT>(a1, b1[j], facc[i][j]);
       } else {
 #pragma unroll
         for (int j = 0; j < TNB; ++j) facc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0[j], facc[i][j], 0, 0, 0);
@@ -416,6 +395,94 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
       __builtin_amdgcn_sched_barrier(0);
     }
     fold_row(TMB - 1, t[(TMB - 1) & 1], t1[F64 ? ((TMB - 1) & 1) : 0]);
+  };
+
+  // One W4A16 stage (DEQ), ordered (32-K half h, column block j) outer and
+  // block row inner: the dequantization of fragment (h, j) + 1 is issued
+  // among the MFMAs of (h, j), which do not read it, so only the first of
+  // the stage's six runs with the matrix core idle (dequantizing all six
+  // before the first MFMA left the MFMA pipe idle for ~100 VALU instructions
+  // per wave and stage, on every wave at once after the stage barrier).
+  // Each output block still takes half 0 before half 1, the stages in order:
+  // the same fp32 sums as the row-outer order.  The stage's 2 x TMB activation
+  // fragments stay in registers (the second half's read in the first steps).
+  // Measured on MI355X against the row-outer order (both with one DMA row per
+  // step): C2 4608 x 12288 x 3072 f16 332 -> 323 us, bf16 341 -> 333 us,
+  // 4608 x 3072 x 12288 f16 311 -> 305 us.
+  auto mfma_stage_deq = [&](int kt) {
+    if constexpr (DEQ) {
+      const bool more = kt + LA < KT;  // uniform
+      const char* sl = smem + (kt % NS) * SLOT;
+      const float* sS = (const float*)(sl + A_BYTES + B_BYTES);
+      DeqScale d[TNB];
+      uint32_t pk[2][TNB];
+#pragma unroll
+      for (int j = 0; j < TNB; ++j) {
+        const char* pb = sl + A_BYTES + j * 16 * 32 + fw;
+        pk[0][j] = *(const uint32_t*)(pb + fsw);
+        pk[1][j] = *(const uint32_t*)(pb + (16u ^ fsw));
+      }
+#pragma unroll
+      for (int j = 0; j < TNB; ++j) d[j] = deq_scale<OUT_DT>(sS[wc * WCOLS + 16 * j + (lane & 15)]);
+      const char* aR0 = sl + lds_off(wr * WROWS + (lane & 15), lane >> 4);
+      const char* aR1 = sl + lds_off(wr * WROWS + (lane & 15), 4 + (lane >> 4));
+      v4i fa[2][TMB];
+#pragma unroll
+      for (int i = 0; i < TMB; ++i) fa[0][i] = *(const v4i*)(aR0 + i * 16 * kBK);
+      auto deq_frag = [&](int q) {
+        uint32_t w[4];
+        deq8<OUT_DT>(pk[q / TNB][q % TNB], d[q % TNB], w);
+        return v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+      };
+      v4i fb[2 * TNB];
+      fb[0] = deq_frag(0);
+#pragma unroll
+      for (int q = 0; q < 2 * TNB; ++q) {
+        const int h = q / TNB, j = q % TNB;
+        if (q == 1) {
+#pragma unroll
+          for (int i = 0; i < TMB; ++i) fa[1][i] = *(const v4i*)(aR1 + i * 16 * kBK);
+        }
+        if (q + 1 < 2 * TNB) fb[q + 1] = deq_frag(q + 1);
+#pragma unroll
+        for (int i = 0; i < TMB; ++i) facc[i][j] = mfma16<OUT_DT>(fa[h][i], fb[q], facc[i][j]);
+        // The empty volatile asm keeps the next fragment's dequantization in
+        // this step (the compiler would otherwise sink it past the DMA branch
+        // below to its first use, after the next step's DMAs).  A wave issues in
+        // order: two VALU instructions after each MFMA run while the matrix
+        // core works on it (~17 per fragment against 9 MFMAs).
+        if (q + 1 < 2 * TNB) asm volatile("" : "+v"(fb[q + 1]));
+#pragma unroll
+        for (int i = 0; i < TMB; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // two VALU
+        }
+        if (more) {
+          // The next stage's DMAs.  Two-slot ring (W16): all in the first
+          // two steps, scales and activations first, so that they have most
+          // of the stage to land before the wait at its end (measured on
+          // MI355X, against one DMA row per step: C2 4608 x 12288 x 3072
+          // f16 312 -> 300 us, bf16 323 -> 309 us, 4096 x 5120 x 5120 bf16
+          // 232 -> 224 us).  Three-slot ring (W16L): one DMA row per step
+          // (the two-step placement measured 297 -> 303 us at
+          // 4608 x 3072 x 12288 f16).
+          constexpr int nd = RT::A_PER + RT::B_PER, hd = (nd + 1) / 2;
+          static_assert(nd <= 2 * TNB, "DMA rows per W4A16 stage");
+          if constexpr (LA == 1) {
+            if (q == 0) {
+#pragma unroll
+              for (int r = 0; r < hd; ++r) dma_next(kt + 1, r);
+            } else if (q == 1) {
+#pragma unroll
+              for (int r = hd; r < nd; ++r) dma_next(kt + 1, r);
+            }
+          } else {
+            dma_next(kt + LA, q);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
   };
 
   // One stage of the 32-column fold (F32).  Per block row, the two 64-K steps
@@ -571,6 +638,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
       wait_stage(s);
       lds_barrier();  // stage s resident; every wave is done with stage s-1
       if constexpr (F32) mfma_stage32(s);
+      else if constexpr (DEQ) mfma_stage_deq(s);
       else mfma_stage(s);
     }
   } else {
