@@ -118,6 +118,10 @@ def _parse():
                          "once per weight, as the drop-in Linear does), packed in the checkpoint's order, or "
                          "unpacked to int8 (what the drop-in Linear uses for launches that fill at most half "
                          "the CUs)")
+    ap.add_argument("--w16-layout", default="staged", choices=["staged", "plain"],
+                    help="operand layout the W4A16 GEMMs read: the staged copy (stage-major weights, "
+                         "group-major scales; what the drop-in Linear keeps for launches of more than 128 "
+                         "rows) or the checkpoint's row-major packed weights and [N, G] scales")
     ap.add_argument("--rows", type=int, default=None,
                     help="override the config's M (GEMM configs; the line then names the override and "
                          "carries no committed traffic figure)")
@@ -199,7 +203,7 @@ def _time_loop(fn, n):
     return s.elapsed_time(e) / n
 
 
-def gpu_bench(cfg, inp, steps, warmup, rt, w4_order="kil"):
+def gpu_bench(cfg, inp, steps, warmup, rt, w4_order="kil", w16_layout="staged"):
     import torch
 
     dev = torch.device("cuda:0")
@@ -218,6 +222,12 @@ def gpu_bench(cfg, inp, steps, warmup, rt, w4_order="kil"):
     elif unpacked:
         ws = [rt.unpack_int4_to_int8(w, K) for w in ws]
     s_w = inp["s_w"].to(dev)
+    # W4A16: the staged operand layout the drop-in Linear keeps per layer, built
+    # once outside the timed steps (big-tile shapes only)
+    staged = (cfg["fmt"] == "w4a16" and w16_layout == "staged"
+              and rt.w4a16_staged_pays(M, N, K, s_w.reshape(N, -1).shape[1]))
+    if staged:
+        ws = [rt.w4a16_stage_layout(w, s_w) for w in ws]
     sr = rt.prepare_factors(inp["smoothrot"].to(dev), act) if inp["smoothrot"] is not None else None
     perm = rt.prepare_perm(inp["perm"].to(dev), K) if inp["perm"] is not None else None
     q = torch.empty(M, K, dtype=torch.int8, device=dev)
@@ -230,7 +240,9 @@ def gpu_bench(cfg, inp, steps, warmup, rt, w4_order="kil"):
 
     def gemm(i):
         w = ws[i % copies]
-        if cfg["fmt"] == "w4a16":
+        if staged:
+            rt.gemm_w4a16_staged(xs[i % copies], w[0], w[1], out=out)
+        elif cfg["fmt"] == "w4a16":
             rt.gemm_w4a16(xs[i % copies], w, s_w, out=out)
         elif cfg["fmt"] == "int8":
             rt.fused_int8_gemm_dequant(q, w, s_w, s_a, out_dtype=act, out=out)
@@ -650,7 +662,8 @@ def set_main(args, rt):
     for key in st["members"]:
         cfg = CONFIGS[key]
         inp = make_inputs(cfg)
-        s_ms, _wall, g_ms, p_ms, copies = gpu_bench(cfg, inp, args.steps, args.warmup, rt, args.w4_order)
+        s_ms, _wall, g_ms, p_ms, copies = gpu_bench(cfg, inp, args.steps, args.warmup, rt, args.w4_order,
+                                                      args.w16_layout)
         ops, _gb, _pb = algorithmic(cfg)
         tot_ops += ops
         step_ms += s_ms
@@ -890,7 +903,8 @@ def main():
         b.copy_(a)
         torch.cuda.synchronize()
         del a, b
-    step_ms, wall, g_ms, p_ms, copies = gpu_bench(cfg, inp, args.steps, args.warmup, rt, args.w4_order)
+    step_ms, wall, g_ms, p_ms, copies = gpu_bench(cfg, inp, args.steps, args.warmup, rt, args.w4_order,
+                                                      args.w16_layout)
     M, K, N = cfg["M"], cfg["K"], cfg["N"]
     ops, gemv_bytes, prep_bytes = algorithmic(cfg)
     is_fp = cfg["fmt"] == "w4a16"
@@ -918,7 +932,8 @@ def main():
                    "group_size": K // cfg["G"],
                    "rot_size": cfg["rot"], "smoothrot": cfg["smoothrot"], "perm": cfg["perm"],
                    "activation": cfg["act"], "input_copies": copies, "parallelism": "single GPU",
-                   **({"w4_order": args.w4_order} if cfg["fmt"] == "int4" else {})},
+                   **({"w4_order": args.w4_order} if cfg["fmt"] == "int4" else {}),
+                   **({"w16_layout": args.w16_layout} if is_fp else {})},
         "roofline": roof,
         "host_wall_ms_per_step": round(wall * 1e3 / args.steps, 5),
     }

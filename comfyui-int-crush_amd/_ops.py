@@ -152,7 +152,11 @@ class _DeviceState:
     the packed weights on the device, N x K/2 bytes per layer;
     INTCRUSH_W4_INTERLEAVE=0 keeps the checkpoint order), and unpacked once
     to int8 for the W4A8 launches that fill at most half the CUs (N x K bytes
-    per layer that meets such a launch; INTCRUSH_W4_UNPACKED=0 turns it off)."""
+    per layer that meets such a launch; INTCRUSH_W4_UNPACKED=0 turns it off),
+    and for W4A16 layers copied once to the staged layout of the big-tile
+    kernel (stage-major weights, group-major scales: N x K/2 + 4 N G bytes
+    per layer with a launch of more than 128 rows; INTCRUSH_W4A16_STAGED=0
+    turns it off)."""
 
     __slots__ = ("smoothrot", "smooth", "perm", "k_w", "k_gemm", "perm_gemm", "smooth_gemm", "_wcache")
 
@@ -176,23 +180,27 @@ class _DeviceState:
                 self.smooth_gemm = _rt.prepare_factors(torch.cat([sm.to(device), ones]), dtype)
 
     def gemm_weights(self, qdata: torch.Tensor, scale: torch.Tensor, kil: bool = False,
-                     cache: bool = True, unpack: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+                     cache: bool = True, unpack: bool = False,
+                     staged: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
         """(weights, scales) at k_gemm columns; the layer's own when no pad
         is needed.  kil (packed INT4, k_gemm a multiple of 8): the weights in
         the K-interleaved nibble order, for gemm_w4a8(..., kil=True).  unpack
         (packed INT4): the weights unpacked to int8 [N, k_gemm], for
-        gemm_w4a8_unpacked.  cache: keep the derived copy for the next call
+        gemm_w4a8_unpacked.  staged (packed INT4, k_gemm a multiple of 64):
+        weights [k_gemm/64, N, 32] and scales [G, N] for gemm_w4a16_staged.
+        cache: keep the derived copy for the next call
         (one per form), keyed by the tensors' addresses -- only for the
         layer's resident weights; a per-call cast copy (offloaded or patched
         weights) may reuse an address with other contents, so its derived
         copy is built for that call alone."""
         int4 = qdata.dtype == torch.uint8
-        unpack = unpack and int4
-        kil = kil and self.k_gemm % 8 == 0 and not unpack
-        if self.k_gemm == self.k_w and not kil and not unpack:
+        staged = staged and int4 and self.k_gemm % 64 == 0
+        unpack = unpack and int4 and not staged
+        kil = kil and self.k_gemm % 8 == 0 and not unpack and not staged
+        if self.k_gemm == self.k_w and not kil and not unpack and not staged:
             return qdata, scale
         N = qdata.shape[0]
-        form = "unpacked" if unpack else ("kil" if kil else "padded")
+        form = "staged" if staged else ("unpacked" if unpack else ("kil" if kil else "padded"))
         key = (qdata.data_ptr(), scale.data_ptr())
         hit = self._wcache.get(form) if cache else None
         if hit is None or hit[0] != key:
@@ -210,6 +218,8 @@ class _DeviceState:
                 wq = _rt.int4_interleave_k(wq)
             elif unpack:
                 wq = _rt.unpack_int4_to_int8(wq, self.k_gemm)
+            elif staged:
+                wq, sc = _rt.w4a16_stage_layout(wq, sc)
             if not cache:
                 return wq, sc
             hit = (key, wq, sc)
@@ -500,8 +510,19 @@ def make_intcrush_ops(quant_format: str, rot_size: int, use_pytorch: bool = Fals
                 x_prep = _rt.prepare_activation(x2, rot_size=self._kernel_rot(), w_in=st.k_gemm,
                                                 smoothrot=st.smoothrot, perm=st.perm_gemm)
                 b = bias if _env_flag("INTCRUSH_W4A16_BIAS") else None
-                wq, ws = st.gemm_weights(qdata, params.scale, cache=weight is self.weight)
-                out = _rt.gemm_w4a16(x_prep, wq, ws, bias=b)
+                own = weight is self.weight
+                N = qdata.shape[0]
+                G = params.scale.reshape(N, -1).shape[1]
+                if G > 1:
+                    G = st.k_gemm // (st.k_w // G)  # groups at the GEMM's (padded) width
+                if (own and _env_flag("INTCRUSH_W4A16_STAGED", "1")
+                        and _rt.w4a16_staged_pays(x_prep.shape[0], N, st.k_gemm, G)):
+                    # the layer's weights in the staged layout, built once and kept
+                    wq, ws = st.gemm_weights(qdata, params.scale, staged=True)
+                    out = _rt.gemm_w4a16_staged(x_prep, wq, ws, bias=b)
+                else:
+                    wq, ws = st.gemm_weights(qdata, params.scale, cache=own)
+                    out = _rt.gemm_w4a16(x_prep, wq, ws, bias=b)
                 if params.zp is not None:
                     self._zp_correction(out, x_prep, params.scale, params.zp)
                 out = self._apply_residuals(x, out, x_prep=x_prep)

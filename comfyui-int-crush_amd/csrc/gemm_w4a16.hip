@@ -314,13 +314,13 @@ hipError_t launch_w4a16(const u16* A, int64_t lda, const uint8_t* B, int64_t ldb
 // each wave dequantizes its own weight fragments in registers beside its
 // v_mfma_f32_16x16x32 instructions, so no dequantized tile is written to or
 // read back from LDS and a stage has one barrier.
-template <int DT, int TMB, int MODE>
+template <int DT, int TMB, int MODE, bool STG>
 hipError_t launch_w4a16_big_t(const u16* A, int64_t lda, const uint8_t* B, int64_t ldb, const float* s_w, int G,
                               const void* bias, int bias_dt, u16* C, int64_t ldc, int M, int N, int K,
                               hipStream_t st) {
   using RT = big::Rows<TMB, MODE>;
   const int tiles = ((M + RT::BM - 1) / RT::BM) * ((N + big::BN - 1) / big::BN);
-  auto kern = gemm_i8_big_kernel<DT, false, MODE, TMB>;
+  auto kern = gemm_i8_big_kernel<DT, false, MODE, TMB, STG>;
   constexpr size_t shm = RT::lds_bytes;
   static unsigned char lds_set[64];  // per device
   if (hipError_t e = ic_set_lds_limit((const void*)kern, (int)shm, lds_set)) return e;
@@ -331,7 +331,7 @@ hipError_t launch_w4a16_big_t(const u16* A, int64_t lda, const uint8_t* B, int64
 
 // Rows per tile (256, 288 or 320) by workgroup rounds x tile area, as for the
 // INT8 big tiles.
-template <int DT, int MODE>
+template <int DT, int MODE, bool STG>
 hipError_t launch_w4a16_big_m(const u16* A, int64_t lda, const uint8_t* B, int64_t ldb, const float* s_w, int G,
                             const void* bias, int bias_dt, u16* C, int64_t ldc, int M, int N, int K, hipStream_t st) {
   const int64_t cus = ic_num_cus();
@@ -341,17 +341,17 @@ hipError_t launch_w4a16_big_m(const u16* A, int64_t lda, const uint8_t* B, int64
   };
   const int64_t c9 = cost(288, 100), c8 = cost(256, 105), c10 = cost(320, 99);
   if (c8 < c9 && c8 <= c10)
-    return launch_w4a16_big_t<DT, 8, MODE>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
-  if (c10 < c9) return launch_w4a16_big_t<DT, 10, MODE>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
-  return launch_w4a16_big_t<DT, 9, MODE>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
+    return launch_w4a16_big_t<DT, 8, MODE, STG>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
+  if (c10 < c9) return launch_w4a16_big_t<DT, 10, MODE, STG>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
+  return launch_w4a16_big_t<DT, 9, MODE, STG>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
 }
 // the three-slot ring past K = 8192 (128 stages; at 8192 the two-slot ring
 // measured 188 against 192 us for 4096 x 3072, at 12288 316 against 356 us)
-template <int DT>
+template <int DT, bool STG = false>
 hipError_t launch_w4a16_big(const u16* A, int64_t lda, const uint8_t* B, int64_t ldb, const float* s_w, int G,
                             const void* bias, int bias_dt, u16* C, int64_t ldc, int M, int N, int K, hipStream_t st) {
-  if (K > 8192) return launch_w4a16_big_m<DT, big::W16L>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
-  return launch_w4a16_big_m<DT, big::W16>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
+  if (K > 8192) return launch_w4a16_big_m<DT, big::W16L, STG>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
+  return launch_w4a16_big_m<DT, big::W16, STG>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
 }
 
 template <int DT>
@@ -403,6 +403,27 @@ __global__ void unpack_fp_kernel(const uint8_t* __restrict__ P, int64_t ldp, con
   O[(int64_t)n * ldo + k] = deq1_bits<DT>(q, s_w[(int64_t)n * G + (G > 1 ? k / gsize : 0)]);
 }
 
+// Staged operand layout of the big-tile W4A16 path (gemm_i8_big_kernel with
+// KIL in a W4A16 mode): packed weights stage-major, O[(s * N + n) * 32 + b] =
+// P[n * ldp + 32 * s + b] for 64-K stage s (16 bytes per thread), and
+// scales group-major, O[g * N + n] = S[n * G + g].
+__global__ void w4a16_stage_w_kernel(const uint8_t* __restrict__ P, int64_t ldp, uint8_t* __restrict__ O, int N,
+                                     int S) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // 16-byte unit of O
+  if (idx >= (int64_t)S * N * 2) return;
+  const int64_t s = idx / (2 * (int64_t)N);
+  const int r = (int)(idx - s * 2 * N);
+  const uint4 v = *(const uint4*)(P + (int64_t)(r >> 1) * ldp + 32 * s + 16 * (r & 1));
+  *(uint4*)(O + idx * 16) = v;
+}
+
+__global__ void w4a16_stage_s_kernel(const float* __restrict__ S, float* __restrict__ O, int N, int G) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)N * G) return;
+  const int g = (int)(idx / N), n = (int)(idx % N);
+  O[idx] = S[(int64_t)n * G + g];
+}
+
 }  // namespace
 
 extern "C" {
@@ -441,6 +462,61 @@ int ic_gemm_w4a16(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, c
                                                (u16*)out, ldo, (int)M, (int)N, (int)K, mfma_ok, big_ok, st)
                      : run_w4a16<IC_DTYPE_BF16>((const u16*)x, ldx, w_packed, ldw, s_w, G, gsize, bias, bias_dtype,
                                                 (u16*)out, ldo, (int)M, (int)N, (int)K, mfma_ok, big_ok, st);
+  if (e != hipSuccess) return ic_set_error(IC_ERR_LAUNCH, "%s: %s", who, hipGetErrorString(e));
+  return IC_OK;
+}
+
+int ic_w4a16_stage_layout(const uint8_t* w_packed, int64_t N, int64_t K, int64_t ldw, const float* s_w,
+                          int64_t num_groups, uint8_t* w_staged, float* s_staged, void* stream) {
+  const char* who = "ic_w4a16_stage_layout";
+  if (N <= 0 || K <= 0 || K % 64 != 0 || ldw * 2 < K || num_groups < 1 || K % num_groups != 0 ||
+      N * num_groups >= (1LL << 31) || N * K / 32 >= (1LL << 31))
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: bad shape N=%lld K=%lld ldw=%lld groups=%lld (K a multiple of 64)",
+                        who, (long long)N, (long long)K, (long long)ldw, (long long)num_groups);
+  if (!w_packed || !s_w || !w_staged || !s_staged) return ic_set_error(IC_ERR_INVALID_ARG, "%s: null pointer", who);
+  if (((uintptr_t)w_packed & 15) || (ldw & 15) || ((uintptr_t)w_staged & 15))
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: packed rows and the staged copy must be 16-byte aligned", who);
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t units = N * K / 32;  // 16-byte units
+  w4a16_stage_w_kernel<<<dim3((unsigned)((units + 255) / 256)), dim3(256), 0, st>>>(w_packed, ldw, w_staged, (int)N,
+                                                                                    (int)(K / 64));
+  const int64_t ns = N * num_groups;
+  w4a16_stage_s_kernel<<<dim3((unsigned)((ns + 255) / 256)), dim3(256), 0, st>>>(s_w, s_staged, (int)N,
+                                                                                 (int)num_groups);
+  return ic_check_launch(who);
+}
+
+int ic_gemm_w4a16_staged(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_staged,
+                         int64_t N, const float* s_staged, int64_t num_groups, const void* bias, int bias_dtype,
+                         void* out, int64_t ldo, void* stream) {
+  const char* who = "ic_gemm_w4a16_staged";
+  if (dtype != IC_DTYPE_F16 && dtype != IC_DTYPE_BF16)
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: activation dtype must be f16/bf16", who);
+  if (M < 0 || N <= 0 || K <= 0 || ldx < K || ldo < N || num_groups < 1 || K % num_groups != 0)
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: bad shape M=%lld N=%lld K=%lld groups=%lld", who, (long long)M,
+                        (long long)N, (long long)K, (long long)num_groups);
+  if (bias && bias_dtype != IC_DTYPE_F16 && bias_dtype != IC_DTYPE_BF16 && bias_dtype != IC_DTYPE_F32)
+    return ic_set_error(IC_ERR_INVALID_ARG, "%s: bias dtype must be f16/bf16/f32", who);
+  if (M == 0) return IC_OK;
+  if (!x || !w_staged || !s_staged || !out) return ic_set_error(IC_ERR_INVALID_ARG, "%s: null pointer", who);
+  const int G = (int)num_groups, gsize = (int)(K / num_groups);
+  // the big tiles' conditions (as in ic_gemm_w4a16), and M above the GEMV
+  // and small-tile range: the staged layout has no other kernel
+  const bool ok = M > 128 && K % 64 == 0 && (G == 1 || gsize % 64 == 0) && !((uintptr_t)x & 15) &&
+                  !((uintptr_t)w_staged & 15) && !((ldx * 2) & 15) && 320 * ldx * 2 < (1LL << 31) &&
+                  N * G < (1LL << 31) && !((uintptr_t)out & 15) && (ldo & 7) == 0 && (N & 7) == 0;
+  if (!ok)
+    return ic_set_error(IC_ERR_INVALID_ARG,
+                        "%s: the staged layout needs M > 128, K and the group size multiples of 64, N and the output "
+                        "row stride multiples of 8 and 16-byte aligned operands (M=%lld N=%lld K=%lld groups=%lld); "
+                        "other shapes take ic_gemm_w4a16",
+                        who, (long long)M, (long long)N, (long long)K, (long long)num_groups);
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e = dtype == IC_DTYPE_F16
+                     ? launch_w4a16_big<IC_DTYPE_F16, true>((const u16*)x, ldx, w_staged, N * 32, s_staged, G, bias,
+                                                            bias_dtype, (u16*)out, ldo, (int)M, (int)N, (int)K, st)
+                     : launch_w4a16_big<IC_DTYPE_BF16, true>((const u16*)x, ldx, w_staged, N * 32, s_staged, G, bias,
+                                                             bias_dtype, (u16*)out, ldo, (int)M, (int)N, (int)K, st);
   if (e != hipSuccess) return ic_set_error(IC_ERR_LAUNCH, "%s: %s", who, hipGetErrorString(e));
   return IC_OK;
 }

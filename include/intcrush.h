@@ -317,6 +317,26 @@ int ic_gemm_w4a16(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, c
                   int bias_dtype, void* out, int64_t ldo, void* stream);
 
 /*
+ * Staged operand layout of the W4A16 big-tile kernel.  ic_w4a16_stage_layout
+ * copies packed INT4 weights w_packed [N, K/2] (row stride ldw, 16-byte
+ * aligned rows) and scales s_w [N, num_groups] to w_staged [K/64][N][32]
+ * (the 32 packed bytes of row n and 64-K stage s at (s * N + n) * 32) and
+ * s_staged [num_groups][N] (K a multiple of 64).  ic_gemm_w4a16_staged is
+ * ic_gemm_w4a16 on that layout: same arithmetic, results bit for bit, in
+ * fewer DMA cache-line requests per stage.  It serves the big-tile shapes
+ * only (M > 128, K and the group size multiples of 64, N and ldo multiples
+ * of 8, 16-byte aligned x, w_staged and out) and rejects the others, which
+ * take ic_gemm_w4a16.  No reference counterpart: a derived copy of the
+ * checkpoint's weights (as the K-interleaved W4A8 one), N * K/2 + 4 * N *
+ * num_groups bytes per layer, for callers that keep it beside the weights.
+ */
+int ic_w4a16_stage_layout(const uint8_t* w_packed, int64_t N, int64_t K, int64_t ldw, const float* s_w,
+                          int64_t num_groups, uint8_t* w_staged, float* s_staged, void* stream);
+int ic_gemm_w4a16_staged(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_staged,
+                         int64_t N, const float* s_staged, int64_t num_groups, const void* bias, int bias_dtype,
+                         void* out, int64_t ldo, void* stream);
+
+/*
  * Small-batch GEMV forms (1 <= M <= IC_GEMV_MAX_M tokens, K a multiple of 128
  * and <= IC_GEMV_MAX_K, 16-byte aligned operands): same arguments, same
  * arithmetic and same results as ic_gemm_w8a8 / ic_gemm_w4a8 (bit-identical)

@@ -62,6 +62,12 @@ def test_version_and_limits(rt):
                                          0, 4, None, 0, None),
     lambda L: L.ic_gemm_w4a8_unpacked_ex(None, 1, 100, 100, None, 4, 50, None, 1, None, None, 0, 0, None, 0, 0, None,
                                          0, 4, None, 0, None),
+    # staged W4A16: K not a multiple of 64; f32 activations; M in the GEMV /
+    # small-tile range (addresses that are never dereferenced: the checks
+    # run before any launch)
+    lambda L: L.ic_w4a16_stage_layout(None, 4, 96, 48, None, 1, None, None, None),
+    lambda L: L.ic_gemm_w4a16_staged(None, 2, 256, 128, 128, None, 64, None, 1, None, 0, None, 64, None),
+    lambda L: L.ic_gemm_w4a16_staged(4096, 0, 64, 128, 128, 4096, 64, 4096, 1, None, 0, 4096, 64, None),
 ])
 def test_argument_validation(rt, call):
     lib = rt.lib()

@@ -859,6 +859,46 @@ def test_w4a16_big_tiles_short_k(rt, oracle, dev, K, G):
     assert _cos(out, ref) >= 0.9999
 
 
+@pytest.mark.parametrize("M,N,K,G,dtype,bias", [
+    (300, 200, 512, 4, torch.float16, True),        # ragged M and N, two row tiles
+    (1000, 1048, 1024, 8, torch.bfloat16, False),   # N past a 192-column tile
+    (260, 64, 8256, 129, torch.float16, True),      # K > 8192: the three-slot ring; 64-column groups
+    (4096, 384, 576, 1, torch.bfloat16, True),      # per-row scales, 256-row tiles
+])
+def test_w4a16_staged_equals_plain(rt, dev, M, N, K, G, dtype, bias):
+    """The staged operand layout (w4a16_stage_layout + gemm_w4a16_staged): the
+    copy is the stated permutation of the packed weights and scales, and the
+    GEMM's outputs equal gemm_w4a16's bit for bit (the same big-tile kernel
+    and summation order, other DMA addresses)."""
+    print(f"[w4a16 staged] M={M} N={N} K={K} G={G} {dtype} bias={bias}", flush=True)
+    assert rt.w4a16_staged_pays(M, N, K, G)
+    x = _acts(M, K, dtype, seed=150).to(dev)
+    packed = torch.randint(0, 256, (N, K // 2), generator=_gen(151), dtype=torch.uint8).to(dev)
+    s_w = (torch.rand(N, G, generator=_gen(152)) * 2e-2 + 1e-3).to(dev)
+    b = torch.randn(N, generator=_gen(153)).to(dtype).to(dev) if bias else None
+    ws, ss = rt.w4a16_stage_layout(packed, s_w)
+    assert ws.shape == (K // 64, N, 32) and ss.shape == (G, N)
+    assert torch.equal(ws.permute(1, 0, 2).reshape(N, K // 2), packed)
+    assert torch.equal(ss, s_w.t())
+    ref = rt.gemm_w4a16(x, packed, s_w, bias=b)
+    out = rt.gemm_w4a16_staged(x, ws, ss, bias=b)
+    assert torch.equal(out, ref)
+
+
+def test_w4a16_staged_rule_and_rejection(rt, dev):
+    """w4a16_staged_pays admits the big-tile shapes only, and the entry point
+    rejects the rest with an error instead of running another kernel."""
+    assert rt.w4a16_staged_pays(4608, 12288, 3072, 24)
+    assert not rt.w4a16_staged_pays(128, 12288, 3072, 24)   # the GEMV / small-tile range
+    assert not rt.w4a16_staged_pays(4608, 12288, 3040, 95)  # K not a multiple of 64
+    assert not rt.w4a16_staged_pays(4608, 12288, 3072, 96)  # 32-column groups
+    assert not rt.w4a16_staged_pays(4608, 12284, 3072, 24)  # N not a multiple of 8
+    packed = torch.randint(0, 256, (64, 64), dtype=torch.uint8, device=dev)
+    ws, ss = rt.w4a16_stage_layout(packed, torch.ones(64, 1, device=dev))
+    with pytest.raises(RuntimeError):
+        rt.gemm_w4a16_staged(torch.zeros(100, 128, dtype=torch.float16, device=dev), ws, ss)
+
+
 def test_w4a16_row_stride_past_the_384_row_tile(rt, oracle, dev):
     """An activation row stride whose 384-row tile offsets pass 2^31 bytes
     (while 256 rows stay below) runs the scalar W4A16 kernel: correct

@@ -199,3 +199,35 @@ def test_dropin_linear_uses_the_unpacked_copy(dev, monkeypatch):
         assert w8.dtype == torch.int8 and w8.shape == (N, st.k_gemm)
         assert torch.equal(out, ref)
         assert lin(x) is not None and st._wcache["unpacked"][1] is w8  # built once
+
+
+def test_dropin_w4a16_uses_the_staged_copy(dev, monkeypatch):
+    """A W4A16 layer (unrotated INT4) called with more than 128 rows runs its
+    staged copy (stage-major weights, group-major scales, kept per device; for
+    K = 1000 built from the weights padded to the prepared width 1024);
+    outputs equal the row-major route's bit for bit.  Calls of at most 128
+    rows keep the row-major route and build no staged copy."""
+    ops_mod = __graft_entry__._submodule("_ops")
+    from test_gpu_ops import _to_dev, _x
+
+    for K, N, G, dtype, seed in ((1024, 192, 8, torch.bfloat16, 170), (768, 136, 6, torch.float16, 171),
+                                 (1000, 192, 1, torch.float16, 172)):
+        ops = ops_mod.make_intcrush_ops("int4_crush", 256)
+        sd = int4_layer(N, K, G=G, seed=seed)
+        lin = _to_dev(load_linear(ops, "single_blocks.0.modulation.lin", sd, K, N), dev)
+        assert not lin._intcrush_rot_need
+        small = _x(100, K, dtype, seed + 2).to(dev)
+        lin(small)
+        st = lin._intcrush_state(small)
+        assert "staged" not in st._wcache
+        x = _x(300, K, dtype, seed + 1).to(dev)
+        monkeypatch.setenv("INTCRUSH_W4A16_STAGED", "0")
+        ref = lin(x).clone()
+        assert "staged" not in st._wcache
+        monkeypatch.setenv("INTCRUSH_W4A16_STAGED", "1")
+        out = lin(x)
+        assert torch.equal(out, ref)
+        assert st.k_gemm % 64 == 0
+        ws = st._wcache["staged"][1]
+        assert ws.dtype == torch.uint8 and ws.shape == (st.k_gemm // 64, N, 32)
+        assert lin(x) is not None and st._wcache["staged"][1] is ws  # built once
