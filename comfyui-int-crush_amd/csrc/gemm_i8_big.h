@@ -218,7 +218,13 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
     const int part = (lane & 3) ^ ((lane >> 4) & 3);
     b_off[c] = (uint32_t)(min(row, N - 1 - n0) * ldb + (part << 4));
   }
-  const uint32_t s_off = (uint32_t)(min(64 * wave + lane, N - 1 - n0) * (STAGED ? 1 : G) * 4);
+  // scale DMA: a dword per lane and column, or (staged layout) one dwordx4
+  // DMA of 48 lanes over the tile's 192 contiguous scales, from wave 7, which
+  // issues the fewest activation and weight DMAs (N is a multiple of 8 there,
+  // so the clamped 4-column chunks stay in the row)
+  const uint32_t s_off = STAGED ? (uint32_t)(min(4 * lane, N - 4 - n0) * 4)
+                                : (uint32_t)(min(64 * wave + lane, N - 1 - n0) * G * 4);
+  const bool s_wave = STAGED ? wave == 7 : wave < S_WAVES;
   const int8_t* a_base = A + (int64_t)m0 * lda;
   const uint8_t* b_base = B + (int64_t)n0 * (STAGED ? 32 : ldb);
   const float* s_base = s_w + (int64_t)n0 * (STAGED ? 1 : G);
@@ -235,8 +241,11 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
             slot_of(kt) + (uint32_t)(A_BYTES + blk * 1024));
   };
   auto dma_s = [&](int kt) {
-    if (SCALED && wave < S_WAVES) {
-      if constexpr (F32) {
+    if (SCALED && s_wave) {
+      if constexpr (STAGED) {
+        if (lane < BN / 4)
+          dma16(s_off, s_base + (int64_t)(kt / bpg) * N, slot_of(kt) + (uint32_t)(A_BYTES + B_BYTES));
+      } else if constexpr (F32) {
 #pragma unroll
         for (int h = 0; h < 4; ++h)
           dma4(s_off, s_base + (4 * kt + h) / bpg,
@@ -245,8 +254,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
         dma4(s_off, s_base + (2 * kt) / bpg, slot_of(kt) + (uint32_t)(A_BYTES + B_BYTES + wave * 256));
         dma4(s_off, s_base + (2 * kt + 1) / bpg, slot_of(kt) + (uint32_t)(A_BYTES + B_BYTES + S_BYTES + wave * 256));
       } else {
-        dma4(s_off, s_base + (int64_t)(kt / bpg) * (STAGED ? N : 1),
-             slot_of(kt) + (uint32_t)(A_BYTES + B_BYTES + wave * 256));
+        dma4(s_off, s_base + kt / bpg, slot_of(kt) + (uint32_t)(A_BYTES + B_BYTES + wave * 256));
       }
     }
   };
@@ -621,7 +629,7 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
   // this wave's DMA instructions per stage (wave-uniform): with two stages in
   // flight, stage s has landed once no more than those of stage s+1 remain
   // outstanding (they retire in issue order)
-  int per_stage = (SCALED && wave < S_WAVES) ? RT::NSC : 0;
+  int per_stage = (SCALED && s_wave) ? RT::NSC : 0;
 #pragma unroll
   for (int c = 0; c < A_PER; ++c) per_stage += wave + 8 * c < A_BLOCKS;
 #pragma unroll
