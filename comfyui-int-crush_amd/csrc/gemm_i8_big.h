@@ -66,8 +66,10 @@ namespace big {
 // 16-bit activations, INT4 weights dequantized in registers to RN_dt(q *
 // RN_dt(s)) and summed in fp32 by v_mfma_f32_16x16x32_{f16,bf16} (64-K
 // stages: the same 128-byte LDS rows and 16-byte fragments as the int8
-// modes), with a two-slot ring (W16) or a three-slot one (W16L, long K)
-enum { G128 = 0, G64 = 1, ROW4 = 2, ROW8 = 3, G32 = 4, G128I8 = 5, W16 = 6, W16L = 7 };
+// modes), with a two-slot ring (W16) or a three-slot one (W16L, long K), on
+// 192-column tiles or (W16X, W16LX) 256-column ones: four 16-column blocks
+// per wave, a quarter fewer activation bytes per output
+enum { G128 = 0, G64 = 1, ROW4 = 2, ROW8 = 3, G32 = 4, G128I8 = 5, W16 = 6, W16L = 7, W16X = 8, W16LX = 9 };
 constexpr int BN = 192, NS = 2;
 constexpr int TNB = 3;                       // 16 x 16 blocks per wave in N
 constexpr int WCOLS = TNB * 16;
@@ -81,7 +83,11 @@ struct Rows {
   static constexpr int TMB = TMB_, MODE = MODE_;
   static constexpr bool GROUPED = MODE <= G64 || MODE == G32 || MODE == G128I8, F64 = MODE == G64, F32 = MODE == G32;
   static constexpr bool INT8W = MODE == ROW8 || MODE == G128I8;
-  static constexpr bool DEQ = MODE == W16 || MODE == W16L;  // W4A16: one scale row per 64-K stage, no fold
+  static constexpr bool DEQ = MODE >= W16;  // W4A16: one scale row per 64-K stage, no fold
+  static constexpr bool WIDE = MODE == W16X || MODE == W16LX;
+  // tile columns and the quantities that follow from them (hiding big::BN ...)
+  static constexpr int BN = WIDE ? 256 : big::BN;
+  static constexpr int TNB = BN / 64, WCOLS = TNB * 16, S_BYTES = BN * 4, S_WAVES = BN / 64, EPI_RS = BN + 8;
   static constexpr bool SCALED = GROUPED || DEQ;  // the slot holds scale rows
   static constexpr int KS = DEQ ? 64 : kBK;       // K values per stage
   // ring slots: W16L keeps two DMA stages in flight in a three-slot ring
@@ -89,7 +95,7 @@ struct Rows {
   // two.  Measured on MI355X: 4608 x 3072 x 12288 (one round, 192 stages)
   // 359 -> 322 us; C2 4608 x 12288 x 3072 (four rounds of 48 stages, each
   // tile paying the deeper prologue) 310 -> 319 us.
-  static constexpr int NSL = MODE == W16L ? 3 : NS;
+  static constexpr int NSL = MODE == W16L || MODE == W16LX ? 3 : NS;
   static constexpr int NSC = F32 ? 4 : (F64 ? 2 : 1);  // scale rows per stage (grouped)
   static constexpr int BM = 32 * TMB, WROWS = 16 * TMB;
   static constexpr int A_BYTES = BM * kBK;
@@ -156,6 +162,9 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
     int K, ic_epi epi) {
   using namespace big;
   using RT = Rows<TMB, MODE>;
+  // tile width and its derived quantities of this mode (hide big::BN ...)
+  constexpr int BN = RT::BN, TNB = RT::TNB, WCOLS = RT::WCOLS, S_BYTES = RT::S_BYTES, S_WAVES = RT::S_WAVES,
+                EPI_RS = RT::EPI_RS;
   constexpr int BM = RT::BM, WROWS = RT::WROWS, A_BYTES = RT::A_BYTES, A_BLOCKS = RT::A_BLOCKS;
   constexpr int A_PER = RT::A_PER, B_BYTES = RT::B_BYTES, B_BLOCKS = RT::B_BLOCKS, B_PER = RT::B_PER;
   constexpr bool GROUPED = RT::GROUPED, F64 = RT::F64, F32 = RT::F32, INT8W = RT::INT8W;
@@ -445,6 +454,10 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
       for (int j = 0; j < TNB; ++j) d[j] = deq_scale<OUT_DT>(sS[wc * WCOLS + 16 * j + (lane & 15)]);
       const char* aR0 = sl + lds_off(wr * WROWS + (lane & 15), lane >> 4);
       const char* aR1 = sl + lds_off(wr * WROWS + (lane & 15), 4 + (lane >> 4));
+      // 192-column tiles hold both halves' activation fragments; 256-column
+      // ones (144 accumulator registers) one set, each fragment re-read for
+      // the second half right after its last first-half MFMA
+      constexpr bool ONE_SET = RT::WIDE;
       v4i fa[2][TMB];
 #pragma unroll
       for (int i = 0; i < TMB; ++i) fa[0][i] = *(const v4i*)(aR0 + i * 16 * kBK);
@@ -458,13 +471,16 @@ __global__ __launch_bounds__(kNT, 1) void gemm_i8_big_kernel(
 #pragma unroll
       for (int q = 0; q < 2 * TNB; ++q) {
         const int h = q / TNB, j = q % TNB;
-        if (q == 1) {
+        if (!ONE_SET && q == 1) {
 #pragma unroll
           for (int i = 0; i < TMB; ++i) fa[1][i] = *(const v4i*)(aR1 + i * 16 * kBK);
         }
         if (q + 1 < 2 * TNB) fb[q + 1] = deq_frag(q + 1);
 #pragma unroll
-        for (int i = 0; i < TMB; ++i) facc[i][j] = mfma16<OUT_DT>(fa[h][i], fb[q], facc[i][j]);
+        for (int i = 0; i < TMB; ++i) {
+          facc[i][j] = mfma16<OUT_DT>(fa[ONE_SET ? 0 : h][i], fb[q], facc[i][j]);
+          if (ONE_SET && q == TNB - 1) fa[0][i] = *(const v4i*)(aR1 + i * 16 * kBK);
+        }
         // The empty volatile asm keeps the next fragment's dequantization in
         // this step (the compiler would otherwise sink it past the DMA branch
         // below to its first use, after the next step's DMAs).  A wave issues in

@@ -319,7 +319,7 @@ hipError_t launch_w4a16_big_t(const u16* A, int64_t lda, const uint8_t* B, int64
                               const void* bias, int bias_dt, u16* C, int64_t ldc, int M, int N, int K,
                               hipStream_t st) {
   using RT = big::Rows<TMB, MODE>;
-  const int tiles = ((M + RT::BM - 1) / RT::BM) * ((N + big::BN - 1) / big::BN);
+  const int tiles = ((M + RT::BM - 1) / RT::BM) * ((N + RT::BN - 1) / RT::BN);
   auto kern = gemm_i8_big_kernel<DT, false, MODE, TMB, STG>;
   constexpr size_t shm = RT::lds_bytes;
   static unsigned char lds_set[64];  // per device
@@ -329,29 +329,46 @@ hipError_t launch_w4a16_big_t(const u16* A, int64_t lda, const uint8_t* B, int64
   return hipGetLastError();
 }
 
-// Rows per tile (256, 288 or 320) by workgroup rounds x tile area, as for the
-// INT8 big tiles.
-template <int DT, int MODE, bool STG>
+// Tile shape by workgroup rounds x tile area x relative cost per output, as
+// for the INT8 big tiles: 256, 288 or 320 rows on 192 columns, or 256 or 288
+// rows on 256 columns (the 320 x 256 staging tile does not fit in LDS), whose
+// stages move a quarter fewer activation bytes per output: 0.95 of the
+// 192-column cost per output (measured on MI355X where both take the same
+// rounds x area, C2 4608 x 12288 x 3072: f16 297 -> 284 us, bf16 309 -> 296
+// us, bit-identical; forced onto shapes where they take more rounds x area,
+// 4608 x 3072 x 3072 75 -> 79 us, 4096 x 5120 x 5120 216 -> 258 us).
+constexpr int kW16WidePct = 95;
+template <int DT, int NARROW, int WIDE, bool STG>
 hipError_t launch_w4a16_big_m(const u16* A, int64_t lda, const uint8_t* B, int64_t ldb, const float* s_w, int G,
-                            const void* bias, int bias_dt, u16* C, int64_t ldc, int M, int N, int K, hipStream_t st) {
+                              const void* bias, int bias_dt, u16* C, int64_t ldc, int M, int N, int K, hipStream_t st) {
   const int64_t cus = ic_num_cus();
-  auto cost = [&](int bm, int pct) {
-    const int64_t t = (int64_t)((M + bm - 1) / bm) * ((N + big::BN - 1) / big::BN);
-    return (t + cus - 1) / cus * bm * pct;
+  auto cost = [&](int bm, int bn, int pct) {
+    const int64_t t = (int64_t)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+    return (t + cus - 1) / cus * bm * bn * pct;
   };
-  const int64_t c9 = cost(288, 100), c8 = cost(256, 105), c10 = cost(320, 99);
+  const int64_t c9 = cost(288, 192, 100), c8 = cost(256, 192, 105), c10 = cost(320, 192, 99);
+  const int64_t w9 = cost(288, 256, kW16WidePct), w8 = cost(256, 256, kW16WidePct * 105 / 100);
+  const int64_t cn = std::min(c9, std::min(c8, c10)), cw = std::min(w9, w8);
+  if (cw < cn) {
+    if (w8 < w9)
+      return launch_w4a16_big_t<DT, 8, WIDE, STG>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
+    return launch_w4a16_big_t<DT, 9, WIDE, STG>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
+  }
   if (c8 < c9 && c8 <= c10)
-    return launch_w4a16_big_t<DT, 8, MODE, STG>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
-  if (c10 < c9) return launch_w4a16_big_t<DT, 10, MODE, STG>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
-  return launch_w4a16_big_t<DT, 9, MODE, STG>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
+    return launch_w4a16_big_t<DT, 8, NARROW, STG>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
+  if (c10 < c9)
+    return launch_w4a16_big_t<DT, 10, NARROW, STG>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
+  return launch_w4a16_big_t<DT, 9, NARROW, STG>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
 }
 // the three-slot ring past K = 8192 (128 stages; at 8192 the two-slot ring
 // measured 188 against 192 us for 4096 x 3072, at 12288 316 against 356 us)
 template <int DT, bool STG = false>
 hipError_t launch_w4a16_big(const u16* A, int64_t lda, const uint8_t* B, int64_t ldb, const float* s_w, int G,
                             const void* bias, int bias_dt, u16* C, int64_t ldc, int M, int N, int K, hipStream_t st) {
-  if (K > 8192) return launch_w4a16_big_m<DT, big::W16L, STG>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
-  return launch_w4a16_big_m<DT, big::W16, STG>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
+  if (K > 8192)
+    return launch_w4a16_big_m<DT, big::W16L, big::W16LX, STG>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K,
+                                                              st);
+  return launch_w4a16_big_m<DT, big::W16, big::W16X, STG>(A, lda, B, ldb, s_w, G, bias, bias_dt, C, ldc, M, N, K, st);
 }
 
 template <int DT>

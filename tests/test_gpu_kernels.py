@@ -885,6 +885,31 @@ def test_w4a16_staged_equals_plain(rt, dev, M, N, K, G, dtype, bias):
     assert torch.equal(out, ref)
 
 
+@pytest.mark.parametrize("K,G", [(128, 1), (192, 3), (8320, 65)])  # two-slot ring; three-slot past K = 8192
+def test_w4a16_wide_tiles_one_hot(rt, oracle, dev, K, G):
+    """The 256-column W4A16 tiles, which the host picks at C2's row and column
+    counts (3 rounds of 288 x 256 against 4 of 288 x 192), on both rings and
+    both operand layouts: one-hot activation rows return the dequantized
+    weights bit for bit at every one of the 4608 x 12288 outputs."""
+    M, N = 4608, 12288
+    print(f"[w4a16 wide] M={M} N={N} K={K} G={G}", flush=True)
+    cols = ((torch.arange(M) * 27 + 5) % K).numpy()
+    hot = torch.zeros(M, K, dtype=torch.float16)
+    hot[torch.arange(M), torch.from_numpy(cols)] = 1
+    packed = torch.randint(0, 256, (N, K // 2), generator=_gen(160), dtype=torch.uint8)
+    s_w = (torch.rand(N, G, generator=_gen(161)) * 2e-2 + 1e-3).to(torch.float16).float()
+    # expected out[m, n] = dequant(w[n, cols[m]]): the selected nibbles packed
+    # as a K = M matrix with one scale per column, through the oracle
+    nib = (packed.numpy()[:, cols // 2] >> (4 * (cols & 1)).astype(np.uint8)) & 0xF
+    sub = (nib[:, 0::2] | (nib[:, 1::2] << 4)).astype(np.uint8)
+    s_sub = np.ascontiguousarray(s_w.numpy()[:, cols // (K // G)])
+    want = oracle.dequant_w4a16(sub, s_sub, M, DT[torch.float16]).T
+    out = rt.gemm_w4a16(hot.to(dev), packed.to(dev), s_w.to(dev))
+    assert np.array_equal(out.float().cpu().numpy(), want)
+    ws, ss = rt.w4a16_stage_layout(packed.to(dev), s_w.to(dev))
+    assert torch.equal(rt.gemm_w4a16_staged(hot.to(dev), ws, ss), out)
+
+
 def test_w4a16_staged_rule_and_rejection(rt, dev):
     """w4a16_staged_pays admits the big-tile shapes only, and the entry point
     rejects the rest with an error instead of running another kernel."""
